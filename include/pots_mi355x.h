@@ -1,0 +1,101 @@
+/* libpots_mi355x — the C ABI of the MI355X verifier and commitment engine.
+ *
+ * Everything here runs on the current HIP device (gfx950). Pointers are plain addresses; a
+ * "device" argument must be device memory of the current device, a "host" argument host
+ * memory, and an argument documented as "host or device" may be either (the library asks HIP
+ * which it is). Streams are passed as `void *` holding a hipStream_t (0 = the null stream).
+ * No entry point throws; each returns a status (POTS_E_*) or a documented value, and
+ * pots_last_error() describes the last HIP failure of the calling thread.
+ *
+ * The first group mirrors the reference's native batch (pacifai/pots-2.0,
+ * verification/commitment/native.c) entry point by entry point, so the reference's ctypes
+ * binding (verification/commitment/native.py:241-261) can load this library instead: the
+ * names, argument order and meaning are the reference's, the hashing runs on the GPU, and
+ * payloads and outputs may live in HBM. `n_threads` is accepted and ignored.
+ */
+#ifndef POTS_MI355X_H
+#define POTS_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define POTS_E_OK 0
+#define POTS_E_NOMEM (-1)   /* the reference's "out of memory, nothing written" */
+#define POTS_E_HIP (-3)     /* a HIP call failed; see pots_last_error() */
+#define POTS_E_ARG (-4)     /* an argument is out of range or inconsistent */
+
+/* Finiteness kinds (native.c:146-150): which payload values are tested for NaN/Inf. */
+#define POTS_KIND_NONE 0
+#define POTS_KIND_F32 1
+#define POTS_KIND_BF16 2
+#define POTS_KIND_F16 3
+
+/* "pots-mi355x <version> gfx950". */
+const char *pots_mi355x_version(void);
+
+/* The last HIP error message of the calling thread, or "" if none. */
+const char *pots_last_error(void);
+
+/* ---- the reference's entry points --------------------------------------------------- */
+
+/* Replaces native.c:243 pots_hash_leaves. Leaf i's digest BLAKE3(0x00 || header || payload)
+ * goes to out + 32 i, the header being hdr_buf[hdr_off[u] : + hdr_len[u]] for u = hdr_idx[i]
+ * and the payload payload_len[i] bytes at the address payload_ptr[i] (host or device memory).
+ * kind[i] selects the NaN/Inf test (POTS_KIND_*). Metadata arrays and `out` are host memory.
+ *
+ * Returns the smallest i whose payload holds a non-finite value, or n when none does; the
+ * digests before it are valid, those at or after it unspecified. Returns SIZE_MAX when a HIP
+ * call fails (nothing valid written). Synchronous. */
+size_t pots_hash_leaves(size_t n, const uint8_t *hdr_buf, const uint64_t *hdr_off,
+                        const uint32_t *hdr_len, const uint32_t *hdr_idx,
+                        const uint64_t *payload_ptr, const uint64_t *payload_len,
+                        const uint8_t *kind, uint8_t *out, uint32_t n_threads);
+
+/* Replaces native.c:299 pots_all_finite: 1 when every value of the nbytes bytes at p (host
+ * or device) is finite under `kind` (kind 0: always 1), 0 when one is NaN or Inf, a negative
+ * POTS_E_* on failure. Synchronous. */
+int pots_all_finite(const uint8_t *p, uint64_t nbytes, uint8_t kind, uint32_t n_threads);
+
+/* Replaces native.c:335 pots_merkle_tree (which returns void): the 2n - 1 node hashes of the
+ * RFC 6962 tree over n >= 1 leaf digests, pre-order (root first; for a range at p with left
+ * half of k leaves, the left child at p + 1 and the right child at p + 2k), H_node(l, r) =
+ * BLAKE3(0x01 || l || r). `leaves` (32 n bytes) and `nodes` (32 (2n - 1) bytes) are host or
+ * device memory. Returns POTS_E_*. Synchronous. */
+int pots_merkle_tree(size_t n, const uint8_t *leaves, uint8_t *nodes);
+
+/* ---- stream-ordered entry points for a transcript resident in HBM ------------------- */
+
+/* A leaf-hashing plan: the leaves' metadata uploaded once, the chunk decomposition and the
+ * per-level reduction schedule computed, and the workspace allocated. Arguments as for
+ * pots_hash_leaves, with every payload already in device memory (payload_ptr holds device
+ * addresses; the arrays themselves are host memory). The caller keeps the payloads alive and
+ * unmodified while runs of the plan are in flight. Returns POTS_E_*; *plan is set on success.
+ * Replaces the batching of verification/commitment/leaves.py:312-437. */
+int pots_leaf_plan_create(size_t n, const uint8_t *hdr_buf, const uint64_t *hdr_off,
+                          const uint32_t *hdr_len, const uint32_t *hdr_idx,
+                          const uint64_t *payload_ptr, const uint64_t *payload_len,
+                          const uint8_t *kind, void **plan);
+
+/* Enqueue the plan on `stream`: digests to d_out (device, 32 n bytes) and the smallest
+ * non-finite leaf index (or n) to *d_first_bad (device uint32). No allocation, no sync. */
+int pots_leaf_plan_run(void *plan, uint8_t *d_out, uint32_t *d_first_bad, void *stream);
+
+/* Chunks (1 KiB BLAKE3 chunks) and message bytes the plan hashes. */
+uint64_t pots_leaf_plan_chunks(const void *plan);
+uint64_t pots_leaf_plan_bytes(const void *plan);
+
+void pots_leaf_plan_destroy(void *plan);
+
+/* The RFC 6962 tree over n leaf digests already in device memory, as pots_merkle_tree,
+ * enqueued on `stream`; d_nodes (32 (2n - 1) bytes) is written in pre-order. */
+int pots_merkle_tree_async(size_t n, const uint8_t *d_leaves, uint8_t *d_nodes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POTS_MI355X_H */

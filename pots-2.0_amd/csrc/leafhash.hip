@@ -1,0 +1,531 @@
+// Leaf hashing on gfx950: H_leaf = BLAKE3(0x00 || header || payload) for every leaf of a
+// transcript in one pass over HBM, with the NaN/Inf test fused into the loads.
+//
+// Reference: verification/commitment/native.c:171-259 (pots_hash_leaves, hash_leaf,
+// leaf_worker) and verification/commitment/leaves.py:312-437 (the batching around it).
+//
+// Decomposition. Every leaf's message is cut into BLAKE3's 1 KiB chunks; one lane compresses
+// one chunk (up to 16 blocks) and writes its chaining value, or the digest itself when the
+// leaf is a single chunk. The chunk CVs of a leaf form BLAKE3's tree, which has the RFC 6962
+// shape (a run of n > 1 chunks splits at the largest power of two below n), so it is reduced
+// level by level: level l+1 node j is the parent of level-l nodes 2j and 2j+1, or node 2j
+// itself when it has no sibling. The node that covers the whole leaf gets the ROOT flag.
+//
+// Message layout in HBM. The 0x00 prefix and the tensor header are 4(1 + ndim) bytes, a whole
+// number of words, so message word w of a leaf is payload word w - H/4 and no byte shifting is
+// needed. A lane reads each 64-byte block as 16-byte aligned loads and picks its 16 words out
+// of the 20-word window with a shift SH (0..3) that is fixed per leaf; SH is a template
+// parameter so the selection is register renaming. Blocks that touch the header, the end of
+// the payload or a partial word take an edge path that patches header words in from a small
+// table and masks bytes past the end. Leaves whose header length or payload address is not
+// word aligned (records, odd views, host memory) are staged: their whole message is copied to
+// an aligned device buffer first and hashed with an empty header.
+//
+// Finiteness. A value is NaN or Inf when its exponent field is all ones. Shifting a word left
+// by 1 (the high half of a 16-bit pair, or an fp32 value) or by 17 (the low half) puts that
+// field at the top, so a running unsigned max of the shifted payload words reaches
+// 0xFF000000 (fp32, bf16) or 0xF8000000 (fp16) exactly when a non-finite value was seen.
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+#include <vector>
+
+#include "blake3_device.h"
+#include "common.h"
+
+namespace pots {
+
+struct LeafDesc {
+  uint64_t payload;    // device address of payload byte 0 (word aligned)
+  uint64_t len;        // payload bytes
+  uint32_t head_word;  // first word of this leaf's 0x00 || header in the head table
+  uint32_t head_len;   // bytes of 0x00 || header, a multiple of 4 (0 for a staged leaf)
+  uint32_t kind;       // POTS_KIND_*
+  uint32_t pad;
+};
+static_assert(sizeof(LeafDesc) == 32, "LeafDesc layout");
+
+struct LevelEntry {     // one leaf with >= 2 nodes at one reduction level
+  uint64_t in_off;      // its first node in the level's input buffer
+  uint64_t out_off;     // its first node in the level's output buffer
+  uint64_t out_first;   // its first output, counted over the level's entries
+  uint32_t n_in;        // its nodes at this level
+  uint32_t leaf;
+};
+static_assert(sizeof(LevelEntry) == 32, "LevelEntry layout");
+
+constexpr int kThreads = 256;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void finite_acc(uint32_t& acc, uint32_t w, bool halves) {
+  uint32_t hi = w << 1;
+  uint32_t lo = halves ? (w << 17) : 0u;
+  acc = max(acc, max(hi, lo));
+}
+
+template <int SH>
+__device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __restrict__ head,
+                                           uint64_t c, bool root, uint32_t cv[8],
+                                           uint32_t& acc) {
+  const uint64_t H = d.head_len;
+  const uint64_t L = H + d.len;
+  const uint64_t cstart = c * 1024u;
+  const uint64_t cbytes = min<uint64_t>(1024u, L - cstart);
+  uint32_t nb = (uint32_t)((cbytes + 63) / 64);
+  if (nb == 0) nb = 1;  // the empty message: one empty block
+  const bool halves = d.kind == POTS_KIND_BF16 || d.kind == POTS_KIND_F16;
+  const bool test = d.kind != POTS_KIND_NONE;
+  const uint64_t pbeg = d.payload, pend = d.payload + d.len;
+  b3_iv(cv);
+  for (uint32_t b = 0; b < nb; b++) {
+    const uint64_t o = cstart + 64u * b;
+    const uint64_t A = d.payload + o - H;  // address of message byte o, in payload terms
+    const uint4* A16 = reinterpret_cast<const uint4*>(A & ~uint64_t(15));
+    uint32_t m[16];
+    if (o >= H && o + 64 <= L) {
+      // Interior block: 16 payload words, the aligned window is in bounds (see header).
+      // Streamed once: nontemporal loads keep the payload from evicting reused lines.
+      const u32x4* V16 = reinterpret_cast<const u32x4*>(A16);
+      u32x4 q[5];
+#pragma unroll
+      for (int u = 0; u < 4; u++) q[u] = __builtin_nontemporal_load(V16 + u);
+      q[4] = SH ? __builtin_nontemporal_load(V16 + 4) : u32x4{0, 0, 0, 0};
+      uint32_t w[20];
+#pragma unroll
+      for (int u = 0; u < 5; u++) {
+        w[4 * u] = q[u].x;
+        w[4 * u + 1] = q[u].y;
+        w[4 * u + 2] = q[u].z;
+        w[4 * u + 3] = q[u].w;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; j++) m[j] = w[j + SH];
+      if (test) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) finite_acc(acc, m[j], halves);
+      }
+    } else {
+      uint32_t w[20];
+#pragma unroll
+      for (int u = 0; u < 5; u++) {
+        const uint64_t X = reinterpret_cast<uint64_t>(A16 + u);
+        uint4 q = make_uint4(0, 0, 0, 0);
+        if ((u < 4 || SH) && X + 16 > pbeg && X < pend) q = A16[u];
+        w[4 * u] = q.x;
+        w[4 * u + 1] = q.y;
+        w[4 * u + 2] = q.z;
+        w[4 * u + 3] = q.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const uint64_t at = o + 4u * j;  // message byte offset of this word
+        uint32_t mw = w[j + SH];
+        if (at < H) {
+          mw = head[d.head_word + (uint32_t)(at >> 2)];
+        } else if (at >= L) {
+          mw = 0;
+        } else {
+          const uint64_t rem = L - at;
+          if (rem < 4) mw &= (1u << (8 * rem)) - 1u;
+          if (test) finite_acc(acc, mw, halves);
+        }
+        m[j] = mw;
+      }
+    }
+    const uint32_t blen = (uint32_t)min<uint64_t>(64u, L > o ? L - o : 0u);
+    uint32_t flags = (b == 0 ? B3_CHUNK_START : 0u);
+    if (b == nb - 1) flags |= B3_CHUNK_END | (root ? B3_ROOT : 0u);
+    b3_compress_cv(cv, m, c, blen, flags, cv);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void chunk_kernel(
+    const LeafDesc* __restrict__ leaves, const uint64_t* __restrict__ chunk_first,
+    const uint32_t* __restrict__ blk_leaf, uint64_t n_chunks, const uint32_t* __restrict__ head,
+    uint32_t* __restrict__ cv_out, uint32_t* __restrict__ digests,
+    uint32_t* __restrict__ first_bad) {
+  const uint64_t g = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (g >= n_chunks) return;
+  uint32_t lo = blk_leaf[blockIdx.x], hi = blk_leaf[blockIdx.x + 1];
+  while (lo < hi) {  // the last leaf whose first chunk is <= g
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (chunk_first[mid] <= g) lo = mid;
+    else hi = mid - 1;
+  }
+  const uint32_t i = lo;
+  const LeafDesc d = leaves[i];
+  const uint64_t c = g - chunk_first[i];
+  const bool root = chunk_first[i + 1] - chunk_first[i] == 1;
+  const uint32_t sh = (uint32_t)((d.payload - d.head_len) >> 2) & 3u;
+  uint32_t cv[8];
+  uint32_t acc = 0;
+  switch (sh) {
+    case 0: hash_chunk<0>(d, head, c, root, cv, acc); break;
+    case 1: hash_chunk<1>(d, head, c, root, cv, acc); break;
+    case 2: hash_chunk<2>(d, head, c, root, cv, acc); break;
+    default: hash_chunk<3>(d, head, c, root, cv, acc); break;
+  }
+  if (d.kind != POTS_KIND_NONE) {
+    const uint32_t thr = d.kind == POTS_KIND_F16 ? 0xF8000000u : 0xFF000000u;
+    if (acc >= thr) atomicMin(first_bad, i);
+  }
+  uint4* dst = reinterpret_cast<uint4*>(root ? digests + 8ull * i : cv_out + 8ull * g);
+  dst[0] = make_uint4(cv[0], cv[1], cv[2], cv[3]);
+  dst[1] = make_uint4(cv[4], cv[5], cv[6], cv[7]);
+}
+
+__global__ __launch_bounds__(kThreads) void level_kernel(
+    const LevelEntry* __restrict__ ents, uint32_t n_ents, uint64_t n_out,
+    const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
+    uint32_t* __restrict__ digests) {
+  const uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= n_out) return;
+  uint32_t lo = 0, hi = n_ents - 1;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (ents[mid].out_first <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  const LevelEntry e = ents[lo];
+  const uint64_t j = t - e.out_first;
+  const uint32_t n_out_leaf = (e.n_in + 1) / 2;
+  const uint4* src = reinterpret_cast<const uint4*>(in + 8ull * (e.in_off + 2 * j));
+  uint32_t res[8];
+  if (2 * j + 1 < e.n_in) {
+    const uint4 a = src[0], b = src[1], c = src[2], dd = src[3];
+    const uint32_t l[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const uint32_t r[8] = {c.x, c.y, c.z, c.w, dd.x, dd.y, dd.z, dd.w};
+    b3_parent_cv(l, r, n_out_leaf == 1 ? B3_ROOT : 0u, res);
+  } else {
+    const uint4 a = src[0], b = src[1];
+    res[0] = a.x; res[1] = a.y; res[2] = a.z; res[3] = a.w;
+    res[4] = b.x; res[5] = b.y; res[6] = b.z; res[7] = b.w;
+  }
+  uint4* dst = reinterpret_cast<uint4*>(n_out_leaf == 1 ? digests + 8ull * e.leaf
+                                                         : out + 8ull * (e.out_off + j));
+  dst[0] = make_uint4(res[0], res[1], res[2], res[3]);
+  dst[1] = make_uint4(res[4], res[5], res[6], res[7]);
+}
+
+__global__ void fill_u32(uint32_t* p, uint32_t v) { *p = v; }
+
+// ---- host side ----------------------------------------------------------------------------
+
+struct StageCopy {  // a staged leaf: its head bytes, then its payload, into one aligned buffer
+  uint64_t dst;         // device address of the staged message
+  uint64_t head_src;    // device address of the head bytes in the metadata region
+  uint64_t head_bytes;
+  uint64_t payload_src; // payload address (host or device)
+  uint64_t payload_bytes;
+  bool host;            // payload in host memory
+};
+
+struct LevelInfo {
+  uint64_t ent_first;  // index of the level's first entry in the entry array
+  uint32_t n_ents;
+  uint64_t n_out;
+  int in_buf, out_buf;  // 0 = cv0, 1 = cv1
+};
+
+struct LeafPlan {
+  size_t n = 0;
+  uint64_t n_chunks = 0, bytes = 0;
+  bool owned = false;
+  char* base = nullptr;  // one device allocation: metadata, then workspace
+  size_t total = 0;
+  // device views
+  LeafDesc* d_leaves = nullptr;
+  uint64_t* d_chunk_first = nullptr;
+  uint32_t* d_blk_leaf = nullptr;
+  uint32_t* d_head = nullptr;
+  LevelEntry* d_levels = nullptr;
+  uint32_t* d_cv[2] = {nullptr, nullptr};
+  uint32_t n_blocks = 0;
+  std::vector<LevelInfo> levels;
+  std::vector<StageCopy> stages;
+};
+
+// Build the plan's host image and sizes. `device_only` refuses host payloads.
+static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
+                      const uint32_t* hdr_len, const uint32_t* hdr_idx,
+                      const uint64_t* payload_ptr, const uint64_t* payload_len,
+                      const uint8_t* kind, bool device_only, bool owned, LeafPlan** out) {
+  if (n == 0 || n >= 0xFFFFFFFFull) return POTS_E_ARG;
+  for (size_t i = 0; i < n; i++)
+    if (kind[i] > POTS_KIND_F16) return POTS_E_ARG;
+  LeafPlan* P = new (std::nothrow) LeafPlan;
+  if (!P) return POTS_E_NOMEM;
+  P->n = n;
+  P->owned = owned;
+
+  // Per leaf: its head bytes (0x00 || header) and whether it must be staged.
+  std::vector<LeafDesc> desc(n);
+  std::vector<uint8_t> headbytes;  // word-aligned heads of direct leaves, then staged heads
+  std::vector<uint64_t> chunk_first(n + 1);
+  std::vector<int64_t> stage_head_at(n, -1);
+  uint64_t stage_bytes = 0;
+  std::vector<uint64_t> stage_off(n, 0);
+  uint64_t nc = 0;
+  for (size_t i = 0; i < n; i++) {
+    const uint32_t u = hdr_idx[i];
+    const uint64_t hl = 1 + (uint64_t)hdr_len[u];
+    const uint64_t len = payload_len[i];
+    const uint64_t ptr = payload_ptr[i];
+    bool host = false;
+    if (len > 0) host = !is_device_pointer(reinterpret_cast<const void*>(ptr));
+    if (host && device_only) {
+      delete P;
+      return POTS_E_ARG;
+    }
+    const bool stage = host || (hl % 4) != 0 || (ptr % 4) != 0;
+    LeafDesc& d = desc[i];
+    d.kind = kind[i];
+    d.pad = 0;
+    const uint64_t at = headbytes.size();
+    headbytes.push_back(0x00);
+    headbytes.insert(headbytes.end(), hdr_buf + hdr_off[u], hdr_buf + hdr_off[u] + hdr_len[u]);
+    while (headbytes.size() % 4) headbytes.push_back(0);
+    if (!stage) {
+      d.payload = ptr;
+      d.len = len;
+      d.head_word = (uint32_t)(at / 4);
+      d.head_len = (uint32_t)hl;
+    } else {
+      stage_head_at[i] = (int64_t)at;
+      stage_off[i] = stage_bytes;
+      stage_bytes += align_up(hl + len, 16);
+      d.payload = 0;  // filled once the workspace address is known
+      d.len = hl + len;
+      d.head_word = 0;
+      d.head_len = 0;
+      P->stages.push_back(StageCopy{stage_off[i], at, hl, ptr, len, host});
+    }
+    const uint64_t L = hl + len;
+    chunk_first[i] = nc;
+    nc += std::max<uint64_t>(1, (L + 1023) / 1024);
+    P->bytes += L;
+  }
+  chunk_first[n] = nc;
+  P->n_chunks = nc;
+  if (headbytes.size() / 4 >= 0xFFFFFFFFull) {
+    delete P;
+    return POTS_E_ARG;
+  }
+
+  // Block -> first leaf table for the chunk kernel.
+  const uint64_t nblocks64 = (nc + kThreads - 1) / kThreads;
+  if (nblocks64 >= 0x7FFFFFFFull) {
+    delete P;
+    return POTS_E_ARG;
+  }
+  P->n_blocks = (uint32_t)nblocks64;
+  std::vector<uint32_t> blk_leaf(P->n_blocks + 1);
+  {
+    size_t i = 0;
+    for (uint32_t b = 0; b < P->n_blocks; b++) {
+      const uint64_t g = (uint64_t)b * kThreads;
+      while (chunk_first[i + 1] <= g) i++;
+      blk_leaf[b] = (uint32_t)i;
+    }
+    blk_leaf[P->n_blocks] = (uint32_t)(n - 1);
+  }
+
+  // Reduction levels. Level 0 nodes of leaf i sit at chunk_first[i] in cv0.
+  std::vector<LevelEntry> ents;
+  std::vector<uint64_t> n_nodes(n), off(n);
+  for (size_t i = 0; i < n; i++) {
+    n_nodes[i] = chunk_first[i + 1] - chunk_first[i];
+    off[i] = chunk_first[i];
+  }
+  uint64_t cv1_need = 0;
+  int in_buf = 0;
+  for (;;) {
+    LevelInfo li{ents.size(), 0, 0, in_buf, 1 - in_buf};
+    uint64_t out_next = 0;
+    for (size_t i = 0; i < n; i++) {
+      if (n_nodes[i] < 2) continue;
+      const uint64_t nout = (n_nodes[i] + 1) / 2;
+      LevelEntry e;
+      e.in_off = off[i];
+      e.out_off = out_next;
+      e.out_first = li.n_out;
+      e.n_in = (uint32_t)n_nodes[i];
+      e.leaf = (uint32_t)i;
+      ents.push_back(e);
+      li.n_out += nout;
+      li.n_ents++;
+      off[i] = out_next;
+      n_nodes[i] = nout;
+      out_next += nout;
+    }
+    if (li.n_ents == 0) break;
+    if (li.out_buf == 1) cv1_need = std::max(cv1_need, out_next);
+    P->levels.push_back(li);
+    in_buf = 1 - in_buf;
+  }
+
+  // One allocation: [metadata | head table | cv0 | cv1 | staging].
+  size_t at = 0;
+  auto place = [&](size_t bytes) {
+    size_t a = at;
+    at = align_up(at + bytes, 256);
+    return a;
+  };
+  const size_t o_leaves = place(n * sizeof(LeafDesc));
+  const size_t o_chunk = place((n + 1) * sizeof(uint64_t));
+  const size_t o_blk = place((P->n_blocks + 1) * sizeof(uint32_t));
+  const size_t o_head = place(std::max<size_t>(headbytes.size(), 4));
+  const size_t o_lev = place(std::max<size_t>(ents.size(), 1) * sizeof(LevelEntry));
+  const size_t meta_bytes = at;
+  const size_t o_cv0 = place(nc * 32);
+  const size_t o_cv1 = place(std::max<uint64_t>(cv1_need, 1) * 32);
+  const size_t o_stage = place(std::max<uint64_t>(stage_bytes, 16));
+  P->total = at;
+
+  int rc;
+  if (owned) {
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&P->base), P->total);
+    if (e != hipSuccess) {
+      note_hip_error(e, "hipMalloc(leaf plan)", __FILE__, __LINE__);
+      delete P;
+      return e == hipErrorOutOfMemory ? POTS_E_NOMEM : POTS_E_HIP;
+    }
+  } else {
+    void* p = nullptr;
+    if ((rc = arena_get(0, P->total, &p)) != POTS_E_OK) {
+      delete P;
+      return rc;
+    }
+    P->base = static_cast<char*>(p);
+  }
+  const uint64_t B = reinterpret_cast<uint64_t>(P->base);
+  for (size_t i = 0, s = 0; i < n; i++) {
+    if (stage_head_at[i] >= 0) {
+      desc[i].payload = B + o_stage + stage_off[i];
+      StageCopy& sc = P->stages[s++];
+      sc.dst = B + o_stage + sc.dst;
+      sc.head_src = B + o_head + sc.head_src;
+    }
+  }
+  P->d_leaves = reinterpret_cast<LeafDesc*>(P->base + o_leaves);
+  P->d_chunk_first = reinterpret_cast<uint64_t*>(P->base + o_chunk);
+  P->d_blk_leaf = reinterpret_cast<uint32_t*>(P->base + o_blk);
+  P->d_head = reinterpret_cast<uint32_t*>(P->base + o_head);
+  P->d_levels = reinterpret_cast<LevelEntry*>(P->base + o_lev);
+  P->d_cv[0] = reinterpret_cast<uint32_t*>(P->base + o_cv0);
+  P->d_cv[1] = reinterpret_cast<uint32_t*>(P->base + o_cv1);
+
+  // Upload the metadata in one copy.
+  std::vector<char> img(meta_bytes, 0);
+  memcpy(img.data() + o_leaves, desc.data(), n * sizeof(LeafDesc));
+  memcpy(img.data() + o_chunk, chunk_first.data(), (n + 1) * sizeof(uint64_t));
+  memcpy(img.data() + o_blk, blk_leaf.data(), (P->n_blocks + 1) * sizeof(uint32_t));
+  if (!headbytes.empty()) memcpy(img.data() + o_head, headbytes.data(), headbytes.size());
+  if (!ents.empty()) memcpy(img.data() + o_lev, ents.data(), ents.size() * sizeof(LevelEntry));
+  hipError_t e = hipMemcpy(P->base, img.data(), meta_bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    note_hip_error(e, "hipMemcpy(leaf plan metadata)", __FILE__, __LINE__);
+    if (owned) (void)hipFree(P->base);
+    delete P;
+    return POTS_E_HIP;
+  }
+  *out = P;
+  return POTS_E_OK;
+}
+
+static int plan_run(LeafPlan* P, uint32_t* d_digests, uint32_t* d_first_bad,
+                    hipStream_t stream) {
+  for (const StageCopy& s : P->stages) {
+    POTS_HIP(hipMemcpyAsync(reinterpret_cast<void*>(s.dst),
+                            reinterpret_cast<const void*>(s.head_src), s.head_bytes,
+                            hipMemcpyDeviceToDevice, stream));
+    if (s.payload_bytes)
+      POTS_HIP(hipMemcpyAsync(reinterpret_cast<void*>(s.dst + s.head_bytes),
+                              reinterpret_cast<const void*>(s.payload_src), s.payload_bytes,
+                              s.host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice,
+                              stream));
+  }
+  hipLaunchKernelGGL(fill_u32, dim3(1), dim3(1), 0, stream, d_first_bad, (uint32_t)P->n);
+  POTS_HIP(hipGetLastError());
+  hipLaunchKernelGGL(chunk_kernel, dim3(P->n_blocks), dim3(kThreads), 0, stream, P->d_leaves,
+                     P->d_chunk_first, P->d_blk_leaf, P->n_chunks, P->d_head, P->d_cv[0],
+                     d_digests, d_first_bad);
+  POTS_HIP(hipGetLastError());
+  for (const LevelInfo& li : P->levels) {
+    const uint64_t blocks = (li.n_out + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(level_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream,
+                       P->d_levels + li.ent_first, li.n_ents, li.n_out, P->d_cv[li.in_buf],
+                       P->d_cv[li.out_buf], d_digests);
+    POTS_HIP(hipGetLastError());
+  }
+  return POTS_E_OK;
+}
+
+static void plan_free(LeafPlan* P) {
+  if (!P) return;
+  if (P->owned && P->base) (void)hipFree(P->base);
+  delete P;
+}
+
+}  // namespace pots
+
+using namespace pots;
+
+extern "C" size_t pots_hash_leaves(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
+                                   const uint32_t* hdr_len, const uint32_t* hdr_idx,
+                                   const uint64_t* payload_ptr, const uint64_t* payload_len,
+                                   const uint8_t* kind, uint8_t* out, uint32_t n_threads) {
+  (void)n_threads;
+  if (n == 0) return 0;
+  LeafPlan* P = nullptr;
+  if (plan_build(n, hdr_buf, hdr_off, hdr_len, hdr_idx, payload_ptr, payload_len, kind,
+                 /*device_only=*/false, /*owned=*/false, &P) != POTS_E_OK)
+    return SIZE_MAX;
+  void* res = nullptr;
+  size_t bad = SIZE_MAX;
+  if (arena_get(1, 32 * n + 16, &res) == POTS_E_OK) {
+    uint32_t* d_dig = static_cast<uint32_t*>(res);
+    uint32_t* d_bad = reinterpret_cast<uint32_t*>(static_cast<char*>(res) + 32 * n);
+    uint32_t h_bad = 0;
+    if (plan_run(P, d_dig, d_bad, 0) == POTS_E_OK) {
+      hipError_t e = hipMemcpy(out, d_dig, 32 * n, hipMemcpyDeviceToHost);
+      if (e == hipSuccess) e = hipMemcpy(&h_bad, d_bad, 4, hipMemcpyDeviceToHost);
+      if (e == hipSuccess) bad = h_bad;
+      else note_hip_error(e, "hipMemcpy(digests)", __FILE__, __LINE__);
+    }
+  }
+  plan_free(P);
+  return bad;
+}
+
+extern "C" int pots_leaf_plan_create(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
+                                     const uint32_t* hdr_len, const uint32_t* hdr_idx,
+                                     const uint64_t* payload_ptr, const uint64_t* payload_len,
+                                     const uint8_t* kind, void** plan) {
+  if (!plan) return POTS_E_ARG;
+  LeafPlan* P = nullptr;
+  int rc = plan_build(n, hdr_buf, hdr_off, hdr_len, hdr_idx, payload_ptr, payload_len, kind,
+                      /*device_only=*/true, /*owned=*/true, &P);
+  if (rc == POTS_E_OK) *plan = P;
+  return rc;
+}
+
+extern "C" int pots_leaf_plan_run(void* plan, uint8_t* d_out, uint32_t* d_first_bad,
+                                  void* stream) {
+  if (!plan || !d_out || !d_first_bad) return POTS_E_ARG;
+  return plan_run(static_cast<LeafPlan*>(plan), reinterpret_cast<uint32_t*>(d_out),
+                  d_first_bad, static_cast<hipStream_t>(stream));
+}
+
+extern "C" uint64_t pots_leaf_plan_chunks(const void* plan) {
+  return plan ? static_cast<const LeafPlan*>(plan)->n_chunks : 0;
+}
+
+extern "C" uint64_t pots_leaf_plan_bytes(const void* plan) {
+  return plan ? static_cast<const LeafPlan*>(plan)->bytes : 0;
+}
+
+extern "C" void pots_leaf_plan_destroy(void* plan) { plan_free(static_cast<LeafPlan*>(plan)); }

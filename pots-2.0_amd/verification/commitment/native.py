@@ -1,0 +1,304 @@
+"""The binding to ``libpots_mi355x.so``, the gfx950 kernels behind the hot path.
+
+Reference: verification/commitment/native.py:229-368. The reference builds BLAKE3's C library
+and its ``native.c`` for the host CPU and loads them with ctypes; this module loads the HIP
+library instead, with the same class name, method names, argument meaning and errors, so its
+callers (``merkle``, ``leaves``, ``challenges``) are unchanged. Payload addresses may be HBM
+addresses; the kernels read the leaves where they lie.
+
+There is no CPU path: if the library is missing or no GPU is visible, :func:`get` raises
+``RuntimeError`` (as the reference's failed build does). :func:`enabled` and :func:`disabled`
+keep their meaning as a switch the callers can read, but this build has one implementation,
+so the hashing runs on the GPU either way.
+
+torch is imported before the library is loaded on purpose: torch ships its own HIP runtime
+with the same soname as ROCm's, and loading torch first makes this library bind to that one
+runtime instead of a second copy.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from collections.abc import Iterator, Sequence
+from contextlib import contextmanager
+from pathlib import Path
+
+import numpy as np
+import torch
+
+PACKAGE_ROOT = Path(__file__).resolve().parents[2]
+LIB_PATH = PACKAGE_ROOT / "libpots_mi355x.so"
+
+KIND_NONE, KIND_F32, KIND_BF16, KIND_F16 = 0, 1, 2, 3
+FINITE_KIND: dict[torch.dtype, int] = {
+    torch.float32: KIND_F32, torch.bfloat16: KIND_BF16, torch.float16: KIND_F16,
+    torch.int32: KIND_NONE,
+}
+
+E_OK, E_NOMEM, E_HIP, E_ARG = 0, -1, -3, -4
+_SIZE_MAX = (1 << (8 * ctypes.sizeof(ctypes.c_size_t))) - 1
+
+
+def build() -> Path:
+    """Compile the library in place (``pots-2.0_amd/build.py``)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("_pots_build", PACKAGE_ROOT / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    assert spec.loader is not None
+    spec.loader.exec_module(mod)
+    return mod.build()
+
+
+def _stream(stream: torch.cuda.Stream | None) -> ctypes.c_void_p:
+    s = torch.cuda.current_stream() if stream is None else stream
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+class NativeError(RuntimeError):
+    """A call into the library failed (a HIP error or a rejected argument)."""
+
+
+_vp, _sz, _u8, _u32, _u64, _int = (ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint8,
+                                   ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int)
+
+
+def _addr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+class Native:
+    """The loaded library."""
+
+    def __init__(self, path: Path) -> None:
+        self.path = path
+        lib = ctypes.CDLL(str(path))
+        sigs = {
+            "pots_mi355x_version": ([], ctypes.c_char_p),
+            "pots_last_error": ([], ctypes.c_char_p),
+            "pots_hash_leaves": ([_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32], _sz),
+            "pots_all_finite": ([_vp, _u64, _u8, _u32], _int),
+            "pots_merkle_tree": ([_sz, _vp, _vp], _int),
+            "pots_leaf_plan_create": ([_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                       ctypes.POINTER(_vp)], _int),
+            "pots_leaf_plan_run": ([_vp, _vp, _vp, _vp], _int),
+            "pots_leaf_plan_chunks": ([_vp], _u64),
+            "pots_leaf_plan_bytes": ([_vp], _u64),
+            "pots_leaf_plan_destroy": ([_vp], None),
+            "pots_merkle_tree_async": ([_sz, _vp, _vp, _vp], _int),
+        }
+        for name, (args, res) in sigs.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        self._lib = lib
+        self.version = lib.pots_mi355x_version().decode()
+        self.blake3_version = "spec (gfx950 kernels)"
+        self.simd_degree = 64  # lanes per wavefront, one chunk per lane
+
+    # ---- errors --------------------------------------------------------------------------
+
+    def _check(self, rc: int, what: str) -> None:
+        if rc == E_OK:
+            return
+        if rc == E_ARG:
+            raise ValueError(f"{what}: argument rejected by libpots_mi355x")
+        msg = self._lib.pots_last_error().decode()
+        raise NativeError(f"{what} failed with {rc}: {msg}")
+
+    # ---- the reference's methods ---------------------------------------------------------
+
+    def hash_leaves(self, hdr_buf: bytes, hdr_off: np.ndarray, hdr_len: np.ndarray,
+                    hdr_idx: np.ndarray, payload_ptr: np.ndarray, payload_len: np.ndarray,
+                    kind: np.ndarray, *, threads: int = 1) -> tuple[np.ndarray, int]:
+        """``(digests, first_bad)`` of native.py:286-311: leaf ``i``'s digest is
+        ``BLAKE3(0x00 ‖ header ‖ payload)``, uint8 ``[n, 32]``; ``first_bad`` is the first leaf
+        whose payload holds NaN or Inf, or ``n``. Payload addresses may be host or device
+        memory; the caller keeps them alive until the call returns."""
+        n = len(payload_ptr)
+        if not len(payload_len) == len(kind) == len(hdr_idx) == n:
+            raise ValueError("payload_ptr, payload_len, kind and hdr_idx must have one length")
+        if len(hdr_off) != len(hdr_len):
+            raise ValueError("hdr_off and hdr_len must have one length")
+        if n and (int(np.max(hdr_idx)) >= len(hdr_off)
+                  or int((np.asarray(hdr_off, dtype=np.uint64)
+                          + np.asarray(hdr_len, dtype=np.uint64)).max()) > len(hdr_buf)):
+            raise ValueError("a header index or range is out of bounds")
+        out = np.empty((n, 32), dtype=np.uint8)
+        if n == 0:
+            return out, 0
+        hb = np.frombuffer(bytes(hdr_buf) or b"\0", dtype=np.uint8)
+        arrs = [np.ascontiguousarray(x, dtype=t) for x, t in (
+            (hdr_off, np.uint64), (hdr_len, np.uint32), (hdr_idx, np.uint32),
+            (payload_ptr, np.uint64), (payload_len, np.uint64), (kind, np.uint8))]
+        bad = self._lib.pots_hash_leaves(n, _addr(hb), *map(_addr, arrs), _addr(out),
+                                         max(1, int(threads)))
+        if bad == _SIZE_MAX:
+            raise NativeError("pots_hash_leaves failed: "
+                              + self._lib.pots_last_error().decode())
+        return out, int(bad)
+
+    def all_finite(self, ptr: int, nbytes: int, kind: int, *, threads: int = 1) -> bool:
+        """Whether every value of the ``nbytes`` bytes at ``ptr`` (host or device) is finite."""
+        if nbytes < 0 or (ptr == 0 and nbytes > 0):
+            raise ValueError(f"bad buffer: ptr={ptr}, nbytes={nbytes}")
+        rc = self._lib.pots_all_finite(ptr, nbytes, kind, max(1, int(threads)))
+        if rc < 0:
+            self._check(rc, "pots_all_finite")
+        return bool(rc)
+
+    def merkle_tree(self, leaves: bytes, n: int) -> bytes:
+        """The ``2n − 1`` pre-order node hashes of the RFC 6962 tree (native.py:319-327)."""
+        if n < 1 or len(leaves) != 32 * n:
+            raise ValueError(f"need n >= 1 and 32·n bytes of leaves, got n={n}, {len(leaves)}")
+        out = ctypes.create_string_buffer(32 * (2 * n - 1))
+        self._check(self._lib.pots_merkle_tree(n, bytes(leaves), out), "pots_merkle_tree")
+        return out.raw
+
+    # ---- device-resident entry points -----------------------------------------------------
+
+    def merkle_tree_device(self, digests: torch.Tensor,
+                           stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """The pre-order node buffer, uint8 ``[2n − 1, 32]`` on the digests' device, of the
+        tree over ``digests`` (uint8 ``[n, 32]`` in HBM). Stream-ordered, no sync."""
+        if digests.dtype != torch.uint8 or digests.dim() != 2 or digests.shape[1] != 32:
+            raise ValueError("digests must be uint8 [n, 32]")
+        if not digests.is_cuda or not digests.is_contiguous():
+            raise ValueError("digests must be a contiguous GPU tensor")
+        n = digests.shape[0]
+        if n < 1:
+            raise ValueError("a Merkle tree needs at least one leaf")
+        nodes = torch.empty(2 * n - 1, 32, dtype=torch.uint8, device=digests.device)
+        self._check(self._lib.pots_merkle_tree_async(n, digests.data_ptr(), nodes.data_ptr(),
+                                                     _stream(stream)), "pots_merkle_tree_async")
+        return nodes
+
+    def leaf_plan(self, headers: Sequence[bytes], payloads: Sequence[torch.Tensor],
+                  kinds: Sequence[int]) -> LeafPlan:
+        """A reusable hashing plan over GPU-resident payloads: leaf ``i`` is
+        ``BLAKE3(0x00 ‖ headers[i] ‖ payload bytes of payloads[i])``."""
+        return LeafPlan(self, headers, payloads, kinds)
+
+
+class LeafPlan:
+    """``pots_leaf_plan_*``: metadata uploaded once, then :meth:`run` enqueues the hashing of
+    every leaf on a stream with no allocation and no host sync."""
+
+    def __init__(self, lib: Native, headers: Sequence[bytes], payloads: Sequence[torch.Tensor],
+                 kinds: Sequence[int]) -> None:
+        n = len(payloads)
+        if not (len(headers) == len(kinds) == n) or n == 0:
+            raise ValueError("one header and one kind per payload, at least one leaf")
+        self._lib = lib
+        self._keep = list(payloads)
+        uniq: dict[bytes, int] = {}
+        idx = np.empty(n, dtype=np.uint32)
+        for i, h in enumerate(headers):
+            idx[i] = uniq.setdefault(bytes(h), len(uniq))
+        hdrs = list(uniq)
+        hdr_len = np.array([len(h) for h in hdrs], dtype=np.uint32)
+        hdr_off = np.zeros(len(hdrs), dtype=np.uint64)
+        if len(hdrs) > 1:
+            hdr_off[1:] = np.cumsum(hdr_len[:-1], dtype=np.uint64)
+        hb = np.frombuffer(b"".join(hdrs) or b"\0", dtype=np.uint8)
+        ptr = np.empty(n, dtype=np.uint64)
+        ln = np.empty(n, dtype=np.uint64)
+        for i, t in enumerate(payloads):
+            if not (t.is_cuda and t.is_contiguous()):
+                raise ValueError(f"payload {i} must be a contiguous GPU tensor")
+            ptr[i], ln[i] = t.data_ptr(), t.nbytes
+        kd = np.asarray(kinds, dtype=np.uint8)
+        h = ctypes.c_void_p()
+        lib._check(lib._lib.pots_leaf_plan_create(n, _addr(hb), _addr(hdr_off), _addr(hdr_len),
+                                                  _addr(idx), _addr(ptr), _addr(ln), _addr(kd),
+                                                  ctypes.byref(h)), "pots_leaf_plan_create")
+        self._h = h
+        self.n = n
+        self.chunks = int(lib._lib.pots_leaf_plan_chunks(h))
+        self.bytes = int(lib._lib.pots_leaf_plan_bytes(h))
+        self.device = payloads[0].device
+
+    def run(self, out: torch.Tensor | None = None, bad: torch.Tensor | None = None,
+            stream: torch.cuda.Stream | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """Enqueue the hashing: ``(digests uint8 [n, 32], first_bad int32 [1])`` on the GPU."""
+        if out is None:
+            out = torch.empty(self.n, 32, dtype=torch.uint8, device=self.device)
+        if bad is None:
+            bad = torch.empty(1, dtype=torch.int32, device=self.device)
+        if out.shape != (self.n, 32) or out.dtype != torch.uint8 or not out.is_contiguous():
+            raise ValueError("out must be contiguous uint8 [n, 32]")
+        self._lib._check(self._lib._lib.pots_leaf_plan_run(self._h, out.data_ptr(),
+                                                           bad.data_ptr(), _stream(stream)),
+                         "pots_leaf_plan_run")
+        return out, bad
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            self._lib._lib.pots_leaf_plan_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+_LIB: Native | None = None
+_LOCK = threading.Lock()
+
+
+def get() -> Native:
+    """The library, loaded once per process. Raises ``RuntimeError`` when it is missing or no
+    GPU is visible: this build has no CPU fallback."""
+    global _LIB
+    with _LOCK:
+        if _LIB is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(f"{LIB_PATH} is missing: build it with "
+                                   "`python pots-2.0_amd/build.py` (hipcc, gfx950)")
+            if not torch.cuda.is_available():
+                raise RuntimeError("libpots_mi355x needs a GPU and none is visible")
+            torch.cuda.init()
+            _LIB = Native(LIB_PATH)
+        return _LIB
+
+
+_disabled = 0
+_disabled_lock = threading.Lock()
+
+
+def enabled() -> bool:
+    """False inside :func:`disabled`. Kept for the reference's callers; the GPU library is
+    used either way."""
+    return _disabled == 0
+
+
+@contextmanager
+def disabled() -> Iterator[None]:
+    """Make :func:`enabled` return False inside the block. Nestable."""
+    global _disabled
+    with _disabled_lock:
+        _disabled += 1
+    try:
+        yield
+    finally:
+        with _disabled_lock:
+            _disabled -= 1
+
+
+def describe() -> dict[str, object]:
+    """The library this process uses, for an environment record. Never builds."""
+    out: dict[str, object] = {"enabled": enabled(), "library": None, "version": None,
+                              "error": None}
+    try:
+        lib = _LIB
+        if lib is None:
+            if not LIB_PATH.exists():
+                return out
+            out["library"] = LIB_PATH.name
+            return out
+        out.update(library=Path(lib.path).name, version=lib.version)
+    except Exception as e:
+        out["error"] = f"{type(e).__name__}: {e}"
+    return out

@@ -1,0 +1,192 @@
+"""The declared computation ``C``: the transcript layout and the product inventory.
+
+Reference: verification/computation/interface.py:60-330. Only the layout contract the hot
+path needs is kept: ``ProductSpec`` (which leaf is ``P_m``, its shapes, its challenge width),
+the leaf order ``[records n_s | W_t n_w | P_1..P_M | W_{t+1} n_w]`` and the index helpers.
+The model replay that rebuilds operands is not part of this build; check 5 takes its
+operands from a :class:`Replay` the caller supplies.
+"""
+
+from __future__ import annotations
+
+import abc
+import enum
+from collections.abc import Sequence
+from dataclasses import dataclass
+from functools import cached_property
+from typing import Any
+
+import torch
+
+HOST = torch.device("cpu")
+
+
+class ProductKind(enum.Enum):
+    FORWARD = "forward"
+    WEIGHT_GRAD = "weight_grad"
+    INPUT_GRAD = "input_grad"
+    OPERAND_GRAD = "operand_grad"
+
+
+@dataclass(frozen=True)
+class ProductSpec:
+    """One product ``P_m = A·B`` of the inventory.
+
+    ``member`` is the ``(s, h)`` index of one member of a batched attention product, or
+    ``None``. ``bias`` names the declared weight ``b`` the same op adds (``P = A·B + 1·bᵀ``);
+    check 5 then checks ``[A | 1]·[B ; bᵀ]`` and ``q`` is one greater.
+    """
+
+    m: int
+    name: str
+    kind: ProductKind
+    a_shape: tuple[int, int]
+    b_shape: tuple[int, int]
+    weight: str | None = None
+    layer: int | None = None
+    member: tuple[int, ...] | None = None
+    bias: str | None = None
+
+    def __post_init__(self) -> None:
+        if self.m < 1:
+            raise ValueError(f"{self.name}: m must be 1-based, got {self.m}")
+        if len(self.a_shape) != 2 or len(self.b_shape) != 2:
+            raise ValueError(f"{self.name}: operands must be matrices")
+        if self.a_shape[1] != self.b_shape[0]:
+            raise ValueError(f"{self.name}: A {self.a_shape} and B {self.b_shape} don't chain")
+
+    @property
+    def p_shape(self) -> tuple[int, int]:
+        return (self.a_shape[0], self.b_shape[1])
+
+    @property
+    def q(self) -> int:
+        """Contracted length of the checked matmul (one more with a bias)."""
+        return self.a_shape[1] + (self.bias is not None)
+
+    @property
+    def width(self) -> int:
+        """Challenge length: the column count of ``P``."""
+        return self.b_shape[1]
+
+
+class Replay(abc.ABC):
+    """The operands of each product, as the verifier serves them to check 5."""
+
+    @abc.abstractmethod
+    def operands(self, m: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """``(A_m, B_m)`` of product ``m``."""
+
+    def operand_group(self, ms: Sequence[int],
+                      dtype: torch.dtype | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """The operands of products ``ms`` (one shape) stacked ``[len(ms), ·, ·]``."""
+        pairs = [self.operands(m) for m in ms]
+        a = torch.stack([p[0] for p in pairs])
+        b = torch.stack([p[1] for p in pairs])
+        if dtype is not None:
+            a, b = a.to(dtype), b.to(dtype)
+        return a, b
+
+
+class DeclaredComputation(abc.ABC):
+    """The layout and inventory of one step's transcript."""
+
+    @property
+    @abc.abstractmethod
+    def n_s(self) -> int:
+        """Records (sequences) per step."""
+
+    @property
+    @abc.abstractmethod
+    def weight_names(self) -> tuple[str, ...]:
+        ...
+
+    @property
+    @abc.abstractmethod
+    def weight_shapes(self) -> dict[str, tuple[int, ...]]:
+        ...
+
+    @property
+    @abc.abstractmethod
+    def products(self) -> tuple[ProductSpec, ...]:
+        ...
+
+    @property
+    def weight_dtype(self) -> torch.dtype:
+        return torch.float32
+
+    @property
+    def product_dtype(self) -> torch.dtype:
+        return torch.float32
+
+    @property
+    def operand_dtype(self) -> torch.dtype:
+        return self.product_dtype
+
+    def encode_record(self, record: Any) -> bytes:
+        from setup.records import encode_record
+        return encode_record(record)
+
+    def product_class(self, spec: ProductSpec) -> str:
+        """The κ class of a product; by default its kind and role with layer digits masked."""
+        import re
+        role = spec.weight if spec.weight is not None else spec.name
+        return f"{spec.kind.value}:{re.sub(r'[0-9]+', '*', role)}"
+
+    @property
+    def M(self) -> int:
+        return len(self.products)
+
+    @property
+    def n_w(self) -> int:
+        return len(self.weight_names)
+
+    @property
+    def n_leaves(self) -> int:
+        return self.n_s + 2 * self.n_w + self.M
+
+    def product(self, m: int) -> ProductSpec:
+        if not 1 <= m <= self.M:
+            raise IndexError(f"product m={m} outside 1..{self.M}")
+        return self.products[m - 1]
+
+    @cached_property
+    def _weight_pos(self) -> dict[str, int]:
+        return {n: i for i, n in enumerate(self.weight_names)}
+
+    def record_index(self, i: int) -> int:
+        if not 0 <= i < self.n_s:
+            raise IndexError(f"record {i} outside 0..{self.n_s - 1}")
+        return i
+
+    def w_t_index(self, name: str) -> int:
+        return self.n_s + self._weight_pos[name]
+
+    def product_index(self, m: int) -> int:
+        self.product(m)
+        return self.n_s + self.n_w + m - 1
+
+    def w_next_index(self, name: str) -> int:
+        return self.n_s + self.n_w + self.M + self._weight_pos[name]
+
+    def validate(self) -> None:
+        """Raise ``ValueError`` if the declaration is internally inconsistent."""
+        names = self.weight_names
+        if len(set(names)) != len(names):
+            raise ValueError("duplicate weight names")
+        if set(self.weight_shapes) != set(names):
+            raise ValueError("weight_shapes keys differ from weight_names")
+        for i, p in enumerate(self.products, start=1):
+            if p.m != i:
+                raise ValueError(f"product {p.name} has m={p.m} at position {i}")
+            if p.q < 2:
+                raise ValueError(f"product {p.name} has q={p.q}; a q=1 product is glue")
+            if p.weight is not None and p.weight not in self._weight_pos:
+                raise ValueError(f"product {p.name} names unknown weight {p.weight}")
+            if p.bias is not None:
+                if p.bias not in self._weight_pos:
+                    raise ValueError(f"product {p.name} names unknown bias {p.bias}")
+                if p.member is not None:
+                    raise ValueError(f"member product {p.name} names a bias")
+                if tuple(self.weight_shapes[p.bias]) != (p.width,):
+                    raise ValueError(f"bias {p.bias} of {p.name} is not of P's width")

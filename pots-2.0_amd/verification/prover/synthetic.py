@@ -1,0 +1,97 @@
+"""A synthetic training-step transcript, resident in HBM, for benchmarks and tests.
+
+Reference: the transcript the prover commits (verification/prover/step.py:171-269) holds the
+batch records, ``W_t``, every matmul output ``P_m`` and ``W_{t+1}`` in the layout of the
+declared computation. This module builds one with the declared shapes and dtypes without
+running the model: each product's operands ``A_m, B_m`` are drawn i.i.d. normal (``B`` scaled
+by ``1/√q`` so ``P`` stays O(1)), in the compute dtype, and ``P_m = A_m·B_m (+ 1·bᵀ)`` is
+computed by torch on the GPU with fp32 accumulation and rounded to the compute dtype, as a
+bf16-autocast step stores it. Attention members of one layer and role are generated and
+multiplied as one stacked batch. ``W_{t+1} = W_t − η·G`` with a synthetic gradient.
+
+The verifier's work per product (hash the leaf, measure ``A(B·r) − P·r``) depends only on
+shapes and dtypes, so the timings equal a real step's; the values are not a trained model's.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from setup.records import Record
+from verification.computation.interface import DeclaredComputation, ProductSpec
+
+
+@dataclass
+class SyntheticStep:
+    c: DeclaredComputation
+    leaves: list
+    operands: dict[int, tuple[torch.Tensor, torch.Tensor]] = field(default_factory=dict)
+
+    def product(self, m: int) -> torch.Tensor:
+        return self.leaves[self.c.product_index(m)]
+
+    def w_t(self, name: str) -> torch.Tensor:
+        return self.leaves[self.c.w_t_index(name)]
+
+
+def _runs(c: DeclaredComputation) -> list[list[ProductSpec]]:
+    """Consecutive products of one layer, member flag and shape pair, generated together."""
+    out: list[list[ProductSpec]] = []
+    for s in c.products:
+        if out and s.member is not None and out[-1][0].member is not None \
+                and out[-1][0].layer == s.layer and out[-1][0].a_shape == s.a_shape \
+                and out[-1][0].b_shape == s.b_shape and out[-1][0].name.split("[")[0] \
+                == s.name.split("[")[0]:
+            out[-1].append(s)
+        else:
+            out.append([s])
+    return out
+
+
+@torch.no_grad()
+def synthetic_step(c: DeclaredComputation, *, seed: int = 0, device: str = "cuda",
+                   operands: bool = True, eta: float = 1e-4) -> SyntheticStep:
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    cg = torch.Generator().manual_seed(seed)
+    dt = c.product_dtype
+    leaves: list = []
+    n_tok = getattr(c, "n", 16)
+    n_v = getattr(c, "n_v", 1000)
+    for _ in range(c.n_s):
+        ids = torch.randint(0, n_v, (n_tok,), generator=cg, dtype=torch.int32)
+        leaves.append(Record(ids, torch.roll(ids, -1), torch.ones(n_tok, dtype=torch.int32)))
+    w_t = {}
+    for name in c.weight_names:
+        shape = c.weight_shapes[name]
+        w = torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+        w.mul_(0.02 if len(shape) == 2 else 1.0)
+        w_t[name] = w
+        leaves.append(w)
+    ops: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+    for run in _runs(c):
+        s0 = run[0]
+        (n, q), (_, w) = s0.a_shape, s0.b_shape
+        k = len(run)
+        a = torch.randn(k, n, q, generator=g, device=dev, dtype=torch.float32).to(dt)
+        b = torch.randn(k, q, w, generator=g, device=dev, dtype=torch.float32)
+        b = b.mul_(q ** -0.5).to(dt)
+        if k == 1:
+            acc = torch.matmul(a[0].float(), b[0].float()) if dt == torch.float32 else \
+                torch.matmul(a[0], b[0]).float()
+            if s0.bias is not None:
+                acc += w_t[s0.bias].to(dt).float()
+            ps = [acc.to(dt)]
+        else:
+            ps = list(torch.bmm(a.contiguous(), b.contiguous()).unbind(0))
+        for i, spec in enumerate(run):
+            leaves.append(ps[i].contiguous())
+            if operands:
+                ops[spec.m] = (a[i], b[i])
+        del a, b
+    for name in c.weight_names:
+        w = w_t[name]
+        leaves.append(w - eta * torch.randn(w.shape, generator=g, device=dev))
+    return SyntheticStep(c, leaves, ops)

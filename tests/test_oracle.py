@@ -1,0 +1,335 @@
+"""The CPU oracle against the reference's known answers, BLAKE3's published vectors, an
+independent second implementation, and the closed forms the mathematics fixes.
+
+These pin the oracle before it is trusted as the GPU kernels' checker: a dropped flag, a
+wrong permutation word, a tree split off by one, a byte-order slip in the label or the entry
+map, or a transposed challenge matrix fails at least one test here.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import blake3_tree
+import oracle as O
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+KA = json.loads((GOLDEN / "blake3_known_answers.json").read_text())
+
+
+def seq(n: int) -> bytes:
+    return bytes(i % 251 for i in range(n))
+
+
+# ---- BLAKE3 --------------------------------------------------------------------------------
+
+def test_reference_keyed_known_answer():
+    ref = KA["reference"]["keyed_empty"]
+    key = ref["key_ascii"].encode()
+    assert O.blake3(b"", key=key).hex() == ref["digest"]
+    assert blake3_tree.blake3(b"", key=key).hex() == ref["digest"]
+
+
+def test_reference_xof_known_answer():
+    ref = KA["reference"]["xof_label"]
+    key, msg = bytes.fromhex(ref["key_hex"]), bytes.fromhex(ref["input_hex"])
+    assert msg == O.encode_label(1, 1)
+    assert O.blake3(msg, key=key, length=16).hex() == ref["xof16"]
+    assert blake3_tree.blake3(msg, key=key, length=16).hex() == ref["xof16"]
+    r = O.challenge_matrices(key, [1], 1, 4)[0, :, 0]
+    assert r.tolist() == [x / 2**24 for x in ref["numerators"]]
+    assert [f"{v:08x}" for v in r.numpy().view(np.uint32)] == ref["fp32_bits"]
+
+
+def test_reference_merkle_abc_known_answer():
+    ref = KA["reference"]["merkle_abc"]
+    hs = [O.hash_leaf(x.encode()) for x in ref["leaves_ascii"]]
+    assert O.merkle_root(hs).hex() == ref["root"]
+    assert O.merkle_root_recursive(hs).hex() == ref["root"]
+    assert O.hash_node(O.hash_node(hs[0], hs[1]), hs[2]).hex() == ref["root"]
+
+
+@pytest.mark.parametrize("n", sorted(int(k) for k in KA["published"]))
+def test_published_vectors(n):
+    want = KA["published"][str(n)]
+    assert O.blake3(seq(n)).hex() == want
+    assert blake3_tree.blake3(seq(n)).hex() == want
+
+
+LENGTHS = [0, 1, 63, 64, 65, 1023, 1024, 1025, 2047, 2048, 2049, 3072, 4096, 5000, 8193,
+           16385, 40000]
+
+
+@pytest.mark.parametrize("n", LENGTHS)
+def test_two_implementations_agree(n):
+    data = np.random.default_rng(n).integers(0, 256, n, dtype=np.uint8).tobytes()
+    assert O.blake3(data) == blake3_tree.blake3(data)
+    key = bytes(range(32))
+    assert O.blake3(data, key=key, length=100) == blake3_tree.blake3(data, key=key, length=100)
+
+
+@pytest.mark.parametrize("seek", [0, 1, 63, 64, 65, 1000])
+def test_xof_seek_is_a_window_of_the_stream(seek):
+    key, msg = bytes(range(32)), O.encode_label(7, 3)
+    whole = O.blake3(msg, key=key, length=seek + 200)
+    assert O.blake3(msg, key=key, length=200, seek=seek) == whole[seek:]
+    assert blake3_tree.blake3(msg, key=key, length=200, seek=seek) == whole[seek:]
+
+
+def test_golden_leaf_digests_match_the_oracle():
+    import sys
+    sys.path.insert(0, str(GOLDEN))
+    from payloads import DTYPES, payload
+    for e in json.loads((GOLDEN / "leaf_digests.json").read_text()):
+        t = payload(tuple(e["shape"]), DTYPES[e["dtype"]], e["seed"])
+        assert O.tensor_leaf_hash(e["tag"], t).hex() == e["digest"], e
+
+
+def test_hash_leaves_first_bad_and_kinds():
+    ts = [torch.randn(300) for _ in range(10)]
+    ts[6][17] = float("nan")
+    ts[3][0] = float("-inf")
+    items = [(O.tensor_leaf_header(3, t), t, 1) for t in ts]
+    digests, bad = O.hash_leaves(items)
+    assert bad == 3
+    assert digests[:3] == [O.tensor_leaf_hash(3, t) for t in ts[:3]]
+    # kind 0 (int32 leaves) never tests
+    _, bad = O.hash_leaves([(b"", ts[3], 0)])
+    assert bad == 1
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_half_kinds_flag_either_half_of_a_word(dtype):
+    kind = O.FINITE_KIND[dtype]
+    for pos in (0, 1, 6, 7):
+        t = torch.ones(8, dtype=dtype)
+        t[pos] = float("inf")
+        assert not O.all_finite(t)
+        _, bad = O.hash_leaves([(b"", t, kind)])
+        assert bad == 0
+    t = torch.full((5,), -0.0, dtype=dtype)
+    assert O.all_finite(t)
+
+
+# ---- leaf encoding -------------------------------------------------------------------------
+
+def test_encoding_literals():
+    ref = KA["reference"]
+    assert O.tensor_leaf_header(O.TAG_WEIGHT, torch.zeros(3, 70000)).hex() == \
+        ref["header_3x70000_f32_weight_hex"]
+    t = torch.tensor([1.0])
+    assert (O.tensor_leaf_header(O.TAG_PRODUCT, t) + O.payload_bytes(t)).hex() == \
+        ref["product_leaf_1p0_hex"]
+
+
+def test_record_encoding_layout():
+    ids = torch.tensor([1, 2, 3], dtype=torch.int32)
+    b = O.encode_record(ids, ids + 1, torch.ones(3, dtype=torch.int32))
+    assert b[:6] == bytes([0x01, 0x10, 0, 0, 0, 3]) and len(b) == 6 + 12 * 3
+    assert struct.unpack("<3i", b[6:18]) == (1, 2, 3)
+
+
+# ---- Merkle tree ---------------------------------------------------------------------------
+
+def _leaves(n):
+    return [O.hash_leaf(i.to_bytes(4, "big")) for i in range(n)]
+
+
+@pytest.mark.parametrize("n", [*range(1, 71), 127, 128, 129, 1000])
+def test_tree_matches_recursive_definition(n):
+    hs = _leaves(n)
+    nodes = O.merkle_tree(hs)
+    assert len(nodes) == 32 * (2 * n - 1)
+    assert nodes[:32] == O.merkle_root_recursive(hs)
+
+    def walk(lo, hi, p):  # every pre-order slot holds its range's recursive root
+        assert nodes[32 * p:32 * p + 32] == O.merkle_root_recursive(hs[lo:hi])
+        if hi - lo > 1:
+            k = 1 << ((hi - lo - 1).bit_length() - 1)
+            walk(lo, lo + k, p + 1)
+            walk(lo + k, hi, p + 2 * k)
+    if n <= 70:
+        walk(0, n, 0)
+
+
+def test_promotion_not_duplication():
+    a, b, c = _leaves(3)
+    assert O.merkle_root([a, b, c]) == O.hash_node(O.hash_node(a, b), c)
+    assert O.merkle_root([a, b, c]) != O.merkle_root([a, b, c, c])
+
+
+@pytest.mark.parametrize("n", range(1, 41))
+def test_audit_paths_verify(n):
+    hs = _leaves(n)
+    nodes = O.merkle_tree(hs)
+    root = nodes[:32]
+
+    def path(i):
+        out, lo, hi, p = [], 0, n, 0
+        while hi - lo > 1:
+            k = 1 << ((hi - lo - 1).bit_length() - 1)
+            if i < lo + k:
+                out.append(nodes[32 * (p + 2 * k):32 * (p + 2 * k) + 32])
+                p, hi = p + 1, lo + k
+            else:
+                out.append(nodes[32 * (p + 1):32 * (p + 1) + 32])
+                p, lo = p + 2 * k, lo + k
+        return out[::-1]
+    for i in range(n):
+        pth = path(i)
+        assert O.verify_path(hs[i], i, n, pth, root)
+        assert not O.verify_path(hs[(i + 1) % n] if n > 1 else b"\0" * 32, i, n, pth, root)
+        for k in range(len(pth)):  # a flipped bit anywhere in the path fails
+            bad = list(pth)
+            bad[k] = bytes([bad[k][0] ^ 1]) + bad[k][1:]
+            assert not O.verify_path(hs[i], i, n, bad, root)
+        assert not O.verify_path(hs[i], i, n, pth + [hs[0]], root)
+        if n > 1:
+            assert not O.verify_path(hs[i], (i + 1) % n, n, pth, root)
+
+
+# ---- challenges ----------------------------------------------------------------------------
+
+def test_entry_map_exhaustive_grid():
+    grid = 1 << 24
+    a = np.arange(grid, dtype=np.uint32)
+    low = np.random.default_rng(0).integers(0, 256, size=grid, dtype=np.uint32)
+    r = O.entries((a << 8) | low)
+    ref = (2 * a.astype(np.float64) + 1 - grid) / grid
+    assert np.array_equal(r.astype(np.float64), ref)          # exact in fp32
+    assert np.array_equal(r[grid - 1 - a.astype(np.int64)], -r)  # symmetric grid
+    assert np.array_equal(O.entries(a << 8), r)               # the low byte is discarded
+
+
+@pytest.mark.parametrize("width", [1, 5, 16, 17, 256, 257, 1000, 4096])
+@pytest.mark.parametrize("k", [1, 3, 9])
+def test_challenge_matrices_equal_per_vector_xof(width, k):
+    h = bytes(range(32))
+    ms = [1, 7, 2**32 - 1]
+    R = O.challenge_matrices(h, ms, k, width)
+    assert R.shape == (3, width, k) and R.dtype == torch.float32
+    for i, m in enumerate(ms):
+        assert torch.equal(R[i], O.challenge_matrix_xof(h, m, k, width))
+
+
+def test_challenge_label_layout_and_python_twin():
+    assert O.encode_label(0x01020304, 255) == b"\x10\x01\x02\x03\x04\xff"
+    h = bytes(range(32))
+    xof = blake3_tree.blake3(O.encode_label(9, 3), key=h, length=4 * 300)
+    want = O.entries(np.frombuffer(xof, dtype="<u4"))
+    got = O.challenge_matrices(h, [9], 3, 300)[0, :, 2].numpy()
+    assert np.array_equal(got, want)
+
+
+def test_challenge_moments():
+    r = O.challenge_matrices(bytes(range(32)), [1], 8, 131_072).numpy().astype(np.float64)
+    assert abs(r.mean()) < 3e-3 and abs(r.var() - 1 / 3) < 2e-3
+
+
+# ---- sizing and finishing ------------------------------------------------------------------
+
+def test_e_m_known_answers():
+    fp32 = 2.0**-24
+    assert O.e_m(64, fp32, fp32) == pytest.approx(5.6e-7, rel=1e-2)
+    assert O.e_m(576, fp32, fp32) == pytest.approx(1.51e-6, rel=1e-2)
+    assert O.e_m(1536, fp32, fp32) == pytest.approx(2.4e-6, rel=2e-2)
+    assert O.e_m(49_152, fp32, fp32) == pytest.approx(1.330e-5, rel=1e-3)
+
+
+def test_band_unit_branches():
+    s = O.SIGMA_R
+    assert O.band_unit(100, 2**-24, 2**-24, 0.0, 3.0) == s * 10 * 2**-24 * 3.0
+    assert math.isnan(O.band_unit(100, 2**-24, 2**-24, 1.0, float("nan")))
+    u = O.band_unit(100, 2**-8, 2**-24, 2.0, 1.0)  # U < ‖P‖: the pre-split unit
+    assert u == s * (math.sqrt(2) * 2**-8 + 10 * 2**-24) * 2.0
+
+
+def test_judge_order_and_nan():
+    base = dict(nu=1.0, p_abs1=1.0, p_norm=1.0, u=1.0, unit=1.0, residuals=(0.5, 0.5))
+    assert O.judge(base, tau=8, kappa_max=10) == (O.ACCEPT, 0)
+    assert O.judge({**base, "residuals": (0.5, 9.0)}, tau=8, kappa_max=10) == (O.RESIDUAL, 2)
+    assert O.judge({**base, "nu": 11.0}, tau=8, kappa_max=10) == (O.KAPPA, 0)
+    assert O.judge({**base, "u": float("nan")}, tau=8, kappa_max=10) == (O.NONFINITE, 0)
+    assert O.judge({**base, "nu": float("inf")}, tau=8, kappa_max=10,
+                   guard=False) == (O.ACCEPT, 0)
+
+
+# ---- Freivalds rows ------------------------------------------------------------------------
+
+def _prod(n, q, w, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(n, q, generator=g).to(dtype).float()
+    b = torch.randn(q, w, generator=g).to(dtype).float()
+    p = (a @ b).to(dtype).float()
+    return a, b, p
+
+
+def test_forged_entry_stands_out():
+    a, b, p = _prod(40, 24, 32, 0)
+    r = O.challenge_matrices(bytes(32), [5], 4, 32)[0]
+    honest = O.finish_row(O.measure_product_row(a, b, p, r), q=24, n=40, eps_in=2**-24,
+                          eps_acc=2**-24)
+    p2 = p.clone()
+    p2[3, 7] += 1e-2 * p.abs().max()
+    forged = O.finish_row(O.measure_product_row(a, b, p2, r), q=24, n=40, eps_in=2**-24,
+                          eps_acc=2**-24)
+    assert max(forged["normalized"]) > 100 * max(max(honest["normalized"]), 1e-3)
+
+
+def test_bias_is_a_ones_column():
+    a, b, _ = _prod(16, 12, 20, 1)
+    bias = torch.randn(20)
+    p = a @ b + bias
+    r = O.challenge_matrices(bytes(32), [3], 2, 20)[0]
+    row = O.measure_product_row(a, b, p, r, bias=bias)
+    a1 = torch.cat([a, torch.ones(16, 1)], 1)
+    b1 = torch.cat([b, bias[None]], 0)
+    ref = O.measure_product_row(a1, b1, p, r)
+    assert row[0] == pytest.approx(ref[0], rel=1e-6)  # nu
+    f = O.finish_row(row, q=13, n=16, eps_in=2**-24, eps_acc=2**-24, biased=True)
+    g = O.finish_row(ref, q=13, n=16, eps_in=2**-24, eps_acc=2**-24)
+    assert f["u"] == pytest.approx(g["u"], rel=1e-6)
+
+
+def test_u_is_the_term_frobenius_norm_and_below_nu():
+    a, b, p = _prod(30, 17, 11, 2)
+    r = O.challenge_matrices(bytes(32), [1], 1, 11)[0]
+    row = O.measure_product_row(a, b, p, r)
+    terms = (a[:, :, None] * b[None, :, :]).double()
+    assert math.sqrt(row[3]) == pytest.approx(float(terms.square().sum().sqrt()), rel=1e-5)
+    assert math.sqrt(row[3]) <= row[0] * (1 + 1e-6)
+
+
+def test_safe_norm_large_and_zero():
+    x = torch.tensor([3e19, -3e19, 1.0])
+    assert math.isfinite(float(O.safe_norm(x)))
+    assert float(O.safe_norm(x)) == pytest.approx(math.sqrt(2) * 3e19, rel=1e-6)
+    assert float(O.safe_norm(torch.zeros(5))) == 0.0
+    assert math.isnan(float(O.safe_norm(torch.tensor([1.0, float("nan")]))))
+
+
+def test_members_equal_single_products():
+    a = torch.randn(3, 16, 12)
+    b = torch.randn(3, 12, 20)
+    p = a @ b
+    h = bytes(range(32))
+    R = O.challenge_matrices(h, [4, 5, 6], 2, 20)
+    rows = O.measure_products_rows(a, b, p, R)
+    for i in range(3):
+        single = O.measure_product_row(a[i], b[i], p[i], R[i])
+        assert rows[i][:3] == pytest.approx(single[:3], rel=1e-4)
+
+
+def test_f64_yardstick_agrees_with_fp32_formulas():
+    a, b, p = _prod(64, 48, 40, 3, torch.bfloat16)
+    r = O.challenge_matrices(bytes(32), [2], 3, 40)[0]
+    f32 = O.measure_product_row(a, b, p, r)
+    f64 = O.measure_row_f64(a, b, p, r)
+    assert f32[:4] == pytest.approx(f64[:4], rel=1e-5)
