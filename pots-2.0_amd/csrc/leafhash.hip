@@ -60,6 +60,12 @@ constexpr int kThreads = 256;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+#ifdef POTS_NT_LOADS
+#define POTS_LOAD(p) __builtin_nontemporal_load(p)
+#else
+#define POTS_LOAD(p) (*(p))
+#endif
+
 __device__ __forceinline__ void finite_acc(uint32_t& acc, uint32_t w, bool halves) {
   uint32_t hi = w << 1;
   uint32_t lo = halves ? (w << 17) : 0u;
@@ -87,12 +93,11 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
     uint32_t m[16];
     if (o >= H && o + 64 <= L) {
       // Interior block: 16 payload words, the aligned window is in bounds (see header).
-      // Streamed once: nontemporal loads keep the payload from evicting reused lines.
       const u32x4* V16 = reinterpret_cast<const u32x4*>(A16);
       u32x4 q[5];
 #pragma unroll
-      for (int u = 0; u < 4; u++) q[u] = __builtin_nontemporal_load(V16 + u);
-      q[4] = SH ? __builtin_nontemporal_load(V16 + 4) : u32x4{0, 0, 0, 0};
+      for (int u = 0; u < 4; u++) q[u] = POTS_LOAD(V16 + u);
+      q[4] = SH ? POTS_LOAD(V16 + 4) : u32x4{0, 0, 0, 0};
       uint32_t w[20];
 #pragma unroll
       for (int u = 0; u < 5; u++) {

@@ -19,6 +19,7 @@ runtime instead of a second copy.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from collections.abc import Iterator, Sequence
 from contextlib import contextmanager
@@ -28,7 +29,7 @@ import numpy as np
 import torch
 
 PACKAGE_ROOT = Path(__file__).resolve().parents[2]
-LIB_PATH = PACKAGE_ROOT / "libpots_mi355x.so"
+LIB_PATH = Path(os.environ.get("POTS_MI355X_LIB", PACKAGE_ROOT / "libpots_mi355x.so"))
 
 KIND_NONE, KIND_F32, KIND_BF16, KIND_F16 = 0, 1, 2, 3
 FINITE_KIND: dict[torch.dtype, int] = {
