@@ -2,10 +2,18 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--no-cpu-baseline]
 
-A step is the verifier's whole hot path over one training step's transcript, already in HBM:
-hash every leaf (BLAKE3 chunks + per-leaf trees, NaN/Inf test fused), build the outer Merkle
-tree and its root. Prints one JSON line (the driver's contract) with the step time, the
-achieved GB/s against MI355X's 8 TB/s HBM roofline, and a CPU baseline timed on the host.
+A step is the verifier's whole hot path over one training step's transcript, already in HBM
+(check 2 and check 5 of the reference, verification/verifier/checks.py:204-272,576-658):
+hash every leaf (BLAKE3 chunks, per-leaf trees, NaN/Inf test fused) and build the Merkle
+root; expand the claimed root into every product's challenge matrix; run the three
+Freivalds passes over every product's B, A and P; reduce to one fp64 row per product; judge
+every product. One host read at the end of the step (root, first non-finite leaf, first
+rejected product).
+
+Prints one JSON line (the driver's contract): `value` is the step's verified throughput,
+(bytes hashed + bytes Freivalds-checked) / step time, in GB/s; `parts` splits it by stage;
+`roofline` is the dominant kernel against MI355X's 8 TB/s; `cpu_baseline` times the CPU
+oracle on a bounded sample of the same transcript on the host's cores.
 
 Only one GPU is used; --gpus above 1 exits with a message.
 """
@@ -14,6 +22,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -26,6 +35,11 @@ for _p in (ROOT / "pots-2.0_amd", ROOT / "oracle"):
 
 HBM_PEAK_GBPS = 8000.0
 METRIC = "Freivalds-verified GB/s + BLAKE3 Merkle GB/s (% HBM roofline); step verify ms"
+CONFIGS = {
+    "c1": ("SmolLM2-135M step, 4x256 tokens, fp32, k=1", "smollm2_135m", 1),
+    "c3": ("Qwen2-0.5B-shaped step, 8x1024 tokens, bf16, k=2", "qwen2_0_5b_shape", 2),
+    "c4": ("Qwen2-1.5B-shaped step, 4x2048 tokens, bf16, k=4", "qwen2_1_5b_shape", 4),
+}
 
 
 def log(msg: str) -> None:
@@ -43,46 +57,62 @@ def cores() -> int:
     return n
 
 
-def config(name: str):
-    from verification.computation.instances import decoder
-    return {"c1": decoder.smollm2_135m, "c3": decoder.qwen2_0_5b_shape,
-            "c4": decoder.qwen2_1_5b_shape}[name]()
+def product_inputs(step):
+    """(a, b, p, bias fp32 or None, m) of every product, operands as the prover used them."""
+    import torch
+    c = step.c
+    out = []
+    for spec in c.products:
+        a, b = step.operands[spec.m]
+        bias = None
+        if spec.bias is not None:
+            bias = step.w_t(spec.bias).to(c.operand_dtype).to(torch.float32)
+        out.append((a, b, step.product(spec.m), bias, spec.m))
+    return out
 
 
-def cpu_baseline(step, budget_s: float = 12.0) -> dict:
-    """The oracle's pthread BLAKE3 (a restatement of the reference's native.c) on a bounded
-    sample of the same transcript's leaves, copied to host memory."""
+def cpu_baseline(step, items, budget_s: float = 20.0) -> dict:
+    """The CPU oracle on a bounded sample of the same transcript, on the host's cores:
+    leaf hashing with the pthread restatement of the reference's native.c, and the
+    reference's Freivalds formulas (torch-CPU fp32) on products of layer 1."""
     import torch
 
     import oracle as O
     c = step.c
-    idx = list(range(c.n_s + c.n_w, c.n_s + c.n_w + c.M))[:400]
-    items = []
-    nbytes = 0
-    for i in idx:
-        t = step.leaves[i].cpu()
-        tag = O.TAG_PRODUCT
-        items.append((O.tensor_leaf_header(tag, t), t, O.FINITE_KIND[t.dtype]))
-        nbytes += 1 + len(items[-1][0]) + t.nbytes
-        if nbytes > 2 << 30:
-            break
     threads = cores()
-    O.hash_leaves(items[:4], threads)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 3 and time.perf_counter() < t_end:
+    torch.set_num_threads(threads)
+    # hashing sample: product leaves until ~1.5 GB
+    hs, hbytes = [], 0
+    for i in range(c.n_s + c.n_w, c.n_s + c.n_w + c.M):
+        t = step.leaves[i].cpu()
+        hs.append((O.tensor_leaf_header(O.TAG_PRODUCT, t), t, O.FINITE_KIND[t.dtype]))
+        hbytes += 1 + len(hs[-1][0]) + t.nbytes
+        if hbytes > 1.5e9:
+            break
+    O.hash_leaves(hs[:2], threads)
+    t0 = time.perf_counter()
+    O.hash_leaves(hs, threads)
+    t_hash = time.perf_counter() - t0
+    # Freivalds sample: the first products in canonical order, until ~budget/2 seconds
+    fbytes, t_fv, nprod = 0, 0.0, 0
+    key = bytes(range(32))
+    for a, b, p, bias, m in items:
+        if t_fv > budget_s / 2:
+            break
+        a_c, b_c, p_c = a.cpu(), b.cpu(), p.cpu()
         t0 = time.perf_counter()
-        O.hash_leaves(items, threads)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    del items
-    torch.cuda.empty_cache()
-    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"leaf hashing of the first {len(idx)} product leaves "
-                      f"({nbytes / 1e9:.2f} GB) of the same transcript, median of "
-                      f"{len(times)} runs, portable scalar BLAKE3 on pthreads"}
+        r = O.challenge_matrices(key, [m], step.k, p_c.shape[1], threads)[0]
+        O.measure_product_row(a_c, b_c, p_c, r, None if bias is None else bias.cpu())
+        t_fv += time.perf_counter() - t0
+        fbytes += a_c.nbytes + b_c.nbytes + p_c.nbytes
+        nprod += 1
+    value = (hbytes + fbytes) / (t_hash + t_fv) / 1e9
+    return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"hash {len(hs)} product leaves ({hbytes / 1e9:.2f} GB, "
+                      f"{hbytes / t_hash / 1e9:.2f} GB/s, portable scalar BLAKE3 on {threads} "
+                      f"pthreads) + Freivalds rows of the first {nprod} products "
+                      f"({fbytes / 1e9:.2f} GB, {fbytes / t_fv / 1e9:.3f} GB/s, torch-CPU "
+                      f"fp32 with {threads} threads, challenges included), one run each"}
 
 
 def main() -> int:
@@ -90,7 +120,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="c4")
+    ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -102,21 +132,40 @@ def main() -> int:
 
     from verification.commitment import native
     from verification.commitment.leaves import StepHasher
+    from verification.computation.instances import decoder
+    from verification.parameters import UNIT_ROUNDOFF
     from verification.prover.synthetic import synthetic_step
+    from verification.verifier.bands import Bands
 
     lib = native.get()
-    c = config(args.config)
-    log(f"[bench] config {args.config}: {c.M} products, {c.n_leaves} leaves")
+    desc, ctor, k = CONFIGS[args.config]
+    c = getattr(decoder, ctor)()
+    log(f"[bench] {args.config}: {c.M} products, {c.n_leaves} leaves, k={k}")
     t0 = time.perf_counter()
-    step = synthetic_step(c, seed=0, operands=False)
+    step = synthetic_step(c, seed=0, operands=True)
+    step.k = k
     torch.cuda.synchronize()
     log(f"[bench] transcript built in {time.perf_counter() - t0:.1f} s, "
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB resident")
-    hasher = StepHasher(c, step.leaves)
-    hash_bytes = hasher.bytes
+
     stream = torch.cuda.current_stream()
+    hasher = StepHasher(c, step.leaves)
+    items = product_inputs(step)
+    plan = lib.fv_plan([native.FvProduct(a, b, p, m, bias) for a, b, p, bias, m in items], k)
+    bands = Bands.provisional()
+    specs = native.verdict_specs([s.q for s in c.products], [s.a_shape[0] for s in c.products],
+                                 [s.bias is not None for s in c.products],
+                                 [bands.kappa_for(c.product_class(s)) for s in c.products])
+    eps_in, eps_acc = UNIT_ROUNDOFF[c.product_dtype], UNIT_ROUNDOFF[torch.float32]
     digests = torch.empty(c.n_leaves, 32, dtype=torch.uint8, device="cuda")
     bad = torch.empty(1, dtype=torch.int32, device="cuda")
+    rows = torch.empty(c.M, 5 + k, dtype=torch.float64, device="cuda")
+    # The claimed root: the honest root of this transcript, as the prover would send it.
+    hasher.digests(digests, bad, stream)
+    claimed = lib.merkle_tree_device(digests, stream)[0].clone()
+    torch.cuda.synchronize()
+    log(f"[bench] claimed root {bytes(claimed.cpu().numpy()).hex()[:16]}…; "
+        f"hash {hasher.bytes / 1e9:.2f} GB, Freivalds {plan.bytes / 1e9:.2f} GB")
 
     def one_step(ev=None):
         if ev:
@@ -127,45 +176,70 @@ def main() -> int:
         nodes = lib.merkle_tree_device(digests, stream)
         if ev:
             ev[2].record(stream)
-        return nodes
+        plan.rows(claimed, rows, stream)
+        if ev:
+            ev[3].record(stream)
+        codes, _, first = lib.verdicts(rows, specs, k=k, eps_in=eps_in, eps_acc=eps_acc,
+                                       tau=bands.tau, stream=stream)
+        if ev:
+            ev[4].record(stream)
+        flags = torch.cat([nodes[0].view(torch.int32), bad, first])
+        return flags.cpu(), codes
 
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        nodes = one_step(evs[i])
+        flags, codes = one_step(evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = wall / args.steps * 1e3
-    hash_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
-    tree_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
-    assert int(bad.item()) == c.n_leaves, "a synthetic leaf was reported non-finite"
-    log(f"[bench] step {ms:.2f} ms: hash {hash_ms:.2f} ms, tree {tree_ms:.3f} ms, "
-        f"root {bytes(nodes[0].cpu().numpy()).hex()[:16]}")
-    hash_gbps = hash_bytes / (hash_ms * 1e-3) / 1e9
-    value = hash_bytes / (ms * 1e-3) / 1e9
+    part = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / args.steps for i in range(4)]
+    hash_ms, tree_ms, fv_ms, verdict_ms = part
+    root = flags[:8].numpy().tobytes()
+    first_bad, first_fail = int(flags[8]), int(flags[9])
+    assert root == bytes(claimed.cpu().numpy()), "recomputed root differs from the claim"
+    assert first_bad == c.n_leaves, "a synthetic leaf was reported non-finite"
+    n_rej = int((codes[:, 0] != 0).sum())
+    log(f"[bench] step {ms:.2f} ms: hash {hash_ms:.2f}, tree {tree_ms:.3f}, Freivalds "
+        f"{fv_ms:.2f}, verdicts {verdict_ms:.3f} ms; {n_rej} rejected (first {first_fail})")
+    hash_gbps = hasher.bytes / (hash_ms * 1e-3) / 1e9
+    fv_gbps = plan.bytes / (fv_ms * 1e-3) / 1e9
+    total = hasher.bytes + plan.bytes
+    value = total / (ms * 1e-3) / 1e9
+    dominant = ("freivalds", fv_gbps, fv_ms) if fv_ms >= hash_ms else ("hash", hash_gbps, hash_ms)
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u32 (BLAKE3) + bf16 operands with fp32 accumulation (Freivalds)",
         "data": "synthetic",
-        "config": {"workload": f"{args.config}: Qwen2-1.5B-shaped step transcript "
-                               "(28 layers, d 1536, 4x2048 tokens, bf16 products), "
-                               "leaf hashing + Merkle root",
-                   "leaves": c.n_leaves, "products": c.M, "hash_bytes": hash_bytes},
-        "parts": {"hash_ms": round(hash_ms, 3), "hash_gbps": round(hash_gbps, 1),
+        "config": {"workload": f"{args.config}: {desc}; whole verify step (check 2 hashing + "
+                               "Merkle root, check 5 challenges + Freivalds + verdicts) on a "
+                               "transcript resident in HBM",
+                   "leaves": c.n_leaves, "products": c.M, "k": k,
+                   "hash_bytes": hasher.bytes, "freivalds_bytes": plan.bytes},
+        "parts": {"step_verify_ms": round(ms, 3),
+                  "hash_ms": round(hash_ms, 3), "hash_gbps": round(hash_gbps, 1),
                   "hash_frac_hbm": round(hash_gbps / HBM_PEAK_GBPS, 4),
-                  "tree_ms": round(tree_ms, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(hash_gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(hash_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": "chunk_kernel + level_kernel (leaf hashing)"},
+                  "tree_ms": round(tree_ms, 4),
+                  "freivalds_ms": round(fv_ms, 3), "freivalds_gbps": round(fv_gbps, 1),
+                  "freivalds_frac_hbm": round(fv_gbps / HBM_PEAK_GBPS, 4),
+                  "verdict_ms": round(verdict_ms, 4),
+                  "step_frac_hbm": round(value / HBM_PEAK_GBPS, 4),
+                  "rejected": n_rej},
+        "roofline": {"bound": "hbm", "achieved": round(dominant[1], 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(dominant[1] / HBM_PEAK_GBPS, 4),
+                     "traffic": None,
+                     "kernel": "row_pass x3 + reduce + finish (Freivalds)" if dominant[0] ==
+                     "freivalds" else "chunk_kernel + level_kernel (leaf hashing)"},
     }
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")
-        out["cpu_baseline"] = cpu_baseline(step)
+        out["cpu_baseline"] = cpu_baseline(step, items)
     print(json.dumps(out), flush=True)
     return 0
 

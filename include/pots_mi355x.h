@@ -94,6 +94,64 @@ void pots_leaf_plan_destroy(void *plan);
  * enqueued on `stream`; d_nodes (32 (2n - 1) bytes) is written in pre-order. */
 int pots_merkle_tree_async(size_t n, const uint8_t *d_leaves, uint8_t *d_nodes, void *stream);
 
+/* ---- Freivalds measurement and verdicts ---------------------------------------------- */
+
+#define POTS_DT_F32 0
+#define POTS_DT_BF16 1
+
+/* One checked product P = A·B (+ 1·biasᵀ). All pointers are device memory; A, B and P are
+ * row-major with the given row strides (elements). `bias` is fp32 [w] already rounded to the
+ * operand format as the reference serves it (checks.py:439), or NULL. `m` is the product's
+ * 1-based index, the challenge label. */
+typedef struct {
+  const void *a, *b, *p;
+  const float *bias;
+  uint64_t lda, ldb, ldp;
+  uint32_t n, q, w, m;
+  uint32_t a_dtype, b_dtype, p_dtype, pad;
+} pots_fv_product;
+
+/* A Freivalds plan over n products with k challenge vectors each: operand layout, column
+ * chunking and workspace fixed once. Replaces the per-product torch op sequence of
+ * verification/verifier/matmul_check/freivalds.py:290-321 and :384-410. guard = 0 leaves the
+ * first two columns NaN (freivalds.py:309-312). */
+int pots_fv_plan_create(size_t n, const pots_fv_product *products, uint32_t k, uint32_t guard,
+                        void **plan);
+
+/* Enqueue on `stream`: the challenge matrices keyed on the 32-byte d_key (device memory,
+ * the claimed root), the three streaming passes and the reduction, writing one fp64 row per
+ * product to d_rows [n][5 + k] in freivalds.ROW order (freivalds.py:255): nu, ‖|P|1‖, ‖P‖_F,
+ * Σ_i (A²(B²1))_i, ‖b‖², residual_1..k. No allocation, no sync. */
+int pots_fv_plan_run(void *plan, const uint8_t *d_key, double *d_rows, void *stream);
+
+/* Copy the last run's row-major challenge matrices (fp32; product i's [w_i, k] block follows
+ * product i-1's) to d_out (device, Σ w_i·k floats), enqueued on `stream`. */
+int pots_fv_plan_copy_challenges(const void *plan, float *d_out, void *stream);
+
+/* Bytes of A, B and P the plan reads (each once). */
+uint64_t pots_fv_plan_bytes(const void *plan);
+
+void pots_fv_plan_destroy(void *plan);
+
+/* Replaces native.c:119 pots_challenges: item i's [widths[i], k] fp32 matrix at out +
+ * offsets[i] (out host or device memory), vector j of product ms[i] the keyed XOF of
+ * 0x10 || ms[i] (BE) || j under key, entries (2(w >> 8) + 1 - 2^24) / 2^24. Synchronous. */
+int pots_challenges(const uint8_t key[32], uint32_t k, size_t n, const uint32_t *ms,
+                    const uint32_t *widths, const uint64_t *offsets, float *out,
+                    uint32_t n_threads);
+
+/* Per-product verdicts from fp64 rows d_rows [n][5 + k] (device), on `stream`. d_specs is
+ * device memory of n records { double kappa_max; uint32_t q, n, biased, pad; } (q the
+ * checked contraction length, +1 with a bias). Writes (code, j) int32 pairs to d_codes
+ * (0 accept, 1 non-finite, 2 cancellation guard, 3 residual of challenge j above tau·unit),
+ * optionally (kappa, unit, U) to d_finished [n][3], and the smallest rejecting index (or n)
+ * to *d_first_fail. sigma_r and sqrt2 are 1/√3 and √2 as the caller's doubles. Replaces
+ * freivalds.py:324-335,450-468 and checks.py:926-956. */
+int pots_verdicts_async(size_t n, const double *d_rows, uint32_t k, const void *d_specs,
+                        double eps_in, double eps_acc, double tau, double sigma_r, double sqrt2,
+                        uint32_t guard, uint32_t judge, int32_t *d_codes, double *d_finished,
+                        uint32_t *d_first_fail, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,915 @@
+// Batched Freivalds measurement of every captured matmul on gfx950.
+//
+// Reference: verification/verifier/matmul_check/freivalds.py:255-321 (ROW, measure_product_row)
+// and :384-410 (measure_products_rows). For each product P = A·B (+ 1·bᵀ), k challenge columns
+// R [w, k] keyed on the claimed root, the row is
+//   [ ‖|A|(|B|1) (+‖b‖₁)‖, ‖|P|1‖, ‖P‖_F, Σ_i (A²(B²1))_i, ‖b‖², ‖A(BR_j) (+bᵀR_j) − PR_j‖_j ]
+// in fp64, the matvec and matmul outputs being fp32 as in the reference and every norm summed
+// in fp64 (squares of fp32 values neither overflow nor underflow in fp64, which gives the
+// reference's scaled-norm semantics without the scaling).
+//
+// Three streaming passes read each operand once from HBM. Each pass is the same kernel,
+// "row pass": for a matrix X [rows, cols] and V [cols, k] it computes, per row,
+//   dot = X·V (k values), s1 = Σ|x|·u, s2 = Σ x²·w     (u, w per-column weights, or ones)
+//   B pass: X = B, V = R      -> B·R, |B|·1, B²·1
+//   A pass: X = A, V = B·R    -> A·(B·R), |A|·(|B|·1), A²·(B²·1)
+//   P pass: X = P, V = R      -> P·R, |P|·1, P²·1 (fp64)
+// X·V runs on the matrix cores: a wave owns 64 rows (4 tiles of 16) and a range of columns
+// and issues v_mfma_f32_16x16x16_bf16 (bf16 X, V as three exact bf16 terms) or
+// v_mfma_f32_16x16x4_f32 (fp32 X). Each lane loads 16 contiguous bytes of one row per tile per
+// step, so a wave reads 16 rows x 64 (bf16) or 64 bytes (fp32) per tile per step; the lane's
+// column order inside a step is a permutation of the MFMA's K index, applied identically to
+// the V operand. The two sums are VALU work on the same registers. Columns are split into
+// chunks (partial sums per chunk, reduced in a fixed order later), so every product yields
+// enough waves and the result does not depend on timing.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+#include <vector>
+
+#include "common.h"
+#include "freivalds.h"
+
+namespace pots {
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef float v4f32 __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
+
+enum : uint32_t { DT_F32 = 0, DT_BF16 = 1 };
+
+// One matrix of one pass.
+struct PassJob {
+  uint64_t x;           // X[0][0]
+  uint64_t ld;          // row stride in elements
+  uint64_t v;           // packed V of this job (uint16 elements for bf16 X, floats for fp32)
+  uint64_t u, w;        // per-column weights (fp32 [cols]) or 0 for ones
+  uint64_t pdot;        // partial X·V: float [n_chunks][rows_pad][k]
+  uint64_t pabs;        // partial Σ|x|u: float [n_chunks][rows_pad]
+  uint64_t psq;         // partial Σx²w: double [n_chunks][rows_pad]
+  uint64_t tile_first;  // prefix of tiles over the jobs before it
+  uint32_t rows, cols;
+  uint32_t rows_pad, chunk_cols;
+  uint32_t n_chunks, n_jg;  // column chunks; groups of 16 challenge columns
+  uint32_t aligned, pad;    // 16-byte aligned rows and base
+};
+static_assert(sizeof(PassJob) == 104, "PassJob layout");
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+template <bool SQ64>
+struct SqAcc;
+template <>
+struct SqAcc<true> {
+  double v = 0.0;
+  __device__ void add(float x, float w) { v = fma((double)x * (double)x, (double)w, v); }
+  __device__ void add1(float x) { v = fma((double)x, (double)x, v); }
+  __device__ double get() const { return v; }
+};
+template <>
+struct SqAcc<false> {
+  float v = 0.0f;
+  __device__ void add(float x, float w) { v = fmaf(x * x, w, v); }
+  __device__ void add1(float x) { v = fmaf(x, x, v); }
+  __device__ double get() const { return (double)v; }
+};
+
+// ---- the row pass ---------------------------------------------------------------------------
+
+// XT = DT_BF16: K-step of 32 columns; lane group g = lane / 16 owns columns c + 8g .. c + 8g + 7.
+// XT = DT_F32: K-step of 16 columns; lane group g owns columns c + 4g .. c + 4g + 3.
+template <uint32_t XT, bool WEIGHTED, bool SQ64>
+__global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
+                                                uint64_t n_tiles,
+                                                const uint32_t* __restrict__ blk_job,
+                                                uint32_t k) {
+  constexpr uint32_t KSTEP = XT == DT_BF16 ? 32 : 16;
+  constexpr uint32_t PER = XT == DT_BF16 ? 8 : 4;  // columns per lane per step
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint64_t tile = (uint64_t)blockIdx.x * 4 + wave;
+  if (tile >= n_tiles) return;
+  uint32_t lo = blk_job[blockIdx.x], hi = blk_job[blockIdx.x + 1];
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (jobs[mid].tile_first <= tile) lo = mid;
+    else hi = mid - 1;
+  }
+  const PassJob J = jobs[lo];
+  uint64_t local = tile - J.tile_first;
+  const uint32_t chunk = (uint32_t)(local % J.n_chunks);
+  local /= J.n_chunks;
+  const uint32_t jg = (uint32_t)(local % J.n_jg);
+  const uint32_t rt = (uint32_t)(local / J.n_jg);
+  const uint32_t r0 = rt * 64;
+  const uint32_t c0 = chunk * J.chunk_cols;
+  const uint32_t c1 = min(c0 + J.chunk_cols, J.cols);
+  const uint32_t g = lane >> 4, i = lane & 15;
+  const uint32_t j = jg * 16 + i;  // this lane's challenge column in the V operand
+  const bool jv = j < k;
+  const bool sums = jg == 0;  // the two sums are taken once, by the first column group
+
+  const char* xbase = reinterpret_cast<const char*>(J.x);
+  const uint32_t esz = XT == DT_BF16 ? 2 : 4;
+  bool rv[4];
+  const char* xrow[4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const uint32_t row = r0 + 16 * t + i;
+    rv[t] = row < J.rows;
+    xrow[t] = xbase + (uint64_t)(rv[t] ? row : 0) * J.ld * esz;
+  }
+  v4f32 acc[4];
+  float s1[4];
+  SqAcc<SQ64> s2[4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    acc[t] = v4f32{0.f, 0.f, 0.f, 0.f};
+    s1[t] = 0.f;
+  }
+  const float* uw = reinterpret_cast<const float*>(J.u);
+  const float* ww = reinterpret_cast<const float*>(J.w);
+
+  for (uint32_t c = c0; c < c1; c += KSTEP) {
+    const uint32_t cl = c + PER * g;  // this lane's first column of the step
+    const bool full = J.aligned && c + KSTEP <= c1;
+    // X: PER consecutive elements of each of the 4 rows.
+    uint32_t xw[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      if (full) {
+        const uint4 q = rv[t] ? *reinterpret_cast<const uint4*>(xrow[t] + (uint64_t)cl * esz)
+                              : make_uint4(0, 0, 0, 0);
+        xw[t][0] = q.x; xw[t][1] = q.y; xw[t][2] = q.z; xw[t][3] = q.w;
+      } else {
+        if (XT == DT_BF16) {
+          const uint16_t* p = reinterpret_cast<const uint16_t*>(xrow[t]);
+          uint16_t e[8];
+#pragma unroll
+          for (int s = 0; s < 8; s++) e[s] = (rv[t] && cl + s < c1) ? p[cl + s] : (uint16_t)0;
+#pragma unroll
+          for (int s = 0; s < 4; s++) xw[t][s] = e[2 * s] | (uint32_t)e[2 * s + 1] << 16;
+        } else {
+          const uint32_t* p = reinterpret_cast<const uint32_t*>(xrow[t]);
+#pragma unroll
+          for (int s = 0; s < 4; s++) xw[t][s] = (rv[t] && cl + s < c1) ? p[cl + s] : 0u;
+        }
+      }
+    }
+    // Weights of this lane's columns.
+    float uc[PER], wc[PER];
+    if (WEIGHTED && sums) {
+#pragma unroll
+      for (uint32_t s = 0; s < PER; s++) {
+        const bool ok = cl + s < c1;
+        uc[s] = ok ? uw[cl + s] : 0.f;
+        wc[s] = ok ? ww[cl + s] : 0.f;
+      }
+    }
+    if (XT == DT_BF16) {
+      // V: 3 planes x 8 bf16 of column j for this lane's 8 rows of V.
+      const uint16_t* vb = reinterpret_cast<const uint16_t*>(J.v);
+      uint4 vp[3] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+      if (jv && cl < c1) {  // a lane past the last column loads nothing
+        const uint4* src = reinterpret_cast<const uint4*>(vb + ((uint64_t)(cl / 8) * k + j) * 24);
+        vp[0] = src[0];
+        vp[1] = src[1];
+        vp[2] = src[2];
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const v4i16 a = __builtin_bit_cast(v4i16, v2u32{xw[t][2 * h], xw[t][2 * h + 1]});
+#pragma unroll
+          for (int p = 0; p < 3; p++) {
+            const v2u32 bw = h == 0 ? v2u32{vp[p].x, vp[p].y} : v2u32{vp[p].z, vp[p].w};
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(v4i16, bw),
+                                                               acc[t], 0, 0, 0);
+          }
+        }
+      }
+      if (sums) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+          for (int s = 0; s < 4; s++) {
+            const float xa = bf_lo(xw[t][s]), xb = bf_hi(xw[t][s]);
+            if (WEIGHTED) {
+              s1[t] = fmaf(fabsf(xa), uc[2 * s], s1[t]);
+              s1[t] = fmaf(fabsf(xb), uc[2 * s + 1], s1[t]);
+              s2[t].add(xa, wc[2 * s]);
+              s2[t].add(xb, wc[2 * s + 1]);
+            } else {
+              s1[t] += fabsf(xa);
+              s1[t] += fabsf(xb);
+              s2[t].add1(xa);
+              s2[t].add1(xb);
+            }
+          }
+        }
+      }
+    } else {
+      const float* vf = reinterpret_cast<const float*>(J.v);
+      float4 vq = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (jv && cl < c1) vq = *reinterpret_cast<const float4*>(vf + ((uint64_t)(cl / 4) * k + j) * 4);
+      const float vv[4] = {vq.x, vq.y, vq.z, vq.w};
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(xw[t][e]), vv[e], acc[t],
+                                                        0, 0, 0);
+      }
+      if (sums) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+          for (int s = 0; s < 4; s++) {
+            const float x = __uint_as_float(xw[t][s]);
+            if (WEIGHTED) {
+              s1[t] = fmaf(fabsf(x), uc[s], s1[t]);
+              s2[t].add(x, wc[s]);
+            } else {
+              s1[t] += fabsf(x);
+              s2[t].add1(x);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // X·V: lane (g, i) holds rows 4g + e of each tile, challenge column j.
+  float* pdot = reinterpret_cast<float*>(J.pdot);
+  const uint64_t cbase = (uint64_t)chunk * J.rows_pad;
+  if (jv) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t row = r0 + 16 * t + 4 * g + e;
+        if (row < J.rows) pdot[(cbase + row) * k + j] = acc[t][e];
+      }
+    }
+  }
+  if (sums) {
+    float* pabs = reinterpret_cast<float*>(J.pabs);
+    double* psq = reinterpret_cast<double*>(J.psq);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      float a = s1[t];
+      double q = s2[t].get();
+      if (!SQ64) {  // combine in the accumulation precision
+        float qf = (float)q;
+        qf += __shfl_xor(qf, 16);
+        qf += __shfl_xor(qf, 32);
+        q = qf;
+      } else {
+        q += __shfl_xor(q, 16);
+        q += __shfl_xor(q, 32);
+      }
+      a += __shfl_xor(a, 16);
+      a += __shfl_xor(a, 32);
+      const uint32_t row = r0 + 16 * t + i;
+      if (g == 0 && row < J.rows) {
+        pabs[cbase + row] = a;
+        psq[cbase + row] = q;
+      }
+    }
+  }
+}
+
+// ---- B-pass reduction: B·R, |B|·1, B²·1 per row of B, packed for the A pass -------------
+
+struct RedJob {
+  uint64_t pdot, pabs, psq;  // the B job's partials
+  uint64_t vout;             // packed B·R for the A pass
+  uint64_t u, w;             // b1 = |B|·1 and b2 = B²·1, fp32 [q]
+  uint64_t group_first;      // prefix of (8-row groups x k) over the jobs before it
+  uint32_t rows, rows_pad;   // q and its padding
+  uint32_t n_chunks, a_dt;   // the A pass's dtype decides the packing
+};
+static_assert(sizeof(RedJob) == 72, "RedJob layout");
+
+__global__ __launch_bounds__(256) void reduce_b(const RedJob* __restrict__ jobs, uint32_t n_jobs,
+                                                uint64_t n_threads, uint32_t k) {
+  const uint64_t g = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= n_threads) return;
+  uint32_t lo = 0, hi = n_jobs - 1;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (jobs[mid].group_first <= g) lo = mid;
+    else hi = mid - 1;
+  }
+  const RedJob J = jobs[lo];
+  const uint64_t local = g - J.group_first;
+  const uint32_t grp = (uint32_t)(local / k), j = (uint32_t)(local % k);
+  const float* pdot = reinterpret_cast<const float*>(J.pdot);
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const uint32_t row = 8 * grp + e;
+    double s = 0.0;
+    if (row < J.rows)
+      for (uint32_t c = 0; c < J.n_chunks; c++)
+        s += (double)pdot[((uint64_t)c * J.rows_pad + row) * k + j];
+    v[e] = (float)s;
+  }
+  if (J.a_dt == DT_BF16) {
+    uint16_t pl[3][8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) split_bf16x3(v[e], pl[0][e], pl[1][e], pl[2][e]);
+    uint4* dst = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(J.vout) +
+                                          ((uint64_t)grp * k + j) * 24);
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+      dst[p] = make_uint4(pl[p][0] | (uint32_t)pl[p][1] << 16, pl[p][2] | (uint32_t)pl[p][3] << 16,
+                          pl[p][4] | (uint32_t)pl[p][5] << 16, pl[p][6] | (uint32_t)pl[p][7] << 16);
+  } else {
+    float* base = reinterpret_cast<float*>(J.vout);
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      *reinterpret_cast<float4*>(base + ((uint64_t)(2 * grp + h) * k + j) * 4) =
+          make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]);
+  }
+  if (j == 0) {
+    const float* pabs = reinterpret_cast<const float*>(J.pabs);
+    const double* psq = reinterpret_cast<const double*>(J.psq);
+    float* u = reinterpret_cast<float*>(J.u);
+    float* w = reinterpret_cast<float*>(J.w);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const uint32_t row = 8 * grp + e;
+      if (row >= J.rows) continue;
+      double a = 0.0, q = 0.0;
+      for (uint32_t c = 0; c < J.n_chunks; c++) {
+        a += (double)pabs[(uint64_t)c * J.rows_pad + row];
+        q += psq[(uint64_t)c * J.rows_pad + row];
+      }
+      u[row] = (float)a;
+      w[row] = (float)q;
+    }
+  }
+}
+
+// ---- finish: one product's row ------------------------------------------------------------
+
+struct FinJob {
+  uint64_t a_dot, a_abs, a_sq;  // A-pass partials (rows n)
+  uint64_t p_dot, p_abs, p_sq;  // P-pass partials (rows n)
+  uint64_t r;                   // canonical R [w][k] (for the bias term)
+  uint64_t bias;                // fp32 [w] or 0
+  uint32_t n, w;
+  uint32_t a_rows_pad, a_chunks;
+  uint32_t p_rows_pad, p_chunks;
+};
+static_assert(sizeof(FinJob) == 88, "FinJob layout");
+
+__device__ __forceinline__ double block_sum(double v, double* sh) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+  __syncthreads();
+  if (ln == 0) sh[wv] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += sh[i];
+  return t;
+}
+
+__global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jobs, uint32_t k,
+                                                   uint32_t guard, double* __restrict__ rows) {
+  __shared__ double sh[4];
+  __shared__ float bias_r[16];
+  __shared__ float bias_abs;
+  const FinJob J = jobs[blockIdx.x];
+  const uint32_t tid = threadIdx.x;
+  double* out = rows + (uint64_t)blockIdx.x * (5 + k);
+  const float* bias = reinterpret_cast<const float*>(J.bias);
+  const float* R = reinterpret_cast<const float*>(J.r);
+  double bsq = 0.0, babs_d = 0.0;
+  if (bias) {
+    double a = 0.0, q = 0.0;
+    for (uint32_t c = tid; c < J.w; c += blockDim.x) {
+      const double b = bias[c];
+      a += fabs(b);
+      q += b * b;
+    }
+    babs_d = block_sum(a, sh);
+    bsq = block_sum(q, sh);
+  }
+  if (tid == 0) bias_abs = (float)babs_d;
+  const float* adot = reinterpret_cast<const float*>(J.a_dot);
+  const float* aabs = reinterpret_cast<const float*>(J.a_abs);
+  const double* asq = reinterpret_cast<const double*>(J.a_sq);
+  const float* pdot = reinterpret_cast<const float*>(J.p_dot);
+  const float* pabs = reinterpret_cast<const float*>(J.p_abs);
+  const double* psq = reinterpret_cast<const double*>(J.p_sq);
+
+  // Row sums (ν, ‖|P|1‖, ‖P‖_F, U²) once, then the residuals 16 columns at a time.
+  double s_nu = 0.0, s_p1 = 0.0, s_psq = 0.0, s_t2 = 0.0;
+  __syncthreads();
+  const float babs = bias_abs;
+  for (uint32_t r = tid; r < J.n; r += blockDim.x) {
+    double nu = 0.0, t2 = 0.0, p1 = 0.0, pq = 0.0;
+    for (uint32_t c = 0; c < J.a_chunks; c++) {
+      nu += (double)aabs[(uint64_t)c * J.a_rows_pad + r];
+      t2 += asq[(uint64_t)c * J.a_rows_pad + r];
+    }
+    for (uint32_t c = 0; c < J.p_chunks; c++) {
+      p1 += (double)pabs[(uint64_t)c * J.p_rows_pad + r];
+      pq += psq[(uint64_t)c * J.p_rows_pad + r];
+    }
+    float nuf = (float)nu;
+    if (bias) nuf = nuf + babs;
+    const float p1f = (float)p1;
+    s_nu += (double)nuf * (double)nuf;
+    s_p1 += (double)p1f * (double)p1f;
+    s_psq += pq;
+    s_t2 += (double)(float)t2;
+  }
+  s_nu = block_sum(s_nu, sh);
+  s_p1 = block_sum(s_p1, sh);
+  s_psq = block_sum(s_psq, sh);
+  s_t2 = block_sum(s_t2, sh);
+  if (tid == 0) {
+    const double nan = __builtin_nan("");
+    out[0] = guard ? sqrt(s_nu) : nan;
+    out[1] = guard ? sqrt(s_p1) : nan;
+    out[2] = sqrt(s_psq);
+    out[3] = s_t2;
+    out[4] = bsq;
+  }
+  for (uint32_t j0 = 0; j0 < k; j0 += 16) {
+    const uint32_t nj = min(16u, k - j0);
+    if (bias) {  // bᵀ·R_j for this column group
+      for (uint32_t jj = 0; jj < nj; jj++) {
+        double a = 0.0;
+        for (uint32_t c = tid; c < J.w; c += blockDim.x)
+          a += (double)bias[c] * (double)R[(uint64_t)c * k + j0 + jj];
+        a = block_sum(a, sh);
+        if (tid == 0) bias_r[jj] = (float)a;
+      }
+    }
+    __syncthreads();
+    double sd[16];
+#pragma unroll
+    for (int jj = 0; jj < 16; jj++) sd[jj] = 0.0;
+    for (uint32_t r = tid; r < J.n; r += blockDim.x) {
+#pragma unroll
+      for (int jj = 0; jj < 16; jj++) {
+        if ((uint32_t)jj >= nj) break;
+        const uint32_t jc = j0 + jj;
+        double ab = 0.0, pr = 0.0;
+        for (uint32_t c = 0; c < J.a_chunks; c++)
+          ab += (double)adot[((uint64_t)c * J.a_rows_pad + r) * k + jc];
+        for (uint32_t c = 0; c < J.p_chunks; c++)
+          pr += (double)pdot[((uint64_t)c * J.p_rows_pad + r) * k + jc];
+        float abf = (float)ab;
+        if (bias) abf = abf + bias_r[jj];
+        const float d = abf - (float)pr;
+        sd[jj] += (double)d * (double)d;
+      }
+    }
+    for (uint32_t jj = 0; jj < nj; jj++) {
+      const double t = block_sum(sd[jj], sh);
+      if (tid == 0) out[5 + j0 + jj] = sqrt(t);
+    }
+    __syncthreads();
+  }
+}
+
+// ---- the plan ---------------------------------------------------------------------------
+
+struct PassLaunch {
+  uint32_t xt, weighted, sq64;
+  uint64_t job_off;  // index into the job array
+  uint32_t n_jobs;
+  uint64_t n_tiles;
+  uint64_t blk_off;  // index into the block->job table
+  uint32_t n_blocks;
+};
+
+struct FvPlan {
+  size_t n = 0;
+  uint32_t k = 0, guard = 1;
+  char* base = nullptr;
+  size_t total = 0;
+  uint32_t* d_key = nullptr;
+  ChallengeItem* d_items_b3 = nullptr;  // items whose R is read by bf16 passes
+  ChallengeItem* d_items_f4 = nullptr;
+  uint32_t n_items = 0;
+  uint64_t n_units = 0;
+  float* d_r = nullptr;
+  uint16_t* d_r_b3 = nullptr;
+  float* d_r_f4 = nullptr;
+  PassJob* d_jobs = nullptr;
+  uint32_t* d_blk = nullptr;
+  RedJob* d_red = nullptr;
+  uint32_t n_red = 0;
+  uint64_t n_red_threads = 0;
+  FinJob* d_fin = nullptr;
+  std::vector<PassLaunch> pass_b, pass_ap;  // B pass; then A and P passes
+  bool need_b3 = false, need_f4 = false;
+  uint64_t bytes = 0;  // algorithmic bytes: A, B, P read once
+  uint64_t r_floats = 0;
+};
+
+// Packed operands (R, B·R) hold whole 32-row groups, one bf16 K-step of the row pass; rows past
+// the matrix are zero.
+static uint64_t pad32(uint64_t rows) { return (rows + 31) / 32 * 32; }
+
+static uint32_t chunk_cols_for(uint32_t cols, uint32_t kstep) {
+  // At most 4096 columns per chunk, in whole K-steps, balanced over the chunks.
+  const uint32_t n = std::max<uint32_t>(1, (cols + 4095) / 4096);
+  uint32_t c = (cols + n - 1) / n;
+  c = (c + kstep - 1) / kstep * kstep;
+  return std::max<uint32_t>(c, kstep);
+}
+
+}  // namespace pots
+
+using namespace pots;
+
+extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint32_t k,
+                                   uint32_t guard, void** plan) {
+  if (!plan || !prods || n == 0 || n >= 0x7FFFFFFFull || k < 1 || k > 255) return POTS_E_ARG;
+  FvPlan* P = new (std::nothrow) FvPlan;
+  if (!P) return POTS_E_NOMEM;
+  P->n = n;
+  P->k = k;
+  P->guard = guard ? 1 : 0;
+
+  // Layout of the workspace, computed on the host.
+  size_t at = 0;
+  auto place = [&](size_t bytes) {
+    size_t a = at;
+    at = align_up(at + std::max<size_t>(bytes, 16), 256);
+    return a;
+  };
+  const size_t o_key = place(32);
+  const uint32_t n_jg = (k + 15) / 16;
+  std::vector<ChallengeItem> items(n);
+  uint64_t r_floats = 0, b3_elems = 0, f4_floats = 0, units = 0;
+  for (size_t i = 0; i < n; i++) {
+    const pots_fv_product& p = prods[i];
+    if (p.n == 0 || p.q == 0 || p.w == 0 || p.m == 0 || !p.a || !p.b || !p.p) {
+      delete P;
+      return POTS_E_ARG;
+    }
+    if (p.a_dtype > 1 || p.b_dtype > 1 || p.p_dtype > 1) {
+      delete P;
+      return POTS_E_ARG;
+    }
+    const uint64_t wpad = pad32(p.w);
+    items[i].m = p.m;
+    items[i].width = p.w;
+    items[i].out_off = r_floats;
+    items[i].unit_first = units;
+    r_floats += (uint64_t)p.w * k;
+    units += wpad / 16;
+    // R packed in the layouts the B and P passes read.
+    P->need_b3 |= p.b_dtype == DT_BF16 || p.p_dtype == DT_BF16;
+    P->need_f4 |= p.b_dtype == DT_F32 || p.p_dtype == DT_F32;
+    items[i].pk_off = 0;
+    b3_elems += wpad * k * 3;
+    f4_floats += wpad * k;
+  }
+  P->n_items = (uint32_t)n;
+  P->n_units = units;
+  P->r_floats = r_floats;
+  // Packed offsets: the same item order in both layouts.
+  std::vector<ChallengeItem> items_b3 = items, items_f4 = items;
+  {
+    uint64_t ob = 0, of = 0;
+    for (size_t i = 0; i < n; i++) {
+      const uint64_t wpad = pad32(prods[i].w);
+      items_b3[i].pk_off = ob;
+      items_f4[i].pk_off = of;
+      ob += wpad * k * 3;
+      of += wpad * k;
+    }
+  }
+  const size_t o_items_b3 = place(n * sizeof(ChallengeItem));
+  const size_t o_items_f4 = place(n * sizeof(ChallengeItem));
+  const size_t o_r = place(r_floats * 4);
+  const size_t o_rb3 = place(P->need_b3 ? b3_elems * 2 : 16);
+  const size_t o_rf4 = place(P->need_f4 ? f4_floats * 4 : 16);
+
+  // Jobs: B pass (one per product), then A pass and P pass.
+  std::vector<PassJob> jobs;
+  std::vector<uint64_t> job_part_bytes;  // where each job's partials go, filled below
+  struct Shape {
+    uint32_t rows, cols, dt;
+    uint64_t x, ld;
+  };
+  auto make_job = [&](const Shape& s, uint32_t kstep) {
+    PassJob J;
+    memset(&J, 0, sizeof J);
+    J.x = s.x;
+    J.ld = s.ld;
+    J.rows = s.rows;
+    J.cols = s.cols;
+    J.rows_pad = (s.rows + 63) / 64 * 64;
+    J.chunk_cols = chunk_cols_for(s.cols, kstep);
+    J.n_chunks = (s.cols + J.chunk_cols - 1) / J.chunk_cols;
+    J.n_jg = n_jg;
+    const uint32_t esz = s.dt == DT_BF16 ? 2 : 4;
+    J.aligned = (s.x % 16 == 0) && ((s.ld * esz) % 16 == 0);
+    return J;
+  };
+  // Partial buffers, per job: dot [chunks][rows_pad][k] f32, abs [chunks][rows_pad] f32,
+  // sq [chunks][rows_pad] f64.
+  size_t part_bytes = 0;
+  std::vector<size_t> off_dot, off_abs, off_sq;
+  auto reserve_part = [&](const PassJob& J) {
+    const uint64_t cr = (uint64_t)J.n_chunks * J.rows_pad;
+    off_dot.push_back(part_bytes);
+    part_bytes = align_up(part_bytes + cr * k * 4, 256);
+    off_abs.push_back(part_bytes);
+    part_bytes = align_up(part_bytes + cr * 4, 256);
+    off_sq.push_back(part_bytes);
+    part_bytes = align_up(part_bytes + cr * 8, 256);
+  };
+  // BR packed + b1 + b2 per product (A pass operands).
+  size_t br_bytes = 0;
+  std::vector<size_t> off_br, off_b1, off_b2;
+  for (size_t i = 0; i < n; i++) {
+    const pots_fv_product& p = prods[i];
+    const uint32_t kb = p.b_dtype == DT_BF16 ? 32 : 16;
+    PassJob J = make_job({p.q, p.w, p.b_dtype, reinterpret_cast<uint64_t>(p.b), p.ldb}, kb);
+    jobs.push_back(J);
+    reserve_part(J);
+    const uint64_t qpad = pad32(p.q);
+    off_br.push_back(br_bytes);
+    br_bytes = align_up(br_bytes + qpad * k * (p.a_dtype == DT_BF16 ? 6 : 4), 256);
+    off_b1.push_back(br_bytes);
+    br_bytes = align_up(br_bytes + (uint64_t)p.q * 4, 256);
+    off_b2.push_back(br_bytes);
+    br_bytes = align_up(br_bytes + (uint64_t)p.q * 4, 256);
+    P->bytes += (uint64_t)p.n * p.q * (p.a_dtype == DT_BF16 ? 2 : 4) +
+                (uint64_t)p.q * p.w * (p.b_dtype == DT_BF16 ? 2 : 4) +
+                (uint64_t)p.n * p.w * (p.p_dtype == DT_BF16 ? 2 : 4);
+  }
+  for (size_t i = 0; i < n; i++) {
+    const pots_fv_product& p = prods[i];
+    PassJob J = make_job({p.n, p.q, p.a_dtype, reinterpret_cast<uint64_t>(p.a), p.lda},
+                         p.a_dtype == DT_BF16 ? 32 : 16);
+    jobs.push_back(J);
+    reserve_part(J);
+  }
+  for (size_t i = 0; i < n; i++) {
+    const pots_fv_product& p = prods[i];
+    PassJob J = make_job({p.n, p.w, p.p_dtype, reinterpret_cast<uint64_t>(p.p), p.ldp},
+                         p.p_dtype == DT_BF16 ? 32 : 16);
+    jobs.push_back(J);
+    reserve_part(J);
+  }
+  const size_t o_parts = place(part_bytes);
+  const size_t o_br = place(br_bytes);
+  // Biases as fp32 are the caller's; the bias pointer is used directly.
+
+  // Group jobs into launches by (dtype, weighted, sq64) and order tiles within each launch.
+  struct Pending {
+    uint32_t xt, weighted, sq64;
+    std::vector<uint32_t> idx;
+  };
+  auto group = [&](size_t first, size_t count, uint32_t weighted, uint32_t sq64,
+                   const uint32_t* dts) {
+    std::vector<Pending> out;
+    for (uint32_t xt = 0; xt < 2; xt++) {
+      Pending pd{xt, weighted, sq64, {}};
+      for (size_t i = 0; i < count; i++)
+        if (dts[i] == xt) pd.idx.push_back((uint32_t)(first + i));
+      if (!pd.idx.empty()) out.push_back(pd);
+    }
+    return out;
+  };
+  std::vector<uint32_t> bdt(n), adt(n), pdt(n);
+  for (size_t i = 0; i < n; i++) {
+    bdt[i] = prods[i].b_dtype;
+    adt[i] = prods[i].a_dtype;
+    pdt[i] = prods[i].p_dtype;
+  }
+  std::vector<Pending> lb = group(0, n, 0, 0, bdt.data());
+  std::vector<Pending> la = group(n, n, 1, 0, adt.data());
+  std::vector<Pending> lp = group(2 * n, n, 0, 1, pdt.data());
+  // Reorder the job array launch by launch and build each launch's block table.
+  std::vector<PassJob> ordered;
+  std::vector<uint32_t> blk_table;
+  std::vector<uint32_t> ordered_src;  // original job index of each ordered job
+  auto emit = [&](const std::vector<Pending>& ls, std::vector<PassLaunch>& dst) {
+    for (const Pending& pd : ls) {
+      PassLaunch L;
+      L.xt = pd.xt;
+      L.weighted = pd.weighted;
+      L.sq64 = pd.sq64;
+      L.job_off = ordered.size();
+      L.n_jobs = (uint32_t)pd.idx.size();
+      uint64_t tiles = 0;
+      std::vector<uint64_t> first;
+      for (uint32_t src : pd.idx) {
+        PassJob J = jobs[src];
+        J.tile_first = tiles;
+        first.push_back(tiles);
+        tiles += (uint64_t)(J.rows_pad / 64) * J.n_chunks * J.n_jg;
+        ordered.push_back(J);
+        ordered_src.push_back(src);
+      }
+      L.n_tiles = tiles;
+      L.n_blocks = (uint32_t)((tiles + 3) / 4);
+      L.blk_off = blk_table.size();
+      size_t jdx = 0;
+      for (uint32_t b = 0; b < L.n_blocks; b++) {
+        const uint64_t t0 = (uint64_t)b * 4;
+        while (jdx + 1 < first.size() && first[jdx + 1] <= t0) jdx++;
+        blk_table.push_back((uint32_t)jdx);
+      }
+      blk_table.push_back(L.n_jobs - 1);
+      dst.push_back(L);
+    }
+  };
+  emit(lb, P->pass_b);
+  emit(la, P->pass_ap);
+  emit(lp, P->pass_ap);
+  const size_t o_jobs = place(ordered.size() * sizeof(PassJob));
+  const size_t o_blk = place(blk_table.size() * 4);
+  const size_t o_red = place(n * sizeof(RedJob));
+  const size_t o_fin = place(n * sizeof(FinJob));
+  P->total = at;
+
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&P->base), P->total);
+  if (e != hipSuccess) {
+    note_hip_error(e, "hipMalloc(freivalds plan)", __FILE__, __LINE__);
+    delete P;
+    return e == hipErrorOutOfMemory ? POTS_E_NOMEM : POTS_E_HIP;
+  }
+  const uint64_t base = reinterpret_cast<uint64_t>(P->base);
+  P->d_key = reinterpret_cast<uint32_t*>(P->base + o_key);
+  P->d_items_b3 = reinterpret_cast<ChallengeItem*>(P->base + o_items_b3);
+  P->d_items_f4 = reinterpret_cast<ChallengeItem*>(P->base + o_items_f4);
+  P->d_r = reinterpret_cast<float*>(P->base + o_r);
+  P->d_r_b3 = reinterpret_cast<uint16_t*>(P->base + o_rb3);
+  P->d_r_f4 = reinterpret_cast<float*>(P->base + o_rf4);
+  P->d_jobs = reinterpret_cast<PassJob*>(P->base + o_jobs);
+  P->d_blk = reinterpret_cast<uint32_t*>(P->base + o_blk);
+  P->d_red = reinterpret_cast<RedJob*>(P->base + o_red);
+  P->d_fin = reinterpret_cast<FinJob*>(P->base + o_fin);
+
+  // Fill the job pointers now that addresses are known.
+  for (size_t oi = 0; oi < ordered.size(); oi++) {
+    PassJob& J = ordered[oi];
+    const uint32_t src = ordered_src[oi];
+    J.pdot = base + o_parts + off_dot[src];
+    J.pabs = base + o_parts + off_abs[src];
+    J.psq = base + o_parts + off_sq[src];
+    const size_t pi = src % n;
+    const pots_fv_product& p = prods[pi];
+    if (src < n) {  // B pass: V = R in B's layout
+      J.v = p.b_dtype == DT_BF16 ? base + o_rb3 + 2 * items_b3[pi].pk_off
+                                 : base + o_rf4 + 4 * items_f4[pi].pk_off;
+    } else if (src < 2 * n) {  // A pass: V = packed B·R, weights b1 and b2
+      J.v = base + o_br + off_br[pi];
+      J.u = base + o_br + off_b1[pi];
+      J.w = base + o_br + off_b2[pi];
+    } else {  // P pass: V = R in P's layout
+      J.v = p.p_dtype == DT_BF16 ? base + o_rb3 + 2 * items_b3[pi].pk_off
+                                 : base + o_rf4 + 4 * items_f4[pi].pk_off;
+    }
+  }
+  // The original job index -> ordered position, for the reduction and finish tables.
+  std::vector<size_t> pos(jobs.size());
+  for (size_t oi = 0; oi < ordered.size(); oi++) pos[ordered_src[oi]] = oi;
+  std::vector<RedJob> red(n);
+  uint64_t gthreads = 0;
+  for (size_t i = 0; i < n; i++) {
+    const PassJob& J = ordered[pos[i]];
+    RedJob& R = red[i];
+    R.pdot = J.pdot;
+    R.pabs = J.pabs;
+    R.psq = J.psq;
+    R.vout = base + o_br + off_br[i];
+    R.u = base + o_br + off_b1[i];
+    R.w = base + o_br + off_b2[i];
+    R.group_first = gthreads;
+    R.rows = prods[i].q;
+    R.rows_pad = J.rows_pad;
+    R.n_chunks = J.n_chunks;
+    R.a_dt = prods[i].a_dtype;
+    gthreads += (uint64_t)(pad32(prods[i].q) / 8) * k;
+  }
+  P->n_red = (uint32_t)n;
+  P->n_red_threads = gthreads;
+  std::vector<FinJob> fin(n);
+  for (size_t i = 0; i < n; i++) {
+    const PassJob& A = ordered[pos[n + i]];
+    const PassJob& Pp = ordered[pos[2 * n + i]];
+    FinJob& F = fin[i];
+    F.a_dot = A.pdot;
+    F.a_abs = A.pabs;
+    F.a_sq = A.psq;
+    F.p_dot = Pp.pdot;
+    F.p_abs = Pp.pabs;
+    F.p_sq = Pp.psq;
+    F.r = base + o_r + 4 * items[i].out_off;
+    F.bias = reinterpret_cast<uint64_t>(prods[i].bias);
+    F.n = prods[i].n;
+    F.w = prods[i].w;
+    F.a_rows_pad = A.rows_pad;
+    F.a_chunks = A.n_chunks;
+    F.p_rows_pad = Pp.rows_pad;
+    F.p_chunks = Pp.n_chunks;
+  }
+  // Upload the tables.
+  auto up = [&](size_t off, const void* src, size_t bytes) -> int {
+    if (!bytes) return POTS_E_OK;
+    POTS_HIP(hipMemcpy(P->base + off, src, bytes, hipMemcpyHostToDevice));
+    return POTS_E_OK;
+  };
+  int rc = POTS_E_OK;
+  if ((rc = up(o_items_b3, items_b3.data(), n * sizeof(ChallengeItem))) ||
+      (rc = up(o_items_f4, items_f4.data(), n * sizeof(ChallengeItem))) ||
+      (rc = up(o_jobs, ordered.data(), ordered.size() * sizeof(PassJob))) ||
+      (rc = up(o_blk, blk_table.data(), blk_table.size() * 4)) ||
+      (rc = up(o_red, red.data(), n * sizeof(RedJob))) ||
+      (rc = up(o_fin, fin.data(), n * sizeof(FinJob)))) {
+    (void)hipFree(P->base);
+    delete P;
+    return rc;
+  }
+  *plan = P;
+  return POTS_E_OK;
+}
+
+template <uint32_t XT, bool W, bool S>
+static void launch_pass(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
+  hipLaunchKernelGGL((row_pass<XT, W, S>), dim3(L.n_blocks), dim3(256), 0, s,
+                     P->d_jobs + L.job_off, L.n_tiles, P->d_blk + L.blk_off, P->k);
+}
+
+static int run_pass(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
+  if (L.n_tiles == 0) return POTS_E_OK;
+  const uint32_t key = L.xt * 4 + L.weighted * 2 + L.sq64;
+  switch (key) {
+    case 0: launch_pass<DT_F32, false, false>(P, L, s); break;
+    case 1: launch_pass<DT_F32, false, true>(P, L, s); break;
+    case 2: launch_pass<DT_F32, true, false>(P, L, s); break;
+    case 4: launch_pass<DT_BF16, false, false>(P, L, s); break;
+    case 5: launch_pass<DT_BF16, false, true>(P, L, s); break;
+    case 6: launch_pass<DT_BF16, true, false>(P, L, s); break;
+    default: return POTS_E_ARG;
+  }
+  POTS_HIP(hipGetLastError());
+  return POTS_E_OK;
+}
+
+extern "C" int pots_fv_plan_run(void* plan, const uint8_t* d_key, double* d_rows, void* stream) {
+  if (!plan || !d_key || !d_rows) return POTS_E_ARG;
+  FvPlan* P = static_cast<FvPlan*>(plan);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc;
+  POTS_HIP(hipMemcpyAsync(P->d_key, d_key, 32, hipMemcpyDeviceToDevice, s));
+  // R in row-major form (for the bias term and the API) and in the packed layouts.
+  if ((rc = challenges_enqueue(P->d_key, P->d_items_b3, P->n_items, P->n_units, P->k, P->d_r,
+                               P->need_b3 ? P->d_r_b3 : nullptr, nullptr, s)) != POTS_E_OK)
+    return rc;
+  if (P->need_f4 &&
+      (rc = challenges_enqueue(P->d_key, P->d_items_f4, P->n_items, P->n_units, P->k, nullptr,
+                               nullptr, P->d_r_f4, s)) != POTS_E_OK)
+    return rc;
+  for (const PassLaunch& L : P->pass_b)
+    if ((rc = run_pass(P, L, s)) != POTS_E_OK) return rc;
+  {
+    const uint64_t blocks = (P->n_red_threads + 255) / 256;
+    hipLaunchKernelGGL(reduce_b, dim3((uint32_t)blocks), dim3(256), 0, s, P->d_red, P->n_red,
+                       P->n_red_threads, P->k);
+    POTS_HIP(hipGetLastError());
+  }
+  for (const PassLaunch& L : P->pass_ap)
+    if ((rc = run_pass(P, L, s)) != POTS_E_OK) return rc;
+  hipLaunchKernelGGL(finish_rows, dim3((uint32_t)P->n), dim3(256), 0, s, P->d_fin, P->k,
+                     P->guard, d_rows);
+  POTS_HIP(hipGetLastError());
+  return POTS_E_OK;
+}
+
+extern "C" int pots_fv_plan_copy_challenges(const void* plan, float* d_out, void* stream) {
+  if (!plan || !d_out) return POTS_E_ARG;
+  const FvPlan* P = static_cast<const FvPlan*>(plan);
+  POTS_HIP(hipMemcpyAsync(d_out, P->d_r, P->r_floats * 4, hipMemcpyDeviceToDevice,
+                          static_cast<hipStream_t>(stream)));
+  return POTS_E_OK;
+}
+
+extern "C" uint64_t pots_fv_plan_bytes(const void* plan) {
+  return plan ? static_cast<const FvPlan*>(plan)->bytes : 0;
+}
+
+extern "C" void pots_fv_plan_destroy(void* plan) {
+  FvPlan* P = static_cast<FvPlan*>(plan);
+  if (!P) return;
+  if (P->base) (void)hipFree(P->base);
+  delete P;
+}

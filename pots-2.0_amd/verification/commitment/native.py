@@ -87,6 +87,15 @@ class Native:
             "pots_leaf_plan_bytes": ([_vp], _u64),
             "pots_leaf_plan_destroy": ([_vp], None),
             "pots_merkle_tree_async": ([_sz, _vp, _vp, _vp], _int),
+            "pots_challenges": ([_vp, _u32, _sz, _vp, _vp, _vp, _vp, _u32], _int),
+            "pots_fv_plan_create": ([_sz, _vp, _u32, _u32, ctypes.POINTER(_vp)], _int),
+            "pots_fv_plan_run": ([_vp, _vp, _vp, _vp], _int),
+            "pots_fv_plan_copy_challenges": ([_vp, _vp, _vp], _int),
+            "pots_fv_plan_bytes": ([_vp], _u64),
+            "pots_fv_plan_destroy": ([_vp], None),
+            "pots_verdicts_async": ([_sz, _vp, _u32, _vp, ctypes.c_double, ctypes.c_double,
+                                     ctypes.c_double, ctypes.c_double, ctypes.c_double, _u32,
+                                     _u32, _vp, _vp, _vp, _vp], _int),
         }
         for name, (args, res) in sigs.items():
             fn = getattr(lib, name)
@@ -174,6 +183,61 @@ class Native:
                                                      _stream(stream)), "pots_merkle_tree_async")
         return nodes
 
+    def challenge_matrices(self, h: bytes, ms: Sequence[int], k: int, width: int, *,
+                           threads: int = 1, device: torch.device | str = "cuda"
+                           ) -> torch.Tensor:
+        """The protocol's ``challenge_matrices``, bit for bit: fp32 ``[len(ms), width, k]``
+        on the GPU (native.py:263-284)."""
+        if len(h) != 32:
+            raise ValueError("h must be 32 bytes")
+        if not 1 <= k <= 255:
+            raise ValueError(f"k must be in [1, 255], got {k}")
+        if not 1 <= width < 1 << 32:
+            raise ValueError(f"width must be in [1, 2^32), got {width}")
+        for m in ms:
+            if not 1 <= m < 1 << 32:
+                raise ValueError(f"m must be in [1, 2^32), got {m}")
+        n = len(ms)
+        out = torch.empty(n, width, k, dtype=torch.float32, device=device)
+        if n == 0:
+            return out
+        msa = np.asarray(ms, dtype=np.uint32)
+        widths = np.full(n, width, dtype=np.uint32)
+        offs = np.arange(n, dtype=np.uint64) * np.uint64(width * k)
+        self._check(self._lib.pots_challenges(bytes(h), k, n, _addr(msa), _addr(widths),
+                                              _addr(offs), out.data_ptr(), 1),
+                    "pots_challenges")
+        return out
+
+    def fv_plan(self, products: Sequence[FvProduct], k: int, guard: bool = True) -> FvPlan:
+        """A Freivalds plan over GPU-resident products (``pots_fv_plan_*``)."""
+        return FvPlan(self, products, k, guard)
+
+    def verdicts(self, rows: torch.Tensor, specs: torch.Tensor, *, k: int, eps_in: float,
+                 eps_acc: float, tau: float, guard: bool = True, judge: bool = True,
+                 finished: bool = False, stream: torch.cuda.Stream | None = None
+                 ) -> tuple[torch.Tensor, torch.Tensor | None, torch.Tensor]:
+        """Per-product verdicts on the GPU: ``(codes int32 [n, 2], finished fp64 [n, 3] or
+        None, first_fail int32 [1])``. ``specs`` is the packed per-product table of
+        :func:`verdict_specs`."""
+        import math
+        n = rows.shape[0]
+        dev = rows.device
+        codes = torch.empty(n, 2, dtype=torch.int32, device=dev)
+        fin = torch.empty(n, 3, dtype=torch.float64, device=dev) if finished else None
+        first = torch.empty(1, dtype=torch.int32, device=dev)
+        if n == 0:
+            first.fill_(0)
+            return codes, fin, first
+        if rows.dtype != torch.float64 or not rows.is_contiguous() or rows.shape[1] != 5 + k:
+            raise ValueError("rows must be contiguous fp64 [n, 5 + k]")
+        self._check(self._lib.pots_verdicts_async(
+            n, rows.data_ptr(), k, specs.data_ptr(), float(eps_in), float(eps_acc), float(tau),
+            1.0 / math.sqrt(3.0), math.sqrt(2.0), int(bool(guard)), int(bool(judge)),
+            codes.data_ptr(), fin.data_ptr() if fin is not None else None, first.data_ptr(),
+            _stream(stream)), "pots_verdicts_async")
+        return codes, fin, first
+
     def leaf_plan(self, headers: Sequence[bytes], payloads: Sequence[torch.Tensor],
                   kinds: Sequence[int]) -> LeafPlan:
         """A reusable hashing plan over GPU-resident payloads: leaf ``i`` is
@@ -236,6 +300,135 @@ class LeafPlan:
     def close(self) -> None:
         if getattr(self, "_h", None) is not None and self._h.value:
             self._lib._lib.pots_leaf_plan_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+DT_F32, DT_BF16 = 0, 1
+_DT = {torch.float32: DT_F32, torch.bfloat16: DT_BF16}
+
+
+class _FvProductC(ctypes.Structure):
+    _fields_ = [("a", _vp), ("b", _vp), ("p", _vp), ("bias", _vp), ("lda", _u64),
+                ("ldb", _u64), ("ldp", _u64), ("n", _u32), ("q", _u32), ("w", _u32),
+                ("m", _u32), ("a_dtype", _u32), ("b_dtype", _u32), ("p_dtype", _u32),
+                ("pad", _u32)]
+
+
+class FvProduct:
+    """One checked product for :class:`FvPlan`: GPU tensors ``a`` [n, q], ``b`` [q, w], ``p``
+    [n, w] (fp32 or bf16, unit column stride), an optional fp32 ``bias`` [w], and the
+    challenge label ``m``."""
+
+    __slots__ = ("a", "b", "p", "bias", "m")
+
+    def __init__(self, a: torch.Tensor, b: torch.Tensor, p: torch.Tensor, m: int,
+                 bias: torch.Tensor | None = None) -> None:
+        self.a, self.b, self.p, self.m, self.bias = a, b, p, m, bias
+
+
+def verdict_specs(qs: Sequence[int], ns: Sequence[int], biased: Sequence[bool],
+                  kappa_max: Sequence[float], device: torch.device | str = "cuda"
+                  ) -> torch.Tensor:
+    """The per-product table ``pots_verdicts_async`` reads: 24-byte records
+    ``{double kappa_max; uint32 q, n, biased, pad}``."""
+    n = len(qs)
+    rec = np.zeros(n, dtype=np.dtype([("kappa", "<f8"), ("q", "<u4"), ("n", "<u4"),
+                                      ("biased", "<u4"), ("pad", "<u4")]))
+    rec["kappa"] = np.asarray(kappa_max, dtype=np.float64)
+    rec["q"] = np.asarray(qs, dtype=np.uint32)
+    rec["n"] = np.asarray(ns, dtype=np.uint32)
+    rec["biased"] = np.asarray(biased, dtype=np.uint32)
+    return torch.from_numpy(rec.view(np.uint8).copy()).to(device)
+
+
+class FvPlan:
+    """``pots_fv_plan_*``: operand layout and workspace fixed once; :meth:`rows` enqueues the
+    challenges, the three streaming passes and the reduction for every product."""
+
+    def __init__(self, lib: Native, products: Sequence[FvProduct], k: int,
+                 guard: bool = True) -> None:
+        n = len(products)
+        if n == 0:
+            raise ValueError("a Freivalds plan needs at least one product")
+        if not 1 <= k <= 255:
+            raise ValueError(f"k must be in [1, 255], got {k}")
+        arr = (_FvProductC * n)()
+        keep = []
+        for i, pr in enumerate(products):
+            a, b, p = pr.a, pr.b, pr.p
+            for name, t in (("a", a), ("b", b), ("p", p)):
+                if not t.is_cuda or t.dim() != 2 or t.stride(1) != 1 or t.dtype not in _DT:
+                    raise ValueError(f"product {i}: {name} must be a 2-D GPU tensor in fp32 or "
+                                     f"bf16 with unit column stride")
+            nn, q = a.shape
+            q2, w = b.shape
+            if q2 != q or tuple(p.shape) != (nn, w):
+                raise ValueError(f"product {i}: shapes {tuple(a.shape)}·{tuple(b.shape)} vs "
+                                 f"{tuple(p.shape)}")
+            if not 1 <= pr.m < 1 << 32:
+                raise ValueError(f"m must be in [1, 2^32), got {pr.m}")
+            bias = pr.bias
+            if bias is not None:
+                bias = bias.detach().to(device=a.device, dtype=torch.float32).contiguous()
+                if bias.shape != (w,):
+                    raise ValueError(f"product {i}: bias of shape {tuple(bias.shape)}, "
+                                     f"expected ({w},)")
+                keep.append(bias)
+            c = arr[i]
+            c.a, c.b, c.p = a.data_ptr(), b.data_ptr(), p.data_ptr()
+            c.bias = bias.data_ptr() if bias is not None else None
+            c.lda, c.ldb, c.ldp = a.stride(0), b.stride(0), p.stride(0)
+            c.n, c.q, c.w, c.m = nn, q, w, pr.m
+            c.a_dtype, c.b_dtype, c.p_dtype = _DT[a.dtype], _DT[b.dtype], _DT[p.dtype]
+            keep += [a, b, p]
+        h = ctypes.c_void_p()
+        lib._check(lib._lib.pots_fv_plan_create(n, ctypes.addressof(arr), k, int(bool(guard)),
+                                                ctypes.byref(h)), "pots_fv_plan_create")
+        self._lib, self._h, self._keep = lib, h, keep
+        self.n, self.k = n, k
+        self.widths = [pr.p.shape[1] for pr in products]
+        self.device = products[0].a.device
+        self.bytes = int(lib._lib.pots_fv_plan_bytes(h))
+        self._key = torch.empty(32, dtype=torch.uint8, device=self.device)
+
+    def rows(self, h: bytes | torch.Tensor, out: torch.Tensor | None = None,
+             stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """fp64 ``[n, 5 + k]`` rows (``freivalds.ROW``), challenges keyed on ``h`` (32 bytes,
+        host bytes or a GPU uint8 tensor). Stream-ordered, no sync."""
+        if isinstance(h, torch.Tensor):
+            key = h
+        else:
+            if len(h) != 32:
+                raise ValueError("h must be 32 bytes")
+            key = self._key
+            key.copy_(torch.frombuffer(bytearray(h), dtype=torch.uint8), non_blocking=False)
+        if out is None:
+            out = torch.empty(self.n, 5 + self.k, dtype=torch.float64, device=self.device)
+        self._lib._check(self._lib._lib.pots_fv_plan_run(self._h, key.data_ptr(), out.data_ptr(),
+                                                         _stream(stream)), "pots_fv_plan_run")
+        return out
+
+    def challenges(self) -> list[torch.Tensor]:
+        """The last run's challenge matrices, fp32 ``[w_i, k]`` per product (GPU views)."""
+        total = sum(self.widths) * self.k
+        flat = torch.empty(total, dtype=torch.float32, device=self.device)
+        self._lib._check(self._lib._lib.pots_fv_plan_copy_challenges(
+            self._h, flat.data_ptr(), _stream(None)), "pots_fv_plan_copy_challenges")
+        out, at = [], 0
+        for w in self.widths:
+            out.append(flat[at:at + w * self.k].view(w, self.k))
+            at += w * self.k
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            self._lib._lib.pots_fv_plan_destroy(self._h)
             self._h = ctypes.c_void_p()
 
     def __del__(self) -> None:
