@@ -131,11 +131,9 @@ def main() -> int:
     import torch
 
     from verification.commitment import native
-    from verification.commitment.leaves import StepHasher
     from verification.computation.instances import decoder
-    from verification.parameters import UNIT_ROUNDOFF
     from verification.prover.synthetic import synthetic_step
-    from verification.verifier.bands import Bands
+    from verification.verifier.step import DeviceStepVerifier
 
     lib = native.get()
     desc, ctor, k = CONFIGS[args.config]
@@ -149,68 +147,98 @@ def main() -> int:
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB resident")
 
     stream = torch.cuda.current_stream()
-    hasher = StepHasher(c, step.leaves)
     items = product_inputs(step)
-    plan = lib.fv_plan([native.FvProduct(a, b, p, m, bias) for a, b, p, bias, m in items], k)
-    bands = Bands.provisional()
-    specs = native.verdict_specs([s.q for s in c.products], [s.a_shape[0] for s in c.products],
-                                 [s.bias is not None for s in c.products],
-                                 [bands.kappa_for(c.product_class(s)) for s in c.products])
-    eps_in, eps_acc = UNIT_ROUNDOFF[c.product_dtype], UNIT_ROUNDOFF[torch.float32]
-    digests = torch.empty(c.n_leaves, 32, dtype=torch.uint8, device="cuda")
-    bad = torch.empty(1, dtype=torch.int32, device="cuda")
-    rows = torch.empty(c.M, 5 + k, dtype=torch.float64, device="cuda")
+    v = DeviceStepVerifier(c, step.leaves, lambda spec: step.operands[spec.m], k=k)
     # The claimed root: the honest root of this transcript, as the prover would send it.
-    hasher.digests(digests, bad, stream)
-    claimed = lib.merkle_tree_device(digests, stream)[0].clone()
+    v.hasher.digests(v.digests, v.bad, stream)
+    claimed = lib.merkle_tree_device(v.digests, stream)[0].clone()
     torch.cuda.synchronize()
-    log(f"[bench] claimed root {bytes(claimed.cpu().numpy()).hex()[:16]}…; "
-        f"hash {hasher.bytes / 1e9:.2f} GB, Freivalds {plan.bytes / 1e9:.2f} GB")
+    claimed_b = bytes(claimed.cpu().numpy())
+    hash_bytes, fv_bytes = v.hash_bytes, v.freivalds_bytes
+    log(f"[bench] claimed root {claimed_b.hex()[:16]}…; hash {hash_bytes / 1e9:.2f} GB, "
+        f"Freivalds {fv_bytes / 1e9:.2f} GB")
 
-    def one_step(ev=None):
-        if ev:
-            ev[0].record(stream)
-        hasher.digests(digests, bad, stream)
-        if ev:
-            ev[1].record(stream)
-        nodes = lib.merkle_tree_device(digests, stream)
-        if ev:
-            ev[2].record(stream)
-        plan.rows(claimed, rows, stream)
-        if ev:
-            ev[3].record(stream)
-        codes, _, first = lib.verdicts(rows, specs, k=k, eps_in=eps_in, eps_acc=eps_acc,
-                                       tau=bands.tau, stream=stream)
-        if ev:
-            ev[4].record(stream)
-        flags = torch.cat([nodes[0].view(torch.int32), bad, first])
+    def one_step(events=None):
+        nodes, codes, first = v.enqueue(claimed, events)
+        flags = torch.cat([nodes[0].view(torch.int32), v.bad, first])
         return flags.cpu(), codes
 
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
+    evs: list = []
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        flags, codes = one_step(evs[i])
+    for _ in range(args.steps):
+        flags, codes = one_step(evs)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = wall / args.steps * 1e3
-    part = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / args.steps for i in range(4)]
-    hash_ms, tree_ms, fv_ms, verdict_ms = part
+    hashed_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    measured_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / args.steps
     root = flags[:8].numpy().tobytes()
     first_bad, first_fail = int(flags[8]), int(flags[9])
-    assert root == bytes(claimed.cpu().numpy()), "recomputed root differs from the claim"
+    assert root == claimed_b, "recomputed root differs from the claim"
     assert first_bad == c.n_leaves, "a synthetic leaf was reported non-finite"
     n_rej = int((codes[:, 0] != 0).sum())
-    log(f"[bench] step {ms:.2f} ms: hash {hash_ms:.2f}, tree {tree_ms:.3f}, Freivalds "
-        f"{fv_ms:.2f}, verdicts {verdict_ms:.3f} ms; {n_rej} rejected (first {first_fail})")
-    hash_gbps = hasher.bytes / (hash_ms * 1e-3) / 1e9
-    fv_gbps = plan.bytes / (fv_ms * 1e-3) / 1e9
-    total = hasher.bytes + plan.bytes
+    log(f"[bench] step {ms:.2f} ms (streams overlapped: hashing done at {hashed_ms:.2f} ms, "
+        f"Freivalds rows at {measured_ms:.2f} ms); {n_rej} rejected (first {first_fail})")
+
+    # Stage leg: the same work serialised on one stream, every stage bracketed by events on
+    # that stream, for the per-kernel figures and the roofline.
+    names = ([f"hash.{s}" for s in native.LeafPlan.STAGES] + ["tree"] +
+             [f"freivalds.{s}" for s in native.FvPlan.STAGES] + ["verdicts"])
+
+    def staged(ev):
+        i = 0
+        ev[i].record(stream)
+        for st in range(len(native.LeafPlan.STAGES)):
+            v.hasher.plan.run_stage(st, v.digests, v.bad, stream)
+            i += 1
+            ev[i].record(stream)
+        lib.merkle_tree_device(v.digests, stream)
+        i += 1
+        ev[i].record(stream)
+        v.key.copy_(claimed)
+        for st in range(len(native.FvPlan.STAGES)):
+            v.plan.run_stage(st, v.key, v.rows, stream)
+            i += 1
+            ev[i].record(stream)
+        lib.verdicts(v.rows, v.specs, k=k, eps_in=v.eps_in, eps_acc=v.eps_acc, tau=v.bands.tau,
+                     stream=stream)
+        i += 1
+        ev[i].record(stream)
+
+    n_stage_runs = max(3, min(args.steps, 5))
+    sev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+           for _ in range(n_stage_runs)]
+    for ev in sev:
+        staged(ev)
+    torch.cuda.synchronize()
+    stage_ms = {nm: sum(ev[i].elapsed_time(ev[i + 1]) for ev in sev) / n_stage_runs
+                for i, nm in enumerate(names)}
+    serial_ms = sum(stage_ms.values())
+    log("[bench] serialised stages (ms): " +
+        ", ".join(f"{nm} {t:.3f}" for nm, t in stage_ms.items()) + f"; total {serial_ms:.2f}")
+
+    # Algorithmic HBM bytes of each single-kernel stage: the operand every element of which
+    # the kernel reads once (A, B or P of every product; every leaf's message bytes plus one
+    # 32-byte chaining value written per 1 KiB chunk).
+    a_bytes = sum(a.nbytes for a, _, _, _, _ in items)
+    b_bytes = sum(b.nbytes for _, b, _, _, _ in items)
+    p_bytes = sum(p.nbytes for _, _, p, _, _ in items)
+    kernels = {
+        "hash.chunks": ("chunk_kernel", hash_bytes + 32 * v.hasher.plan.chunks),
+        "freivalds.a_pass": ("row_pass<bf16, weighted> (A pass)", a_bytes),
+        "freivalds.p_pass": ("row_pass<bf16, fp64 squares> (P pass)", p_bytes),
+        "freivalds.b_pass": ("row_pass<bf16> (B pass)", b_bytes),
+    }
+    dom = max(kernels, key=lambda nm: stage_ms[nm])
+    dom_name, dom_bytes = kernels[dom]
+    achieved = dom_bytes / (stage_ms[dom] * 1e-3) / 1e9
+    hash_ms = sum(stage_ms[f"hash.{s}"] for s in native.LeafPlan.STAGES)
+    fv_ms = sum(stage_ms[f"freivalds.{s}"] for s in native.FvPlan.STAGES)
+    total = hash_bytes + fv_bytes
     value = total / (ms * 1e-3) / 1e9
-    dominant = ("freivalds", fv_gbps, fv_ms) if fv_ms >= hash_ms else ("hash", hash_gbps, hash_ms)
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
@@ -221,21 +249,22 @@ def main() -> int:
                                "Merkle root, check 5 challenges + Freivalds + verdicts) on a "
                                "transcript resident in HBM",
                    "leaves": c.n_leaves, "products": c.M, "k": k,
-                   "hash_bytes": hasher.bytes, "freivalds_bytes": plan.bytes},
+                   "hash_bytes": hash_bytes, "freivalds_bytes": fv_bytes},
         "parts": {"step_verify_ms": round(ms, 3),
-                  "hash_ms": round(hash_ms, 3), "hash_gbps": round(hash_gbps, 1),
-                  "hash_frac_hbm": round(hash_gbps / HBM_PEAK_GBPS, 4),
-                  "tree_ms": round(tree_ms, 4),
-                  "freivalds_ms": round(fv_ms, 3), "freivalds_gbps": round(fv_gbps, 1),
-                  "freivalds_frac_hbm": round(fv_gbps / HBM_PEAK_GBPS, 4),
-                  "verdict_ms": round(verdict_ms, 4),
                   "step_frac_hbm": round(value / HBM_PEAK_GBPS, 4),
+                  "overlap": {"hashed_at_ms": round(hashed_ms, 3),
+                              "rows_at_ms": round(measured_ms, 3),
+                              "serial_ms": round(serial_ms, 3)},
+                  "hash_ms": round(hash_ms, 3),
+                  "hash_gbps": round(hash_bytes / (hash_ms * 1e-3) / 1e9, 1),
+                  "freivalds_ms": round(fv_ms, 3),
+                  "freivalds_gbps": round(fv_bytes / (fv_ms * 1e-3) / 1e9, 1),
+                  "stages_ms": {nm: round(t, 4) for nm, t in stage_ms.items()},
                   "rejected": n_rej},
-        "roofline": {"bound": "hbm", "achieved": round(dominant[1], 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(dominant[1] / HBM_PEAK_GBPS, 4),
-                     "traffic": None,
-                     "kernel": "row_pass x3 + reduce + finish (Freivalds)" if dominant[0] ==
-                     "freivalds" else "chunk_kernel + level_kernel (leaf hashing)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "kernel": dom_name,
+                     "algorithmic_bytes": dom_bytes, "launch_ms": round(stage_ms[dom], 4)},
     }
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")

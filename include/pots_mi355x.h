@@ -84,6 +84,21 @@ int pots_leaf_plan_create(size_t n, const uint8_t *hdr_buf, const uint64_t *hdr_
  * non-finite leaf index (or n) to *d_first_bad (device uint32). No allocation, no sync. */
 int pots_leaf_plan_run(void *plan, uint8_t *d_out, uint32_t *d_first_bad, void *stream);
 
+/* pots_leaf_plan_run is these stages in order: 0 the staging copies and the first-bad reset,
+ * 1 the chunk kernel (every 1 KiB chunk's chaining value, the NaN/Inf test fused), 2 the
+ * per-leaf BLAKE3 trees above the chunks. Enqueued on `stream` one at a time, so a caller can
+ * time each stage; the caller keeps the order. No counterpart in the reference. */
+#define POTS_LEAF_STAGES 3
+int pots_leaf_plan_run_stage(void *plan, int stage, uint8_t *d_out, uint32_t *d_first_bad,
+                             void *stream);
+
+/* Limit the chunk kernel's grid to max_blocks blocks of 256 lanes (0: no limit, one block per
+ * 256 chunks). Each block then hashes several slots of 256 chunks in turn, and the kernel
+ * holds at most that many blocks' worth of the GPU, leaving the rest to work on other
+ * streams (the Freivalds passes, which are bound by HBM, not by the VALUs hashing needs).
+ * Results do not depend on it. No counterpart in the reference. */
+int pots_leaf_plan_set_grid(void *plan, uint32_t max_blocks);
+
 /* Chunks (1 KiB BLAKE3 chunks) and message bytes the plan hashes. */
 uint64_t pots_leaf_plan_chunks(const void *plan);
 uint64_t pots_leaf_plan_bytes(const void *plan);
@@ -123,6 +138,15 @@ int pots_fv_plan_create(size_t n, const pots_fv_product *products, uint32_t k, u
  * product to d_rows [n][5 + k] in freivalds.ROW order (freivalds.py:255): nu, ‖|P|1‖, ‖P‖_F,
  * Σ_i (A²(B²1))_i, ‖b‖², residual_1..k. No allocation, no sync. */
 int pots_fv_plan_run(void *plan, const uint8_t *d_key, double *d_rows, void *stream);
+
+/* pots_fv_plan_run is these stages in order: 0 the challenge matrices, 1 the B pass
+ * (b1 = B·R, b2 = (B²)·1), 2 the reduction of B's split-K partials, 3 the A pass (A·b1 and
+ * (A²)·b2), 4 the P pass (P·R, Σ|P|, ΣP²), 5 the rows. Enqueued on `stream` one at a time,
+ * so a caller can time each stage; the caller keeps the order. No counterpart in the
+ * reference. */
+#define POTS_FV_STAGES 6
+int pots_fv_plan_run_stage(void *plan, int stage, const uint8_t *d_key, double *d_rows,
+                           void *stream);
 
 /* Copy the last run's row-major challenge matrices (fp32; product i's [w_i, k] block follows
  * product i-1's) to d_out (device, Σ w_i·k floats), enqueued on `stream`. */

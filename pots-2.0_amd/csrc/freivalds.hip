@@ -31,12 +31,14 @@
 
 #include "common.h"
 #include "freivalds.h"
+#include "gmem.h"
 
 namespace pots {
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef float v4f32 __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 enum : uint32_t { DT_F32 = 0, DT_BF16 = 1 };
 
@@ -79,8 +81,159 @@ struct SqAcc<false> {
 
 // ---- the row pass ---------------------------------------------------------------------------
 
+// Rows per wave (RT tiles of 16) and K-steps per pipeline stage (KU) of the row pass.
+#ifndef POTS_FV_RT
+#define POTS_FV_RT 4
+#endif
+#ifndef POTS_FV_KU
+#define POTS_FV_KU 1
+#endif
+constexpr int RT = POTS_FV_RT;
+constexpr int KU = POTS_FV_KU;
+
+// One pipeline stage's operands in registers: for each of KU K-steps, PER consecutive X
+// elements of each of the RT row tiles (4 words), the V operand of this lane's challenge
+// column for its PER columns (bf16: 3 planes x 8 bf16; fp32: 4 floats in v[0]), and the
+// per-column weights.
+template <uint32_t XT>
+struct StepRegs {
+  uint32_t xw[KU][RT][4];
+  u32x4 v[KU][3];
+  float uc[KU][XT == DT_BF16 ? 8 : 4], wc[KU][XT == DT_BF16 ? 8 : 4];
+};
+
+// Load KU K-steps starting at the step whose first column for this lane is `cl`. `full`: the
+// job is aligned and every step lies before c1, so every load is a 16-byte vector load with
+// no column guard (rows past the matrix read a valid row; their results are never written).
+template <uint32_t XT, bool WEIGHTED>
+__device__ __forceinline__ void load_stage(StepRegs<XT>& r, const char* const xrow[RT],
+                                           const bool rv[RT], uint32_t cl, uint32_t c1,
+                                           bool full, const PassJob& J, uint32_t k, uint32_t j,
+                                           bool vload, bool sums, int nsteps = KU) {
+  constexpr uint32_t PER = XT == DT_BF16 ? 8 : 4;
+  constexpr uint32_t KSTEP = XT == DT_BF16 ? 32 : 16;
+  constexpr uint32_t esz = XT == DT_BF16 ? 2 : 4;
+#pragma unroll
+  for (int u = 0; u < KU; u++) {
+    const uint32_t cu = cl + u * KSTEP;
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+      if (full) {
+        const u32x4 q = gload<u32x4>(xrow[t] + (uint64_t)cu * esz);
+        r.xw[u][t][0] = q.x; r.xw[u][t][1] = q.y; r.xw[u][t][2] = q.z; r.xw[u][t][3] = q.w;
+      } else if (XT == DT_BF16) {
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(xrow[t]);
+        uint16_t e[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+          e[s] = (u < nsteps && rv[t] && cu + s < c1) ? gload<uint16_t>(p + cu + s) : (uint16_t)0;
+#pragma unroll
+        for (int s = 0; s < 4; s++) r.xw[u][t][s] = e[2 * s] | (uint32_t)e[2 * s + 1] << 16;
+      } else {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(xrow[t]);
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+          r.xw[u][t][s] = (u < nsteps && rv[t] && cu + s < c1) ? gload<uint32_t>(p + cu + s) : 0u;
+      }
+    }
+    r.v[u][0] = r.v[u][1] = r.v[u][2] = u32x4{0, 0, 0, 0};
+    if (vload && (full || (u < nsteps && cu < c1))) {
+      if (XT == DT_BF16) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(J.v) +
+                                                          ((uint64_t)(cu / 8) * k + j) * 24);
+        r.v[u][0] = gload<u32x4>(src);
+        r.v[u][1] = gload<u32x4>(src + 1);
+        r.v[u][2] = gload<u32x4>(src + 2);
+      } else {
+        r.v[u][0] = gload<u32x4>(reinterpret_cast<const float*>(J.v) +
+                                 ((uint64_t)(cu / 4) * k + j) * 4);
+      }
+    }
+    if (WEIGHTED && sums) {
+      const float* uw = reinterpret_cast<const float*>(J.u);
+      const float* ww = reinterpret_cast<const float*>(J.w);
+#pragma unroll
+      for (uint32_t s = 0; s < PER; s++) {
+        const bool ok = full || (u < nsteps && cu + s < c1);
+        r.uc[u][s] = ok ? gload<float>(uw + cu + s) : 0.f;
+        r.wc[u][s] = ok ? gload<float>(ww + cu + s) : 0.f;
+      }
+    }
+  }
+}
+
+template <uint32_t XT, bool WEIGHTED, bool SQ64>
+__device__ __forceinline__ void compute_stage(const StepRegs<XT>& r, v4f32 acc[RT], float s1[RT],
+                                              SqAcc<SQ64> s2[RT], bool sums) {
+#pragma unroll
+  for (int u = 0; u < KU; u++) {
+    if (XT == DT_BF16) {
+#pragma unroll
+      for (int t = 0; t < RT; t++) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const v4i16 a = __builtin_bit_cast(v4i16, v2u32{r.xw[u][t][2 * h], r.xw[u][t][2 * h + 1]});
+#pragma unroll
+          for (int p = 0; p < 3; p++) {
+            const v2u32 bw = h == 0 ? v2u32{r.v[u][p].x, r.v[u][p].y} : v2u32{r.v[u][p].z, r.v[u][p].w};
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(v4i16, bw),
+                                                               acc[t], 0, 0, 0);
+          }
+        }
+      }
+      if (sums) {
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+#pragma unroll
+          for (int s = 0; s < 4; s++) {
+            const float xa = bf_lo(r.xw[u][t][s]), xb = bf_hi(r.xw[u][t][s]);
+            if (WEIGHTED) {
+              s1[t] = fmaf(fabsf(xa), r.uc[u][2 * s], s1[t]);
+              s1[t] = fmaf(fabsf(xb), r.uc[u][2 * s + 1], s1[t]);
+              s2[t].add(xa, r.wc[u][2 * s]);
+              s2[t].add(xb, r.wc[u][2 * s + 1]);
+            } else {
+              s1[t] += fabsf(xa);
+              s1[t] += fabsf(xb);
+              s2[t].add1(xa);
+              s2[t].add1(xb);
+            }
+          }
+        }
+      }
+    } else {
+      const float vv[4] = {__uint_as_float(r.v[u][0].x), __uint_as_float(r.v[u][0].y),
+                           __uint_as_float(r.v[u][0].z), __uint_as_float(r.v[u][0].w)};
+#pragma unroll
+      for (int t = 0; t < RT; t++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(r.xw[u][t][e]), vv[e],
+                                                        acc[t], 0, 0, 0);
+      }
+      if (sums) {
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+#pragma unroll
+          for (int s = 0; s < 4; s++) {
+            const float x = __uint_as_float(r.xw[u][t][s]);
+            if (WEIGHTED) {
+              s1[t] = fmaf(fabsf(x), r.uc[u][s], s1[t]);
+              s2[t].add(x, r.wc[u][s]);
+            } else {
+              s1[t] += fabsf(x);
+              s2[t].add1(x);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
 // XT = DT_BF16: K-step of 32 columns; lane group g = lane / 16 owns columns c + 8g .. c + 8g + 7.
 // XT = DT_F32: K-step of 16 columns; lane group g owns columns c + 4g .. c + 4g + 3.
+// A wave owns 16·RT rows; a tile is (job, 16·RT-row block, column chunk, challenge group).
 template <uint32_t XT, bool WEIGHTED, bool SQ64>
 __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
                                                 uint64_t n_tiles,
@@ -88,7 +241,11 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
                                                 uint32_t k) {
   constexpr uint32_t KSTEP = XT == DT_BF16 ? 32 : 16;
   constexpr uint32_t PER = XT == DT_BF16 ? 8 : 4;  // columns per lane per step
-  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // The wave index is uniform; readfirstlane lets the compiler keep everything derived from
+  // it (the tile, its job, its column range) in scalar registers, so the loop has no
+  // divergent branches and its waits cover only the loads they need.
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63;
   const uint64_t tile = (uint64_t)blockIdx.x * 4 + wave;
   if (tile >= n_tiles) return;
   uint32_t lo = blk_job[blockIdx.x], hi = blk_job[blockIdx.x + 1];
@@ -103,143 +260,58 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
   local /= J.n_chunks;
   const uint32_t jg = (uint32_t)(local % J.n_jg);
   const uint32_t rt = (uint32_t)(local / J.n_jg);
-  const uint32_t r0 = rt * 64;
+  const uint32_t r0 = rt * 16 * RT;
   const uint32_t c0 = chunk * J.chunk_cols;
   const uint32_t c1 = min(c0 + J.chunk_cols, J.cols);
   const uint32_t g = lane >> 4, i = lane & 15;
   const uint32_t j = jg * 16 + i;  // this lane's challenge column in the V operand
   const bool jv = j < k;
+  // Lanes past the last challenge column read column k - 1; their outputs are never written.
+  const uint32_t jl = jv ? j : k - 1;
   const bool sums = jg == 0;  // the two sums are taken once, by the first column group
 
   const char* xbase = reinterpret_cast<const char*>(J.x);
-  const uint32_t esz = XT == DT_BF16 ? 2 : 4;
-  bool rv[4];
-  const char* xrow[4];
+  constexpr uint32_t esz = XT == DT_BF16 ? 2 : 4;
+  bool rv[RT];
+  const char* xrow[RT];
 #pragma unroll
-  for (int t = 0; t < 4; t++) {
+  for (int t = 0; t < RT; t++) {
     const uint32_t row = r0 + 16 * t + i;
     rv[t] = row < J.rows;
-    xrow[t] = xbase + (uint64_t)(rv[t] ? row : 0) * J.ld * esz;
+    xrow[t] = xbase + (uint64_t)(rv[t] ? row : J.rows - 1) * J.ld * esz;
   }
-  v4f32 acc[4];
-  float s1[4];
-  SqAcc<SQ64> s2[4];
+  v4f32 acc[RT];
+  float s1[RT];
+  SqAcc<SQ64> s2[RT];
 #pragma unroll
-  for (int t = 0; t < 4; t++) {
+  for (int t = 0; t < RT; t++) {
     acc[t] = v4f32{0.f, 0.f, 0.f, 0.f};
     s1[t] = 0.f;
   }
-  const float* uw = reinterpret_cast<const float*>(J.u);
-  const float* ww = reinterpret_cast<const float*>(J.w);
 
-  for (uint32_t c = c0; c < c1; c += KSTEP) {
-    const uint32_t cl = c + PER * g;  // this lane's first column of the step
-    const bool full = J.aligned && c + KSTEP <= c1;
-    // X: PER consecutive elements of each of the 4 rows.
-    uint32_t xw[4][4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-      if (full) {
-        const uint4 q = rv[t] ? *reinterpret_cast<const uint4*>(xrow[t] + (uint64_t)cl * esz)
-                              : make_uint4(0, 0, 0, 0);
-        xw[t][0] = q.x; xw[t][1] = q.y; xw[t][2] = q.z; xw[t][3] = q.w;
-      } else {
-        if (XT == DT_BF16) {
-          const uint16_t* p = reinterpret_cast<const uint16_t*>(xrow[t]);
-          uint16_t e[8];
-#pragma unroll
-          for (int s = 0; s < 8; s++) e[s] = (rv[t] && cl + s < c1) ? p[cl + s] : (uint16_t)0;
-#pragma unroll
-          for (int s = 0; s < 4; s++) xw[t][s] = e[2 * s] | (uint32_t)e[2 * s + 1] << 16;
-        } else {
-          const uint32_t* p = reinterpret_cast<const uint32_t*>(xrow[t]);
-#pragma unroll
-          for (int s = 0; s < 4; s++) xw[t][s] = (rv[t] && cl + s < c1) ? p[cl + s] : 0u;
-        }
-      }
+  // Full stages (KU K-steps each) of an aligned job run as a software pipeline: the loads of
+  // stage s + 1 are issued before the matrix-core and VALU work of stage s, so every wave
+  // keeps a stage of loads in flight. The remaining steps and unaligned jobs take the guarded
+  // path.
+  constexpr uint32_t SSTEP = KSTEP * KU;
+  const uint32_t nfull = J.aligned ? (c1 - c0) / SSTEP : 0;
+  if (nfull > 0) {
+    StepRegs<XT> cur, nxt;
+    load_stage<XT, WEIGHTED>(cur, xrow, rv, c0 + PER * g, c1, true, J, k, jl, true, sums);
+    for (uint32_t s = 1; s < nfull; s++) {
+      load_stage<XT, WEIGHTED>(nxt, xrow, rv, c0 + s * SSTEP + PER * g, c1, true, J, k, jl, true,
+                               sums);
+      compute_stage<XT, WEIGHTED, SQ64>(cur, acc, s1, s2, sums);
+      cur = nxt;
     }
-    // Weights of this lane's columns.
-    float uc[PER], wc[PER];
-    if (WEIGHTED && sums) {
-#pragma unroll
-      for (uint32_t s = 0; s < PER; s++) {
-        const bool ok = cl + s < c1;
-        uc[s] = ok ? uw[cl + s] : 0.f;
-        wc[s] = ok ? ww[cl + s] : 0.f;
-      }
-    }
-    if (XT == DT_BF16) {
-      // V: 3 planes x 8 bf16 of column j for this lane's 8 rows of V.
-      const uint16_t* vb = reinterpret_cast<const uint16_t*>(J.v);
-      uint4 vp[3] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-      if (jv && cl < c1) {  // a lane past the last column loads nothing
-        const uint4* src = reinterpret_cast<const uint4*>(vb + ((uint64_t)(cl / 8) * k + j) * 24);
-        vp[0] = src[0];
-        vp[1] = src[1];
-        vp[2] = src[2];
-      }
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const v4i16 a = __builtin_bit_cast(v4i16, v2u32{xw[t][2 * h], xw[t][2 * h + 1]});
-#pragma unroll
-          for (int p = 0; p < 3; p++) {
-            const v2u32 bw = h == 0 ? v2u32{vp[p].x, vp[p].y} : v2u32{vp[p].z, vp[p].w};
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(v4i16, bw),
-                                                               acc[t], 0, 0, 0);
-          }
-        }
-      }
-      if (sums) {
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-#pragma unroll
-          for (int s = 0; s < 4; s++) {
-            const float xa = bf_lo(xw[t][s]), xb = bf_hi(xw[t][s]);
-            if (WEIGHTED) {
-              s1[t] = fmaf(fabsf(xa), uc[2 * s], s1[t]);
-              s1[t] = fmaf(fabsf(xb), uc[2 * s + 1], s1[t]);
-              s2[t].add(xa, wc[2 * s]);
-              s2[t].add(xb, wc[2 * s + 1]);
-            } else {
-              s1[t] += fabsf(xa);
-              s1[t] += fabsf(xb);
-              s2[t].add1(xa);
-              s2[t].add1(xb);
-            }
-          }
-        }
-      }
-    } else {
-      const float* vf = reinterpret_cast<const float*>(J.v);
-      float4 vq = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (jv && cl < c1) vq = *reinterpret_cast<const float4*>(vf + ((uint64_t)(cl / 4) * k + j) * 4);
-      const float vv[4] = {vq.x, vq.y, vq.z, vq.w};
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(xw[t][e]), vv[e], acc[t],
-                                                        0, 0, 0);
-      }
-      if (sums) {
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-#pragma unroll
-          for (int s = 0; s < 4; s++) {
-            const float x = __uint_as_float(xw[t][s]);
-            if (WEIGHTED) {
-              s1[t] = fmaf(fabsf(x), uc[s], s1[t]);
-              s2[t].add(x, wc[s]);
-            } else {
-              s1[t] += fabsf(x);
-              s2[t].add1(x);
-            }
-          }
-        }
-      }
-    }
+    compute_stage<XT, WEIGHTED, SQ64>(cur, acc, s1, s2, sums);
+  }
+  for (uint32_t c = c0 + nfull * SSTEP; c < c1; c += SSTEP) {
+    const uint32_t cl = c + PER * g;
+    const int nsteps = (int)min<uint32_t>(KU, (c1 - c + KSTEP - 1) / KSTEP);
+    StepRegs<XT> r;
+    load_stage<XT, WEIGHTED>(r, xrow, rv, cl, c1, false, J, k, jl, jv, sums, nsteps);
+    compute_stage<XT, WEIGHTED, SQ64>(r, acc, s1, s2, sums);
   }
 
   // X·V: lane (g, i) holds rows 4g + e of each tile, challenge column j.
@@ -247,11 +319,11 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
   const uint64_t cbase = (uint64_t)chunk * J.rows_pad;
   if (jv) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
+    for (int t = 0; t < RT; t++) {
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const uint32_t row = r0 + 16 * t + 4 * g + e;
-        if (row < J.rows) pdot[(cbase + row) * k + j] = acc[t][e];
+        if (row < J.rows) gstore<float>(pdot + (cbase + row) * k + j, acc[t][e]);
       }
     }
   }
@@ -259,7 +331,7 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
     float* pabs = reinterpret_cast<float*>(J.pabs);
     double* psq = reinterpret_cast<double*>(J.psq);
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
+    for (int t = 0; t < RT; t++) {
       float a = s1[t];
       double q = s2[t].get();
       if (!SQ64) {  // combine in the accumulation precision
@@ -275,8 +347,8 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
       a += __shfl_xor(a, 32);
       const uint32_t row = r0 + 16 * t + i;
       if (g == 0 && row < J.rows) {
-        pabs[cbase + row] = a;
-        psq[cbase + row] = q;
+        gstore<float>(pabs + cbase + row, a);
+        gstore<double>(psq + cbase + row, q);
       }
     }
   }
@@ -315,25 +387,28 @@ __global__ __launch_bounds__(256) void reduce_b(const RedJob* __restrict__ jobs,
     double s = 0.0;
     if (row < J.rows)
       for (uint32_t c = 0; c < J.n_chunks; c++)
-        s += (double)pdot[((uint64_t)c * J.rows_pad + row) * k + j];
+        s += (double)gload<float>(pdot + ((uint64_t)c * J.rows_pad + row) * k + j);
     v[e] = (float)s;
   }
   if (J.a_dt == DT_BF16) {
     uint16_t pl[3][8];
 #pragma unroll
     for (int e = 0; e < 8; e++) split_bf16x3(v[e], pl[0][e], pl[1][e], pl[2][e]);
-    uint4* dst = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(J.vout) +
+    u32x4* dst = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(J.vout) +
                                           ((uint64_t)grp * k + j) * 24);
 #pragma unroll
     for (int p = 0; p < 3; p++)
-      dst[p] = make_uint4(pl[p][0] | (uint32_t)pl[p][1] << 16, pl[p][2] | (uint32_t)pl[p][3] << 16,
-                          pl[p][4] | (uint32_t)pl[p][5] << 16, pl[p][6] | (uint32_t)pl[p][7] << 16);
+      gstore<u32x4>(dst + p, u32x4{pl[p][0] | (uint32_t)pl[p][1] << 16,
+                                   pl[p][2] | (uint32_t)pl[p][3] << 16,
+                                   pl[p][4] | (uint32_t)pl[p][5] << 16,
+                                   pl[p][6] | (uint32_t)pl[p][7] << 16});
   } else {
     float* base = reinterpret_cast<float*>(J.vout);
 #pragma unroll
     for (int h = 0; h < 2; h++)
-      *reinterpret_cast<float4*>(base + ((uint64_t)(2 * grp + h) * k + j) * 4) =
-          make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]);
+      gstore<u32x4>(base + ((uint64_t)(2 * grp + h) * k + j) * 4,
+                    u32x4{__float_as_uint(v[4 * h]), __float_as_uint(v[4 * h + 1]),
+                          __float_as_uint(v[4 * h + 2]), __float_as_uint(v[4 * h + 3])});
   }
   if (j == 0) {
     const float* pabs = reinterpret_cast<const float*>(J.pabs);
@@ -346,11 +421,11 @@ __global__ __launch_bounds__(256) void reduce_b(const RedJob* __restrict__ jobs,
       if (row >= J.rows) continue;
       double a = 0.0, q = 0.0;
       for (uint32_t c = 0; c < J.n_chunks; c++) {
-        a += (double)pabs[(uint64_t)c * J.rows_pad + row];
-        q += psq[(uint64_t)c * J.rows_pad + row];
+        a += (double)gload<float>(pabs + (uint64_t)c * J.rows_pad + row);
+        q += gload<double>(psq + (uint64_t)c * J.rows_pad + row);
       }
-      u[row] = (float)a;
-      w[row] = (float)q;
+      gstore<float>(u + row, (float)a);
+      gstore<float>(w + row, (float)q);
     }
   }
 }
@@ -393,7 +468,7 @@ __global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jo
   if (bias) {
     double a = 0.0, q = 0.0;
     for (uint32_t c = tid; c < J.w; c += blockDim.x) {
-      const double b = bias[c];
+      const double b = gload<float>(bias + c);
       a += fabs(b);
       q += b * b;
     }
@@ -408,19 +483,21 @@ __global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jo
   const float* pabs = reinterpret_cast<const float*>(J.p_abs);
   const double* psq = reinterpret_cast<const double*>(J.p_sq);
 
-  // Row sums (ν, ‖|P|1‖, ‖P‖_F, U²) once, then the residuals 16 columns at a time.
+  // Row sums (ν, ‖|P|1‖, ‖P‖_F, U²) once, then the residuals 16 columns at a time. A row's
+  // chunk partials are summed in fp64 in chunk order, then rounded to fp32 where the
+  // reference's matmul output is fp32.
   double s_nu = 0.0, s_p1 = 0.0, s_psq = 0.0, s_t2 = 0.0;
   __syncthreads();
   const float babs = bias_abs;
   for (uint32_t r = tid; r < J.n; r += blockDim.x) {
     double nu = 0.0, t2 = 0.0, p1 = 0.0, pq = 0.0;
     for (uint32_t c = 0; c < J.a_chunks; c++) {
-      nu += (double)aabs[(uint64_t)c * J.a_rows_pad + r];
-      t2 += asq[(uint64_t)c * J.a_rows_pad + r];
+      nu += (double)gload<float>(aabs + (uint64_t)c * J.a_rows_pad + r);
+      t2 += gload<double>(asq + (uint64_t)c * J.a_rows_pad + r);
     }
     for (uint32_t c = 0; c < J.p_chunks; c++) {
-      p1 += (double)pabs[(uint64_t)c * J.p_rows_pad + r];
-      pq += psq[(uint64_t)c * J.p_rows_pad + r];
+      p1 += (double)gload<float>(pabs + (uint64_t)c * J.p_rows_pad + r);
+      pq += gload<double>(psq + (uint64_t)c * J.p_rows_pad + r);
     }
     float nuf = (float)nu;
     if (bias) nuf = nuf + babs;
@@ -448,7 +525,7 @@ __global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jo
       for (uint32_t jj = 0; jj < nj; jj++) {
         double a = 0.0;
         for (uint32_t c = tid; c < J.w; c += blockDim.x)
-          a += (double)bias[c] * (double)R[(uint64_t)c * k + j0 + jj];
+          a += (double)gload<float>(bias + c) * (double)gload<float>(R + (uint64_t)c * k + j0 + jj);
         a = block_sum(a, sh);
         if (tid == 0) bias_r[jj] = (float)a;
       }
@@ -458,19 +535,29 @@ __global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jo
 #pragma unroll
     for (int jj = 0; jj < 16; jj++) sd[jj] = 0.0;
     for (uint32_t r = tid; r < J.n; r += blockDim.x) {
+      double ab[16], pr[16];
+#pragma unroll
+      for (int jj = 0; jj < 16; jj++) ab[jj] = pr[jj] = 0.0;
+      for (uint32_t c = 0; c < J.a_chunks; c++) {
+        const float* src = adot + ((uint64_t)c * J.a_rows_pad + r) * k + j0;
+#pragma unroll
+        for (int jj = 0; jj < 16; jj++)
+          if ((uint32_t)jj < nj) ab[jj] += (double)gload<float>(src + jj);
+      }
+      for (uint32_t c = 0; c < J.p_chunks; c++) {
+        const float* src = pdot + ((uint64_t)c * J.p_rows_pad + r) * k + j0;
+#pragma unroll
+        for (int jj = 0; jj < 16; jj++)
+          if ((uint32_t)jj < nj) pr[jj] += (double)gload<float>(src + jj);
+      }
 #pragma unroll
       for (int jj = 0; jj < 16; jj++) {
-        if ((uint32_t)jj >= nj) break;
-        const uint32_t jc = j0 + jj;
-        double ab = 0.0, pr = 0.0;
-        for (uint32_t c = 0; c < J.a_chunks; c++)
-          ab += (double)adot[((uint64_t)c * J.a_rows_pad + r) * k + jc];
-        for (uint32_t c = 0; c < J.p_chunks; c++)
-          pr += (double)pdot[((uint64_t)c * J.p_rows_pad + r) * k + jc];
-        float abf = (float)ab;
-        if (bias) abf = abf + bias_r[jj];
-        const float d = abf - (float)pr;
-        sd[jj] += (double)d * (double)d;
+        if ((uint32_t)jj < nj) {
+          float abf = (float)ab[jj];
+          if (bias) abf = abf + bias_r[jj];
+          const float d = abf - (float)pr[jj];
+          sd[jj] += (double)d * (double)d;
+        }
       }
     }
     for (uint32_t jj = 0; jj < nj; jj++) {
@@ -612,8 +699,8 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     J.ld = s.ld;
     J.rows = s.rows;
     J.cols = s.cols;
-    J.rows_pad = (s.rows + 63) / 64 * 64;
-    J.chunk_cols = chunk_cols_for(s.cols, kstep);
+    J.rows_pad = (s.rows + 16 * RT - 1) / (16 * RT) * (16 * RT);
+    J.chunk_cols = chunk_cols_for(s.cols, kstep * KU);
     J.n_chunks = (s.cols + J.chunk_cols - 1) / J.chunk_cols;
     J.n_jg = n_jg;
     const uint32_t esz = s.dt == DT_BF16 ? 2 : 4;
@@ -714,7 +801,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
         PassJob J = jobs[src];
         J.tile_first = tiles;
         first.push_back(tiles);
-        tiles += (uint64_t)(J.rows_pad / 64) * J.n_chunks * J.n_jg;
+        tiles += (uint64_t)(J.rows_pad / (16 * RT)) * J.n_chunks * J.n_jg;
         ordered.push_back(J);
         ordered_src.push_back(src);
       }
@@ -865,34 +952,68 @@ static int run_pass(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
   return POTS_E_OK;
 }
 
+// One stage of a plan's run: 0 challenges, 1 B pass, 2 reduce of B's vectors, 3 A pass,
+// 4 P pass, 5 rows. The stages run in this order on one stream; each reads what the earlier
+// ones wrote.
+static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
+                     hipStream_t s) {
+  int rc;
+  switch (stage) {
+    case 0:
+      POTS_HIP(hipMemcpyAsync(P->d_key, d_key, 32, hipMemcpyDeviceToDevice, s));
+      // R in row-major form (for the bias term and the API) and in the packed layouts.
+      if ((rc = challenges_enqueue(P->d_key, P->d_items_b3, P->n_items, P->n_units, P->k,
+                                   P->d_r, P->need_b3 ? P->d_r_b3 : nullptr, nullptr, s)) !=
+          POTS_E_OK)
+        return rc;
+      if (P->need_f4 &&
+          (rc = challenges_enqueue(P->d_key, P->d_items_f4, P->n_items, P->n_units, P->k,
+                                   nullptr, nullptr, P->d_r_f4, s)) != POTS_E_OK)
+        return rc;
+      return POTS_E_OK;
+    case 1:
+      for (const PassLaunch& L : P->pass_b)
+        if ((rc = run_pass(P, L, s)) != POTS_E_OK) return rc;
+      return POTS_E_OK;
+    case 2: {
+      const uint64_t blocks = (P->n_red_threads + 255) / 256;
+      if (blocks == 0) return POTS_E_OK;
+      hipLaunchKernelGGL(reduce_b, dim3((uint32_t)blocks), dim3(256), 0, s, P->d_red, P->n_red,
+                         P->n_red_threads, P->k);
+      POTS_HIP(hipGetLastError());
+      return POTS_E_OK;
+    }
+    case 3:
+    case 4:
+      for (const PassLaunch& L : P->pass_ap)
+        if ((L.weighted != 0) == (stage == 3) && (rc = run_pass(P, L, s)) != POTS_E_OK)
+          return rc;
+      return POTS_E_OK;
+    case 5:
+      hipLaunchKernelGGL(finish_rows, dim3((uint32_t)P->n), dim3(256), 0, s, P->d_fin, P->k,
+                         P->guard, d_rows);
+      POTS_HIP(hipGetLastError());
+      return POTS_E_OK;
+    default:
+      return POTS_E_ARG;
+  }
+}
+
 extern "C" int pots_fv_plan_run(void* plan, const uint8_t* d_key, double* d_rows, void* stream) {
   if (!plan || !d_key || !d_rows) return POTS_E_ARG;
   FvPlan* P = static_cast<FvPlan*>(plan);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc;
-  POTS_HIP(hipMemcpyAsync(P->d_key, d_key, 32, hipMemcpyDeviceToDevice, s));
-  // R in row-major form (for the bias term and the API) and in the packed layouts.
-  if ((rc = challenges_enqueue(P->d_key, P->d_items_b3, P->n_items, P->n_units, P->k, P->d_r,
-                               P->need_b3 ? P->d_r_b3 : nullptr, nullptr, s)) != POTS_E_OK)
-    return rc;
-  if (P->need_f4 &&
-      (rc = challenges_enqueue(P->d_key, P->d_items_f4, P->n_items, P->n_units, P->k, nullptr,
-                               nullptr, P->d_r_f4, s)) != POTS_E_OK)
-    return rc;
-  for (const PassLaunch& L : P->pass_b)
-    if ((rc = run_pass(P, L, s)) != POTS_E_OK) return rc;
-  {
-    const uint64_t blocks = (P->n_red_threads + 255) / 256;
-    hipLaunchKernelGGL(reduce_b, dim3((uint32_t)blocks), dim3(256), 0, s, P->d_red, P->n_red,
-                       P->n_red_threads, P->k);
-    POTS_HIP(hipGetLastError());
+  for (int stage = 0; stage < POTS_FV_STAGES; stage++) {
+    const int rc = run_stage(P, stage, d_key, d_rows, static_cast<hipStream_t>(stream));
+    if (rc != POTS_E_OK) return rc;
   }
-  for (const PassLaunch& L : P->pass_ap)
-    if ((rc = run_pass(P, L, s)) != POTS_E_OK) return rc;
-  hipLaunchKernelGGL(finish_rows, dim3((uint32_t)P->n), dim3(256), 0, s, P->d_fin, P->k,
-                     P->guard, d_rows);
-  POTS_HIP(hipGetLastError());
   return POTS_E_OK;
+}
+
+extern "C" int pots_fv_plan_run_stage(void* plan, int stage, const uint8_t* d_key,
+                                      double* d_rows, void* stream) {
+  if (!plan || !d_key || !d_rows || stage < 0 || stage >= POTS_FV_STAGES) return POTS_E_ARG;
+  return run_stage(static_cast<FvPlan*>(plan), stage, d_key, d_rows,
+                   static_cast<hipStream_t>(stream));
 }
 
 extern "C" int pots_fv_plan_copy_challenges(const void* plan, float* d_out, void* stream) {

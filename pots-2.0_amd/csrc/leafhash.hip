@@ -34,6 +34,7 @@
 
 #include "blake3_device.h"
 #include "common.h"
+#include "gmem.h"
 
 namespace pots {
 
@@ -60,11 +61,7 @@ constexpr int kThreads = 256;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-#ifdef POTS_NT_LOADS
-#define POTS_LOAD(p) __builtin_nontemporal_load(p)
-#else
-#define POTS_LOAD(p) (*(p))
-#endif
+
 
 __device__ __forceinline__ void finite_acc(uint32_t& acc, uint32_t w, bool halves) {
   uint32_t hi = w << 1;
@@ -89,15 +86,15 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
   for (uint32_t b = 0; b < nb; b++) {
     const uint64_t o = cstart + 64u * b;
     const uint64_t A = d.payload + o - H;  // address of message byte o, in payload terms
-    const uint4* A16 = reinterpret_cast<const uint4*>(A & ~uint64_t(15));
+    const u32x4* A16 = reinterpret_cast<const u32x4*>(A & ~uint64_t(15));
     uint32_t m[16];
     if (o >= H && o + 64 <= L) {
       // Interior block: 16 payload words, the aligned window is in bounds (see header).
-      const u32x4* V16 = reinterpret_cast<const u32x4*>(A16);
+      const u32x4* V16 = A16;
       u32x4 q[5];
 #pragma unroll
-      for (int u = 0; u < 4; u++) q[u] = POTS_LOAD(V16 + u);
-      q[4] = SH ? POTS_LOAD(V16 + 4) : u32x4{0, 0, 0, 0};
+      for (int u = 0; u < 4; u++) q[u] = gload<u32x4>(V16 + u);
+      q[4] = SH ? gload<u32x4>(V16 + 4) : u32x4{0, 0, 0, 0};
       uint32_t w[20];
 #pragma unroll
       for (int u = 0; u < 5; u++) {
@@ -117,8 +114,8 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
 #pragma unroll
       for (int u = 0; u < 5; u++) {
         const uint64_t X = reinterpret_cast<uint64_t>(A16 + u);
-        uint4 q = make_uint4(0, 0, 0, 0);
-        if ((u < 4 || SH) && X + 16 > pbeg && X < pend) q = A16[u];
+        u32x4 q = u32x4{0, 0, 0, 0};
+        if ((u < 4 || SH) && X + 16 > pbeg && X < pend) q = gload<u32x4>(A16 + u);
         w[4 * u] = q.x;
         w[4 * u + 1] = q.y;
         w[4 * u + 2] = q.z;
@@ -129,7 +126,7 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
         const uint64_t at = o + 4u * j;  // message byte offset of this word
         uint32_t mw = w[j + SH];
         if (at < H) {
-          mw = head[d.head_word + (uint32_t)(at >> 2)];
+          mw = gload<uint32_t>(head + d.head_word + (uint32_t)(at >> 2));
         } else if (at >= L) {
           mw = 0;
         } else {
@@ -147,14 +144,14 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
   }
 }
 
-__global__ __launch_bounds__(kThreads) void chunk_kernel(
-    const LeafDesc* __restrict__ leaves, const uint64_t* __restrict__ chunk_first,
-    const uint32_t* __restrict__ blk_leaf, uint64_t n_chunks, const uint32_t* __restrict__ head,
-    uint32_t* __restrict__ cv_out, uint32_t* __restrict__ digests,
-    uint32_t* __restrict__ first_bad) {
-  const uint64_t g = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (g >= n_chunks) return;
-  uint32_t lo = blk_leaf[blockIdx.x], hi = blk_leaf[blockIdx.x + 1];
+// One lane's chunk: global chunk index g, in block-table slot `blk` (every chunk of that slot
+// belongs to a leaf in blk_leaf[blk] .. blk_leaf[blk + 1]).
+__device__ __forceinline__ void chunk_one(
+    uint64_t g, uint32_t blk, const LeafDesc* __restrict__ leaves,
+    const uint64_t* __restrict__ chunk_first, const uint32_t* __restrict__ blk_leaf,
+    const uint32_t* __restrict__ head, uint32_t* __restrict__ cv_out,
+    uint32_t* __restrict__ digests, uint32_t* __restrict__ first_bad) {
+  uint32_t lo = blk_leaf[blk], hi = blk_leaf[blk + 1];
   while (lo < hi) {  // the last leaf whose first chunk is <= g
     const uint32_t mid = (lo + hi + 1) >> 1;
     if (chunk_first[mid] <= g) lo = mid;
@@ -177,9 +174,25 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel(
     const uint32_t thr = d.kind == POTS_KIND_F16 ? 0xF8000000u : 0xFF000000u;
     if (acc >= thr) atomicMin(first_bad, i);
   }
-  uint4* dst = reinterpret_cast<uint4*>(root ? digests + 8ull * i : cv_out + 8ull * g);
-  dst[0] = make_uint4(cv[0], cv[1], cv[2], cv[3]);
-  dst[1] = make_uint4(cv[4], cv[5], cv[6], cv[7]);
+  u32x4* dst = reinterpret_cast<u32x4*>(root ? digests + 8ull * i : cv_out + 8ull * g);
+  gstore<u32x4>(dst, u32x4{cv[0], cv[1], cv[2], cv[3]});
+  gstore<u32x4>(dst + 1, u32x4{cv[4], cv[5], cv[6], cv[7]});
+}
+
+// Every chunk's chaining value (or, for a one-chunk leaf, its digest). The chunks are cut
+// into n_slots slots of kThreads consecutive chunks; block b hashes slots b, b + gridDim.x,
+// ... so a grid smaller than n_slots holds a bounded share of the GPU and leaves the rest to
+// kernels on other streams.
+__global__ __launch_bounds__(kThreads) void chunk_kernel(
+    const LeafDesc* __restrict__ leaves, const uint64_t* __restrict__ chunk_first,
+    const uint32_t* __restrict__ blk_leaf, uint64_t n_chunks, uint32_t n_slots,
+    const uint32_t* __restrict__ head, uint32_t* __restrict__ cv_out,
+    uint32_t* __restrict__ digests, uint32_t* __restrict__ first_bad) {
+  for (uint32_t blk = blockIdx.x; blk < n_slots; blk += gridDim.x) {
+    const uint64_t g = (uint64_t)blk * kThreads + threadIdx.x;
+    if (g < n_chunks)
+      chunk_one(g, blk, leaves, chunk_first, blk_leaf, head, cv_out, digests, first_bad);
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void level_kernel(
@@ -248,7 +261,8 @@ struct LeafPlan {
   uint32_t* d_head = nullptr;
   LevelEntry* d_levels = nullptr;
   uint32_t* d_cv[2] = {nullptr, nullptr};
-  uint32_t n_blocks = 0;
+  uint32_t n_blocks = 0;  // chunk slots of kThreads chunks
+  uint32_t max_grid = 0;  // chunk kernel's grid limit; 0 = one block per slot
   std::vector<LevelInfo> levels;
   std::vector<StageCopy> stages;
 };
@@ -441,30 +455,52 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
   return POTS_E_OK;
 }
 
+// One stage of a plan's run: 0 staging copies and the first-bad reset, 1 the chunk kernel,
+// 2 the per-leaf tree levels.
+static int plan_stage(LeafPlan* P, int stage, uint32_t* d_digests, uint32_t* d_first_bad,
+                      hipStream_t stream) {
+  switch (stage) {
+    case 0:
+      for (const StageCopy& s : P->stages) {
+        POTS_HIP(hipMemcpyAsync(reinterpret_cast<void*>(s.dst),
+                                reinterpret_cast<const void*>(s.head_src), s.head_bytes,
+                                hipMemcpyDeviceToDevice, stream));
+        if (s.payload_bytes)
+          POTS_HIP(hipMemcpyAsync(reinterpret_cast<void*>(s.dst + s.head_bytes),
+                                  reinterpret_cast<const void*>(s.payload_src), s.payload_bytes,
+                                  s.host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice,
+                                  stream));
+      }
+      hipLaunchKernelGGL(fill_u32, dim3(1), dim3(1), 0, stream, d_first_bad, (uint32_t)P->n);
+      POTS_HIP(hipGetLastError());
+      return POTS_E_OK;
+    case 1:
+      hipLaunchKernelGGL(chunk_kernel,
+                         dim3(P->max_grid ? std::min(P->max_grid, P->n_blocks) : P->n_blocks),
+                         dim3(kThreads), 0, stream, P->d_leaves, P->d_chunk_first,
+                         P->d_blk_leaf, P->n_chunks, P->n_blocks, P->d_head, P->d_cv[0],
+                         d_digests, d_first_bad);
+      POTS_HIP(hipGetLastError());
+      return POTS_E_OK;
+    case 2:
+      for (const LevelInfo& li : P->levels) {
+        const uint64_t blocks = (li.n_out + kThreads - 1) / kThreads;
+        hipLaunchKernelGGL(level_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream,
+                           P->d_levels + li.ent_first, li.n_ents, li.n_out, P->d_cv[li.in_buf],
+                           P->d_cv[li.out_buf], d_digests);
+        POTS_HIP(hipGetLastError());
+      }
+      return POTS_E_OK;
+    default:
+      return POTS_E_ARG;
+  }
+}
+
 static int plan_run(LeafPlan* P, uint32_t* d_digests, uint32_t* d_first_bad,
                     hipStream_t stream) {
-  for (const StageCopy& s : P->stages) {
-    POTS_HIP(hipMemcpyAsync(reinterpret_cast<void*>(s.dst),
-                            reinterpret_cast<const void*>(s.head_src), s.head_bytes,
-                            hipMemcpyDeviceToDevice, stream));
-    if (s.payload_bytes)
-      POTS_HIP(hipMemcpyAsync(reinterpret_cast<void*>(s.dst + s.head_bytes),
-                              reinterpret_cast<const void*>(s.payload_src), s.payload_bytes,
-                              s.host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice,
-                              stream));
-  }
-  hipLaunchKernelGGL(fill_u32, dim3(1), dim3(1), 0, stream, d_first_bad, (uint32_t)P->n);
-  POTS_HIP(hipGetLastError());
-  hipLaunchKernelGGL(chunk_kernel, dim3(P->n_blocks), dim3(kThreads), 0, stream, P->d_leaves,
-                     P->d_chunk_first, P->d_blk_leaf, P->n_chunks, P->d_head, P->d_cv[0],
-                     d_digests, d_first_bad);
-  POTS_HIP(hipGetLastError());
-  for (const LevelInfo& li : P->levels) {
-    const uint64_t blocks = (li.n_out + kThreads - 1) / kThreads;
-    hipLaunchKernelGGL(level_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream,
-                       P->d_levels + li.ent_first, li.n_ents, li.n_out, P->d_cv[li.in_buf],
-                       P->d_cv[li.out_buf], d_digests);
-    POTS_HIP(hipGetLastError());
+  for (int stage = 0; stage < POTS_LEAF_STAGES; stage++) {
+    const int rc = plan_stage(P, stage, d_digests, d_first_bad, stream);
+    if (rc != POTS_E_OK) return rc;
   }
   return POTS_E_OK;
 }
@@ -523,6 +559,20 @@ extern "C" int pots_leaf_plan_run(void* plan, uint8_t* d_out, uint32_t* d_first_
   if (!plan || !d_out || !d_first_bad) return POTS_E_ARG;
   return plan_run(static_cast<LeafPlan*>(plan), reinterpret_cast<uint32_t*>(d_out),
                   d_first_bad, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pots_leaf_plan_run_stage(void* plan, int stage, uint8_t* d_out,
+                                        uint32_t* d_first_bad, void* stream) {
+  if (!plan || !d_out || !d_first_bad || stage < 0 || stage >= POTS_LEAF_STAGES)
+    return POTS_E_ARG;
+  return plan_stage(static_cast<LeafPlan*>(plan), stage, reinterpret_cast<uint32_t*>(d_out),
+                    d_first_bad, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pots_leaf_plan_set_grid(void* plan, uint32_t max_blocks) {
+  if (!plan) return POTS_E_ARG;
+  static_cast<LeafPlan*>(plan)->max_grid = max_blocks;
+  return POTS_E_OK;
 }
 
 extern "C" uint64_t pots_leaf_plan_chunks(const void* plan) {

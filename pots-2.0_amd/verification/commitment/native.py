@@ -83,6 +83,8 @@ class Native:
             "pots_leaf_plan_create": ([_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                        ctypes.POINTER(_vp)], _int),
             "pots_leaf_plan_run": ([_vp, _vp, _vp, _vp], _int),
+            "pots_leaf_plan_run_stage": ([_vp, _int, _vp, _vp, _vp], _int),
+            "pots_leaf_plan_set_grid": ([_vp, _u32], _int),
             "pots_leaf_plan_chunks": ([_vp], _u64),
             "pots_leaf_plan_bytes": ([_vp], _u64),
             "pots_leaf_plan_destroy": ([_vp], None),
@@ -90,6 +92,7 @@ class Native:
             "pots_challenges": ([_vp, _u32, _sz, _vp, _vp, _vp, _vp, _u32], _int),
             "pots_fv_plan_create": ([_sz, _vp, _u32, _u32, ctypes.POINTER(_vp)], _int),
             "pots_fv_plan_run": ([_vp, _vp, _vp, _vp], _int),
+            "pots_fv_plan_run_stage": ([_vp, _int, _vp, _vp, _vp], _int),
             "pots_fv_plan_copy_challenges": ([_vp, _vp, _vp], _int),
             "pots_fv_plan_bytes": ([_vp], _u64),
             "pots_fv_plan_destroy": ([_vp], None),
@@ -297,6 +300,26 @@ class LeafPlan:
                          "pots_leaf_plan_run")
         return out, bad
 
+    STAGES = ("stage", "chunks", "levels")
+
+    def set_grid(self, max_blocks: int) -> None:
+        """Limit the chunk kernel to ``max_blocks`` blocks (0: no limit); results are the same,
+        the kernel just leaves the rest of the GPU to other streams."""
+        if not 0 <= max_blocks < 1 << 32:
+            raise ValueError(f"max_blocks must be in [0, 2^32), got {max_blocks}")
+        self._lib._check(self._lib._lib.pots_leaf_plan_set_grid(self._h, max_blocks),
+                         "pots_leaf_plan_set_grid")
+
+    def run_stage(self, stage: int, out: torch.Tensor, bad: torch.Tensor,
+                  stream: torch.cuda.Stream | None = None) -> None:
+        """Enqueue one stage of :meth:`run` (``STAGES``: staging copies, the chunk kernel,
+        the per-leaf tree levels); running all of them in order is :meth:`run`."""
+        if out.shape != (self.n, 32) or out.dtype != torch.uint8 or not out.is_contiguous():
+            raise ValueError("out must be contiguous uint8 [n, 32]")
+        self._lib._check(self._lib._lib.pots_leaf_plan_run_stage(
+            self._h, stage, out.data_ptr(), bad.data_ptr(), _stream(stream)),
+            "pots_leaf_plan_run_stage")
+
     def close(self) -> None:
         if getattr(self, "_h", None) is not None and self._h.value:
             self._lib._lib.pots_leaf_plan_destroy(self._h)
@@ -413,6 +436,18 @@ class FvPlan:
         self._lib._check(self._lib._lib.pots_fv_plan_run(self._h, key.data_ptr(), out.data_ptr(),
                                                          _stream(stream)), "pots_fv_plan_run")
         return out
+
+    STAGES = ("challenges", "b_pass", "reduce", "a_pass", "p_pass", "rows")
+
+    def run_stage(self, stage: int, key: torch.Tensor, out: torch.Tensor,
+                  stream: torch.cuda.Stream | None = None) -> None:
+        """Enqueue one stage of :meth:`rows` (``STAGES``) with the key already a GPU uint8
+        tensor; running all of them in order is :meth:`rows`."""
+        if out.shape != (self.n, 5 + self.k) or out.dtype != torch.float64:
+            raise ValueError("out must be fp64 [n, 5 + k]")
+        self._lib._check(self._lib._lib.pots_fv_plan_run_stage(
+            self._h, stage, key.data_ptr(), out.data_ptr(), _stream(stream)),
+            "pots_fv_plan_run_stage")
 
     def challenges(self) -> list[torch.Tensor]:
         """The last run's challenge matrices, fp32 ``[w_i, k]`` per product (GPU views)."""

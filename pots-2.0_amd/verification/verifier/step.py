@@ -1,0 +1,135 @@
+"""One step's check 2 and check 5 on a transcript resident in HBM, in one pass of the GPU.
+
+Reference: verification/verifier/checks.py:204-272 (check 2's read-hash-validate and its root
+comparison) and :576-956 (check 5: challenges keyed on the claimed root, Freivalds
+measurement of every product in canonical order, judging). The checks' order of effects is
+kept: a non-finite leaf is check 2's malformed rejection; otherwise the first product that
+fails its tests is check 5's rejection; otherwise a root that differs from the claim rejects
+as check 2 at the end (F15a: check 5 keys on the claimed root, so it need not wait for the
+recomputed one).
+
+What runs where. Check 2's hashing (leaf digests, then the Merkle tree) and check 5's
+measuring (challenges, the three Freivalds passes, rows) read disjoint work and both depend
+only on the leaves and the claimed root, so they run on two streams at once: hashing is
+integer-VALU bound and uses a fraction of HBM bandwidth, the Freivalds passes are memory bound
+and leave the VALUs mostly idle. The verdicts follow on the main stream. One host read at the
+end returns the root, the first non-finite leaf and the first rejected product.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from verification.commitment import native
+from verification.commitment.leaves import StepHasher
+from verification.computation.interface import DeclaredComputation
+from verification.parameters import UNIT_ROUNDOFF
+from verification.verifier.bands import Bands, product_class
+
+CODE_NAMES = {0: "accept", 1: "non-finite", 2: "cancellation", 3: "residual"}
+
+
+@dataclass
+class StepVerdict:
+    """The outcome of one step's checks 2 and 5."""
+
+    root: bytes                 # the recomputed Merkle root
+    first_bad: int              # first leaf holding NaN/Inf, or n_leaves
+    first_fail: int             # index (0-based, canonical order) of the first rejected product, or M
+    codes: torch.Tensor         # int32 [M, 2]: (code, failing challenge j) per product
+    rows: torch.Tensor          # fp64 [M, 5 + k] Freivalds rows (freivalds.ROW)
+    check: str | None           # "2", "5" or None (accept)
+    detail: str | None
+
+
+class DeviceStepVerifier:
+    """Plans for one step's transcript, built once: the leaf-hashing plan, the Freivalds plan
+    over every product (operands served by ``operands(spec)``), and the verdict table. Call
+    :meth:`run` with the claimed root."""
+
+    def __init__(self, c: DeclaredComputation, leaves: Sequence[Any], operands: Any, *, k: int,
+                 bands: Bands | None = None, guard: bool = True) -> None:
+        self.c, self.k, self.guard = c, k, guard
+        self.bands = bands or Bands.provisional()
+        lib = self.lib = native.get()
+        self.hasher = StepHasher(c, leaves)
+        prods = []
+        for spec in c.products:
+            a, b = operands(spec)
+            p = leaves[c.product_index(spec.m)]
+            bias = None
+            if spec.bias is not None:  # checks.py:439: the W_t leaf in the operand format
+                bias = leaves[c.w_t_index(spec.bias)].to(c.operand_dtype).to(torch.float32)
+            prods.append(native.FvProduct(a, b, p, spec.m, bias))
+        self.plan = lib.fv_plan(prods, k, guard)
+        self.specs = native.verdict_specs(
+            [s.q for s in c.products], [s.a_shape[0] for s in c.products],
+            [s.bias is not None for s in c.products],
+            [self.bands.kappa_for(product_class(c, s)) for s in c.products])
+        self.eps_in = UNIT_ROUNDOFF[c.product_dtype]
+        self.eps_acc = UNIT_ROUNDOFF[torch.float32]
+        dev = self.hasher.plan.device
+        self.digests = torch.empty(c.n_leaves, 32, dtype=torch.uint8, device=dev)
+        self.bad = torch.empty(1, dtype=torch.int32, device=dev)
+        self.rows = torch.empty(c.M, 5 + k, dtype=torch.float64, device=dev)
+        self.key = torch.empty(32, dtype=torch.uint8, device=dev)
+        self.side = torch.cuda.Stream(device=dev)
+        self.hash_bytes = self.hasher.bytes
+        self.freivalds_bytes = self.plan.bytes
+
+    def enqueue(self, claimed: bytes | torch.Tensor, events: list | None = None):
+        """Enqueue the whole step on the current stream (Freivalds, verdicts) and a side
+        stream (hashing, tree); returns GPU tensors ``(nodes, codes, first_fail)``.
+        ``events``, if given, receives (start, hashed, measured, judged) CUDA events."""
+        main = torch.cuda.current_stream()
+        if isinstance(claimed, torch.Tensor):
+            self.key.copy_(claimed)
+        else:
+            self.key.copy_(torch.frombuffer(bytearray(claimed), dtype=torch.uint8))
+        start = torch.cuda.Event(enable_timing=events is not None)
+        start.record(main)
+        self.side.wait_event(start)
+        with torch.cuda.stream(self.side):
+            self.hasher.digests(self.digests, self.bad, self.side)
+            nodes = self.lib.merkle_tree_device(self.digests, self.side)
+        hashed = torch.cuda.Event(enable_timing=events is not None)
+        hashed.record(self.side)
+        self.plan.rows(self.key, self.rows, main)
+        measured = torch.cuda.Event(enable_timing=events is not None)
+        measured.record(main)
+        main.wait_event(hashed)
+        codes, _, first = self.lib.verdicts(self.rows, self.specs, k=self.k, eps_in=self.eps_in,
+                                            eps_acc=self.eps_acc, tau=self.bands.tau,
+                                            guard=self.guard, stream=main)
+        judged = torch.cuda.Event(enable_timing=events is not None)
+        judged.record(main)
+        # keep the side stream's tensors alive for the main stream's consumers
+        nodes.record_stream(main)
+        if events is not None:
+            events.append((start, hashed, measured, judged))
+        return nodes, codes, first
+
+    def run(self, claimed: bytes) -> StepVerdict:
+        """The step's verdict, after one host read."""
+        nodes, codes, first = self.enqueue(claimed)
+        flags = torch.cat([nodes[0].view(torch.int32), self.bad, first]).cpu()
+        root = flags[:8].numpy().tobytes()
+        first_bad, first_fail = int(flags[8]), int(flags[9])
+        check = detail = None
+        c = self.c
+        if first_bad < c.n_leaves:
+            check, detail = "2", f"leaf {first_bad}: float tensor contains NaN or Inf"
+        elif first_fail < c.M:
+            code, j = codes[first_fail].tolist()
+            spec = c.products[first_fail]
+            detail = f"P_{spec.m} ({spec.name}): {CODE_NAMES[code]}" + (
+                f", challenge j={j}" if code == 3 else "")
+            check = "5"
+        elif root != bytes(claimed):
+            check, detail = "2", (f"recomputed root {root.hex()[:16]}… != claimed "
+                                  f"{bytes(claimed).hex()[:16]}…")
+        return StepVerdict(root, first_bad, first_fail, codes, self.rows, check, detail)
