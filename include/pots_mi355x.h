@@ -40,6 +40,14 @@ const char *pots_mi355x_version(void);
 /* The last HIP error message of the calling thread, or "" if none. */
 const char *pots_last_error(void);
 
+/* Replaces native.c:341 pots_simd_degree: chunks compressed per instruction (64, one BLAKE3
+ * chunk per lane of a wavefront). */
+size_t pots_simd_degree(void);
+
+/* Replaces native.c:343 pots_blake3_version: which BLAKE3 implementation hashes ("spec
+ * (gfx950 kernels)": this library's own, written from the BLAKE3 specification). */
+const char *pots_blake3_version(void);
+
 /* ---- the reference's entry points --------------------------------------------------- */
 
 /* Replaces native.c:243 pots_hash_leaves. Leaf i's digest BLAKE3(0x00 || header || payload)

@@ -81,3 +81,8 @@ bool is_device_pointer(const void* p) {
 extern "C" const char* pots_mi355x_version(void) { return "pots-mi355x 0.1.0 gfx950"; }
 
 extern "C" const char* pots_last_error(void) { return pots::g_last_error.c_str(); }
+
+// One BLAKE3 chunk per lane: a wavefront compresses 64 chunks with each instruction.
+extern "C" size_t pots_simd_degree(void) { return 64; }
+
+extern "C" const char* pots_blake3_version(void) { return "spec (gfx950 kernels)"; }

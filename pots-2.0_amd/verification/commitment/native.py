@@ -77,6 +77,8 @@ class Native:
         sigs = {
             "pots_mi355x_version": ([], ctypes.c_char_p),
             "pots_last_error": ([], ctypes.c_char_p),
+            "pots_simd_degree": ([], _sz),
+            "pots_blake3_version": ([], ctypes.c_char_p),
             "pots_hash_leaves": ([_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32], _sz),
             "pots_all_finite": ([_vp, _u64, _u8, _u32], _int),
             "pots_merkle_tree": ([_sz, _vp, _vp], _int),
@@ -106,8 +108,8 @@ class Native:
             fn.restype = res
         self._lib = lib
         self.version = lib.pots_mi355x_version().decode()
-        self.blake3_version = "spec (gfx950 kernels)"
-        self.simd_degree = 64  # lanes per wavefront, one chunk per lane
+        self.blake3_version = lib.pots_blake3_version().decode()
+        self.simd_degree = int(lib.pots_simd_degree())
 
     # ---- errors --------------------------------------------------------------------------
 
