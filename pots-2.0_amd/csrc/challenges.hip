@@ -14,9 +14,9 @@
 // neighbouring columns.
 //
 // Besides the row-major matrix, a lane can write the same entries in the two operand
-// layouts the Freivalds kernels read (see freivalds.hip): "bf16x3" (each fp32 entry as three
-// bf16 terms whose sum is exact, grouped by 8 rows per column) and "f32x4" (fp32, grouped by
-// 4 rows per column). Rows past `width` up to the next multiple of 16 are written as zero.
+// layouts the Freivalds row pass reads (freivalds.h): "bf16x3" (each fp32 entry as three
+// bf16 terms whose sum is exact, 8 rows per K-group) and "f32x4" (fp32, 4 rows per K-group).
+// Rows past `width` up to the next multiple of 16 are written as zero.
 #include <string.h>
 
 #include <new>
@@ -69,26 +69,29 @@ __global__ __launch_bounds__(256) void xof_kernel(const uint32_t* __restrict__ k
       if (16u * t + s < it.width) col[(uint64_t)(16u * t + s) * k] = r[s];
   }
   if (out_b3) {
-    // Two groups of 8 rows: group index 2t and 2t+1, each [3 planes][8] bf16 at
-    // ((group * k + j) * 3 + plane) * 8.
+    // K-groups 2t and 2t + 1 (8 rows each); the three terms of column j go to slots
+    // 3(j mod 5) + term of group j / 5.
+    const uint32_t njg = groups_b3(k), jg = j / 5, slot = 3 * (j % 5);
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       uint16_t pl[3][8];
 #pragma unroll
       for (int e = 0; e < 8; e++) split_bf16x3(r[8 * h + e], pl[0][e], pl[1][e], pl[2][e]);
-      uint4* dst = reinterpret_cast<uint4*>(
-          out_b3 + it.pk_off + ((uint64_t)(2 * t + h) * k + j) * 24);
+      uint16_t* grp = out_b3 + it.pk_off + (((uint64_t)(2 * t + h) * njg + jg) * 16 + slot) * 8;
 #pragma unroll
       for (int p = 0; p < 3; p++)
-        dst[p] = make_uint4(pl[p][0] | (uint32_t)pl[p][1] << 16, pl[p][2] | (uint32_t)pl[p][3] << 16,
-                            pl[p][4] | (uint32_t)pl[p][5] << 16, pl[p][6] | (uint32_t)pl[p][7] << 16);
+        *reinterpret_cast<uint4*>(grp + 8 * p) =
+            make_uint4(pl[p][0] | (uint32_t)pl[p][1] << 16, pl[p][2] | (uint32_t)pl[p][3] << 16,
+                       pl[p][4] | (uint32_t)pl[p][5] << 16, pl[p][6] | (uint32_t)pl[p][7] << 16);
     }
   }
   if (out_f4) {
-    // Four groups of 4 rows: group 4t + h at (group * k + j) * 4.
+    // K-groups 4t .. 4t + 3 (4 rows each); column j in slot j mod 16 of group j / 16.
+    const uint32_t njg = groups_f4(k), jg = j / 16, slot = j % 16;
 #pragma unroll
     for (int h = 0; h < 4; h++) {
-      float4* dst = reinterpret_cast<float4*>(out_f4 + it.pk_off + ((uint64_t)(4 * t + h) * k + j) * 4);
+      float4* dst = reinterpret_cast<float4*>(
+          out_f4 + it.pk_off + (((uint64_t)(4 * t + h) * njg + jg) * 16 + slot) * 4);
       *dst = make_float4(r[4 * h], r[4 * h + 1], r[4 * h + 2], r[4 * h + 3]);
     }
   }

@@ -18,6 +18,14 @@ struct ChallengeItem {
 };
 static_assert(sizeof(ChallengeItem) == 32, "ChallengeItem layout");
 
+// The packed operands of the row pass hold each K-group of PER rows (8 for bf16 X, 4 for
+// fp32 X) as groups of 16 slots of PER values: slot 3·jl + t of group jg is term t of
+// challenge column 5·jg + jl for bf16 X (hi, mid, lo), slot jl of group jg is column
+// 16·jg + jl for fp32 X. The slots of K-group G, group jg start at ((G·n_jg + jg)·16) · PER
+// elements.
+__host__ __device__ inline uint32_t groups_b3(uint32_t k) { return (k + 4) / 5; }
+__host__ __device__ inline uint32_t groups_f4(uint32_t k) { return (k + 15) / 16; }
+
 int challenges_enqueue(const uint32_t* d_key, const ChallengeItem* d_items, uint32_t n_items,
                        uint64_t n_units, uint32_t k, float* d_out, uint16_t* d_b3, float* d_f4,
                        hipStream_t s);

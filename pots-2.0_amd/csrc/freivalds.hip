@@ -14,14 +14,30 @@
 //   B pass: X = B, V = R      -> B·R, |B|·1, B²·1
 //   A pass: X = A, V = B·R    -> A·(B·R), |A|·(|B|·1), A²·(B²·1)
 //   P pass: X = P, V = R      -> P·R, |P|·1, P²·1 (fp64)
-// X·V runs on the matrix cores: a wave owns 64 rows (4 tiles of 16) and a range of columns
-// and issues v_mfma_f32_16x16x16_bf16 (bf16 X, V as three exact bf16 terms) or
-// v_mfma_f32_16x16x4_f32 (fp32 X). Each lane loads 16 contiguous bytes of one row per tile per
-// step, so a wave reads 16 rows x 64 (bf16) or 64 bytes (fp32) per tile per step; the lane's
-// column order inside a step is a permutation of the MFMA's K index, applied identically to
-// the V operand. The two sums are VALU work on the same registers. Columns are split into
-// chunks (partial sums per chunk, reduced in a fixed order later), so every product yields
-// enough waves and the result does not depend on timing.
+//
+// Work split. A block is 4 waves over 64 consecutive rows (16 per wave) and one column chunk
+// of at most 4096 columns; consecutive blocks take consecutive row groups of the same chunk,
+// so the chunk's V stays in each XCD's L2 while its row groups stream. Each lane (g, i) of a
+// wave reads row i: 16 contiguous bytes at columns c + PER·g of every K-step c (PER = 8 bf16
+// or 4 fp32), KU = 4 K-steps per pipeline stage, so a stage reads 256 contiguous bytes of
+// each of the wave's 16 rows, and the loads of stage s+1 are in flight while stage s is
+// multiplied.
+//
+// X·V runs on the matrix cores. The lane's K index inside a K-step is a permutation of the
+// MFMA's, applied identically to V. bf16 X uses v_mfma_f32_16x16x16_bf16 with V as three
+// exact bf16 terms (hi + mid + lo == the fp32 value) placed in separate output columns: a
+// group of 16 MFMA columns holds 5 challenge columns x 3 terms (slot 3·jl + term), and the
+// three terms' fp32 results are added after the loop. fp32 X uses v_mfma_f32_16x16x4_f32
+// with V in fp32, 16 challenge columns per group. A block computes NJG groups at once, so X
+// is read once for k <= 5·NJG (bf16) or 16·NJG (fp32).
+//
+// V, packed per K-group of PER columns: the 16 slots of group jg for K-group G occupy 256
+// bytes at ((G · n_jg + jg) · 16 + slot) · 16, each slot holding PER consecutive rows of V
+// (bf16 terms, or fp32). Rows past the matrix and unused slots are zero.
+//
+// The two sums are VALU work on the loaded registers; the A pass's weights u, w are staged in
+// LDS once per block. Columns are split into chunks whose partial sums are reduced in a fixed
+// order later, so every product yields enough blocks and no result depends on timing.
 #include <math.h>
 #include <string.h>
 
@@ -42,22 +58,46 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 enum : uint32_t { DT_F32 = 0, DT_BF16 = 1 };
 
+constexpr uint32_t kRowsPerBlock = 64;  // 4 waves x 16 rows
+
+// K-steps per pipeline stage of the row pass.
+#ifndef POTS_FV_KU
+#define POTS_FV_KU 4
+#endif
+constexpr uint32_t KU = POTS_FV_KU;
+
+template <uint32_t XT>
+struct Geo;
+// CHUNK: columns per chunk at most. A chunk's dot products accumulate in fp32 on the matrix
+// cores, one K-step after another, and chunks are added in fp64; 1024 fp32 columns keep that
+// rounding below the reference's own fp32 matvec error (about one band unit at q ~ 8000).
+// The A pass's weights of a chunk sit in LDS (2 x 4 x CHUNK bytes).
+template <>
+struct Geo<DT_BF16> {
+  static constexpr uint32_t KSTEP = 32, PER = 8, ESZ = 2, CHUNK = 4096;
+};
+template <>
+struct Geo<DT_F32> {
+  static constexpr uint32_t KSTEP = 16, PER = 4, ESZ = 4, CHUNK = 1024;
+};
+
 // One matrix of one pass.
 struct PassJob {
   uint64_t x;           // X[0][0]
   uint64_t ld;          // row stride in elements
-  uint64_t v;           // packed V of this job (uint16 elements for bf16 X, floats for fp32)
+  uint64_t v;           // packed V of this job
   uint64_t u, w;        // per-column weights (fp32 [cols]) or 0 for ones
   uint64_t pdot;        // partial X·V: float [n_chunks][rows_pad][k]
   uint64_t pabs;        // partial Σ|x|u: float [n_chunks][rows_pad]
   uint64_t psq;         // partial Σx²w: double [n_chunks][rows_pad]
-  uint64_t tile_first;  // prefix of tiles over the jobs before it
   uint32_t rows, cols;
   uint32_t rows_pad, chunk_cols;
-  uint32_t n_chunks, n_jg;  // column chunks; groups of 16 challenge columns
+  uint32_t n_chunks, n_rg;  // column chunks; 64-row groups
+  uint32_t n_jg, n_jt;      // 16-slot column groups; blocks per (row group, chunk)
+  uint64_t block_first;     // prefix of blocks over the launch's jobs before it
   uint32_t aligned, pad;    // 16-byte aligned rows and base
 };
-static_assert(sizeof(PassJob) == 104, "PassJob layout");
+static_assert(sizeof(PassJob) == 112, "PassJob layout");
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
@@ -81,275 +121,267 @@ struct SqAcc<false> {
 
 // ---- the row pass ---------------------------------------------------------------------------
 
-// Rows per wave (RT tiles of 16) and K-steps per pipeline stage (KU) of the row pass.
-#ifndef POTS_FV_RT
-#define POTS_FV_RT 4
-#endif
-#ifndef POTS_FV_KU
-#define POTS_FV_KU 1
-#endif
-constexpr int RT = POTS_FV_RT;
-constexpr int KU = POTS_FV_KU;
-
-// One pipeline stage's operands in registers: for each of KU K-steps, PER consecutive X
-// elements of each of the RT row tiles (4 words), the V operand of this lane's challenge
-// column for its PER columns (bf16: 3 planes x 8 bf16; fp32: 4 floats in v[0]), and the
-// per-column weights.
-template <uint32_t XT>
-struct StepRegs {
-  uint32_t xw[KU][RT][4];
-  u32x4 v[KU][3];
-  float uc[KU][XT == DT_BF16 ? 8 : 4], wc[KU][XT == DT_BF16 ? 8 : 4];
+template <uint32_t NJG>
+struct StageRegs {
+  u32x4 x[KU];
+  u32x4 v[KU][NJG];
 };
 
-// Load KU K-steps starting at the step whose first column for this lane is `cl`. `full`: the
-// job is aligned and every step lies before c1, so every load is a 16-byte vector load with
-// no column guard (rows past the matrix read a valid row; their results are never written).
-template <uint32_t XT, bool WEIGHTED>
-__device__ __forceinline__ void load_stage(StepRegs<XT>& r, const char* const xrow[RT],
-                                           const bool rv[RT], uint32_t cl, uint32_t c1,
-                                           bool full, const PassJob& J, uint32_t k, uint32_t j,
-                                           bool vload, bool sums, int nsteps = KU) {
-  constexpr uint32_t PER = XT == DT_BF16 ? 8 : 4;
-  constexpr uint32_t KSTEP = XT == DT_BF16 ? 32 : 16;
-  constexpr uint32_t esz = XT == DT_BF16 ? 2 : 4;
+// The per-lane view of one tile: X row, V slot base, weights and bounds.
+struct Lane {
+  const char* xrow;   // this lane's X row (clamped to the matrix)
+  const char* vlane;  // V slot of this lane for K-group g of group jt·NJG
+  uint64_t vstep;     // bytes of V per K-group
+  uint32_t g, c1;
+  uint32_t nvalid;    // groups of this block that exist (the last block of a row may hold fewer)
+};
+
+// A whole stage of an aligned job, every column inside the chunk: plain 16-byte loads.
+template <uint32_t XT, uint32_t NJG>
+__device__ __forceinline__ void load_full(StageRegs<NJG>& r, const Lane& L, uint32_t cs) {
+  using G = Geo<XT>;
 #pragma unroll
-  for (int u = 0; u < KU; u++) {
-    const uint32_t cu = cl + u * KSTEP;
+  for (uint32_t u = 0; u < KU; u++) {
+    const uint32_t cu = cs + u * G::KSTEP;
+    r.x[u] = gload<u32x4>(L.xrow + (uint64_t)(cu + G::PER * L.g) * G::ESZ);
+    const char* vp = L.vlane + (uint64_t)(cu / G::PER) * L.vstep;
+    // Every load is unconditional, so the compiler's wait counts stay exact across the
+    // pipeline: a group past n_jg (only in a row's last column-group block) rereads the last
+    // valid group, and its results are not stored.
 #pragma unroll
-    for (int t = 0; t < RT; t++) {
-      if (full) {
-        const u32x4 q = gload<u32x4>(xrow[t] + (uint64_t)cu * esz);
-        r.xw[u][t][0] = q.x; r.xw[u][t][1] = q.y; r.xw[u][t][2] = q.z; r.xw[u][t][3] = q.w;
-      } else if (XT == DT_BF16) {
-        const uint16_t* p = reinterpret_cast<const uint16_t*>(xrow[t]);
-        uint16_t e[8];
-#pragma unroll
-        for (int s = 0; s < 8; s++)
-          e[s] = (u < nsteps && rv[t] && cu + s < c1) ? gload<uint16_t>(p + cu + s) : (uint16_t)0;
-#pragma unroll
-        for (int s = 0; s < 4; s++) r.xw[u][t][s] = e[2 * s] | (uint32_t)e[2 * s + 1] << 16;
-      } else {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(xrow[t]);
-#pragma unroll
-        for (int s = 0; s < 4; s++)
-          r.xw[u][t][s] = (u < nsteps && rv[t] && cu + s < c1) ? gload<uint32_t>(p + cu + s) : 0u;
-      }
-    }
-    r.v[u][0] = r.v[u][1] = r.v[u][2] = u32x4{0, 0, 0, 0};
-    if (vload && (full || (u < nsteps && cu < c1))) {
-      if (XT == DT_BF16) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(J.v) +
-                                                          ((uint64_t)(cu / 8) * k + j) * 24);
-        r.v[u][0] = gload<u32x4>(src);
-        r.v[u][1] = gload<u32x4>(src + 1);
-        r.v[u][2] = gload<u32x4>(src + 2);
-      } else {
-        r.v[u][0] = gload<u32x4>(reinterpret_cast<const float*>(J.v) +
-                                 ((uint64_t)(cu / 4) * k + j) * 4);
-      }
-    }
-    if (WEIGHTED && sums) {
-      const float* uw = reinterpret_cast<const float*>(J.u);
-      const float* ww = reinterpret_cast<const float*>(J.w);
-#pragma unroll
-      for (uint32_t s = 0; s < PER; s++) {
-        const bool ok = full || (u < nsteps && cu + s < c1);
-        r.uc[u][s] = ok ? gload<float>(uw + cu + s) : 0.f;
-        r.wc[u][s] = ok ? gload<float>(ww + cu + s) : 0.f;
-      }
-    }
+    for (uint32_t q = 0; q < NJG; q++)
+      r.v[u][q] = gload<u32x4>(vp + (q < L.nvalid ? q : L.nvalid - 1) * 256);
   }
 }
 
-template <uint32_t XT, bool WEIGHTED, bool SQ64>
-__device__ __forceinline__ void compute_stage(const StepRegs<XT>& r, v4f32 acc[RT], float s1[RT],
-                                              SqAcc<SQ64> s2[RT], bool sums) {
+// A stage that may run past the chunk's end, or of an unaligned job: element loads with a
+// column guard; columns past c1 read as zero, and so does V of K-steps past c1 (V rows past
+// the matrix are zero in memory).
+template <uint32_t XT, uint32_t NJG>
+__device__ __forceinline__ void load_guarded(StageRegs<NJG>& r, const Lane& L, uint32_t cs) {
+  using G = Geo<XT>;
 #pragma unroll
-  for (int u = 0; u < KU; u++) {
+  for (uint32_t u = 0; u < KU; u++) {
+    const uint32_t cu = cs + u * G::KSTEP;
+    const uint32_t cl = cu + G::PER * L.g;
+    if (XT == DT_BF16) {
+      const uint16_t* p = reinterpret_cast<const uint16_t*>(L.xrow);
+      uint32_t e[8];
+#pragma unroll
+      for (uint32_t t = 0; t < 8; t++) e[t] = cl + t < L.c1 ? gload<uint16_t>(p + cl + t) : 0u;
+      r.x[u] = u32x4{e[0] | e[1] << 16, e[2] | e[3] << 16, e[4] | e[5] << 16, e[6] | e[7] << 16};
+    } else {
+      const uint32_t* p = reinterpret_cast<const uint32_t*>(L.xrow);
+      uint32_t e[4];
+#pragma unroll
+      for (uint32_t t = 0; t < 4; t++) e[t] = cl + t < L.c1 ? gload<uint32_t>(p + cl + t) : 0u;
+      r.x[u] = u32x4{e[0], e[1], e[2], e[3]};
+    }
+    const char* vp = L.vlane + (uint64_t)(cu / G::PER) * L.vstep;
+#pragma unroll
+    for (uint32_t q = 0; q < NJG; q++)
+      r.v[u][q] = (q < L.nvalid && cu < L.c1) ? gload<u32x4>(vp + q * 256) : u32x4{0, 0, 0, 0};
+  }
+}
+
+template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
+__device__ __forceinline__ void compute_stage(const StageRegs<NJG>& r, v4f32 acc[NJG],
+                                              float& s1, SqAcc<SQ64>& s2, bool sums,
+                                              const float* wu, const float* ww, uint32_t off) {
+  using G = Geo<XT>;
+#pragma unroll
+  for (uint32_t u = 0; u < KU; u++) {
     if (XT == DT_BF16) {
 #pragma unroll
-      for (int t = 0; t < RT; t++) {
+      for (int h = 0; h < 2; h++) {
+        const v4i16 a = __builtin_bit_cast(v4i16, v2u32{r.x[u][2 * h], r.x[u][2 * h + 1]});
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const v4i16 a = __builtin_bit_cast(v4i16, v2u32{r.xw[u][t][2 * h], r.xw[u][t][2 * h + 1]});
-#pragma unroll
-          for (int p = 0; p < 3; p++) {
-            const v2u32 bw = h == 0 ? v2u32{r.v[u][p].x, r.v[u][p].y} : v2u32{r.v[u][p].z, r.v[u][p].w};
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(v4i16, bw),
-                                                               acc[t], 0, 0, 0);
-          }
-        }
-      }
-      if (sums) {
-#pragma unroll
-        for (int t = 0; t < RT; t++) {
-#pragma unroll
-          for (int s = 0; s < 4; s++) {
-            const float xa = bf_lo(r.xw[u][t][s]), xb = bf_hi(r.xw[u][t][s]);
-            if (WEIGHTED) {
-              s1[t] = fmaf(fabsf(xa), r.uc[u][2 * s], s1[t]);
-              s1[t] = fmaf(fabsf(xb), r.uc[u][2 * s + 1], s1[t]);
-              s2[t].add(xa, r.wc[u][2 * s]);
-              s2[t].add(xb, r.wc[u][2 * s + 1]);
-            } else {
-              s1[t] += fabsf(xa);
-              s1[t] += fabsf(xb);
-              s2[t].add1(xa);
-              s2[t].add1(xb);
-            }
-          }
+        for (uint32_t q = 0; q < NJG; q++) {
+          const v4i16 b = __builtin_bit_cast(v4i16, v2u32{r.v[u][q][2 * h], r.v[u][q][2 * h + 1]});
+          acc[q] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc[q], 0, 0, 0);
         }
       }
     } else {
-      const float vv[4] = {__uint_as_float(r.v[u][0].x), __uint_as_float(r.v[u][0].y),
-                           __uint_as_float(r.v[u][0].z), __uint_as_float(r.v[u][0].w)};
 #pragma unroll
-      for (int t = 0; t < RT; t++) {
+      for (int e = 0; e < 4; e++) {
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(r.xw[u][t][e]), vv[e],
-                                                        acc[t], 0, 0, 0);
+        for (uint32_t q = 0; q < NJG; q++)
+          acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(r.x[u][e]),
+                                                        __uint_as_float(r.v[u][q][e]), acc[q],
+                                                        0, 0, 0);
       }
-      if (sums) {
+    }
+    if (sums) {
+      float xs[G::PER];
 #pragma unroll
-        for (int t = 0; t < RT; t++) {
+      for (int e = 0; e < 4; e++) {
+        if (XT == DT_BF16) {
+          xs[2 * e] = bf_lo(r.x[u][e]);
+          xs[2 * e + 1] = bf_hi(r.x[u][e]);
+        } else {
+          xs[e] = __uint_as_float(r.x[u][e]);
+        }
+      }
+      if (WEIGHTED) {
+        const uint32_t o = off + u * G::KSTEP;
+        float uc[G::PER], wc[G::PER];
 #pragma unroll
-          for (int s = 0; s < 4; s++) {
-            const float x = __uint_as_float(r.xw[u][t][s]);
-            if (WEIGHTED) {
-              s1[t] = fmaf(fabsf(x), r.uc[u][s], s1[t]);
-              s2[t].add(x, r.wc[u][s]);
-            } else {
-              s1[t] += fabsf(x);
-              s2[t].add1(x);
-            }
+        for (uint32_t t = 0; t < G::PER; t += 4) {
+          const v4f32 a = *reinterpret_cast<const v4f32*>(wu + o + t);
+          const v4f32 b = *reinterpret_cast<const v4f32*>(ww + o + t);
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            uc[t + e] = a[e];
+            wc[t + e] = b[e];
           }
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < G::PER; t++) {
+          s1 = fmaf(fabsf(xs[t]), uc[t], s1);
+          s2.add(xs[t], wc[t]);
+        }
+      } else {
+#pragma unroll
+        for (uint32_t t = 0; t < G::PER; t++) {
+          s1 += fabsf(xs[t]);
+          s2.add1(xs[t]);
         }
       }
     }
   }
 }
 
-// XT = DT_BF16: K-step of 32 columns; lane group g = lane / 16 owns columns c + 8g .. c + 8g + 7.
-// XT = DT_F32: K-step of 16 columns; lane group g owns columns c + 4g .. c + 4g + 3.
-// A wave owns 16·RT rows; a tile is (job, 16·RT-row block, column chunk, challenge group).
-template <uint32_t XT, bool WEIGHTED, bool SQ64>
+// One block: job blk_job[blockIdx.x], 64-row group, column chunk and column-group block
+// decoded from its index within the job (row group fastest).
+template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
 __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
-                                                uint64_t n_tiles,
                                                 const uint32_t* __restrict__ blk_job,
                                                 uint32_t k) {
-  constexpr uint32_t KSTEP = XT == DT_BF16 ? 32 : 16;
-  constexpr uint32_t PER = XT == DT_BF16 ? 8 : 4;  // columns per lane per step
+  using G = Geo<XT>;
+  constexpr uint32_t SSTEP = G::KSTEP * KU;
+  __shared__ float s_u[WEIGHTED ? G::CHUNK : 4], s_w[WEIGHTED ? G::CHUNK : 4];
   // The wave index is uniform; readfirstlane lets the compiler keep everything derived from
-  // it (the tile, its job, its column range) in scalar registers, so the loop has no
-  // divergent branches and its waits cover only the loads they need.
+  // it in scalar registers, so the loop has no divergent branches.
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63;
-  const uint64_t tile = (uint64_t)blockIdx.x * 4 + wave;
-  if (tile >= n_tiles) return;
-  uint32_t lo = blk_job[blockIdx.x], hi = blk_job[blockIdx.x + 1];
-  while (lo < hi) {
-    const uint32_t mid = (lo + hi + 1) >> 1;
-    if (jobs[mid].tile_first <= tile) lo = mid;
-    else hi = mid - 1;
-  }
-  const PassJob J = jobs[lo];
-  uint64_t local = tile - J.tile_first;
-  const uint32_t chunk = (uint32_t)(local % J.n_chunks);
-  local /= J.n_chunks;
-  const uint32_t jg = (uint32_t)(local % J.n_jg);
-  const uint32_t rt = (uint32_t)(local / J.n_jg);
-  const uint32_t r0 = rt * 16 * RT;
+  const PassJob J = jobs[blk_job[blockIdx.x]];
+  uint32_t local = blockIdx.x - (uint32_t)J.block_first;
+  const uint32_t rg = local % J.n_rg;
+  local /= J.n_rg;
+  const uint32_t chunk = local % J.n_chunks;
+  const uint32_t jt = local / J.n_chunks;
   const uint32_t c0 = chunk * J.chunk_cols;
   const uint32_t c1 = min(c0 + J.chunk_cols, J.cols);
-  const uint32_t g = lane >> 4, i = lane & 15;
-  const uint32_t j = jg * 16 + i;  // this lane's challenge column in the V operand
-  const bool jv = j < k;
-  // Lanes past the last challenge column read column k - 1; their outputs are never written.
-  const uint32_t jl = jv ? j : k - 1;
-  const bool sums = jg == 0;  // the two sums are taken once, by the first column group
-
-  const char* xbase = reinterpret_cast<const char*>(J.x);
-  constexpr uint32_t esz = XT == DT_BF16 ? 2 : 4;
-  bool rv[RT];
-  const char* xrow[RT];
-#pragma unroll
-  for (int t = 0; t < RT; t++) {
-    const uint32_t row = r0 + 16 * t + i;
-    rv[t] = row < J.rows;
-    xrow[t] = xbase + (uint64_t)(rv[t] ? row : J.rows - 1) * J.ld * esz;
-  }
-  v4f32 acc[RT];
-  float s1[RT];
-  SqAcc<SQ64> s2[RT];
-#pragma unroll
-  for (int t = 0; t < RT; t++) {
-    acc[t] = v4f32{0.f, 0.f, 0.f, 0.f};
-    s1[t] = 0.f;
-  }
-
-  // Full stages (KU K-steps each) of an aligned job run as a software pipeline: the loads of
-  // stage s + 1 are issued before the matrix-core and VALU work of stage s, so every wave
-  // keeps a stage of loads in flight. The remaining steps and unaligned jobs take the guarded
-  // path.
-  constexpr uint32_t SSTEP = KSTEP * KU;
-  const uint32_t nfull = J.aligned ? (c1 - c0) / SSTEP : 0;
-  if (nfull > 0) {
-    StepRegs<XT> cur, nxt;
-    load_stage<XT, WEIGHTED>(cur, xrow, rv, c0 + PER * g, c1, true, J, k, jl, true, sums);
-    for (uint32_t s = 1; s < nfull; s++) {
-      load_stage<XT, WEIGHTED>(nxt, xrow, rv, c0 + s * SSTEP + PER * g, c1, true, J, k, jl, true,
-                               sums);
-      compute_stage<XT, WEIGHTED, SQ64>(cur, acc, s1, s2, sums);
-      cur = nxt;
+  const bool sums = jt == 0;  // the two sums are taken once, by the first column-group block
+  if (WEIGHTED) {
+    if (sums) {
+      const float* up = reinterpret_cast<const float*>(J.u);
+      const float* wp = reinterpret_cast<const float*>(J.w);
+      for (uint32_t t = threadIdx.x; t < J.chunk_cols; t += 256) {
+        s_u[t] = c0 + t < c1 ? gload<float>(up + c0 + t) : 0.f;
+        s_w[t] = c0 + t < c1 ? gload<float>(wp + c0 + t) : 0.f;
+      }
     }
-    compute_stage<XT, WEIGHTED, SQ64>(cur, acc, s1, s2, sums);
+    __syncthreads();
   }
-  for (uint32_t c = c0 + nfull * SSTEP; c < c1; c += SSTEP) {
-    const uint32_t cl = c + PER * g;
-    const int nsteps = (int)min<uint32_t>(KU, (c1 - c + KSTEP - 1) / KSTEP);
-    StepRegs<XT> r;
-    load_stage<XT, WEIGHTED>(r, xrow, rv, cl, c1, false, J, k, jl, jv, sums, nsteps);
-    compute_stage<XT, WEIGHTED, SQ64>(r, acc, s1, s2, sums);
+  const uint32_t r0 = rg * kRowsPerBlock + wave * 16;
+  if (r0 >= J.rows) return;
+  const uint32_t g = lane >> 4, i = lane & 15;
+  const uint32_t row = r0 + i;
+  Lane L;
+  // Rows past the matrix read its last row; their results are never written.
+  L.xrow = reinterpret_cast<const char*>(J.x) +
+           (uint64_t)(row < J.rows ? row : J.rows - 1) * J.ld * G::ESZ;
+  L.vstep = (uint64_t)J.n_jg * 256;
+  L.vlane = reinterpret_cast<const char*>(J.v) + (uint64_t)g * L.vstep +
+            (uint64_t)jt * NJG * 256 + i * 16;
+  L.g = g;
+  L.c1 = c1;
+  L.nvalid = min(NJG, J.n_jg - jt * NJG);
+
+  v4f32 acc[NJG];
+#pragma unroll
+  for (uint32_t q = 0; q < NJG; q++) acc[q] = v4f32{0.f, 0.f, 0.f, 0.f};
+  float s1 = 0.f;
+  SqAcc<SQ64> s2;
+  const uint32_t woff = G::PER * g - c0;  // LDS weight index = column - c0
+
+  // Full stages of an aligned job run as a two-buffer software pipeline; the rest (the
+  // chunk's last partial stage, or every stage of an unaligned job) takes the guarded loads.
+  const uint32_t nfull = J.aligned ? (c1 - c0) / SSTEP : 0;
+  uint32_t cs = c0;
+  if (nfull > 0) {
+    StageRegs<NJG> ra, rb;
+    load_full<XT, NJG>(ra, L, cs);
+    uint32_t s = 1;
+    for (; s + 1 < nfull; s += 2) {
+      load_full<XT, NJG>(rb, L, cs + SSTEP);
+      compute_stage<XT, WEIGHTED, SQ64, NJG>(ra, acc, s1, s2, sums, s_u, s_w, cs + woff);
+      load_full<XT, NJG>(ra, L, cs + 2 * SSTEP);
+      compute_stage<XT, WEIGHTED, SQ64, NJG>(rb, acc, s1, s2, sums, s_u, s_w,
+                                             cs + SSTEP + woff);
+      cs += 2 * SSTEP;
+    }
+    if (s < nfull) {
+      load_full<XT, NJG>(rb, L, cs + SSTEP);
+      compute_stage<XT, WEIGHTED, SQ64, NJG>(ra, acc, s1, s2, sums, s_u, s_w, cs + woff);
+      compute_stage<XT, WEIGHTED, SQ64, NJG>(rb, acc, s1, s2, sums, s_u, s_w,
+                                             cs + SSTEP + woff);
+      cs += 2 * SSTEP;
+    } else {
+      compute_stage<XT, WEIGHTED, SQ64, NJG>(ra, acc, s1, s2, sums, s_u, s_w, cs + woff);
+      cs += SSTEP;
+    }
+  }
+  for (; cs < c1; cs += SSTEP) {
+    StageRegs<NJG> r;
+    load_guarded<XT, NJG>(r, L, cs);
+    compute_stage<XT, WEIGHTED, SQ64, NJG>(r, acc, s1, s2, sums, s_u, s_w, cs + woff);
   }
 
-  // X·V: lane (g, i) holds rows 4g + e of each tile, challenge column j.
+  // X·V: lane (g, i) holds rows 4g + e of the wave's 16 and slot i of each group.
   float* pdot = reinterpret_cast<float*>(J.pdot);
   const uint64_t cbase = (uint64_t)chunk * J.rows_pad;
-  if (jv) {
 #pragma unroll
-    for (int t = 0; t < RT; t++) {
+  for (uint32_t q = 0; q < NJG; q++) {
+    const uint32_t jg = jt * NJG + q;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const uint32_t row = r0 + 16 * t + 4 * g + e;
-        if (row < J.rows) gstore<float>(pdot + (cbase + row) * k + j, acc[t][e]);
+    for (int e = 0; e < 4; e++) {
+      const uint32_t orow = r0 + 4 * g + e;
+      if (XT == DT_BF16) {
+        // The three terms of challenge column jl sit in slots 3jl, 3jl + 1, 3jl + 2.
+        const float v0 = acc[q][e];
+        const float v1 = __shfl(v0, (int)lane + 1);
+        const float v2 = __shfl(v0, (int)lane + 2);
+        const uint32_t j = 5 * jg + i / 3;
+        if (i % 3 == 0 && i < 15 && q < L.nvalid && j < k && orow < J.rows)
+          gstore<float>(pdot + (cbase + orow) * k + j, (v0 + v1) + v2);
+      } else {
+        const uint32_t j = 16 * jg + i;
+        if (q < L.nvalid && j < k && orow < J.rows)
+          gstore<float>(pdot + (cbase + orow) * k + j, acc[q][e]);
       }
     }
   }
   if (sums) {
     float* pabs = reinterpret_cast<float*>(J.pabs);
     double* psq = reinterpret_cast<double*>(J.psq);
-#pragma unroll
-    for (int t = 0; t < RT; t++) {
-      float a = s1[t];
-      double q = s2[t].get();
-      if (!SQ64) {  // combine in the accumulation precision
-        float qf = (float)q;
-        qf += __shfl_xor(qf, 16);
-        qf += __shfl_xor(qf, 32);
-        q = qf;
-      } else {
-        q += __shfl_xor(q, 16);
-        q += __shfl_xor(q, 32);
-      }
-      a += __shfl_xor(a, 16);
-      a += __shfl_xor(a, 32);
-      const uint32_t row = r0 + 16 * t + i;
-      if (g == 0 && row < J.rows) {
-        gstore<float>(pabs + cbase + row, a);
-        gstore<double>(psq + cbase + row, q);
-      }
+    float a = s1;
+    double q = s2.get();
+    if (!SQ64) {  // combine in the accumulation precision
+      float qf = (float)q;
+      qf += __shfl_xor(qf, 16);
+      qf += __shfl_xor(qf, 32);
+      q = qf;
+    } else {
+      q += __shfl_xor(q, 16);
+      q += __shfl_xor(q, 32);
+    }
+    a += __shfl_xor(a, 16);
+    a += __shfl_xor(a, 32);
+    if (g == 0 && row < J.rows) {
+      gstore<float>(pabs + cbase + row, a);
+      gstore<double>(psq + cbase + row, q);
     }
   }
 }
@@ -394,19 +426,20 @@ __global__ __launch_bounds__(256) void reduce_b(const RedJob* __restrict__ jobs,
     uint16_t pl[3][8];
 #pragma unroll
     for (int e = 0; e < 8; e++) split_bf16x3(v[e], pl[0][e], pl[1][e], pl[2][e]);
-    u32x4* dst = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(J.vout) +
-                                          ((uint64_t)grp * k + j) * 24);
+    uint16_t* dst = reinterpret_cast<uint16_t*>(J.vout) +
+                    (((uint64_t)grp * groups_b3(k) + j / 5) * 16 + 3 * (j % 5)) * 8;
 #pragma unroll
     for (int p = 0; p < 3; p++)
-      gstore<u32x4>(dst + p, u32x4{pl[p][0] | (uint32_t)pl[p][1] << 16,
-                                   pl[p][2] | (uint32_t)pl[p][3] << 16,
-                                   pl[p][4] | (uint32_t)pl[p][5] << 16,
-                                   pl[p][6] | (uint32_t)pl[p][7] << 16});
+      gstore<u32x4>(dst + 8 * p, u32x4{pl[p][0] | (uint32_t)pl[p][1] << 16,
+                                       pl[p][2] | (uint32_t)pl[p][3] << 16,
+                                       pl[p][4] | (uint32_t)pl[p][5] << 16,
+                                       pl[p][6] | (uint32_t)pl[p][7] << 16});
   } else {
     float* base = reinterpret_cast<float*>(J.vout);
+    const uint32_t njg = groups_f4(k);
 #pragma unroll
     for (int h = 0; h < 2; h++)
-      gstore<u32x4>(base + ((uint64_t)(2 * grp + h) * k + j) * 4,
+      gstore<u32x4>(base + (((uint64_t)(2 * grp + h) * njg + j / 16) * 16 + j % 16) * 4,
                     u32x4{__float_as_uint(v[4 * h]), __float_as_uint(v[4 * h + 1]),
                           __float_as_uint(v[4 * h + 2]), __float_as_uint(v[4 * h + 3])});
   }
@@ -571,10 +604,9 @@ __global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jo
 // ---- the plan ---------------------------------------------------------------------------
 
 struct PassLaunch {
-  uint32_t xt, weighted, sq64;
+  uint32_t xt, weighted, sq64, njg;  // kernel variant
   uint64_t job_off;  // index into the job array
   uint32_t n_jobs;
-  uint64_t n_tiles;
   uint64_t blk_off;  // index into the block->job table
   uint32_t n_blocks;
 };
@@ -608,13 +640,21 @@ struct FvPlan {
 // the matrix are zero.
 static uint64_t pad32(uint64_t rows) { return (rows + 31) / 32 * 32; }
 
-static uint32_t chunk_cols_for(uint32_t cols, uint32_t kstep) {
-  // At most 4096 columns per chunk, in whole K-steps, balanced over the chunks.
-  const uint32_t n = std::max<uint32_t>(1, (cols + 4095) / 4096);
+static uint32_t chunk_cols_for(uint32_t cols, uint32_t sstep, uint32_t cmax) {
+  // At most cmax columns per chunk, in whole pipeline stages, balanced over the chunks (cmax
+  // is a multiple of the stage width, so rounding up stays within it).
+  const uint32_t n = std::max<uint32_t>(1, (cols + cmax - 1) / cmax);
   uint32_t c = (cols + n - 1) / n;
-  c = (c + kstep - 1) / kstep * kstep;
-  return std::max<uint32_t>(c, kstep);
+  c = (c + sstep - 1) / sstep * sstep;
+  return std::max<uint32_t>(c, sstep);
 }
+
+// 16-slot column groups of a packed operand read by X of dtype xt, and how many of them one
+// block computes (the kernel variant): all of them up to 4, else 4 per block.
+static uint32_t groups_for(uint32_t xt, uint32_t k) {
+  return xt == DT_BF16 ? groups_b3(k) : groups_f4(k);
+}
+static uint32_t njg_for(uint32_t xt, uint32_t k) { return std::min<uint32_t>(4, groups_for(xt, k)); }
 
 }  // namespace pots
 
@@ -637,7 +677,8 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     return a;
   };
   const size_t o_key = place(32);
-  const uint32_t n_jg = (k + 15) / 16;
+  const uint64_t b3_per_row = (uint64_t)groups_b3(k) * 16;  // bf16 elements per row of V
+  const uint64_t f4_per_row = (uint64_t)groups_f4(k) * 16;  // floats per row of V
   std::vector<ChallengeItem> items(n);
   uint64_t r_floats = 0, b3_elems = 0, f4_floats = 0, units = 0;
   for (size_t i = 0; i < n; i++) {
@@ -661,8 +702,8 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     P->need_b3 |= p.b_dtype == DT_BF16 || p.p_dtype == DT_BF16;
     P->need_f4 |= p.b_dtype == DT_F32 || p.p_dtype == DT_F32;
     items[i].pk_off = 0;
-    b3_elems += wpad * k * 3;
-    f4_floats += wpad * k;
+    b3_elems += wpad * b3_per_row;
+    f4_floats += wpad * f4_per_row;
   }
   P->n_items = (uint32_t)n;
   P->n_units = units;
@@ -675,8 +716,8 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
       const uint64_t wpad = pad32(prods[i].w);
       items_b3[i].pk_off = ob;
       items_f4[i].pk_off = of;
-      ob += wpad * k * 3;
-      of += wpad * k;
+      ob += wpad * b3_per_row;
+      of += wpad * f4_per_row;
     }
   }
   const size_t o_items_b3 = place(n * sizeof(ChallengeItem));
@@ -692,17 +733,21 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     uint32_t rows, cols, dt;
     uint64_t x, ld;
   };
-  auto make_job = [&](const Shape& s, uint32_t kstep) {
+  auto make_job = [&](const Shape& s) {
     PassJob J;
     memset(&J, 0, sizeof J);
     J.x = s.x;
     J.ld = s.ld;
     J.rows = s.rows;
     J.cols = s.cols;
-    J.rows_pad = (s.rows + 16 * RT - 1) / (16 * RT) * (16 * RT);
-    J.chunk_cols = chunk_cols_for(s.cols, kstep * KU);
+    J.rows_pad = (s.rows + kRowsPerBlock - 1) / kRowsPerBlock * kRowsPerBlock;
+    J.chunk_cols = s.dt == DT_BF16
+                       ? chunk_cols_for(s.cols, Geo<DT_BF16>::KSTEP * KU, Geo<DT_BF16>::CHUNK)
+                       : chunk_cols_for(s.cols, Geo<DT_F32>::KSTEP * KU, Geo<DT_F32>::CHUNK);
     J.n_chunks = (s.cols + J.chunk_cols - 1) / J.chunk_cols;
-    J.n_jg = n_jg;
+    J.n_rg = J.rows_pad / kRowsPerBlock;
+    J.n_jg = groups_for(s.dt, k);
+    J.n_jt = (J.n_jg + njg_for(s.dt, k) - 1) / njg_for(s.dt, k);
     const uint32_t esz = s.dt == DT_BF16 ? 2 : 4;
     J.aligned = (s.x % 16 == 0) && ((s.ld * esz) % 16 == 0);
     return J;
@@ -725,13 +770,13 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   std::vector<size_t> off_br, off_b1, off_b2;
   for (size_t i = 0; i < n; i++) {
     const pots_fv_product& p = prods[i];
-    const uint32_t kb = p.b_dtype == DT_BF16 ? 32 : 16;
-    PassJob J = make_job({p.q, p.w, p.b_dtype, reinterpret_cast<uint64_t>(p.b), p.ldb}, kb);
+    PassJob J = make_job({p.q, p.w, p.b_dtype, reinterpret_cast<uint64_t>(p.b), p.ldb});
     jobs.push_back(J);
     reserve_part(J);
     const uint64_t qpad = pad32(p.q);
     off_br.push_back(br_bytes);
-    br_bytes = align_up(br_bytes + qpad * k * (p.a_dtype == DT_BF16 ? 6 : 4), 256);
+    br_bytes = align_up(br_bytes + qpad * (p.a_dtype == DT_BF16 ? 2 * b3_per_row
+                                                                : 4 * f4_per_row), 256);
     off_b1.push_back(br_bytes);
     br_bytes = align_up(br_bytes + (uint64_t)p.q * 4, 256);
     off_b2.push_back(br_bytes);
@@ -742,15 +787,13 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   }
   for (size_t i = 0; i < n; i++) {
     const pots_fv_product& p = prods[i];
-    PassJob J = make_job({p.n, p.q, p.a_dtype, reinterpret_cast<uint64_t>(p.a), p.lda},
-                         p.a_dtype == DT_BF16 ? 32 : 16);
+    PassJob J = make_job({p.n, p.q, p.a_dtype, reinterpret_cast<uint64_t>(p.a), p.lda});
     jobs.push_back(J);
     reserve_part(J);
   }
   for (size_t i = 0; i < n; i++) {
     const pots_fv_product& p = prods[i];
-    PassJob J = make_job({p.n, p.w, p.p_dtype, reinterpret_cast<uint64_t>(p.p), p.ldp},
-                         p.p_dtype == DT_BF16 ? 32 : 16);
+    PassJob J = make_job({p.n, p.w, p.p_dtype, reinterpret_cast<uint64_t>(p.p), p.ldp});
     jobs.push_back(J);
     reserve_part(J);
   }
@@ -787,40 +830,36 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   std::vector<PassJob> ordered;
   std::vector<uint32_t> blk_table;
   std::vector<uint32_t> ordered_src;  // original job index of each ordered job
-  auto emit = [&](const std::vector<Pending>& ls, std::vector<PassLaunch>& dst) {
+  auto emit = [&](const std::vector<Pending>& ls, std::vector<PassLaunch>& dst) -> bool {
     for (const Pending& pd : ls) {
       PassLaunch L;
       L.xt = pd.xt;
       L.weighted = pd.weighted;
       L.sq64 = pd.sq64;
+      L.njg = njg_for(pd.xt, k);
       L.job_off = ordered.size();
       L.n_jobs = (uint32_t)pd.idx.size();
-      uint64_t tiles = 0;
-      std::vector<uint64_t> first;
+      L.blk_off = blk_table.size();
+      uint64_t blocks = 0;
       for (uint32_t src : pd.idx) {
         PassJob J = jobs[src];
-        J.tile_first = tiles;
-        first.push_back(tiles);
-        tiles += (uint64_t)(J.rows_pad / (16 * RT)) * J.n_chunks * J.n_jg;
+        J.block_first = blocks;
+        const uint64_t nb = (uint64_t)J.n_rg * J.n_chunks * J.n_jt;
+        blk_table.insert(blk_table.end(), nb, (uint32_t)(ordered.size() - L.job_off));
+        blocks += nb;
         ordered.push_back(J);
         ordered_src.push_back(src);
       }
-      L.n_tiles = tiles;
-      L.n_blocks = (uint32_t)((tiles + 3) / 4);
-      L.blk_off = blk_table.size();
-      size_t jdx = 0;
-      for (uint32_t b = 0; b < L.n_blocks; b++) {
-        const uint64_t t0 = (uint64_t)b * 4;
-        while (jdx + 1 < first.size() && first[jdx + 1] <= t0) jdx++;
-        blk_table.push_back((uint32_t)jdx);
-      }
-      blk_table.push_back(L.n_jobs - 1);
+      if (blocks >= 0x7FFFFFFFull) return false;
+      L.n_blocks = (uint32_t)blocks;
       dst.push_back(L);
     }
+    return true;
   };
-  emit(lb, P->pass_b);
-  emit(la, P->pass_ap);
-  emit(lp, P->pass_ap);
+  if (!emit(lb, P->pass_b) || !emit(la, P->pass_ap) || !emit(lp, P->pass_ap)) {
+    delete P;
+    return POTS_E_ARG;
+  }
   const size_t o_jobs = place(ordered.size() * sizeof(PassJob));
   const size_t o_blk = place(blk_table.size() * 4);
   const size_t o_red = place(n * sizeof(RedJob));
@@ -832,6 +871,15 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     note_hip_error(e, "hipMalloc(freivalds plan)", __FILE__, __LINE__);
     delete P;
     return e == hipErrorOutOfMemory ? POTS_E_NOMEM : POTS_E_HIP;
+  }
+  // Packed operands: rows past each matrix and unused slots must read as zero (a zero column of
+  // X times a NaN would not be zero); the runs rewrite only the used entries.
+  e = hipMemset(P->base, 0, P->total);
+  if (e != hipSuccess) {
+    note_hip_error(e, "hipMemset(freivalds plan)", __FILE__, __LINE__);
+    (void)hipFree(P->base);
+    delete P;
+    return POTS_E_HIP;
   }
   const uint64_t base = reinterpret_cast<uint64_t>(P->base);
   P->d_key = reinterpret_cast<uint32_t*>(P->base + o_key);
@@ -930,24 +978,37 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   return POTS_E_OK;
 }
 
-template <uint32_t XT, bool W, bool S>
+template <uint32_t XT, bool W, bool S, uint32_t NJG>
 static void launch_pass(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
-  hipLaunchKernelGGL((row_pass<XT, W, S>), dim3(L.n_blocks), dim3(256), 0, s,
-                     P->d_jobs + L.job_off, L.n_tiles, P->d_blk + L.blk_off, P->k);
+  hipLaunchKernelGGL((row_pass<XT, W, S, NJG>), dim3(L.n_blocks), dim3(256), 0, s,
+                     P->d_jobs + L.job_off, P->d_blk + L.blk_off, P->k);
+}
+
+template <uint32_t XT, bool W, bool S>
+static int launch_njg(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
+  switch (L.njg) {
+    case 1: launch_pass<XT, W, S, 1>(P, L, s); return POTS_E_OK;
+    case 2: launch_pass<XT, W, S, 2>(P, L, s); return POTS_E_OK;
+    case 3: launch_pass<XT, W, S, 3>(P, L, s); return POTS_E_OK;
+    case 4: launch_pass<XT, W, S, 4>(P, L, s); return POTS_E_OK;
+    default: return POTS_E_ARG;
+  }
 }
 
 static int run_pass(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
-  if (L.n_tiles == 0) return POTS_E_OK;
+  if (L.n_blocks == 0) return POTS_E_OK;
   const uint32_t key = L.xt * 4 + L.weighted * 2 + L.sq64;
+  int rc;
   switch (key) {
-    case 0: launch_pass<DT_F32, false, false>(P, L, s); break;
-    case 1: launch_pass<DT_F32, false, true>(P, L, s); break;
-    case 2: launch_pass<DT_F32, true, false>(P, L, s); break;
-    case 4: launch_pass<DT_BF16, false, false>(P, L, s); break;
-    case 5: launch_pass<DT_BF16, false, true>(P, L, s); break;
-    case 6: launch_pass<DT_BF16, true, false>(P, L, s); break;
+    case 0: rc = launch_njg<DT_F32, false, false>(P, L, s); break;
+    case 1: rc = launch_njg<DT_F32, false, true>(P, L, s); break;
+    case 2: rc = launch_njg<DT_F32, true, false>(P, L, s); break;
+    case 4: rc = launch_njg<DT_BF16, false, false>(P, L, s); break;
+    case 5: rc = launch_njg<DT_BF16, false, true>(P, L, s); break;
+    case 6: rc = launch_njg<DT_BF16, true, false>(P, L, s); break;
     default: return POTS_E_ARG;
   }
+  if (rc != POTS_E_OK) return rc;
   POTS_HIP(hipGetLastError());
   return POTS_E_OK;
 }

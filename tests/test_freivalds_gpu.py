@@ -90,12 +90,16 @@ def _check_row(got, a, b, p, r, bias, dtype, planted=False):
             assert abs(x - y) <= 2 * mp["unit"], (j, x, y, mp["unit"])
 
 
-SHAPES = [(64, 32, 48), (100, 77, 130), (13, 8, 12), (256, 576, 192), (1, 5, 3), (65, 33, 17)]
+# (n, q, w): aligned and unaligned rows, partial pipeline stages, and q or w past one
+# 4096-column chunk (several chunks reduced in order).
+SHAPES = [(64, 32, 48), (100, 77, 130), (13, 8, 12), (256, 576, 192), (1, 5, 3), (65, 33, 17),
+          (70, 4500, 40), (33, 48, 8300)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", SHAPES)
-@pytest.mark.parametrize("k", [1, 4, 16, 20])
+# k spans one to five 16-slot column groups (bf16: 5 columns a group; fp32: 16).
+@pytest.mark.parametrize("k", [1, 4, 12, 16, 20, 24])
 def test_rows_match_oracle(lib, dtype, shape, k):
     from verification.verifier.matmul_check.freivalds import measure_batch_rows
     n, q, w = shape
