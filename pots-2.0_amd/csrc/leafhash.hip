@@ -13,18 +13,17 @@
 //
 // Message layout in HBM. The 0x00 prefix and the tensor header are 4(1 + ndim) bytes, a whole
 // number of words, so message word w of a leaf is payload word w - H/4 and no byte shifting is
-// needed. A lane reads each 64-byte block as 16-byte aligned loads and picks its 16 words out
-// of the 20-word window with a shift SH (0..3) that is fixed per leaf; SH is a template
-// parameter so the selection is register renaming. Blocks that touch the header, the end of
+// needed. A lane reads two 64-byte blocks at a time as 16-byte aligned loads and picks their
+// 32 words out of the 36-word window with a shift SH (0..3) that is fixed per leaf; SH is a
+// template parameter so the selection is register renaming. Blocks that touch the header, the end of
 // the payload or a partial word take an edge path that patches header words in from a small
 // table and masks bytes past the end. Leaves whose header length or payload address is not
 // word aligned (records, odd views, host memory) are staged: their whole message is copied to
 // an aligned device buffer first and hashed with an empty header.
 //
-// Finiteness. A value is NaN or Inf when its exponent field is all ones. Shifting a word left
-// by 1 (the high half of a 16-bit pair, or an fp32 value) or by 17 (the low half) puts that
-// field at the top, so a running unsigned max of the shifted payload words reaches
-// 0xFF000000 (fp32, bf16) or 0xF8000000 (fp16) exactly when a non-finite value was seen.
+// Finiteness. A value is NaN or Inf when its exponent field is all ones. Masking each payload
+// word to its exponent fields and keeping a running per-16-bit-half maximum (one and, one
+// packed max per word) reaches the all-ones pattern exactly when a non-finite value was seen.
 #include <stdlib.h>
 #include <string.h>
 
@@ -63,84 +62,109 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 
 
-__device__ __forceinline__ void finite_acc(uint32_t& acc, uint32_t w, bool halves) {
-  uint32_t hi = w << 1;
-  uint32_t lo = halves ? (w << 17) : 0u;
-  acc = max(acc, max(hi, lo));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// The NaN/Inf test: `mask` keeps each value's exponent field (fp32 0x7F800000, bf16
+// 0x7F807F80, fp16 0x7C007C00, none 0), and the running per-half maximum of the masked words
+// reaches the all-ones exponent (0x7F80 for fp32 and bf16, 0x7C00 for fp16) exactly when a
+// non-finite value was seen. Two VALU operations per word (and, packed 16-bit max).
+__device__ __forceinline__ void finite_acc(u16x2& acc, uint32_t w, uint32_t mask) {
+  acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, w & mask));
 }
 
+// Message block b of chunk c for the general case: blocks that touch the header, the end of
+// the payload or a partial word. Header words come from the head table; bytes past the end
+// are zero; only payload words feed the NaN/Inf test.
+template <int SH>
+__device__ __forceinline__ void edge_block(const LeafDesc& d, const uint32_t* __restrict__ head,
+                                           uint64_t o, uint32_t mask, uint32_t m[16],
+                                           u16x2& acc) {
+  const uint64_t H = d.head_len, L = H + d.len;
+  const uint64_t pbeg = d.payload, pend = d.payload + d.len;
+  const uint64_t A = d.payload + o - H;  // address of message byte o, in payload terms
+  const u32x4* A16 = reinterpret_cast<const u32x4*>(A & ~uint64_t(15));
+  uint32_t w[20];
+#pragma unroll
+  for (int u = 0; u < 5; u++) {
+    const uint64_t X = reinterpret_cast<uint64_t>(A16 + u);
+    u32x4 q = u32x4{0, 0, 0, 0};
+    if ((u < 4 || SH) && X + 16 > pbeg && X < pend) q = gload<u32x4>(A16 + u);
+    w[4 * u] = q.x;
+    w[4 * u + 1] = q.y;
+    w[4 * u + 2] = q.z;
+    w[4 * u + 3] = q.w;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const uint64_t at = o + 4u * j;  // message byte offset of this word
+    uint32_t mw = w[j + SH];
+    if (at < H) {
+      mw = gload<uint32_t>(head + d.head_word + (uint32_t)(at >> 2));
+    } else if (at >= L) {
+      mw = 0;
+    } else {
+      const uint64_t rem = L - at;
+      if (rem < 4) mw &= (1u << (8 * rem)) - 1u;
+      finite_acc(acc, mw, mask);
+    }
+    m[j] = mw;
+  }
+}
+
+// One lane's chunk c of leaf d: its chaining value (or the leaf digest when `root`). Blocks
+// go in pairs: a pair wholly inside the payload is read as one 144-byte aligned window (nine
+// 16-byte loads), so each 128-byte line a lane touches is used up by one group of loads
+// instead of being fetched again for the second half; other pairs take edge_block.
 template <int SH>
 __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __restrict__ head,
-                                           uint64_t c, bool root, uint32_t cv[8],
-                                           uint32_t& acc) {
+                                           uint64_t c, bool root, uint32_t mask, uint32_t cv[8],
+                                           u16x2& acc) {
   const uint64_t H = d.head_len;
   const uint64_t L = H + d.len;
   const uint64_t cstart = c * 1024u;
   const uint64_t cbytes = min<uint64_t>(1024u, L - cstart);
   uint32_t nb = (uint32_t)((cbytes + 63) / 64);
   if (nb == 0) nb = 1;  // the empty message: one empty block
-  const bool halves = d.kind == POTS_KIND_BF16 || d.kind == POTS_KIND_F16;
-  const bool test = d.kind != POTS_KIND_NONE;
-  const uint64_t pbeg = d.payload, pend = d.payload + d.len;
   b3_iv(cv);
-  for (uint32_t b = 0; b < nb; b++) {
+#pragma unroll 1
+  for (uint32_t b = 0; b < nb; b += 2) {
     const uint64_t o = cstart + 64u * b;
-    const uint64_t A = d.payload + o - H;  // address of message byte o, in payload terms
-    const u32x4* A16 = reinterpret_cast<const u32x4*>(A & ~uint64_t(15));
-    uint32_t m[16];
-    if (o >= H && o + 64 <= L) {
-      // Interior block: 16 payload words, the aligned window is in bounds (see header).
-      const u32x4* V16 = A16;
-      u32x4 q[5];
+    uint32_t m0[16], m1[16];
+    if (o >= H && o + 128 <= L) {
+      const u32x4* A16 =
+          reinterpret_cast<const u32x4*>((d.payload + o - H) & ~uint64_t(15));
+      u32x4 q[9];
 #pragma unroll
-      for (int u = 0; u < 4; u++) q[u] = gload<u32x4>(V16 + u);
-      q[4] = SH ? gload<u32x4>(V16 + 4) : u32x4{0, 0, 0, 0};
-      uint32_t w[20];
+      for (int u = 0; u < 8; u++) q[u] = gload<u32x4>(A16 + u);
+      q[8] = SH ? gload<u32x4>(A16 + 8) : u32x4{0, 0, 0, 0};
+      uint32_t w[36];
 #pragma unroll
-      for (int u = 0; u < 5; u++) {
+      for (int u = 0; u < 9; u++) {
         w[4 * u] = q[u].x;
         w[4 * u + 1] = q[u].y;
         w[4 * u + 2] = q[u].z;
         w[4 * u + 3] = q[u].w;
       }
 #pragma unroll
-      for (int j = 0; j < 16; j++) m[j] = w[j + SH];
-      if (test) {
-#pragma unroll
-        for (int j = 0; j < 16; j++) finite_acc(acc, m[j], halves);
-      }
-    } else {
-      uint32_t w[20];
-#pragma unroll
-      for (int u = 0; u < 5; u++) {
-        const uint64_t X = reinterpret_cast<uint64_t>(A16 + u);
-        u32x4 q = u32x4{0, 0, 0, 0};
-        if ((u < 4 || SH) && X + 16 > pbeg && X < pend) q = gload<u32x4>(A16 + u);
-        w[4 * u] = q.x;
-        w[4 * u + 1] = q.y;
-        w[4 * u + 2] = q.z;
-        w[4 * u + 3] = q.w;
-      }
-#pragma unroll
       for (int j = 0; j < 16; j++) {
-        const uint64_t at = o + 4u * j;  // message byte offset of this word
-        uint32_t mw = w[j + SH];
-        if (at < H) {
-          mw = gload<uint32_t>(head + d.head_word + (uint32_t)(at >> 2));
-        } else if (at >= L) {
-          mw = 0;
-        } else {
-          const uint64_t rem = L - at;
-          if (rem < 4) mw &= (1u << (8 * rem)) - 1u;
-          if (test) finite_acc(acc, mw, halves);
-        }
-        m[j] = mw;
+        m0[j] = w[j + SH];
+        m1[j] = w[16 + j + SH];
       }
+#pragma unroll
+      for (int j = 0; j < 32; j++) finite_acc(acc, w[j + SH], mask);
+    } else {
+      edge_block<SH>(d, head, o, mask, m0, acc);
+      if (b + 1 < nb) edge_block<SH>(d, head, o + 64, mask, m1, acc);
     }
-    const uint32_t blen = (uint32_t)min<uint64_t>(64u, L > o ? L - o : 0u);
-    uint32_t flags = (b == 0 ? B3_CHUNK_START : 0u);
-    if (b == nb - 1) flags |= B3_CHUNK_END | (root ? B3_ROOT : 0u);
-    b3_compress_cv(cv, m, c, blen, flags, cv);
+    const uint32_t blen0 = (uint32_t)min<uint64_t>(64u, L > o ? L - o : 0u);
+    uint32_t f0 = b == 0 ? B3_CHUNK_START : 0u;
+    if (b + 1 == nb) f0 |= B3_CHUNK_END | (root ? B3_ROOT : 0u);
+    b3_compress_cv(cv, m0, c, blen0, f0, cv);
+    if (b + 1 < nb) {
+      const uint32_t blen1 = (uint32_t)min<uint64_t>(64u, L - o - 64);
+      const uint32_t f1 = b + 2 == nb ? (B3_CHUNK_END | (root ? B3_ROOT : 0u)) : 0u;
+      b3_compress_cv(cv, m1, c, blen1, f1, cv);
+    }
   }
 }
 
@@ -162,18 +186,20 @@ __device__ __forceinline__ void chunk_one(
   const uint64_t c = g - chunk_first[i];
   const bool root = chunk_first[i + 1] - chunk_first[i] == 1;
   const uint32_t sh = (uint32_t)((d.payload - d.head_len) >> 2) & 3u;
+  const uint32_t mask = d.kind == POTS_KIND_F32    ? 0x7F800000u
+                        : d.kind == POTS_KIND_BF16 ? 0x7F807F80u
+                        : d.kind == POTS_KIND_F16  ? 0x7C007C00u
+                                                   : 0u;
   uint32_t cv[8];
-  uint32_t acc = 0;
+  u16x2 acc = {0, 0};
   switch (sh) {
-    case 0: hash_chunk<0>(d, head, c, root, cv, acc); break;
-    case 1: hash_chunk<1>(d, head, c, root, cv, acc); break;
-    case 2: hash_chunk<2>(d, head, c, root, cv, acc); break;
-    default: hash_chunk<3>(d, head, c, root, cv, acc); break;
+    case 0: hash_chunk<0>(d, head, c, root, mask, cv, acc); break;
+    case 1: hash_chunk<1>(d, head, c, root, mask, cv, acc); break;
+    case 2: hash_chunk<2>(d, head, c, root, mask, cv, acc); break;
+    default: hash_chunk<3>(d, head, c, root, mask, cv, acc); break;
   }
-  if (d.kind != POTS_KIND_NONE) {
-    const uint32_t thr = d.kind == POTS_KIND_F16 ? 0xF8000000u : 0xFF000000u;
-    if (acc >= thr) atomicMin(first_bad, i);
-  }
+  const unsigned short thr = d.kind == POTS_KIND_F16 ? 0x7C00 : 0x7F80;
+  if (mask != 0u && (acc.x >= thr || acc.y >= thr)) atomicMin(first_bad, i);
   u32x4* dst = reinterpret_cast<u32x4*>(root ? digests + 8ull * i : cv_out + 8ull * g);
   gstore<u32x4>(dst, u32x4{cv[0], cv[1], cv[2], cv[3]});
   gstore<u32x4>(dst + 1, u32x4{cv[4], cv[5], cv[6], cv[7]});
