@@ -464,6 +464,15 @@ __global__ __launch_bounds__(256) void reduce_b(const RedJob* __restrict__ jobs,
 }
 
 // ---- finish: one product's row ------------------------------------------------------------
+//
+// Three kernels. bias_terms: per biased product, ‖b‖₁, ‖b‖² and bᵀR_j. finish_slices: per
+// slice of at most kSliceRows rows of a product, the fp64 sums over its rows of ν_i², |P|1_i²,
+// ‖P_i‖², (A²(B²1))_i and d_ij², written as one record. finish_final: per product, the slices'
+// records added in slice order, then the square roots. Every sum has a fixed order, so the
+// row does not depend on timing; slicing keeps the largest products (150k rows) from running
+// on one block.
+
+constexpr uint32_t kSliceRows = 2048;
 
 struct FinJob {
   uint64_t a_dot, a_abs, a_sq;  // A-pass partials (rows n)
@@ -473,8 +482,20 @@ struct FinJob {
   uint32_t n, w;
   uint32_t a_rows_pad, a_chunks;
   uint32_t p_rows_pad, p_chunks;
+  uint32_t slice_first, n_slices;  // this product's slice records
 };
-static_assert(sizeof(FinJob) == 88, "FinJob layout");
+static_assert(sizeof(FinJob) == 96, "FinJob layout");
+
+struct SliceJob {
+  uint32_t prod, r0, r1, pad;
+};
+static_assert(sizeof(SliceJob) == 16, "SliceJob layout");
+
+// Per product: ‖b‖₁ (fp32, as the reference adds it to each ν_i), ‖b‖² and bᵀR_j (fp32).
+struct BiasOut {
+  uint64_t babs;  // float bits in the low word
+  double bsq;
+};
 
 __device__ __forceinline__ double block_sum(double v, double* sh) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -484,31 +505,56 @@ __device__ __forceinline__ double block_sum(double v, double* sh) {
   __syncthreads();
   double t = 0.0;
   for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += sh[i];
+  __syncthreads();
   return t;
 }
 
-__global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jobs, uint32_t k,
-                                                   uint32_t guard, double* __restrict__ rows) {
+// One block per biased product (index list `which`).
+__global__ __launch_bounds__(256) void bias_terms(const FinJob* __restrict__ jobs,
+                                                  const uint32_t* __restrict__ which, uint32_t k,
+                                                  BiasOut* __restrict__ bout,
+                                                  float* __restrict__ br) {
   __shared__ double sh[4];
-  __shared__ float bias_r[16];
-  __shared__ float bias_abs;
-  const FinJob J = jobs[blockIdx.x];
-  const uint32_t tid = threadIdx.x;
-  double* out = rows + (uint64_t)blockIdx.x * (5 + k);
+  const uint32_t pi = which[blockIdx.x];
+  const FinJob J = jobs[pi];
   const float* bias = reinterpret_cast<const float*>(J.bias);
   const float* R = reinterpret_cast<const float*>(J.r);
-  double bsq = 0.0, babs_d = 0.0;
-  if (bias) {
-    double a = 0.0, q = 0.0;
-    for (uint32_t c = tid; c < J.w; c += blockDim.x) {
-      const double b = gload<float>(bias + c);
-      a += fabs(b);
-      q += b * b;
-    }
-    babs_d = block_sum(a, sh);
-    bsq = block_sum(q, sh);
+  double a = 0.0, q = 0.0;
+  for (uint32_t c = threadIdx.x; c < J.w; c += blockDim.x) {
+    const double b = gload<float>(bias + c);
+    a += fabs(b);
+    q += b * b;
   }
-  if (tid == 0) bias_abs = (float)babs_d;
+  a = block_sum(a, sh);
+  q = block_sum(q, sh);
+  if (threadIdx.x == 0) {
+    BiasOut o;
+    o.babs = __float_as_uint((float)a);
+    o.bsq = q;
+    bout[pi] = o;
+  }
+  for (uint32_t j = 0; j < k; j++) {
+    double t = 0.0;
+    for (uint32_t c = threadIdx.x; c < J.w; c += blockDim.x)
+      t += (double)gload<float>(bias + c) * (double)gload<float>(R + (uint64_t)c * k + j);
+    t = block_sum(t, sh);
+    if (threadIdx.x == 0) br[(uint64_t)pi * k + j] = (float)t;
+  }
+}
+
+// One block per slice. Record layout: [Σν², Σ|P|1², Σ‖P_i‖², Σ(A²(B²1))_i, Σd_1², ..., Σd_k²].
+__global__ __launch_bounds__(256) void finish_slices(const FinJob* __restrict__ jobs,
+                                                     const SliceJob* __restrict__ slices,
+                                                     uint32_t k, const BiasOut* __restrict__ bout,
+                                                     const float* __restrict__ br,
+                                                     double* __restrict__ recs) {
+  __shared__ double sh[4];
+  const SliceJob S = slices[blockIdx.x];
+  const FinJob J = jobs[S.prod];
+  const uint32_t tid = threadIdx.x;
+  double* out = recs + (uint64_t)blockIdx.x * (4 + k);
+  const bool biased = J.bias != 0;
+  const float babs = biased ? __uint_as_float((uint32_t)bout[S.prod].babs) : 0.f;
   const float* adot = reinterpret_cast<const float*>(J.a_dot);
   const float* aabs = reinterpret_cast<const float*>(J.a_abs);
   const double* asq = reinterpret_cast<const double*>(J.a_sq);
@@ -516,13 +562,10 @@ __global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jo
   const float* pabs = reinterpret_cast<const float*>(J.p_abs);
   const double* psq = reinterpret_cast<const double*>(J.p_sq);
 
-  // Row sums (ν, ‖|P|1‖, ‖P‖_F, U²) once, then the residuals 16 columns at a time. A row's
-  // chunk partials are summed in fp64 in chunk order, then rounded to fp32 where the
-  // reference's matmul output is fp32.
+  // A row's chunk partials are summed in fp64 in chunk order, then rounded to fp32 where the
+  // reference's matvec output is fp32.
   double s_nu = 0.0, s_p1 = 0.0, s_psq = 0.0, s_t2 = 0.0;
-  __syncthreads();
-  const float babs = bias_abs;
-  for (uint32_t r = tid; r < J.n; r += blockDim.x) {
+  for (uint32_t r = S.r0 + tid; r < S.r1; r += blockDim.x) {
     double nu = 0.0, t2 = 0.0, p1 = 0.0, pq = 0.0;
     for (uint32_t c = 0; c < J.a_chunks; c++) {
       nu += (double)gload<float>(aabs + (uint64_t)c * J.a_rows_pad + r);
@@ -533,7 +576,7 @@ __global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jo
       pq += gload<double>(psq + (uint64_t)c * J.p_rows_pad + r);
     }
     float nuf = (float)nu;
-    if (bias) nuf = nuf + babs;
+    if (biased) nuf = nuf + babs;
     const float p1f = (float)p1;
     s_nu += (double)nuf * (double)nuf;
     s_p1 += (double)p1f * (double)p1f;
@@ -545,49 +588,42 @@ __global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jo
   s_psq = block_sum(s_psq, sh);
   s_t2 = block_sum(s_t2, sh);
   if (tid == 0) {
-    const double nan = __builtin_nan("");
-    out[0] = guard ? sqrt(s_nu) : nan;
-    out[1] = guard ? sqrt(s_p1) : nan;
-    out[2] = sqrt(s_psq);
+    out[0] = s_nu;
+    out[1] = s_p1;
+    out[2] = s_psq;
     out[3] = s_t2;
-    out[4] = bsq;
   }
-  for (uint32_t j0 = 0; j0 < k; j0 += 16) {
-    const uint32_t nj = min(16u, k - j0);
-    if (bias) {  // bᵀ·R_j for this column group
-      for (uint32_t jj = 0; jj < nj; jj++) {
-        double a = 0.0;
-        for (uint32_t c = tid; c < J.w; c += blockDim.x)
-          a += (double)gload<float>(bias + c) * (double)gload<float>(R + (uint64_t)c * k + j0 + jj);
-        a = block_sum(a, sh);
-        if (tid == 0) bias_r[jj] = (float)a;
-      }
-    }
-    __syncthreads();
-    double sd[16];
+  // Residuals d_ij = A(Br_j)_i (+ bᵀr_j) − (Pr_j)_i in fp32, 8 columns at a time.
+  for (uint32_t j0 = 0; j0 < k; j0 += 8) {
+    const uint32_t nj = min(8u, k - j0);
+    float bj[8];
 #pragma unroll
-    for (int jj = 0; jj < 16; jj++) sd[jj] = 0.0;
-    for (uint32_t r = tid; r < J.n; r += blockDim.x) {
-      double ab[16], pr[16];
+    for (int jj = 0; jj < 8; jj++)
+      bj[jj] = (biased && (uint32_t)jj < nj) ? br[(uint64_t)S.prod * k + j0 + jj] : 0.f;
+    double sd[8];
 #pragma unroll
-      for (int jj = 0; jj < 16; jj++) ab[jj] = pr[jj] = 0.0;
+    for (int jj = 0; jj < 8; jj++) sd[jj] = 0.0;
+    for (uint32_t r = S.r0 + tid; r < S.r1; r += blockDim.x) {
+      double ab[8], pr[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++) ab[jj] = pr[jj] = 0.0;
       for (uint32_t c = 0; c < J.a_chunks; c++) {
         const float* src = adot + ((uint64_t)c * J.a_rows_pad + r) * k + j0;
 #pragma unroll
-        for (int jj = 0; jj < 16; jj++)
+        for (int jj = 0; jj < 8; jj++)
           if ((uint32_t)jj < nj) ab[jj] += (double)gload<float>(src + jj);
       }
       for (uint32_t c = 0; c < J.p_chunks; c++) {
         const float* src = pdot + ((uint64_t)c * J.p_rows_pad + r) * k + j0;
 #pragma unroll
-        for (int jj = 0; jj < 16; jj++)
+        for (int jj = 0; jj < 8; jj++)
           if ((uint32_t)jj < nj) pr[jj] += (double)gload<float>(src + jj);
       }
 #pragma unroll
-      for (int jj = 0; jj < 16; jj++) {
+      for (int jj = 0; jj < 8; jj++) {
         if ((uint32_t)jj < nj) {
           float abf = (float)ab[jj];
-          if (bias) abf = abf + bias_r[jj];
+          if (biased) abf = abf + bj[jj];
           const float d = abf - (float)pr[jj];
           sd[jj] += (double)d * (double)d;
         }
@@ -595,10 +631,32 @@ __global__ __launch_bounds__(256) void finish_rows(const FinJob* __restrict__ jo
     }
     for (uint32_t jj = 0; jj < nj; jj++) {
       const double t = block_sum(sd[jj], sh);
-      if (tid == 0) out[5 + j0 + jj] = sqrt(t);
+      if (tid == 0) out[4 + j0 + jj] = t;
     }
-    __syncthreads();
   }
+}
+
+// One thread per product: the slices' records in order, then the row.
+__global__ __launch_bounds__(256) void finish_final(const FinJob* __restrict__ jobs,
+                                                    uint32_t n, uint32_t k, uint32_t guard,
+                                                    const BiasOut* __restrict__ bout,
+                                                    const double* __restrict__ recs,
+                                                    double* __restrict__ rows) {
+  const uint32_t pi = blockIdx.x * blockDim.x + threadIdx.x;
+  if (pi >= n) return;
+  const FinJob J = jobs[pi];
+  double* out = rows + (uint64_t)pi * (5 + k);
+  const double nan = __builtin_nan("");
+  for (uint32_t col = 0; col < 4 + k; col++) {
+    double t = 0.0;
+    for (uint32_t sl = 0; sl < J.n_slices; sl++)
+      t += recs[(uint64_t)(J.slice_first + sl) * (4 + k) + col];
+    if (col < 2) out[col] = guard ? sqrt(t) : nan;
+    else if (col == 2) out[2] = sqrt(t);
+    else if (col == 3) out[3] = t;
+    else out[1 + col] = sqrt(t);
+  }
+  out[4] = J.bias != 0 ? bout[pi].bsq : 0.0;
 }
 
 // ---- the plan ---------------------------------------------------------------------------
@@ -630,6 +688,13 @@ struct FvPlan {
   uint32_t n_red = 0;
   uint64_t n_red_threads = 0;
   FinJob* d_fin = nullptr;
+  SliceJob* d_slices = nullptr;
+  uint32_t n_slices = 0;
+  uint32_t* d_biased = nullptr;  // indices of the products with a bias
+  uint32_t n_biased = 0;
+  BiasOut* d_bout = nullptr;
+  float* d_br = nullptr;      // bᵀR_j per product, [n][k]
+  double* d_recs = nullptr;   // slice records, [n_slices][4 + k]
   std::vector<PassLaunch> pass_b, pass_ap;  // B pass; then A and P passes
   bool need_b3 = false, need_f4 = false;
   uint64_t bytes = 0;  // algorithmic bytes: A, B, P read once
@@ -864,6 +929,21 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   const size_t o_blk = place(blk_table.size() * 4);
   const size_t o_red = place(n * sizeof(RedJob));
   const size_t o_fin = place(n * sizeof(FinJob));
+  // Finish: row slices of every product, the biased products, their bias terms, and one
+  // record of 4 + k sums per slice.
+  std::vector<SliceJob> slices;
+  std::vector<uint32_t> slice_first(n), biased;
+  for (size_t i = 0; i < n; i++) {
+    slice_first[i] = (uint32_t)slices.size();
+    for (uint32_t r0 = 0; r0 < prods[i].n; r0 += kSliceRows)
+      slices.push_back(SliceJob{(uint32_t)i, r0, std::min(prods[i].n, r0 + kSliceRows), 0});
+    if (prods[i].bias) biased.push_back((uint32_t)i);
+  }
+  const size_t o_slices = place(slices.size() * sizeof(SliceJob));
+  const size_t o_biased = place(biased.size() * 4);
+  const size_t o_bout = place(n * sizeof(BiasOut));
+  const size_t o_bias_r = place(n * k * 4);
+  const size_t o_recs = place(slices.size() * (4 + k) * 8);
   P->total = at;
 
   hipError_t e = hipMalloc(reinterpret_cast<void**>(&P->base), P->total);
@@ -892,6 +972,13 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   P->d_blk = reinterpret_cast<uint32_t*>(P->base + o_blk);
   P->d_red = reinterpret_cast<RedJob*>(P->base + o_red);
   P->d_fin = reinterpret_cast<FinJob*>(P->base + o_fin);
+  P->d_slices = reinterpret_cast<SliceJob*>(P->base + o_slices);
+  P->n_slices = (uint32_t)slices.size();
+  P->d_biased = reinterpret_cast<uint32_t*>(P->base + o_biased);
+  P->n_biased = (uint32_t)biased.size();
+  P->d_bout = reinterpret_cast<BiasOut*>(P->base + o_bout);
+  P->d_br = reinterpret_cast<float*>(P->base + o_bias_r);
+  P->d_recs = reinterpret_cast<double*>(P->base + o_recs);
 
   // Fill the job pointers now that addresses are known.
   for (size_t oi = 0; oi < ordered.size(); oi++) {
@@ -956,6 +1043,8 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     F.a_chunks = A.n_chunks;
     F.p_rows_pad = Pp.rows_pad;
     F.p_chunks = Pp.n_chunks;
+    F.slice_first = slice_first[i];
+    F.n_slices = (uint32_t)((prods[i].n + kSliceRows - 1) / kSliceRows);
   }
   // Upload the tables.
   auto up = [&](size_t off, const void* src, size_t bytes) -> int {
@@ -969,7 +1058,9 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
       (rc = up(o_jobs, ordered.data(), ordered.size() * sizeof(PassJob))) ||
       (rc = up(o_blk, blk_table.data(), blk_table.size() * 4)) ||
       (rc = up(o_red, red.data(), n * sizeof(RedJob))) ||
-      (rc = up(o_fin, fin.data(), n * sizeof(FinJob)))) {
+      (rc = up(o_fin, fin.data(), n * sizeof(FinJob))) ||
+      (rc = up(o_slices, slices.data(), slices.size() * sizeof(SliceJob))) ||
+      (rc = up(o_biased, biased.data(), biased.size() * 4))) {
     (void)hipFree(P->base);
     delete P;
     return rc;
@@ -1051,8 +1142,17 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
           return rc;
       return POTS_E_OK;
     case 5:
-      hipLaunchKernelGGL(finish_rows, dim3((uint32_t)P->n), dim3(256), 0, s, P->d_fin, P->k,
-                         P->guard, d_rows);
+      if (P->n_biased) {
+        hipLaunchKernelGGL(bias_terms, dim3(P->n_biased), dim3(256), 0, s, P->d_fin,
+                           P->d_biased, P->k, P->d_bout, P->d_br);
+        POTS_HIP(hipGetLastError());
+      }
+      hipLaunchKernelGGL(finish_slices, dim3(P->n_slices), dim3(256), 0, s, P->d_fin,
+                         P->d_slices, P->k, P->d_bout, P->d_br, P->d_recs);
+      POTS_HIP(hipGetLastError());
+      hipLaunchKernelGGL(finish_final, dim3((uint32_t)((P->n + 255) / 256)), dim3(256), 0, s,
+                         P->d_fin, (uint32_t)P->n, P->k, P->guard, P->d_bout, P->d_recs,
+                         d_rows);
       POTS_HIP(hipGetLastError());
       return POTS_E_OK;
     default:
