@@ -123,6 +123,29 @@ class DeclaredComputation(abc.ABC):
     def operand_dtype(self) -> torch.dtype:
         return self.product_dtype
 
+    @property
+    def accumulator_dtype(self) -> torch.dtype:
+        """The matmuls accumulate in fp32 (reference interface.py:269)."""
+        return torch.float32
+
+    def replay(self, leaves: Any) -> Replay:
+        """Check 5's operands for the committed ``leaves`` (reference interface.py:380).
+
+        Rebuilding ``A_m, B_m`` by replaying the model from the committed leaves is not part of
+        this build: a computation serves operands it was given with :meth:`use_operands` (the
+        exact operands the prover used, as a capture records them), or a subclass overrides
+        this method."""
+        r = getattr(self, "_operands", None)
+        if r is None:
+            raise NotImplementedError(
+                f"{type(self).__name__} has no operand source: the model replay is not part "
+                f"of this build; give the captured operands with use_operands()")
+        return r
+
+    def use_operands(self, replay: Replay | None) -> None:
+        """Serve ``replay``'s operands to check 5 (``None`` removes them)."""
+        self._operands = replay
+
     def encode_record(self, record: Any) -> bytes:
         from setup.records import encode_record
         return encode_record(record)

@@ -20,7 +20,7 @@ from dataclasses import dataclass, field
 import torch
 
 from setup.records import Record
-from verification.computation.interface import DeclaredComputation, ProductSpec
+from verification.computation.interface import DeclaredComputation, ProductSpec, Replay
 
 
 @dataclass
@@ -34,6 +34,23 @@ class SyntheticStep:
 
     def w_t(self, name: str) -> torch.Tensor:
         return self.leaves[self.c.w_t_index(name)]
+
+    def replay(self) -> CapturedReplay:
+        """The captured operands as check 5's operand source."""
+        return CapturedReplay(self.operands)
+
+
+class CapturedReplay(Replay):
+    """Check 5's operands as the prover used them: ``operands[m] = (A_m, B_m)``."""
+
+    def __init__(self, operands: dict[int, tuple[torch.Tensor, torch.Tensor]]) -> None:
+        self._ops = operands
+
+    def operands(self, m: int) -> tuple[torch.Tensor, torch.Tensor]:
+        try:
+            return self._ops[m]
+        except KeyError:
+            raise IndexError(f"no captured operands for product m={m}") from None
 
 
 def _runs(c: DeclaredComputation) -> list[list[ProductSpec]]:

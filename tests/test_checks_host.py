@@ -1,0 +1,145 @@
+"""Host-side logic of the check layer: rejections, the error guard, committed leaves, the
+in-memory store and check 5's judging messages (no GPU needed).
+
+The judging tests feed hand-made ProductMeasure values to the judge and compare its
+Rejection with the reference's rules and detail strings
+(verification/verifier/checks.py:926-956).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from verification.computation.interface import ProductKind, ProductSpec
+from verification.transcript.errors import LeafShapeError, StoreMutationError
+from verification.transcript.store import InMemoryStore
+from verification.verifier.bands import Bands
+from verification.verifier.checks import DEFAULT_ORDER, _judge_product, protocol_id
+from verification.verifier.context import (CommittedLeaves, Rejection, StepContext, _checked,
+                                           _guard, _is_digest)
+from verification.verifier.matmul_check.freivalds import ProductMeasure, finish_row
+
+
+class _C:
+    """Enough of a computation for the judge: its product classes."""
+
+    def product_class(self, spec):
+        return f"{spec.kind.value}:{spec.name}"
+
+
+SPEC = ProductSpec(m=7, name="Y_q[0]", kind=ProductKind.FORWARD, a_shape=(4, 8), b_shape=(8, 3))
+
+
+def _ctx(**kw):
+    base = dict(step=3, indices=(), h_D=b"", n_records=0, prev_w_hashes=(), chain_check_id="7",
+                k=2, eps_in=2.0**-8, eps_acc=2.0**-24, eps_w=2.0**-24)
+    base.update(kw)
+    return StepContext(**base)
+
+
+def _mp(nu=1.0, p_abs1=1.0, res=(0.0, 0.0), p_norm=1.0, unit=1e-3, u=1.0):
+    kappa = nu / p_abs1 if p_abs1 > 0 else (1.0 if nu == 0 else math.inf)
+    normalized = tuple(x / unit for x in res)
+    return ProductMeasure(nu, p_abs1, kappa, tuple(res), p_norm, unit, normalized, u)
+
+
+def test_slot_order_and_ids():
+    assert DEFAULT_ORDER == ("2", "5", "2.root")
+    assert protocol_id("2.root") == "2" and protocol_id("5") == "5"
+
+
+def test_guard_maps_prover_errors_to_malformed():
+    ctx = _ctx()
+
+    @_checked
+    def check():
+        with _guard(ctx, "2"):
+            raise LeafShapeError("leaf 4 W_t[x]: shape (2, 2), declared (2, 3)")
+
+    rej = check()
+    assert rej == Rejection(3, "2", "malformed prover data: LeafShapeError: leaf 4 W_t[x]: "
+                                    "shape (2, 2), declared (2, 3)", "malformed")
+
+    @_checked
+    def bug():
+        with _guard(ctx, "2"):
+            raise RuntimeError("a verifier bug propagates")
+
+    with pytest.raises(RuntimeError):
+        bug()
+
+
+def test_committed_leaves_detect_in_place_writes():
+    leaves = CommittedLeaves()
+    t = torch.zeros(3)
+    leaves.add(t)
+    assert leaves.leaf(0) is t and not leaves.changed(0)
+    t.add_(1)
+    assert leaves.changed(0)
+    with pytest.raises(StoreMutationError):
+        leaves.leaf(0)
+    with pytest.raises(RuntimeError):
+        leaves.leaf(5)
+
+
+def test_in_memory_store_versions_and_root():
+    t = torch.ones(4)
+    s = InMemoryStore([t], claimed_root=b"\x01" * 32)
+    assert s.root == b"\x01" * 32 and s.leaf(0) is t
+    t.mul_(2)
+    with pytest.raises(StoreMutationError):
+        s.leaf(0)
+    with pytest.raises(IndexError):
+        s.leaf(1)
+    with pytest.raises(LookupError):
+        s.path(0)
+    assert _is_digest(b"\0" * 32) and not _is_digest(b"\0" * 31) and not _is_digest("x" * 32)
+
+
+def test_judge_accepts_and_records():
+    ctx = _ctx()
+    assert _judge_product(_C(), SPEC, _mp(res=(1e-3, 2e-3)), ctx, Bands.provisional()) is None
+    (st,) = ctx.stats.products
+    assert (st.m, st.name, st.cls, st.kappa, st.normalized) == \
+        (7, "Y_q[0]", "forward:Y_q[0]", 1.0, (1.0, 2.0))
+
+
+def test_judge_residual_message():
+    ctx = _ctx()
+    rej = _judge_product(_C(), SPEC, _mp(res=(1e-3, 9e-3)), ctx, Bands.provisional())
+    assert rej == Rejection(3, "5", "P_7 (Y_q[0]), challenge j=2: normalized residual 9 > τ = 8")
+
+
+def test_judge_cancellation_message():
+    ctx = _ctx()
+    bands = Bands(tau=8.0, kappa_max=10.0)
+    rej = _judge_product(_C(), SPEC, _mp(nu=50.0, p_abs1=2.0), ctx, bands)
+    assert rej == Rejection(3, "5", "P_7 (Y_q[0]): cancellation factor κ = 25 > κ_max = 10 "
+                                    "[forward:Y_q[0]]")
+    # with the guard off, test 1 is skipped and ν, ‖|P|·1‖ may be NaN
+    ctx = _ctx(kappa_guard=False)
+    assert _judge_product(_C(), SPEC, _mp(nu=math.nan, p_abs1=math.nan), ctx, bands) is None
+
+
+def test_judge_non_finite_message_lists_every_bad_value():
+    ctx = _ctx()
+    rej = _judge_product(_C(), SPEC, _mp(nu=math.inf, res=(math.nan, 0.0)), ctx,
+                         Bands.provisional())
+    assert rej == Rejection(3, "5", "P_7 (Y_q[0]): non-finite ν, residual j=1")
+    # calibration mode records and never judges, but non-finite still rejects
+    ctx = _ctx(judge=False)
+    assert _judge_product(_C(), SPEC, _mp(res=(1.0, 1.0)), ctx, Bands.provisional()) is None
+    assert _judge_product(_C(), SPEC, _mp(u=math.nan), ctx, Bands.provisional()) is not None
+
+
+def test_nan_never_passes_a_band():
+    """A NaN residual that is not caught as non-finite would pass ``x > bound``; the judge
+    writes every comparison as ``not (x <= bound)``."""
+    ctx = _ctx()
+    mp = finish_row([1.0, 1.0, 1.0, 1.0, 0.0, 0.0, 1e30], q=8, n=4, eps_in=2.0**-8,
+                    eps_acc=2.0**-24)
+    rej = _judge_product(_C(), SPEC, mp, ctx, Bands.provisional())
+    assert rej is not None and rej.check_id == "5" and "challenge j=2" in rej.detail
