@@ -71,48 +71,116 @@ def product_inputs(step):
     return out
 
 
-def cpu_baseline(step, items, budget_s: float = 20.0) -> dict:
-    """The CPU oracle on a bounded sample of the same transcript, on the host's cores:
-    leaf hashing with the pthread restatement of the reference's native.c, and the
-    reference's Freivalds formulas (torch-CPU fp32) on products of layer 1."""
+def cpu_baseline(step, items, fv_budget_s: float = 3.0, runs: int = 3) -> dict:
+    """The CPU oracle on a bounded sample of the same transcript, on the host's cores, each
+    part timed as the median of ``runs`` runs after a warm-up: leaf hashing with the pthread
+    restatement of the reference's native.c, and the reference's Freivalds formulas
+    (torch-CPU fp32, challenges included) on products spread over the inventory."""
+    import statistics
+
     import torch
 
     import oracle as O
     c = step.c
     threads = cores()
     torch.set_num_threads(threads)
-    # hashing sample: product leaves until ~1.5 GB
+    # hashing sample: product leaves spread over the step, about 1 GB
     hs, hbytes = [], 0
-    for i in range(c.n_s + c.n_w, c.n_s + c.n_w + c.M):
+    prod = list(range(c.n_s + c.n_w, c.n_s + c.n_w + c.M))
+    for i in prod[::7]:
         t = step.leaves[i].cpu()
         hs.append((O.tensor_leaf_header(O.TAG_PRODUCT, t), t, O.FINITE_KIND[t.dtype]))
         hbytes += 1 + len(hs[-1][0]) + t.nbytes
-        if hbytes > 1.5e9:
+        if hbytes > 1e9:
             break
-    O.hash_leaves(hs[:2], threads)
-    t0 = time.perf_counter()
-    O.hash_leaves(hs, threads)
-    t_hash = time.perf_counter() - t0
-    # Freivalds sample: the first products in canonical order, until ~budget/2 seconds
-    fbytes, t_fv, nprod = 0, 0.0, 0
-    key = bytes(range(32))
-    for a, b, p, bias, m in items:
-        if t_fv > budget_s / 2:
-            break
-        a_c, b_c, p_c = a.cpu(), b.cpu(), p.cpu()
+    O.hash_leaves(hs[:4], threads)
+    t_hash = []
+    for _ in range(runs):
         t0 = time.perf_counter()
-        r = O.challenge_matrices(key, [m], step.k, p_c.shape[1], threads)[0]
-        O.measure_product_row(a_c, b_c, p_c, r, None if bias is None else bias.cpu())
-        t_fv += time.perf_counter() - t0
-        fbytes += a_c.nbytes + b_c.nbytes + p_c.nbytes
-        nprod += 1
-    value = (hbytes + fbytes) / (t_hash + t_fv) / 1e9
+        O.hash_leaves(hs, threads)
+        t_hash.append(time.perf_counter() - t0)
+    # Freivalds sample: every 11th product in canonical order, until about fv_budget_s
+    key = bytes(range(32))
+    sample, spent = [], 0.0
+    for it in items[::11]:
+        a, b, p, bias, m = it
+        cpu = (a.cpu(), b.cpu(), p.cpu(), None if bias is None else bias.cpu(), m)
+        t0 = time.perf_counter()
+        r = O.challenge_matrices(key, [m], step.k, cpu[2].shape[1], threads)[0]
+        O.measure_product_row(cpu[0], cpu[1], cpu[2], r, cpu[3])
+        spent += time.perf_counter() - t0
+        sample.append(cpu)
+        if spent > fv_budget_s:
+            break
+    fbytes = sum(x[0].nbytes + x[1].nbytes + x[2].nbytes for x in sample)
+    t_fv = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        for a, b, p, bias, m in sample:
+            r = O.challenge_matrices(key, [m], step.k, p.shape[1], threads)[0]
+            O.measure_product_row(a, b, p, r, bias)
+        t_fv.append(time.perf_counter() - t0)
+    th, tf = statistics.median(t_hash), statistics.median(t_fv)
+    value = (hbytes + fbytes) / (th + tf) / 1e9
     return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"hash {len(hs)} product leaves ({hbytes / 1e9:.2f} GB, "
-                      f"{hbytes / t_hash / 1e9:.2f} GB/s, portable scalar BLAKE3 on {threads} "
-                      f"pthreads) + Freivalds rows of the first {nprod} products "
-                      f"({fbytes / 1e9:.2f} GB, {fbytes / t_fv / 1e9:.3f} GB/s, torch-CPU "
-                      f"fp32 with {threads} threads, challenges included), one run each"}
+            "sample": f"median of {runs} runs after a warm-up: hashing {len(hs)} product leaves "
+                      f"(every 7th, {hbytes / 1e9:.2f} GB, {hbytes / th / 1e9:.2f} GB/s, "
+                      f"portable scalar BLAKE3 on {threads} pthreads) + Freivalds rows of "
+                      f"{len(sample)} products (every 11th, {fbytes / 1e9:.2f} GB, "
+                      f"{fbytes / tf / 1e9:.3f} GB/s, torch-CPU fp32 with {threads} threads, "
+                      f"challenges included)"}
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "chunk_kernel_c4_traffic.md"
+
+
+def counter_summary(d: Path, copy_mib: int) -> int:
+    """Mean FETCH_SIZE / WRITE_SIZE (KiB) per dispatch of each kernel in a rocprofv3 --pmc
+    CSV run, and the chunk kernel's HBM bytes per launch scaled by the same counter's reading
+    for the calibration copy (two copies of ``copy_mib`` MiB, read and written once each)."""
+    import collections
+    import csv
+    sums: dict = collections.defaultdict(float)
+    disp: dict = collections.defaultdict(set)
+    for f in d.rglob("*counter_collection.csv"):
+        for r in csv.DictReader(f.open()):
+            key = (r["Kernel_Name"].split("(")[0], r["Counter_Name"])
+            sums[key] += float(r["Counter_Value"])
+            disp[key].add(r["Dispatch_Id"])
+    if not sums:
+        print(f"no counter_collection.csv under {d}", file=sys.stderr)
+        return 1
+    print("| kernel | counter | dispatches | mean KiB per dispatch | total KiB |")
+    print("|---|---|---|---|---|")
+    for (k, cn), v in sorted(sums.items()):
+        print(f"| `{k}` | {cn} | {len(disp[(k, cn)])} | {v / len(disp[(k, cn)]):.1f} | {v:.1f} |")
+    if copy_mib:
+        for cn in sorted({cn for _, cn in sums}):
+            copy_kib = sum(v for (k, c2), v in sums.items() if c2 == cn and "copyBuffer" in k)
+            chunk = [(v, len(disp[(k, c2)])) for (k, c2), v in sums.items()
+                     if c2 == cn and k.endswith("chunk_kernel")]
+            if not copy_kib or not chunk:
+                continue
+            factor = 2 * copy_mib * 1024 / copy_kib  # true KiB per reported KiB
+            v, n = chunk[0]
+            print(f"\n{cn}: calibration copy reports {copy_kib:.0f} KiB for "
+                  f"{2 * copy_mib * 1024} KiB moved, factor {factor:.3f}; chunk_kernel "
+                  f"{v / n * factor * 1024 / 1e9:.3f} GB per launch")
+    return 0
+
+
+def traffic_from_profile(kernel: str) -> int | None:
+    """HBM bytes per launch of ``kernel`` from the committed counter summary (the fenced
+    JSON block of TRAFFIC_FILE), or None when it holds no figure for that kernel."""
+    try:
+        text = TRAFFIC_FILE.read_text()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        d = json.loads(block)
+    except (OSError, IndexError, ValueError):
+        return None
+    if d.get("kernel") != kernel:
+        return None
+    return int(d["fetch_bytes_per_launch"]) + int(d["write_bytes_per_launch"])
 
 
 def main() -> int:
@@ -122,7 +190,14 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="copy this many MiB device to device twice before timing, so a "
+                         "counter run sees a plain copy kernel of known size")
+    ap.add_argument("--counter-summary", metavar="DIR",
+                    help="summarise rocprofv3 --pmc CSV output under DIR and exit")
     args = ap.parse_args()
+    if args.counter_summary:
+        return counter_summary(Path(args.counter_summary), args.calibration_copy_mib)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               "sharding is a design in DESIGN.md, not a measured path.", file=sys.stderr)
@@ -145,6 +220,14 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"[bench] transcript built in {time.perf_counter() - t0:.1f} s, "
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB resident")
+
+    if args.calibration_copy_mib:
+        src = torch.ones(args.calibration_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     stream = torch.cuda.current_stream()
     items = product_inputs(step)
@@ -263,7 +346,8 @@ def main() -> int:
                   "rejected": n_rej},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": dom_name,
+                     "traffic": traffic_from_profile(dom_name) if dom == "hash.chunks" else None,
+                     "kernel": dom_name,
                      "algorithmic_bytes": dom_bytes, "launch_ms": round(stage_ms[dom], 4)},
     }
     if not args.no_cpu_baseline:

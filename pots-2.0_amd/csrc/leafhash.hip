@@ -126,6 +126,11 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
   uint32_t nb = (uint32_t)((cbytes + 63) / 64);
   if (nb == 0) nb = 1;  // the empty message: one empty block
   b3_iv(cv);
+  // With SH != 0 a pair's window starts with the last 16 bytes of the previous pair's line;
+  // they are carried over in registers rather than loaded again (a second load of a line
+  // already streamed past is often an HBM refetch).
+  u32x4 carry = u32x4{0, 0, 0, 0};
+  bool have_carry = false;
 #pragma unroll 1
   for (uint32_t b = 0; b < nb; b += 2) {
     const uint64_t o = cstart + 64u * b;
@@ -134,9 +139,18 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
       const u32x4* A16 =
           reinterpret_cast<const u32x4*>((d.payload + o - H) & ~uint64_t(15));
       u32x4 q[9];
+      if (SH) {
+        if (have_carry) q[0] = carry;
+        else q[0] = gload<u32x4>(A16);
 #pragma unroll
-      for (int u = 0; u < 8; u++) q[u] = gload<u32x4>(A16 + u);
-      q[8] = SH ? gload<u32x4>(A16 + 8) : u32x4{0, 0, 0, 0};
+        for (int u = 1; u < 9; u++) q[u] = gload<u32x4>(A16 + u);
+        carry = q[8];
+        have_carry = true;
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; u++) q[u] = gload<u32x4>(A16 + u);
+        q[8] = u32x4{0, 0, 0, 0};
+      }
       uint32_t w[36];
 #pragma unroll
       for (int u = 0; u < 9; u++) {
@@ -155,6 +169,7 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
     } else {
       edge_block<SH>(d, head, o, mask, m0, acc);
       if (b + 1 < nb) edge_block<SH>(d, head, o + 64, mask, m1, acc);
+      have_carry = false;
     }
     const uint32_t blen0 = (uint32_t)min<uint64_t>(64u, L > o ? L - o : 0u);
     uint32_t f0 = b == 0 ? B3_CHUNK_START : 0u;
