@@ -112,3 +112,30 @@ def synthetic_step(c: DeclaredComputation, *, seed: int = 0, device: str = "cuda
         w = w_t[name]
         leaves.append(w - eta * torch.randn(w.shape, generator=g, device=dev))
     return SyntheticStep(c, leaves, ops)
+
+
+@torch.no_grad()
+def perturb_products(step: SyntheticStep, fraction: float = 0.01, *, seed: int = 0,
+                     lo: float = 1e-6, hi: float = 1.0) -> list[tuple[int, int, float]]:
+    """Adversarial products: a seeded ``fraction`` of the product leaves each get one seeded
+    entry multiplied by ``1 ± x``, with ``x`` log-uniform in ``[lo, hi]`` (in place, in the
+    leaf's own dtype). Returns ``(m, flat index, factor)`` per perturbed product, in canonical
+    order. The transcript's root changes with it, as a prover committing the forged leaves
+    would re-root."""
+    import math
+    c = step.c
+    g = torch.Generator().manual_seed(seed)
+    n = max(1, round(fraction * c.M))
+    ms = sorted(int(x) + 1 for x in torch.randperm(c.M, generator=g)[:n])
+    out = []
+    for m in ms:
+        p = step.product(m)
+        idx = int(torch.randint(0, p.numel(), (1,), generator=g))
+        u = float(torch.rand(1, generator=g))
+        x = math.exp(math.log(lo) + u * (math.log(hi) - math.log(lo)))
+        sign = 1.0 if float(torch.rand(1, generator=g)) < 0.5 else -1.0
+        factor = 1.0 + sign * x
+        flat = p.view(-1)
+        flat[idx] = (flat[idx].float() * factor).to(p.dtype)
+        out.append((m, idx, factor))
+    return out
