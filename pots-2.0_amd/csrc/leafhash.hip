@@ -47,9 +47,9 @@ struct LeafDesc {
 };
 static_assert(sizeof(LeafDesc) == 32, "LeafDesc layout");
 
-struct LevelEntry {     // one leaf with >= 2 nodes at one reduction level
+struct LevelEntry {     // one leaf with >= 2 nodes at the input level of one fold
   uint64_t in_off;      // its first node in the level's input buffer
-  uint64_t out_off;     // its first node in the level's output buffer
+  uint64_t out_off;     // its first node in the fold's output buffer
   uint64_t out_first;   // its first output, counted over the level's entries
   uint32_t n_in;        // its nodes at this level
   uint32_t leaf;
@@ -57,6 +57,8 @@ struct LevelEntry {     // one leaf with >= 2 nodes at one reduction level
 static_assert(sizeof(LevelEntry) == 32, "LevelEntry layout");
 
 constexpr int kThreads = 256;
+// Tree levels one launch of level_kernel reduces.
+constexpr uint32_t kFold = 3;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -236,37 +238,63 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel(
   }
 }
 
+// Levels kFold at a time: thread t makes output node o of its leaf at level l + kFold from the
+// (at most 2^kFold) nodes o·2^kFold .. of level l, level by level in registers with
+// BLAKE3's rule (pairs are hashed, a last odd node is promoted). A leaf whose tree closes
+// inside the fold writes its digest (the compression that makes the single top node carries
+// ROOT). Block b's outputs lie in entries blk_ent[b] .. blk_ent[b + 1].
 __global__ __launch_bounds__(kThreads) void level_kernel(
-    const LevelEntry* __restrict__ ents, uint32_t n_ents, uint64_t n_out,
+    const LevelEntry* __restrict__ ents, const uint32_t* __restrict__ blk_ent, uint64_t n_out,
     const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
     uint32_t* __restrict__ digests) {
   const uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
   if (t >= n_out) return;
-  uint32_t lo = 0, hi = n_ents - 1;
+  uint32_t lo = blk_ent[blockIdx.x], hi = blk_ent[blockIdx.x + 1];
   while (lo < hi) {
     const uint32_t mid = (lo + hi + 1) >> 1;
     if (ents[mid].out_first <= t) lo = mid;
     else hi = mid - 1;
   }
   const LevelEntry e = ents[lo];
-  const uint64_t j = t - e.out_first;
-  const uint32_t n_out_leaf = (e.n_in + 1) / 2;
-  const uint4* src = reinterpret_cast<const uint4*>(in + 8ull * (e.in_off + 2 * j));
-  uint32_t res[8];
-  if (2 * j + 1 < e.n_in) {
-    const uint4 a = src[0], b = src[1], c = src[2], dd = src[3];
-    const uint32_t l[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    const uint32_t r[8] = {c.x, c.y, c.z, c.w, dd.x, dd.y, dd.z, dd.w};
-    b3_parent_cv(l, r, n_out_leaf == 1 ? B3_ROOT : 0u, res);
-  } else {
-    const uint4 a = src[0], b = src[1];
-    res[0] = a.x; res[1] = a.y; res[2] = a.z; res[3] = a.w;
-    res[4] = b.x; res[5] = b.y; res[6] = b.z; res[7] = b.w;
+  const uint64_t o = t - e.out_first;
+  constexpr uint32_t W = 1u << kFold;
+  const uint64_t first = o * W;
+  const uint32_t cnt = (uint32_t)min<uint64_t>(W, e.n_in - first);
+  uint32_t cv[W][8];
+  const uint4* src = reinterpret_cast<const uint4*>(in + 8ull * (e.in_off + first));
+#pragma unroll
+  for (uint32_t a = 0; a < W; a++) {
+    uint4 x = make_uint4(0, 0, 0, 0), y = make_uint4(0, 0, 0, 0);
+    if (a < cnt) {
+      x = src[2 * a];
+      y = src[2 * a + 1];
+    }
+    cv[a][0] = x.x; cv[a][1] = x.y; cv[a][2] = x.z; cv[a][3] = x.w;
+    cv[a][4] = y.x; cv[a][5] = y.y; cv[a][6] = y.z; cv[a][7] = y.w;
   }
-  uint4* dst = reinterpret_cast<uint4*>(n_out_leaf == 1 ? digests + 8ull * e.leaf
-                                                         : out + 8ull * (e.out_off + j));
-  dst[0] = make_uint4(res[0], res[1], res[2], res[3]);
-  dst[1] = make_uint4(res[4], res[5], res[6], res[7]);
+  // m: this thread's nodes at the current level; n: the leaf's nodes at the current level.
+  uint32_t m = cnt;
+  uint64_t n = e.n_in;
+#pragma unroll
+  for (uint32_t lvl = 0; lvl < kFold; lvl++) {
+    const uint64_t n_next = (n + 1) / 2;
+    const uint32_t flags = n_next == 1 ? B3_ROOT : 0u;
+#pragma unroll
+    for (uint32_t a = 0; a < (W >> (lvl + 1)); a++) {
+      if (2 * a + 1 < m) {
+        b3_parent_cv(cv[2 * a], cv[2 * a + 1], flags, cv[a]);
+      } else if (2 * a < m) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) cv[a][q] = cv[2 * a][q];
+      }
+    }
+    m = (m + 1) / 2;
+    n = n_next;
+  }
+  uint4* dst = reinterpret_cast<uint4*>(n == 1 ? digests + 8ull * e.leaf
+                                               : out + 8ull * (e.out_off + o));
+  dst[0] = make_uint4(cv[0][0], cv[0][1], cv[0][2], cv[0][3]);
+  dst[1] = make_uint4(cv[0][4], cv[0][5], cv[0][6], cv[0][7]);
 }
 
 __global__ void fill_u32(uint32_t* p, uint32_t v) { *p = v; }
@@ -283,9 +311,10 @@ struct StageCopy {  // a staged leaf: its head bytes, then its payload, into one
 };
 
 struct LevelInfo {
-  uint64_t ent_first;  // index of the level's first entry in the entry array
+  uint64_t ent_first;  // index of the fold's first entry in the entry array
   uint32_t n_ents;
   uint64_t n_out;
+  uint64_t blk_first;  // index of the fold's block -> entry table in blk_ent
   int in_buf, out_buf;  // 0 = cv0, 1 = cv1
 };
 
@@ -301,6 +330,7 @@ struct LeafPlan {
   uint32_t* d_blk_leaf = nullptr;
   uint32_t* d_head = nullptr;
   LevelEntry* d_levels = nullptr;
+  uint32_t* d_blk_ent = nullptr;
   uint32_t* d_cv[2] = {nullptr, nullptr};
   uint32_t n_blocks = 0;  // chunk slots of kThreads chunks
   uint32_t max_grid = 0;  // chunk kernel's grid limit; 0 = one block per slot
@@ -393,8 +423,11 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
     blk_leaf[P->n_blocks] = (uint32_t)(n - 1);
   }
 
-  // Reduction levels. Level 0 nodes of leaf i sit at chunk_first[i] in cv0.
+  // Reduction folds of kFold levels each. Level 0 nodes of leaf i sit at chunk_first[i] in
+  // cv0; a fold takes a leaf's n nodes to ceil(n / 2^kFold) (BLAKE3's halving with a
+  // promoted odd node, kFold times, composes to that ceiling).
   std::vector<LevelEntry> ents;
+  std::vector<uint32_t> blk_ent;
   std::vector<uint64_t> n_nodes(n), off(n);
   for (size_t i = 0; i < n; i++) {
     n_nodes[i] = chunk_first[i + 1] - chunk_first[i];
@@ -403,11 +436,11 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
   uint64_t cv1_need = 0;
   int in_buf = 0;
   for (;;) {
-    LevelInfo li{ents.size(), 0, 0, in_buf, 1 - in_buf};
+    LevelInfo li{ents.size(), 0, 0, blk_ent.size(), in_buf, 1 - in_buf};
     uint64_t out_next = 0;
     for (size_t i = 0; i < n; i++) {
       if (n_nodes[i] < 2) continue;
-      const uint64_t nout = (n_nodes[i] + 1) / 2;
+      const uint64_t nout = (n_nodes[i] + (1u << kFold) - 1) >> kFold;
       LevelEntry e;
       e.in_off = off[i];
       e.out_off = out_next;
@@ -422,6 +455,16 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
       out_next += nout;
     }
     if (li.n_ents == 0) break;
+    // Per block of kThreads outputs: the fold-relative index of the entry holding its first
+    // output, and a closing bound.
+    const uint64_t nb = (li.n_out + kThreads - 1) / kThreads;
+    uint32_t k = 0;
+    for (uint64_t b = 0; b < nb; b++) {
+      const uint64_t first_out = b * kThreads;
+      while (k + 1 < li.n_ents && ents[li.ent_first + k + 1].out_first <= first_out) k++;
+      blk_ent.push_back(k);
+    }
+    blk_ent.push_back(li.n_ents - 1);
     if (li.out_buf == 1) cv1_need = std::max(cv1_need, out_next);
     P->levels.push_back(li);
     in_buf = 1 - in_buf;
@@ -439,6 +482,7 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
   const size_t o_blk = place((P->n_blocks + 1) * sizeof(uint32_t));
   const size_t o_head = place(std::max<size_t>(headbytes.size(), 4));
   const size_t o_lev = place(std::max<size_t>(ents.size(), 1) * sizeof(LevelEntry));
+  const size_t o_blk_ent = place(std::max<size_t>(blk_ent.size(), 1) * sizeof(uint32_t));
   const size_t meta_bytes = at;
   const size_t o_cv0 = place(nc * 32);
   const size_t o_cv1 = place(std::max<uint64_t>(cv1_need, 1) * 32);
@@ -475,6 +519,7 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
   P->d_blk_leaf = reinterpret_cast<uint32_t*>(P->base + o_blk);
   P->d_head = reinterpret_cast<uint32_t*>(P->base + o_head);
   P->d_levels = reinterpret_cast<LevelEntry*>(P->base + o_lev);
+  P->d_blk_ent = reinterpret_cast<uint32_t*>(P->base + o_blk_ent);
   P->d_cv[0] = reinterpret_cast<uint32_t*>(P->base + o_cv0);
   P->d_cv[1] = reinterpret_cast<uint32_t*>(P->base + o_cv1);
 
@@ -485,6 +530,8 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
   memcpy(img.data() + o_blk, blk_leaf.data(), (P->n_blocks + 1) * sizeof(uint32_t));
   if (!headbytes.empty()) memcpy(img.data() + o_head, headbytes.data(), headbytes.size());
   if (!ents.empty()) memcpy(img.data() + o_lev, ents.data(), ents.size() * sizeof(LevelEntry));
+  if (!blk_ent.empty())
+    memcpy(img.data() + o_blk_ent, blk_ent.data(), blk_ent.size() * sizeof(uint32_t));
   hipError_t e = hipMemcpy(P->base, img.data(), meta_bytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     note_hip_error(e, "hipMemcpy(leaf plan metadata)", __FILE__, __LINE__);
@@ -527,8 +574,8 @@ static int plan_stage(LeafPlan* P, int stage, uint32_t* d_digests, uint32_t* d_f
       for (const LevelInfo& li : P->levels) {
         const uint64_t blocks = (li.n_out + kThreads - 1) / kThreads;
         hipLaunchKernelGGL(level_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream,
-                           P->d_levels + li.ent_first, li.n_ents, li.n_out, P->d_cv[li.in_buf],
-                           P->d_cv[li.out_buf], d_digests);
+                           P->d_levels + li.ent_first, P->d_blk_ent + li.blk_first, li.n_out,
+                           P->d_cv[li.in_buf], P->d_cv[li.out_buf], d_digests);
         POTS_HIP(hipGetLastError());
       }
       return POTS_E_OK;

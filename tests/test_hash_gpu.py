@@ -89,6 +89,22 @@ def test_views_of_one_storage_and_unaligned_views(lib):
     assert bad == len(views) and got == _expected(views)
 
 
+def test_tree_shapes_across_fold_boundaries(lib):
+    """Leaves of n chunks around the powers of two where the per-leaf tree is reduced several
+    levels per launch (2, 3, 8, 9, 64, 65, 512, 513, 4096, 4097 chunks, ...), batched with
+    one-chunk leaves between them so that launch blocks span many leaves."""
+    counts = [2, 3, 4, 5, 7, 8, 9, 15, 16, 17, 31, 33, 63, 64, 65, 127, 129, 511, 512, 513,
+              1023, 1025, 4095, 4096, 4097, 9000]
+    ts = []
+    for i, n in enumerate(counts):
+        # int32 payload of 1024·n − 100 bytes: with its header the message spans n chunks
+        ts.append(payload(((1024 * n - 100) // 4,), torch.int32, 900 + i))
+        ts.append(payload((3,), torch.float32, 950 + i))
+    got, bad = _tensor_batch(lib, ts)
+    assert bad == len(ts)
+    assert got == _expected(ts)
+
+
 def test_host_payloads_are_staged(lib):
     ts = [payload((1000 + i,), torch.float32, 40 + i) for i in range(5)]
     got, bad = _tensor_batch(lib, ts, device=False)
