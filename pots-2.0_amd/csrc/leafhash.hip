@@ -43,7 +43,7 @@ struct LeafDesc {
   uint32_t head_word;  // first word of this leaf's 0x00 || header in the head table
   uint32_t head_len;   // bytes of 0x00 || header, a multiple of 4 (0 for a staged leaf)
   uint32_t kind;       // POTS_KIND_*
-  uint32_t pad;
+  uint32_t fin_from;   // message byte where the payload (the NaN/Inf-tested bytes) begins
 };
 static_assert(sizeof(LeafDesc) == 32, "LeafDesc layout");
 
@@ -75,8 +75,9 @@ __device__ __forceinline__ void finite_acc(u16x2& acc, uint32_t w, uint32_t mask
 }
 
 // Message block b of chunk c for the general case: blocks that touch the header, the end of
-// the payload or a partial word. Header words come from the head table; bytes past the end
-// are zero; only payload words feed the NaN/Inf test.
+// the payload or a partial word. Header words come from the head table (a staged leaf holds
+// its header in the staged message instead); bytes past the end are zero; only payload words
+// (from fin_from on) feed the NaN/Inf test.
 template <int SH>
 __device__ __forceinline__ void edge_block(const LeafDesc& d, const uint32_t* __restrict__ head,
                                            uint64_t o, uint32_t mask, uint32_t m[16],
@@ -107,7 +108,7 @@ __device__ __forceinline__ void edge_block(const LeafDesc& d, const uint32_t* __
     } else {
       const uint64_t rem = L - at;
       if (rem < 4) mw &= (1u << (8 * rem)) - 1u;
-      finite_acc(acc, mw, mask);
+      if (at >= d.fin_from) finite_acc(acc, mw, mask);
     }
     m[j] = mw;
   }
@@ -137,7 +138,7 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
   for (uint32_t b = 0; b < nb; b += 2) {
     const uint64_t o = cstart + 64u * b;
     uint32_t m0[16], m1[16];
-    if (o >= H && o + 128 <= L) {
+    if (o >= d.fin_from && o + 128 <= L) {
       const u32x4* A16 =
           reinterpret_cast<const u32x4*>((d.payload + o - H) & ~uint64_t(15));
       u32x4 q[9];
@@ -373,11 +374,11 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
     const bool stage = host || (hl % 4) != 0 || (ptr % 4) != 0;
     LeafDesc& d = desc[i];
     d.kind = kind[i];
-    d.pad = 0;
     const uint64_t at = headbytes.size();
     headbytes.push_back(0x00);
     headbytes.insert(headbytes.end(), hdr_buf + hdr_off[u], hdr_buf + hdr_off[u] + hdr_len[u]);
     while (headbytes.size() % 4) headbytes.push_back(0);
+    d.fin_from = (uint32_t)hl;  // the 0x00 || header bytes are never NaN/Inf-tested
     if (!stage) {
       d.payload = ptr;
       d.len = len;

@@ -111,6 +111,28 @@ def test_host_payloads_are_staged(lib):
     assert bad == len(ts) and got == _expected(ts)
 
 
+def test_staged_headers_are_not_tested_for_nan(lib):
+    """A staged leaf (host payload, or a view not 4-byte aligned) carries its 0x00 || header
+    bytes in the staged message; only the payload is NaN/Inf-tested, as in native.c. The
+    big-endian dims below put an all-ones exponent into a header half-word or word: 124 for
+    fp16 (bytes 00 7C), 32895 = 0x807F for bf16 and fp32."""
+    ts = [payload((124,), torch.float16, 1), payload((3, 124), torch.float16, 2),
+          payload((32895,), torch.bfloat16, 3), payload((2, 32895), torch.float32, 4),
+          payload((32895,), torch.float16, 5)]
+    got, bad = _tensor_batch(lib, ts, device=False)
+    assert bad == len(ts) and got == _expected(ts)
+    for dt, n in ((torch.float16, 124), (torch.bfloat16, 32895), (torch.float16, 32895)):
+        flat = payload((n + 1,), dt, 6).to(DEV)
+        v = flat[1:]  # 2-byte aligned: staged
+        got, bad = _tensor_batch(lib, [v])
+        assert bad == 1 and got == _expected([v])
+    # the payload of a staged leaf is still tested
+    t = payload((124,), torch.float16, 7)
+    t[100] = float("inf")
+    _, bad = _tensor_batch(lib, [payload((5,), torch.float32, 8), t], device=False)
+    assert bad == 1
+
+
 def test_many_small_leaves(lib):
     ts = [payload((13,), torch.float32, i) for i in range(5000)]
     got, bad = _tensor_batch(lib, ts)
