@@ -84,6 +84,16 @@ __device__ __forceinline__ void b3_compress_cv(const uint32_t cv[8], const uint3
   for (int i = 0; i < 8; i++) out[i] = v[i] ^ v[i + 8];
 }
 
+// The same with a 32-bit counter (its high word a compile-time zero).
+__device__ __forceinline__ void b3_compress_cv32(const uint32_t cv[8], const uint32_t m[16],
+                                                 uint32_t counter, uint32_t block_len,
+                                                 uint32_t flags, uint32_t out[8]) {
+  uint32_t v[16];
+  b3_rounds(cv, m, counter, 0u, block_len, flags, v);
+#pragma unroll
+  for (int i = 0; i < 8; i++) out[i] = v[i] ^ v[i + 8];
+}
+
 // All 16 output words (the extendable-output block of a root compression).
 __device__ __forceinline__ void b3_compress_xof(const uint32_t cv[8], const uint32_t m[16],
                                                 uint64_t counter, uint32_t block_len,

@@ -61,18 +61,31 @@ constexpr int kThreads = 256;
 constexpr uint32_t kFold = 3;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-
-
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-// The NaN/Inf test: `mask` keeps each value's exponent field (fp32 0x7F800000, bf16
-// 0x7F807F80, fp16 0x7C007C00, none 0), and the running per-half maximum of the masked words
-// reaches the all-ones exponent (0x7F80 for fp32 and bf16, 0x7C00 for fp16) exactly when a
-// non-finite value was seen. Two VALU operations per word (and, packed 16-bit max).
-__device__ __forceinline__ void finite_acc(u16x2& acc, uint32_t w, uint32_t mask) {
-  acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, w & mask));
-}
+// The NaN/Inf test of a chunk's payload words, one accumulator per lane: `mask` keeps each
+// value's exponent field (fp32 0x7F800000, bf16 0x7F807F80, fp16 0x7C007C00, none 0), and the
+// running per-half maximum of the masked words reaches the all-ones exponent (0x7F80 for fp32
+// and bf16, 0x7C00 for fp16) exactly when a non-finite value was seen. Two VALU operations per
+// word (and, packed 16-bit max). (A per-kind test with one v_dot2c_f32_bf16 per word measured
+// slower: the chunk kernel's code doubles and its time went up by 5%.)
+struct Fin {
+  u16x2 acc = {0, 0};
+  uint32_t mask;
+  unsigned short thr;
+  __device__ explicit Fin(uint32_t kind)
+      : mask(kind == POTS_KIND_F32    ? 0x7F800000u
+             : kind == POTS_KIND_BF16 ? 0x7F807F80u
+             : kind == POTS_KIND_F16  ? 0x7C007C00u
+                                      : 0u),
+        thr(kind == POTS_KIND_F16 ? 0x7C00 : 0x7F80) {}
+  __device__ __forceinline__ void add(uint32_t w) {
+    acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, w & mask));
+  }
+  __device__ __forceinline__ bool bad() const {
+    return mask != 0u && (acc.x >= thr || acc.y >= thr);
+  }
+};
 
 // Message block b of chunk c for the general case: blocks that touch the header, the end of
 // the payload or a partial word. Header words come from the head table (a staged leaf holds
@@ -80,8 +93,7 @@ __device__ __forceinline__ void finite_acc(u16x2& acc, uint32_t w, uint32_t mask
 // (from fin_from on) feed the NaN/Inf test.
 template <int SH>
 __device__ __forceinline__ void edge_block(const LeafDesc& d, const uint32_t* __restrict__ head,
-                                           uint64_t o, uint32_t mask, uint32_t m[16],
-                                           u16x2& acc) {
+                                           uint64_t o, uint32_t m[16], Fin& fin) {
   const uint64_t H = d.head_len, L = H + d.len;
   const uint64_t pbeg = d.payload, pend = d.payload + d.len;
   const uint64_t A = d.payload + o - H;  // address of message byte o, in payload terms
@@ -108,7 +120,7 @@ __device__ __forceinline__ void edge_block(const LeafDesc& d, const uint32_t* __
     } else {
       const uint64_t rem = L - at;
       if (rem < 4) mw &= (1u << (8 * rem)) - 1u;
-      if (at >= d.fin_from) finite_acc(acc, mw, mask);
+      if (at >= d.fin_from) fin.add(mw);
     }
     m[j] = mw;
   }
@@ -120,8 +132,7 @@ __device__ __forceinline__ void edge_block(const LeafDesc& d, const uint32_t* __
 // instead of being fetched again for the second half; other pairs take edge_block.
 template <int SH>
 __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __restrict__ head,
-                                           uint64_t c, bool root, uint32_t mask, uint32_t cv[8],
-                                           u16x2& acc) {
+                                           uint64_t c, bool root, uint32_t cv[8], Fin& fin) {
   const uint64_t H = d.head_len;
   const uint64_t L = H + d.len;
   const uint64_t cstart = c * 1024u;
@@ -168,12 +179,18 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
         m1[j] = w[16 + j + SH];
       }
 #pragma unroll
-      for (int j = 0; j < 32; j++) finite_acc(acc, w[j + SH], mask);
-    } else {
-      edge_block<SH>(d, head, o, mask, m0, acc);
-      if (b + 1 < nb) edge_block<SH>(d, head, o + 64, mask, m1, acc);
-      have_carry = false;
+      for (int j = 0; j < 32; j++) fin.add(w[j + SH]);
+      // Two whole 64-byte blocks of which the first never ends the chunk: the block lengths
+      // are constant, and the chunk counter fits 32 bits (plan creation refuses a leaf of
+      // 4 TiB or more).
+      b3_compress_cv32(cv, m0, (uint32_t)c, 64u, b == 0 ? B3_CHUNK_START : 0u, cv);
+      b3_compress_cv32(cv, m1, (uint32_t)c, 64u,
+                       b + 2 == nb ? (B3_CHUNK_END | (root ? B3_ROOT : 0u)) : 0u, cv);
+      continue;
     }
+    edge_block<SH>(d, head, o, m0, fin);
+    if (b + 1 < nb) edge_block<SH>(d, head, o + 64, m1, fin);
+    have_carry = false;
     const uint32_t blen0 = (uint32_t)min<uint64_t>(64u, L > o ? L - o : 0u);
     uint32_t f0 = b == 0 ? B3_CHUNK_START : 0u;
     if (b + 1 == nb) f0 |= B3_CHUNK_END | (root ? B3_ROOT : 0u);
@@ -204,20 +221,15 @@ __device__ __forceinline__ void chunk_one(
   const uint64_t c = g - chunk_first[i];
   const bool root = chunk_first[i + 1] - chunk_first[i] == 1;
   const uint32_t sh = (uint32_t)((d.payload - d.head_len) >> 2) & 3u;
-  const uint32_t mask = d.kind == POTS_KIND_F32    ? 0x7F800000u
-                        : d.kind == POTS_KIND_BF16 ? 0x7F807F80u
-                        : d.kind == POTS_KIND_F16  ? 0x7C007C00u
-                                                   : 0u;
   uint32_t cv[8];
-  u16x2 acc = {0, 0};
+  Fin fin(d.kind);
   switch (sh) {
-    case 0: hash_chunk<0>(d, head, c, root, mask, cv, acc); break;
-    case 1: hash_chunk<1>(d, head, c, root, mask, cv, acc); break;
-    case 2: hash_chunk<2>(d, head, c, root, mask, cv, acc); break;
-    default: hash_chunk<3>(d, head, c, root, mask, cv, acc); break;
+    case 0: hash_chunk<0>(d, head, c, root, cv, fin); break;
+    case 1: hash_chunk<1>(d, head, c, root, cv, fin); break;
+    case 2: hash_chunk<2>(d, head, c, root, cv, fin); break;
+    default: hash_chunk<3>(d, head, c, root, cv, fin); break;
   }
-  const unsigned short thr = d.kind == POTS_KIND_F16 ? 0x7C00 : 0x7F80;
-  if (mask != 0u && (acc.x >= thr || acc.y >= thr)) atomicMin(first_bad, i);
+  if (fin.bad()) atomicMin(first_bad, i);
   u32x4* dst = reinterpret_cast<u32x4*>(root ? digests + 8ull * i : cv_out + 8ull * g);
   gstore<u32x4>(dst, u32x4{cv[0], cv[1], cv[2], cv[3]});
   gstore<u32x4>(dst + 1, u32x4{cv[4], cv[5], cv[6], cv[7]});
@@ -395,6 +407,10 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
       P->stages.push_back(StageCopy{stage_off[i], at, hl, ptr, len, host});
     }
     const uint64_t L = hl + len;
+    if (L >> 42) {  // 2^32 chunks: the chunk kernel's 32-bit counter
+      delete P;
+      return POTS_E_ARG;
+    }
     chunk_first[i] = nc;
     nc += std::max<uint64_t>(1, (L + 1023) / 1024);
     P->bytes += L;
