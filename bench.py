@@ -169,6 +169,41 @@ def counter_summary(d: Path, copy_mib: int) -> int:
     return 0
 
 
+def trace_summary(d: Path, steps: int, warmup: int) -> int:
+    """Per-kernel dispatch durations of a rocprofv3 --kernel-trace CSV run of this bench, and
+    the chunk kernel's launches split by phase: the claimed root and the warm-up steps, the
+    timed steps (overlapped with the Freivalds passes), and the serialised stage leg whose
+    mean is the roofline's ``launch_ms``."""
+    import collections
+    import csv
+    rows = []
+    for f in d.rglob("*kernel_trace.csv"):
+        for r in csv.DictReader(f.open()):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                         r["Kernel_Name"].split("(")[0].replace("void ", "")))
+    if not rows:
+        print(f"no kernel_trace.csv under {d}", file=sys.stderr)
+        return 1
+    rows.sort()
+    by = collections.defaultdict(list)
+    for t0, t1, k in rows:
+        by[k].append((t1 - t0) / 1e6)
+    print("| kernel | calls | mean ms | min ms | max ms |")
+    print("|---|---|---|---|---|")
+    for k, ds in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        if k.startswith("pots::") or k.startswith("__amd"):
+            print(f"| `{k}` | {len(ds)} | {sum(ds) / len(ds):.3f} | {min(ds):.3f} | "
+                  f"{max(ds):.3f} |")
+    ck = by.get("pots::chunk_kernel", [])
+    n_pre = 1 + warmup
+    timed, leg = ck[n_pre:n_pre + steps], ck[n_pre + steps:]
+    if timed and leg:
+        print(f"\nchunk_kernel: {len(timed)} launches in the timed steps, mean "
+              f"{sum(timed) / len(timed):.3f} ms (beside the Freivalds passes); {len(leg)} "
+              f"launches in the serialised stage leg, mean {sum(leg) / len(leg):.3f} ms")
+    return 0
+
+
 def traffic_from_profile(kernel: str) -> int | None:
     """HBM bytes per launch of ``kernel`` from the committed counter summary (the fenced
     JSON block of TRAFFIC_FILE), or None when it holds no figure for that kernel."""
@@ -195,9 +230,14 @@ def main() -> int:
                          "counter run sees a plain copy kernel of known size")
     ap.add_argument("--counter-summary", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSV output under DIR and exit")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="summarise rocprofv3 --kernel-trace CSV output under DIR of a run "
+                         "with the same --steps/--warmup, and exit")
     args = ap.parse_args()
     if args.counter_summary:
         return counter_summary(Path(args.counter_summary), args.calibration_copy_mib)
+    if args.trace_summary:
+        return trace_summary(Path(args.trace_summary), args.steps, args.warmup)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               "sharding is a design in DESIGN.md, not a measured path.", file=sys.stderr)
@@ -258,6 +298,8 @@ def main() -> int:
     ms = wall / args.steps * 1e3
     hashed_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     measured_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / args.steps
+    # the chunk kernel inside the timed steps, on its own (side) stream, beside the Freivalds
+    chunks_in_step_ms = sum(e[4].elapsed_time(e[5]) for e in evs) / args.steps
     root = flags[:8].numpy().tobytes()
     first_bad, first_fail = int(flags[8]), int(flags[9])
     assert root == claimed_b, "recomputed root differs from the claim"
@@ -348,7 +390,9 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic_from_profile(dom_name) if dom == "hash.chunks" else None,
                      "kernel": dom_name,
-                     "algorithmic_bytes": dom_bytes, "launch_ms": round(stage_ms[dom], 4)},
+                     "algorithmic_bytes": dom_bytes, "launch_ms": round(stage_ms[dom], 4),
+                     "launch_ms_in_step": (round(chunks_in_step_ms, 4)
+                                           if dom == "hash.chunks" else None)},
     }
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")

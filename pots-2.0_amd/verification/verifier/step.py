@@ -84,7 +84,8 @@ class DeviceStepVerifier:
     def enqueue(self, claimed: bytes | torch.Tensor, events: list | None = None):
         """Enqueue the whole step on the current stream (Freivalds, verdicts) and a side
         stream (hashing, tree); returns GPU tensors ``(nodes, codes, first_fail)``.
-        ``events``, if given, receives (start, hashed, measured, judged) CUDA events."""
+        ``events``, if given, receives (start, hashed, measured, judged, chunks_begin,
+        chunks_end) CUDA events; the last two bracket the chunk kernel on the side stream."""
         main = torch.cuda.current_stream()
         if isinstance(claimed, torch.Tensor):
             self.key.copy_(claimed)
@@ -93,8 +94,16 @@ class DeviceStepVerifier:
         start = torch.cuda.Event(enable_timing=events is not None)
         start.record(main)
         self.side.wait_event(start)
+        timing = events is not None
+        c_begin = torch.cuda.Event(enable_timing=timing)
+        c_end = torch.cuda.Event(enable_timing=timing)
         with torch.cuda.stream(self.side):
-            self.hasher.digests(self.digests, self.bad, self.side)
+            hp = self.hasher.plan
+            hp.run_stage(0, self.digests, self.bad, self.side)
+            c_begin.record(self.side)
+            hp.run_stage(1, self.digests, self.bad, self.side)
+            c_end.record(self.side)
+            hp.run_stage(2, self.digests, self.bad, self.side)
             nodes = self.lib.merkle_tree_device(self.digests, self.side)
         hashed = torch.cuda.Event(enable_timing=events is not None)
         hashed.record(self.side)
@@ -110,7 +119,7 @@ class DeviceStepVerifier:
         # keep the side stream's tensors alive for the main stream's consumers
         nodes.record_stream(main)
         if events is not None:
-            events.append((start, hashed, measured, judged))
+            events.append((start, hashed, measured, judged, c_begin, c_end))
         return nodes, codes, first
 
     def run(self, claimed: bytes) -> StepVerdict:
