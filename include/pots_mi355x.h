@@ -184,6 +184,46 @@ int pots_verdicts_async(size_t n, const double *d_rows, uint32_t k, const void *
                         uint32_t guard, uint32_t judge, int32_t *d_codes, double *d_finished,
                         uint32_t *d_first_fail, void *stream);
 
+/* ---- check 6a: the SGD update identity of the linear weights ----------------------- */
+
+/* One linear weight: W_t and W_{t+1} (fp32, n entries each) and the parts of its gradient G
+ * (its committed weight-gradient products, fp32 or bf16, n entries each, summed in order in
+ * fp32: chain_gradient, verification/computation/interface.py:169-180). All device memory,
+ * contiguous. tau_w is the weight's band (bands.py tau_w_for). */
+#define POTS_UPDATE_MAX_PARTS 8
+typedef struct pots_update_weight {
+  const void *w_t;
+  const void *w_next;
+  const void *parts[POTS_UPDATE_MAX_PARTS];
+  uint32_t part_dtype[POTS_UPDATE_MAX_PARTS]; /* 0 fp32, 1 bf16 */
+  uint32_t n_parts;
+  uint32_t pad;
+  uint64_t n;
+  double tau_w;
+} pots_update_weight;
+
+/* Per weight, in device memory: rho_bits is ρ_max = max_i ρ_i as the bits of a double (NaN
+ * if any ρ_i is NaN, 0 for an empty weight); first_nonfinite and first_over are the smallest
+ * index whose R_i or scale_i is not finite, and whose ρ_i is not ≤ tau_w, or UINT64_MAX. */
+typedef struct pots_update_result {
+  uint64_t rho_bits;
+  uint64_t first_nonfinite;
+  uint64_t first_over;
+} pots_update_result;
+
+/* A plan over n weights, with the step size eta and ε_W (eps_w) already rounded to fp32 (the
+ * reference multiplies fp32 tensors by them as fp32 scalars). Replaces the per-weight work of
+ * checks.py:380-451 (_update_identity, _update_identity_reference; ρ_max bit for bit as
+ * _fast_rho_max, checks.py:301-377, obtains it): R = |W_{t+1} − (W_t − η·G)|,
+ * scale = ε_W·(|W_t| + |η·G|) in fp32, ρ_i = 0 if R_i = 0 else fl64(R_i)/fl64(scale_i). */
+int pots_update_plan_create(size_t n, const pots_update_weight *weights, float eta, float eps_w,
+                            void **plan);
+/* Enqueue the pass; d_out holds n results (device). Stream-ordered, no allocation, no sync. */
+int pots_update_plan_run(void *plan, pots_update_result *d_out, void *stream);
+/* Bytes one run reads: W_t, W_{t+1} and every gradient part once. */
+uint64_t pots_update_plan_bytes(void *plan);
+void pots_update_plan_destroy(void *plan);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,10 @@ name is the reference code it follows:
   residuals are compared with in band units.
 - ``finish_row`` / ``band_unit`` / ``judge`` — ``freivalds.py:324-335,450-468``,
   ``sizing.py:16-43``, ``verification/verifier/checks.py:926-956``.
+- ``chain_gradient`` / ``update_identity`` — check 6a's update identity,
+  ``verification/computation/interface.py:169-180`` and
+  ``verification/verifier/checks.py:380-451`` (``_update_identity_reference``), in torch-CPU
+  fp32 with the ratio in float64.
 
 Pinning (what checks this oracle, so a wrong restatement fails a test): the reference's
 known-answer tests (``tests/verification/verifier/matmul_check/test_challenges.py:86-137``,
@@ -29,8 +33,10 @@ known-answer tests (``tests/verification/verifier/matmul_check/test_challenges.p
 ``test_sizing.py:20-25``), BLAKE3's published test vectors for the unkeyed empty and
 short inputs, agreement with the independent recursive BLAKE3 of ``blake3_tree.py`` on
 multi-chunk inputs, brute-force tree shapes, and the closed-form invariants of the Freivalds
-rows (a forged entry stands out, bias as a ones column, U <= nu, scale invariance); see
-``tests/test_oracle.py``.
+rows (a forged entry stands out, bias as a ones column, U <= nu, scale invariance), and the
+update identity's exact small cases (R = 0 for an exactly rounded step, closed-form ρ for
+power-of-two entries, 0/0 and r/0, an fp32 quotient that underflows) together with the
+outcomes the reference's own update-identity tests state; see ``tests/test_oracle.py``.
 """
 
 from __future__ import annotations
@@ -391,3 +397,44 @@ def judge(mp: dict, *, tau: float, kappa_max: float, guard: bool = True) -> tupl
         if not x <= tau * mp["unit"]:
             return RESIDUAL, j
     return ACCEPT, 0
+
+
+# ---- check 6a: the update identity --------------------------------------------------------
+
+def chain_gradient(parts: Sequence[torch.Tensor], dtype: torch.dtype = torch.float32
+                   ) -> torch.Tensor:
+    """``interface.chain_gradient`` (interface.py:169-180): the parts widened to ``dtype``
+    and added in order, out of place."""
+    g = None
+    for p in parts:
+        p = p.detach().cpu()
+        g = p.to(dtype) if g is None else g + p.to(dtype)
+    if g is None:
+        raise ValueError("a gradient needs at least one product")
+    return g
+
+
+def update_identity(w_t: torch.Tensor, w_next: torch.Tensor, parts: Sequence[torch.Tensor],
+                    eta: float, eps_w: float, tau_w: float) -> dict:
+    """``checks._update_identity_reference`` (checks.py:380-451) on whole CPU tensors:
+    ``R = |W_{t+1} − (W_t − η·G)|`` and ``scale = ε_W·(|W_t| + |η·G|)`` in fp32 (``η`` and
+    ``ε_W`` multiply as fp32 scalars, as torch does), ``ρ = 0`` where ``R = 0`` else
+    ``fl64(R)/fl64(scale)``. Returns ``rho_max`` (torch's max, NaN-propagating; 0 when
+    empty), ``first_nonfinite`` (first index whose R or scale is not finite) and
+    ``first_over`` (first index with ``not ρ ≤ τ_W``), each ``None`` when there is none, and
+    the flat ``r`` and ``scale``."""
+    g = chain_gradient(parts, torch.float32)
+    w_t, w_next = w_t.detach().cpu(), w_next.detach().cpu()
+    with torch.no_grad():
+        eta_g = eta * g
+        r = (w_next - (w_t - eta_g)).abs()
+        scale = eps_w * (w_t.abs() + eta_g.abs())
+        finite = torch.isfinite(r) & torch.isfinite(scale)
+        r64 = r.double()
+        rho = torch.where(r64 == 0, torch.zeros_like(r64), r64 / scale.double())
+    rho_max = float(rho.max()) if rho.numel() else 0.0
+    nf = (~finite).reshape(-1).nonzero()
+    ov = (~(rho <= tau_w)).reshape(-1).nonzero()
+    return {"rho_max": rho_max, "first_nonfinite": int(nf[0]) if nf.numel() else None,
+            "first_over": int(ov[0]) if ov.numel() else None,
+            "r": r.reshape(-1), "scale": scale.reshape(-1)}

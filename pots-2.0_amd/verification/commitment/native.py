@@ -101,6 +101,11 @@ class Native:
             "pots_verdicts_async": ([_sz, _vp, _u32, _vp, ctypes.c_double, ctypes.c_double,
                                      ctypes.c_double, ctypes.c_double, ctypes.c_double, _u32,
                                      _u32, _vp, _vp, _vp, _vp], _int),
+            "pots_update_plan_create": ([_sz, _vp, ctypes.c_float, ctypes.c_float,
+                                         ctypes.POINTER(_vp)], _int),
+            "pots_update_plan_run": ([_vp, _vp, _vp], _int),
+            "pots_update_plan_bytes": ([_vp], _u64),
+            "pots_update_plan_destroy": ([_vp], None),
         }
         for name, (args, res) in sigs.items():
             fn = getattr(lib, name)
@@ -242,6 +247,11 @@ class Native:
             codes.data_ptr(), fin.data_ptr() if fin is not None else None, first.data_ptr(),
             _stream(stream)), "pots_verdicts_async")
         return codes, fin, first
+
+    def update_plan(self, weights: Sequence[UpdateWeight], eta: float, eps_w: float
+                    ) -> UpdatePlan:
+        """Check 6a's update-identity plan over GPU-resident weights (``pots_update_plan_*``)."""
+        return UpdatePlan(self, weights, eta, eps_w)
 
     def leaf_plan(self, headers: Sequence[bytes], payloads: Sequence[torch.Tensor],
                   kinds: Sequence[int]) -> LeafPlan:
@@ -466,6 +476,109 @@ class FvPlan:
     def close(self) -> None:
         if getattr(self, "_h", None) is not None and self._h.value:
             self._lib._lib.pots_fv_plan_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+UPDATE_MAX_PARTS = 8
+
+
+class _UpdateWeightC(ctypes.Structure):
+    _fields_ = [("w_t", _vp), ("w_next", _vp), ("parts", _vp * UPDATE_MAX_PARTS),
+                ("part_dtype", _u32 * UPDATE_MAX_PARTS), ("n_parts", _u32), ("pad", _u32),
+                ("n", _u64), ("tau_w", ctypes.c_double)]
+
+
+class UpdateWeight:
+    """One weight for :class:`UpdatePlan`: GPU tensors ``w_t``, ``w_next`` (fp32) and the
+    gradient's ``parts`` (fp32 or bf16, each of ``w_t``'s shape, summed in order), and its
+    band ``tau_w``."""
+
+    __slots__ = ("w_t", "w_next", "parts", "tau_w")
+
+    def __init__(self, w_t: torch.Tensor, w_next: torch.Tensor, parts: Sequence[torch.Tensor],
+                 tau_w: float) -> None:
+        self.w_t, self.w_next, self.parts, self.tau_w = w_t, w_next, tuple(parts), tau_w
+
+
+class UpdatePlan:
+    """``pots_update_plan_*``: check 6a's pass over every weight, enqueued per run; results
+    land in a device array of ``(ρ_max bits, first non-finite, first over τ_W)`` per weight
+    (``UINT64_MAX`` for none)."""
+
+    NONE = (1 << 64) - 1
+
+    def __init__(self, lib: Native, weights: Sequence[UpdateWeight], eta: float,
+                 eps_w: float) -> None:
+        n = len(weights)
+        if n == 0:
+            raise ValueError("an update plan needs at least one weight")
+        arr = (_UpdateWeightC * n)()
+        keep = []
+        for i, w in enumerate(weights):
+            ts = (w.w_t, w.w_next, *w.parts)
+            for t in ts:
+                if not (t.is_cuda and t.is_contiguous()):
+                    raise ValueError(f"weight {i}: tensors must be contiguous GPU tensors")
+                if t.shape != w.w_t.shape:
+                    raise ValueError(f"weight {i}: shape {tuple(t.shape)} != "
+                                     f"{tuple(w.w_t.shape)}")
+            if w.w_t.dtype != torch.float32 or w.w_next.dtype != torch.float32:
+                raise ValueError(f"weight {i}: W_t and W_t+1 must be fp32")
+            if not 1 <= len(w.parts) <= UPDATE_MAX_PARTS:
+                raise ValueError(f"weight {i}: 1..{UPDATE_MAX_PARTS} gradient parts")
+            c = arr[i]
+            c.w_t, c.w_next = w.w_t.data_ptr(), w.w_next.data_ptr()
+            for j, p in enumerate(w.parts):
+                if p.dtype not in (torch.float32, torch.bfloat16):
+                    raise ValueError(f"weight {i}: gradient parts must be fp32 or bf16")
+                c.parts[j] = p.data_ptr()
+                c.part_dtype[j] = 1 if p.dtype == torch.bfloat16 else 0
+            c.n_parts = len(w.parts)
+            c.n = w.w_t.numel()
+            c.tau_w = float(w.tau_w)
+            keep += list(ts)
+        h = ctypes.c_void_p()
+        lib._check(lib._lib.pots_update_plan_create(n, ctypes.addressof(arr),
+                                                    float(np.float32(eta)),
+                                                    float(np.float32(eps_w)), ctypes.byref(h)),
+                   "pots_update_plan_create")
+        self._lib, self._h, self._keep = lib, h, keep
+        self.n = n
+        self.device = weights[0].w_t.device
+        self.bytes = int(lib._lib.pots_update_plan_bytes(h))
+
+    def run(self, out: torch.Tensor | None = None,
+            stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """Enqueue the pass: uint64 results ``[n, 3]`` (as int64) on the GPU, no sync."""
+        if out is None:
+            out = torch.empty(self.n, 3, dtype=torch.int64, device=self.device)
+        self._lib._check(self._lib._lib.pots_update_plan_run(self._h, out.data_ptr(),
+                                                             _stream(stream)),
+                         "pots_update_plan_run")
+        return out
+
+    @staticmethod
+    def decode(out: torch.Tensor) -> list[tuple[float, int | None, int | None]]:
+        """Host view of :meth:`run`'s results: ``(ρ_max, first_nonfinite, first_over)`` per
+        weight, the indices ``None`` where no entry qualifies."""
+        raw = out.cpu().numpy().view(np.uint64)
+        rho = raw[:, 0].copy().view(np.float64)
+        res = []
+        for i in range(raw.shape[0]):
+            nf, ov = int(raw[i, 1]), int(raw[i, 2])
+            res.append((float(rho[i]), None if nf == UpdatePlan.NONE else nf,
+                        None if ov == UpdatePlan.NONE else ov))
+        return res
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            self._lib._lib.pots_update_plan_destroy(self._h)
             self._h = ctypes.c_void_p()
 
     def __del__(self) -> None:

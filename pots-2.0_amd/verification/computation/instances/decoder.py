@@ -43,7 +43,7 @@ class DecoderComputation(DeclaredComputation):
     def __init__(self, *, L: int, d: int, d_f: int, n_h: int, n_kv: int, n_v: int,
                  n_s: int, n: int, d_h: int | None = None, tied: bool = True,
                  qkv_bias: bool = False, compute_dtype: torch.dtype = torch.float32,
-                 head_blocks: int = 1) -> None:
+                 head_blocks: int = 1, eta: float = 1e-4) -> None:
         if n_h % n_kv:
             raise ValueError(f"n_h={n_h} is not a multiple of n_kv={n_kv}")
         if head_blocks < 1 or n_s % head_blocks:
@@ -54,6 +54,9 @@ class DecoderComputation(DeclaredComputation):
         self.tied, self.qkv_bias = tied, qkv_bias
         self.compute_dtype = compute_dtype
         self.head_blocks = head_blocks
+        if not (isinstance(eta, float) and 0.0 < eta < float("inf")):
+            raise ValueError(f"eta must be a positive finite float, got {eta!r}")
+        self._eta = eta
         self.validate()
 
     # ---- the layout ---------------------------------------------------------------------
@@ -65,6 +68,22 @@ class DecoderComputation(DeclaredComputation):
     @property
     def N(self) -> int:
         return self.n_s * self.n
+
+    @property
+    def eta(self) -> float:
+        return self._eta
+
+    @cached_property
+    def linear_weights(self) -> dict[str, tuple[int, ...]]:
+        """Each linear weight's weight-gradient products (reference decoder.py:522-528): one
+        ``L{l}.G_{x}`` per layer weight, and the head's row blocks when the head is untied."""
+        by_name = {spec.name: spec.m for spec in self.products}
+        out = {self.w(l, x): (by_name[f"L{l}.G_{x}"],)
+               for l in range(1, self.L + 1) for x in LINEARS}
+        if not self.tied:
+            out[_W_OUT] = tuple(by_name[self.head_name("G", b)]
+                                for b in range(self.head_blocks))
+        return out
 
     @property
     def weight_dtype(self) -> torch.dtype:

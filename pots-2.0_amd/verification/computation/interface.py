@@ -2,7 +2,8 @@
 
 Reference: verification/computation/interface.py:60-330. Only the layout contract the hot
 path needs is kept: ``ProductSpec`` (which leaf is ``P_m``, its shapes, its challenge width),
-the leaf order ``[records n_s | W_t n_w | P_1..P_M | W_{t+1} n_w]`` and the index helpers.
+the leaf order ``[records n_s | W_t n_w | P_1..P_M | W_{t+1} n_w]``, the index helpers, and
+check 6a's declaration (the step size ``eta``, ``linear_weights``, ``chain_gradient``).
 The model replay that rebuilds operands is not part of this build; check 5 takes its
 operands from a :class:`Replay` the caller supplies.
 """
@@ -11,7 +12,7 @@ from __future__ import annotations
 
 import abc
 import enum
-from collections.abc import Sequence
+from collections.abc import Iterable, Sequence
 from dataclasses import dataclass
 from functools import cached_property
 from typing import Any
@@ -88,6 +89,18 @@ class Replay(abc.ABC):
         return a, b
 
 
+def chain_gradient(parts: Iterable[torch.Tensor], dtype: torch.dtype) -> torch.Tensor:
+    """A weight's gradient from its committed weight-gradient products: each widened to
+    ``dtype`` and added in order, out of place, ``((P_0 + P_1) + P_2) + …`` (reference
+    interface.py:169-180). One part is that part widened."""
+    g: torch.Tensor | None = None
+    for p in parts:
+        g = p.to(dtype) if g is None else g + p.to(dtype)
+    if g is None:
+        raise ValueError("a gradient needs at least one product")
+    return g
+
+
 class DeclaredComputation(abc.ABC):
     """The layout and inventory of one step's transcript."""
 
@@ -110,6 +123,18 @@ class DeclaredComputation(abc.ABC):
     @abc.abstractmethod
     def products(self) -> tuple[ProductSpec, ...]:
         ...
+
+    @property
+    def eta(self) -> float:
+        """The constant SGD step size, fixed in ``C`` (reference interface.py:225-228)."""
+        raise NotImplementedError(f"{type(self).__name__} declares no step size")
+
+    @property
+    def linear_weights(self) -> dict[str, tuple[int, ...]]:
+        """Check 6a: weight name -> the ``m`` of the committed weight-gradient products whose
+        :func:`chain_gradient`, in this order, is its whole gradient (reference
+        interface.py:245-249). None by default."""
+        return {}
 
     @property
     def weight_dtype(self) -> torch.dtype:

@@ -7,7 +7,9 @@ running the model: each product's operands ``A_m, B_m`` are drawn i.i.d. normal 
 by ``1/√q`` so ``P`` stays O(1)), in the compute dtype, and ``P_m = A_m·B_m (+ 1·bᵀ)`` is
 computed by torch on the GPU with fp32 accumulation and rounded to the compute dtype, as a
 bf16-autocast step stores it. Attention members of one layer and role are generated and
-multiplied as one stacked batch. ``W_{t+1} = W_t − η·G`` with a synthetic gradient.
+multiplied as one stacked batch. A linear weight's ``W_{t+1}`` is ``W_t − η·G`` with ``G`` the
+chain of its committed weight-gradient products (so check 6a holds), a glue weight's moves
+by a random step.
 
 The verifier's work per product (hash the leaf, measure ``A(B·r) − P·r``) depends only on
 shapes and dtypes, so the timings equal a real step's; the values are not a trained model's.
@@ -20,7 +22,8 @@ from dataclasses import dataclass, field
 import torch
 
 from setup.records import Record
-from verification.computation.interface import DeclaredComputation, ProductSpec, Replay
+from verification.computation.interface import (DeclaredComputation, ProductSpec, Replay,
+                                               chain_gradient)
 
 
 @dataclass
@@ -108,9 +111,22 @@ def synthetic_step(c: DeclaredComputation, *, seed: int = 0, device: str = "cuda
             if operands:
                 ops[spec.m] = (a[i], b[i])
         del a, b
+    # W_{t+1}: a linear weight takes the SGD step from its committed gradient products, as
+    # the optimizer writes it (``W_t.add(G, alpha=-η)``, check 6a's honest case); the other
+    # (glue) weights move by a random step of the same size.
+    try:
+        eta = c.eta
+    except NotImplementedError:
+        pass
+    linear = c.linear_weights
     for name in c.weight_names:
         w = w_t[name]
-        leaves.append(w - eta * torch.randn(w.shape, generator=g, device=dev))
+        if name in linear:
+            grad = chain_gradient((leaves[c.product_index(m)] for m in linear[name]),
+                                  torch.float32)
+            leaves.append(torch.add(w, grad, alpha=-eta))
+        else:
+            leaves.append(w - eta * torch.randn(w.shape, generator=g, device=dev))
     return SyntheticStep(c, leaves, ops)
 
 

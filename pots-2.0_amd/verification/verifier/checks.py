@@ -5,9 +5,10 @@ Reference: verification/verifier/checks.py:204-251 (``check_2_commitment``), :25
 ``_judge_product``). Each check returns ``None`` on acceptance or a :class:`Rejection`, with
 the reference's check ids, rejection kinds and detail strings.
 
-Of the reference's order ``4 → 7 → 2 → 6a → 5 → 6b → 2.root`` this build runs the slots of the
-hot path, :data:`DEFAULT_ORDER` = ``2 → 5 → 2.root``. Checks 4 (batch anchor), 7 (chaining),
-6a and 6b (update identity) are not part of it.
+Of the reference's order ``4 → 7 → 2 → 6a → 5 → 6b → 2.root`` this build runs
+:data:`DEFAULT_ORDER` = ``2 → 6a → 5 → 2.root``. Checks 4 (batch anchor), 7 (chaining) and 6b
+(the glue weights' update identity, which needs the model replay's glue gradients) are not
+part of it.
 
 - **Check 2's read** reads every leaf once, in order, hashes them on the GPU (through
   ``leaf_hashes_of``, which keeps the first-error-in-order semantics: a malformed or
@@ -18,6 +19,8 @@ hot path, :data:`DEFAULT_ORDER` = ``2 → 5 → 2.root``. Checks 4 (batch anchor
   back once, then records and judges the products in canonical order on the host exactly as
   the reference does, so the first failing product rejects with the reference's message. The
   device verdict kernel judges the same rows; the two must agree on the first failure.
+- **Check 6a** streams every linear weight's ``W_t``, ``W_{t+1}`` and gradient product leaves
+  once on the GPU and words the first failing weight's rejection as the reference does.
 - **Check 2's root comparison** runs last and compares the Merkle root over check 2's hashes
   (built on the GPU) with the claimed root.
 
@@ -37,7 +40,8 @@ import torch
 from verification.commitment import native
 from verification.commitment.leaves import leaf_hashes_of
 from verification.commitment.merkle import DIGEST_SIZE, merkle_root
-from verification.computation.interface import DeclaredComputation, ProductSpec
+from verification.computation.interface import (DeclaredComputation, ProductSpec,
+                                                 chain_gradient)
 from verification.transcript.store import TranscriptStore
 from verification.verifier.bands import Bands, product_class
 from verification.verifier.context import (
@@ -46,6 +50,7 @@ from verification.verifier.context import (
     ProductStat,
     Rejection,
     StepContext,
+    TensorStat,
     _checked,
     _guard,
     _is_digest,
@@ -53,7 +58,7 @@ from verification.verifier.context import (
 from verification.verifier.matmul_check.freivalds import ProductMeasure, finish_row
 
 __all__ = ["DEFAULT_ORDER", "ROOT_SLOT", "CHECKS", "protocol_id", "check_2_commitment",
-           "check_2_root", "check_5_matmuls"]
+           "check_2_root", "check_6a_linear_update", "check_5_matmuls"]
 
 ROOT_SLOT = "2.root"
 
@@ -116,6 +121,73 @@ def check_2_root(store: TranscriptStore, c: DeclaredComputation, ctx: StepContex
     if root != claimed:
         return ctx.reject("2", f"recomputed root {root.hex()[:16]}… != claimed "
                                f"{claimed.hex()[:16]}…")
+    return None
+
+
+# ---- check 6a: the update identity of the linear weights -------------------------------
+
+
+def _entry_values(w: native.UpdateWeight, i: int, eta: float, eps_w: float
+                  ) -> tuple[float, float]:
+    """``(|R_i|, scale_i)`` of one entry for a rejection's wording, with the reference's fp32
+    operations (checks.py:430-432) on that entry alone."""
+    one = [x.reshape(-1)[i:i + 1].cpu() for x in (w.w_t, w.w_next)]
+    g = chain_gradient([p.reshape(-1)[i:i + 1].cpu() for p in w.parts], torch.float32)
+    eta_g = eta * g
+    r = (one[1] - (one[0] - eta_g)).abs()
+    scale = eps_w * (one[0].abs() + eta_g.abs())
+    return float(r), float(scale)
+
+
+@_checked
+def check_6a_linear_update(store: TranscriptStore, c: DeclaredComputation, ctx: StepContext,
+                           bands: Bands) -> Rejection | None:
+    """Check 6 for every linear weight, from its committed weight-gradient leaves
+    (checks.py:454-467 with ``_update_identity``, :380-451).
+
+    ``W_t``, ``W_{t+1}`` and the gradient's product leaves are read from check 2's committed
+    leaves; one GPU pass over every linear weight gives each weight's ``ρ_max`` (bit for bit
+    the reference's), its first non-finite ``R`` or scale and its first ``ρ`` over ``τ_W``.
+    The weights are then recorded and judged in declaration order: the first one with a
+    non-finite entry, or (when judging) an entry over its band, rejects with the reference's
+    wording, and the weights after it are not recorded.
+    """
+    names = list(c.linear_weights)
+    if not names:
+        return None
+    leaves = ctx.state.committed()
+    dev = torch.device("cuda", torch.cuda.current_device())
+    with _guard(ctx, "6a", _AFTER_COMMIT):
+        weights = []
+        for name in names:
+            w_t = leaves.leaf(c.w_t_index(name)).to(dev)
+            w_next = leaves.leaf(c.w_next_index(name)).to(dev)
+            parts = [leaves.leaf(c.product_index(m)).to(dev) for m in c.linear_weights[name]]
+            for t in (w_next, *parts):
+                if tuple(t.shape) != tuple(w_t.shape):
+                    raise RuntimeError(f"{name}: gradient or update of shape {tuple(t.shape)} "
+                                       f"!= {tuple(w_t.shape)}")
+            weights.append(native.UpdateWeight(w_t.contiguous(), w_next.contiguous(),
+                                               [p.contiguous() for p in parts],
+                                               bands.tau_w_for(name)))
+    with ctx.timed("6a.measure"):
+        plan = native.get().update_plan(weights, c.eta, ctx.eps_w)
+        try:
+            results = native.UpdatePlan.decode(plan.run())
+        finally:
+            plan.close()
+    for name, w, (rho_max, first_nf, first_over) in zip(names, weights, results):
+        ctx.stats.tensors.append(TensorStat(name, "6a", rho_max))
+        if first_nf is not None:
+            r, scale = _entry_values(w, first_nf, c.eta, ctx.eps_w)
+            return ctx.reject("6a", f"{name}: entry {first_nf} has a non-finite residual or "
+                                    f"bound (|R| = {r:.3e}, scale {scale:.3e})")
+        if ctx.judge and first_over is not None:
+            r, scale = _entry_values(w, first_over, c.eta, ctx.eps_w)
+            tau_w = w.tau_w
+            return ctx.reject("6a", f"{name}: entry {first_over} has |R| = {r:.3e}, bound "
+                                    f"{tau_w * scale:.3e} (ρ_max = {rho_max:.3g}, "
+                                    f"τ_W = {tau_w:g})")
     return None
 
 
@@ -221,7 +293,8 @@ def _judge_product(c: DeclaredComputation, spec: ProductSpec, mp: ProductMeasure
 
 CHECKS: dict[str, Callable[..., Rejection | None]] = {
     "2": check_2_commitment,
+    "6a": check_6a_linear_update,
     "5": check_5_matmuls,
     ROOT_SLOT: check_2_root,
 }
-DEFAULT_ORDER: tuple[str, ...] = ("2", "5", ROOT_SLOT)
+DEFAULT_ORDER: tuple[str, ...] = ("2", "6a", "5", ROOT_SLOT)

@@ -86,8 +86,8 @@ class ProductStat:
 
 @dataclass(frozen=True)
 class TensorStat:
-    """Check 6's number for one weight (kept for the statistics' shape; check 6 is not part
-    of this build)."""
+    """Check 6's number for one weight: ``ρ_max = max_i |R_i| / (ε_W·(|W_t,i| + |η·G_i|))``
+    (reference context.py:128-133)."""
 
     weight: str
     check_id: str

@@ -1,11 +1,11 @@
 """The per-step verifier for the hot path's checks (reference: verification/verifier/driver.py
 :223-271, ``Verifier.verify_step``).
 
-``verify_step(t, store)`` runs :data:`checks.DEFAULT_ORDER` (``2 → 5 → 2.root``) on step
+``verify_step(t, store)`` runs :data:`checks.DEFAULT_ORDER` (``2 → 6a → 5 → 2.root``) on step
 ``t`` with one :class:`StepContext`, stops at the first rejection and keeps it, and keeps the
 step's statistics and per-slot timings as the reference does (``stats[t]``, ``timings[t]``).
 The run-level state of the reference's verifier (the data schedule, the weight-hash chain,
-checks 0, 1, 4, 6a, 6b, 7 and 8, the record pass after a rejection) is not part of this build.
+checks 0, 1, 4, 6b, 7 and 8, the record pass after a rejection) is not part of this build.
 """
 
 from __future__ import annotations
@@ -23,7 +23,7 @@ __all__ = ["Verifier"]
 
 
 class Verifier:
-    """Checks 2, 5 and 2.root of consecutive steps of one run under one computation."""
+    """Checks 2, 6a, 5 and 2.root of consecutive steps of one run under one computation."""
 
     def __init__(self, c: DeclaredComputation, *, k: int, bands: Bands | None = None,
                  calibrate: bool = False, kappa_guard: bool = True,

@@ -333,3 +333,109 @@ def test_f64_yardstick_agrees_with_fp32_formulas():
     f32 = O.measure_product_row(a, b, p, r)
     f64 = O.measure_row_f64(a, b, p, r)
     assert f32[:4] == pytest.approx(f64[:4], rel=1e-5)
+
+
+# ---- check 6a: the update identity ---------------------------------------------------------
+# Pinned by exact cases (power-of-two entries make every fp32 operation exact, so R, scale and
+# ρ have closed forms) and by the outcomes the reference's own tests state
+# (tests/verification/verifier/test_update_identity.py).
+
+EPS_W, TAU_W, ETA = 2.0**-24, 4.0, 1e-3
+
+
+def _honest_update(shape, seed=0, eta=ETA):
+    gen = torch.Generator().manual_seed(seed)
+    w = torch.randn(shape, generator=gen)
+    g = torch.randn(shape, generator=gen)
+    return w, torch.add(w, g, alpha=-eta), g  # the optimizer's step
+
+
+def _ulps(x, i, q):
+    x = x.clone()
+    for _ in range(q):
+        x.view(-1)[i] = torch.nextafter(x.view(-1)[i], torch.tensor(math.inf))
+    return x
+
+
+def test_update_reference_rounding_gives_zero_rho():
+    w, _, g = _honest_update((64, 32))
+    out = O.update_identity(w, w - ETA * g, [g], ETA, EPS_W, TAU_W)
+    assert out["rho_max"] == 0.0 and out["first_nonfinite"] is None and out["first_over"] is None
+
+
+def test_update_closed_forms():
+    # entry 0: R = 2^-20, scale = 2^-24 -> ρ = 16; entry 1: ηG = 1, W − ηG = 0, R = 2^-30,
+    # scale = 2^-24·2 -> ρ = 2^-7; entry 2: 0/0 -> 0; entry 3: R > 0 over scale 0 -> inf;
+    # entry 4: R = 0 -> 0.
+    w = torch.tensor([1.0, 1.0, 0.0, 0.0, 2.0])
+    g = torch.tensor([0.0, 1024.0, 0.0, 0.0, 0.0])
+    wn = torch.tensor([1.0 + 2.0**-20, 2.0**-30, 0.0, 2.0**-100, 2.0])
+    out = O.update_identity(w, wn, [g], 2.0**-10, EPS_W, TAU_W)
+    r, s = out["r"].double(), out["scale"].double()
+    assert r.tolist() == [2.0**-20, 2.0**-30, 0.0, 2.0**-100, 0.0]
+    assert s.tolist() == [2.0**-24, 2.0**-23, 0.0, 0.0, 2.0**-23]
+    assert out["rho_max"] == math.inf
+    assert out["first_over"] == 0 and out["first_nonfinite"] is None
+    out = O.update_identity(w[:2], wn[:2], [g[:2]], 2.0**-10, EPS_W, 100.0)
+    assert out["rho_max"] == 16.0 and out["first_over"] is None
+
+
+def test_update_chain_gradient_adds_in_order():
+    # ((1 + 2^-24) + 2^-24) rounds to 1 in fp32; 1 + (2^-24 + 2^-24) would not
+    parts = [torch.tensor([1.0]), torch.tensor([2.0**-24]), torch.tensor([2.0**-24])]
+    assert O.chain_gradient([p.to(torch.bfloat16) for p in parts]).item() == 1.0
+    assert O.chain_gradient([parts[0], parts[1] + parts[2]]).item() == 1.0 + 2.0**-23
+
+
+def test_update_honest_step_accepts():
+    for seed, shape in enumerate([(48, 40), (7, 3, 33), (300,)]):
+        w, wn, g = _honest_update(shape, seed)
+        out = O.update_identity(w, wn, [g], ETA, EPS_W, TAU_W)
+        assert out["first_nonfinite"] is None and out["first_over"] is None
+        assert out["rho_max"] <= TAU_W
+
+
+def test_update_forged_and_tied_entries():
+    w, _, g = _honest_update((40, 40), seed=3)
+    wn = w - ETA * g
+    for i in range(0, w.numel(), 7):
+        wn = _ulps(wn, i, 1)
+    assert 1.0 < O.update_identity(w, wn, [g], ETA, EPS_W, TAU_W)["rho_max"] <= 2.0
+    w, wn, g = _honest_update((50, 30), seed=1)
+    out = O.update_identity(w, _ulps(wn, 777, 9), [g], ETA, EPS_W, TAU_W)
+    assert out["rho_max"] > TAU_W and out["first_over"] == 777
+    # ρ exactly at τ accepts; the next double below rejects
+    w, wn, g = _honest_update((20, 20), seed=2)
+    forged = _ulps(wn, 5, 5)
+    rho = O.update_identity(w, forged, [g], ETA, EPS_W, math.inf)["rho_max"]
+    assert O.update_identity(w, forged, [g], ETA, EPS_W, rho)["first_over"] is None
+    assert O.update_identity(w, forged, [g], ETA, EPS_W, math.nextafter(rho, 0.0))[
+        "first_over"] == 5
+
+
+@pytest.mark.parametrize("bad", [math.nan, math.inf, -math.inf])
+def test_update_non_finite_inputs(bad):
+    w, wn, g = _honest_update((30, 30), seed=4)
+    g = g.clone()
+    g.view(-1)[123] = bad
+    assert O.update_identity(w, wn, [g], ETA, EPS_W, TAU_W)["first_nonfinite"] == 123
+    w, wn, g = _honest_update((30, 30), seed=5)
+    wn = wn.clone()
+    wn.view(-1)[17] = math.nan
+    out = O.update_identity(w, wn, [g], ETA, EPS_W, TAU_W)
+    assert out["first_nonfinite"] == 17 and math.isnan(out["rho_max"])
+
+
+def test_update_scale_overflow_and_underflowing_ratio():
+    # |W_t| + |η·G| overflows while W_t − η·G = 0 and R stay finite
+    w, wn, g = _honest_update((10, 10), seed=6, eta=1.0)
+    w, wn, g = w.clone(), wn.clone(), g.clone()
+    w.view(-1)[9] = g.view(-1)[9] = 3e38
+    wn.view(-1)[9] = 0.0
+    assert O.update_identity(w, wn, [g], 1.0, EPS_W, TAU_W)["first_nonfinite"] == 9
+    # an fp32 quotient that underflows keeps its float64 value; 0/0 entries count as 0
+    w, g, wn = torch.zeros(4, 4), torch.zeros(4, 4), torch.zeros(4, 4)
+    w.view(-1)[9] = g.view(-1)[9] = 1e38
+    wn.view(-1)[9] = 1.4e-45
+    out = O.update_identity(w, wn, [g], 1.0, EPS_W, TAU_W)
+    assert out["first_over"] is None and 0.0 < out["rho_max"] < 1e-70
