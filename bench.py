@@ -345,6 +345,32 @@ def main() -> int:
     log("[bench] serialised stages (ms): " +
         ", ".join(f"{nm} {t:.3f}" for nm, t in stage_ms.items()) + f"; total {serial_ms:.2f}")
 
+    # Check 6a (the update identity of every linear weight) beside the headline step: it is
+    # part of the reference's verify_step but not of the metric's bytes, so it is timed on its
+    # own and reported in parts.
+    check_6a = None
+    if c.linear_weights:
+        uw = [native.UpdateWeight(step.leaves[c.w_t_index(nm)], step.leaves[c.w_next_index(nm)],
+                                  [step.leaves[c.product_index(m)] for m in ms], 4.0)
+              for nm, ms in c.linear_weights.items()]
+        uplan = lib.update_plan(uw, c.eta, 2.0**-24)
+        uout = uplan.run(stream=stream)
+        torch.cuda.synchronize()
+        n_over = sum(r[2] is not None or r[1] is not None for r in native.UpdatePlan.decode(uout))
+        ue = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ue[0].record(stream)
+        for _ in range(n_stage_runs):
+            uplan.run(uout, stream)
+        ue[1].record(stream)
+        torch.cuda.synchronize()
+        u_ms = ue[0].elapsed_time(ue[1]) / n_stage_runs
+        check_6a = {"ms": round(u_ms, 4), "bytes": uplan.bytes,
+                    "gbps": round(uplan.bytes / (u_ms * 1e-3) / 1e9, 1),
+                    "weights": len(uw), "rejected": n_over}
+        log(f"[bench] check 6a: {len(uw)} linear weights, {uplan.bytes / 1e9:.2f} GB in "
+            f"{u_ms:.3f} ms ({check_6a['gbps']:.0f} GB/s), {n_over} rejected")
+        uplan.close()
+
     # Algorithmic HBM bytes of each single-kernel stage: the operand every element of which
     # the kernel reads once (A, B or P of every product; every leaf's message bytes plus one
     # 32-byte chaining value written per 1 KiB chunk).
@@ -385,7 +411,8 @@ def main() -> int:
                   "freivalds_ms": round(fv_ms, 3),
                   "freivalds_gbps": round(fv_bytes / (fv_ms * 1e-3) / 1e9, 1),
                   "stages_ms": {nm: round(t, 4) for nm, t in stage_ms.items()},
-                  "rejected": n_rej},
+                  "rejected": n_rej,
+                  "check_6a": check_6a},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic_from_profile(dom_name) if dom == "hash.chunks" else None,

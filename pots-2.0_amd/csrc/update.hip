@@ -13,9 +13,10 @@
 // scale_i is not finite, and the first index whose ρ_i is not ≤ τ_W; the host words the
 // reference's rejection from those.
 //
-// Work split: a block of 256 threads takes 4096 consecutive entries of one weight (16 per
-// thread, coalesced 4-byte loads); the block reduces its maximum and first indices and makes
-// one atomic update per output. ρ_max is kept as the bit pattern of a non-negative double,
+// Work split: a block of 256 threads takes 8192 consecutive entries of one weight, a thread 8
+// consecutive entries per step with 16-byte loads (4-byte loads where a pointer is not 16-byte
+// aligned, and for a weight's last partial step); each wave reduces its maximum and first
+// indices and makes one atomic update per output. ρ_max is kept as the bit pattern of a non-negative double,
 // whose unsigned order is its numeric order with NaN above +inf.
 #include <math.h>
 #include <string.h>
@@ -29,14 +30,17 @@
 namespace pots {
 
 constexpr uint32_t kUpdThreads = 256;
-constexpr uint32_t kUpdPerThread = 16;
-constexpr uint32_t kUpdTile = kUpdThreads * kUpdPerThread;
+constexpr uint32_t kUpdVec = 8;    // consecutive entries a thread takes per step
+constexpr uint32_t kUpdSteps = 4;  // steps per block
+constexpr uint32_t kUpdTile = kUpdThreads * kUpdVec * kUpdSteps;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct UpdJob {
   uint64_t w_t, w_next;                    // fp32 [n]
   uint64_t parts[POTS_UPDATE_MAX_PARTS];   // gradient parts, [n] each
   uint32_t part_dt[POTS_UPDATE_MAX_PARTS]; // 0 fp32, 1 bf16
-  uint32_t n_parts, pad;
+  uint32_t n_parts, vec;  // vec: every pointer 16-byte aligned (8-entry vector loads)
   uint64_t n;
   uint64_t block_first;
   double tau_w;
@@ -63,6 +67,46 @@ __global__ __launch_bounds__(kUpdThreads) void update_init(UpdOut* __restrict__ 
   }
 }
 
+// The per-thread state of the reduction.
+struct UpdAcc {
+  double rho_max = 0.0;
+  bool nan_seen = false;
+  uint64_t first_nf = ~0ull, first_over = ~0ull;
+  __device__ __forceinline__ void add(float w, float w1, float g, float eta, float eps_w,
+                                      double tau_w, uint64_t i) {
+    const float eg = eta * g;
+    const float r = fabsf(w1 - (w - eg));
+    const float s = eps_w * (fabsf(w) + fabsf(eg));
+    if (!(isfinite(r) && isfinite(s)) && i < first_nf) first_nf = i;
+    const double rho = r == 0.f ? 0.0 : (double)r / (double)s;
+    if (rho != rho) nan_seen = true;
+    else if (rho > rho_max) rho_max = rho;
+    if (!(rho <= tau_w) && i < first_over) first_over = i;
+  }
+};
+
+__device__ __forceinline__ void load8(const float* p, uint64_t i, float v[8]) {
+  const u32x4 a = gload<u32x4>(p + i), b = gload<u32x4>(p + i + 4);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    v[e] = __uint_as_float(a[e]);
+    v[4 + e] = __uint_as_float(b[e]);
+  }
+}
+
+__device__ __forceinline__ void load8_part(uint64_t base, uint32_t dt, uint64_t i, float v[8]) {
+  if (dt == 1) {
+    const u32x4 a = gload<u32x4>(reinterpret_cast<const uint16_t*>(base) + i);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[2 * e] = __uint_as_float(a[e] << 16);
+      v[2 * e + 1] = __uint_as_float(a[e] & 0xFFFF0000u);
+    }
+  } else {
+    load8(reinterpret_cast<const float*>(base), i, v);
+  }
+}
+
 __global__ __launch_bounds__(kUpdThreads) void update_kernel(const UpdJob* __restrict__ jobs,
                                                              const uint32_t* __restrict__ blk_job,
                                                              float eta, float eps_w,
@@ -73,26 +117,36 @@ __global__ __launch_bounds__(kUpdThreads) void update_kernel(const UpdJob* __res
   const uint64_t base = (uint64_t)(blockIdx.x - J.block_first) * kUpdTile;
   const float* wt = reinterpret_cast<const float*>(J.w_t);
   const float* wn = reinterpret_cast<const float*>(J.w_next);
-  double rho_max = 0.0;
-  bool nan_seen = false;
-  uint64_t first_nf = ~0ull, first_over = ~0ull;
-#pragma unroll 4
-  for (uint32_t e = 0; e < kUpdPerThread; e++) {
-    const uint64_t i = base + (uint64_t)e * kUpdThreads + threadIdx.x;
-    if (i >= n) break;
-    float g = load_part(J.parts[0], J.part_dt[0], i);
-    for (uint32_t p = 1; p < J.n_parts; p++) g = g + load_part(J.parts[p], J.part_dt[p], i);
-    const float w = gload<float>(wt + i), w1 = gload<float>(wn + i);
-    const float eg = eta * g;
-    const float r = fabsf(w1 - (w - eg));
-    const float s = eps_w * (fabsf(w) + fabsf(eg));
-    if (!(isfinite(r) && isfinite(s)) && i < first_nf) first_nf = i;
-    const double rho = r == 0.f ? 0.0 : (double)r / (double)s;
-    if (rho != rho) nan_seen = true;
-    else if (rho > rho_max) rho_max = rho;
-    if (!(rho <= J.tau_w) && i < first_over) first_over = i;
+  const double tau_w = J.tau_w;
+  UpdAcc acc;
+#pragma unroll 1
+  for (uint32_t st = 0; st < kUpdSteps; st++) {
+    const uint64_t i0 = base + ((uint64_t)st * kUpdThreads + threadIdx.x) * kUpdVec;
+    if (i0 >= n) break;
+    if (J.vec && i0 + kUpdVec <= n) {
+      // 8 consecutive entries with 16-byte loads, every load issued before the arithmetic
+      float w[8], w1[8], g[8], h[8];
+      load8(wt, i0, w);
+      load8(wn, i0, w1);
+      load8_part(J.parts[0], J.part_dt[0], i0, g);
+      for (uint32_t p = 1; p < J.n_parts; p++) {
+        load8_part(J.parts[p], J.part_dt[p], i0, h);
+#pragma unroll
+        for (int e = 0; e < 8; e++) g[e] = g[e] + h[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc.add(w[e], w1[e], g[e], eta, eps_w, tau_w, i0 + e);
+    } else {
+      for (uint64_t i = i0; i < i0 + kUpdVec && i < n; i++) {
+        float g = load_part(J.parts[0], J.part_dt[0], i);
+        for (uint32_t p = 1; p < J.n_parts; p++) g = g + load_part(J.parts[p], J.part_dt[p], i);
+        acc.add(gload<float>(wt + i), gload<float>(wn + i), g, eta, eps_w, tau_w, i);
+      }
+    }
   }
-  uint64_t bits = nan_seen ? 0x7FF8000000000000ull : (uint64_t)__double_as_longlong(rho_max);
+  uint64_t bits = acc.nan_seen ? 0x7FF8000000000000ull
+                               : (uint64_t)__double_as_longlong(acc.rho_max);
+  uint64_t first_nf = acc.first_nf, first_over = acc.first_over;
   // wave reductions, then one lane per wave updates the weight's outputs
   for (int o = 32; o > 0; o >>= 1) {
     const uint64_t b2 = __shfl_xor(bits, o);
@@ -149,6 +203,9 @@ extern "C" int pots_update_plan_create(size_t n, const pots_update_weight* weigh
     }
     J.n = w.n;
     J.tau_w = w.tau_w;
+    bool aligned = (J.w_t % 16 == 0) && (J.w_next % 16 == 0);
+    for (uint32_t p = 0; p < w.n_parts; p++) aligned = aligned && J.parts[p] % 16 == 0;
+    J.vec = aligned ? 1 : 0;
     J.block_first = blk.size();
     const uint64_t nb = (w.n + kUpdTile - 1) / kUpdTile;
     if (blk.size() + nb >= 0x7FFFFFFFull) return POTS_E_ARG;
