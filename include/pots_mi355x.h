@@ -107,6 +107,33 @@ int pots_leaf_plan_run_stage(void *plan, int stage, uint8_t *d_out, uint32_t *d_
  * Results do not depend on it. No counterpart in the reference. */
 int pots_leaf_plan_set_grid(void *plan, uint32_t max_blocks);
 
+/* As pots_leaf_plan_create, and the leaves that are the P operand of a product of fv_plan (a
+ * Freivalds plan, below) also have that product's P-pass sums taken by the chunk kernel while
+ * it hashes them, so P is read from HBM once for both checks. A product qualifies when the
+ * plan's k is 4, its P is the leaf's whole payload (contiguous, same dtype: bf16 or fp32, at a
+ * 16-byte aligned address after a 12-byte 0x00 || header, i.e. a 2-D tensor leaf), its rows
+ * hold at least 1 KiB, and no other product shares that P. The Freivalds plan's stage 4 then
+ * reads what the chunk stage (stage 1 of this plan) wrote for the same claimed root: run
+ * fv stage 0, then this plan's stage 1, before fv stage 4 (pots_step_run keeps that order on
+ * one stream; pots_fv_plan_run refuses a fused plan). A Freivalds plan is fused with at most
+ * one leaf plan; destroy the leaf plan first. Digests are those of pots_leaf_plan_create; the
+ * rows agree with the unfused plan's to fp32 rounding of the sums' order. No counterpart in
+ * the reference: it reads P once in check 2 and again in check 5. */
+int pots_leaf_plan_create_fused(size_t n, const uint8_t *hdr_buf, const uint64_t *hdr_off,
+                                const uint32_t *hdr_len, const uint32_t *hdr_idx,
+                                const uint64_t *payload_ptr, const uint64_t *payload_len,
+                                const uint8_t *kind, void *fv_plan, void **plan);
+
+/* Leaves of the plan whose product's P-pass sums its chunk stage takes (0 for an unfused
+ * plan). */
+uint32_t pots_leaf_plan_fused(const void *plan);
+
+/* One step on one stream: fv stage 0, the leaf plan's stages, fv stages 1-5 (digests and
+ * first-bad as pots_leaf_plan_run, rows as pots_fv_plan_run). For a fused pair of plans and
+ * for two independent ones alike. No counterpart in the reference. */
+int pots_step_run(void *leaf_plan, void *fv_plan, const uint8_t *d_key, uint8_t *d_digests,
+                  uint32_t *d_first_bad, double *d_rows, void *stream);
+
 /* Chunks (1 KiB BLAKE3 chunks) and message bytes the plan hashes. */
 uint64_t pots_leaf_plan_chunks(const void *plan);
 uint64_t pots_leaf_plan_bytes(const void *plan);

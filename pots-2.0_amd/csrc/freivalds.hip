@@ -43,6 +43,7 @@
 
 #include <algorithm>
 #include <new>
+#include <unordered_map>
 #include <vector>
 
 #include "common.h"
@@ -659,6 +660,72 @@ __global__ __launch_bounds__(256) void finish_final(const FinJob* __restrict__ j
   out[4] = J.bias != 0 ? bout[pi].bsq : 0.0;
 }
 
+// ---- P-pass sums of fused products, from the chunk kernel's run records -------------------
+
+// One fused product (freivalds.h): its P is a leaf whose message is 0x00 || header (head
+// bytes) || P, and the chunk kernel wrote one record per run of a row.
+struct FixJob {
+  uint64_t p, r, seg;        // P, R [w][4], run records [n][J]
+  uint64_t pdot, pabs, psq;  // the P job's partials: column chunk 0 of [rows_pad]
+  uint64_t row_first;        // prefix of rows over the jobs before it
+  uint32_t n, w;
+  uint32_t head, esz;
+  uint32_t J, pad;
+};
+static_assert(sizeof(FixJob) == 80, "FixJob layout");
+
+// One thread per row: the row's records in chunk order (fp64), then the elements of the
+// leaf's first bytes up to the first 128-byte boundary of the message (row 0) and of its last
+// bytes after the last one (the last row), which no chunk's interior pairs took. Rounded to
+// the P job's partial formats as one column chunk.
+__global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ jobs,
+                                                  uint32_t n_jobs, uint64_t n_threads) {
+  const uint64_t g = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= n_threads) return;
+  uint32_t lo = 0, hi = n_jobs - 1;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (jobs[mid].row_first <= g) lo = mid;
+    else hi = mid - 1;
+  }
+  const FixJob J = jobs[lo];
+  const uint32_t i = (uint32_t)(g - J.row_first);
+  const uint64_t rb = (uint64_t)J.w * J.esz, H = J.head, L = H + (uint64_t)J.n * rb;
+  const uint64_t hc = (H + 127) & ~uint64_t(127), lf = L & ~uint64_t(127);
+  const uint64_t fs = max<uint64_t>(H + i * rb, hc), fe = min<uint64_t>(H + (i + 1) * rb, lf);
+  double d[4] = {0.0, 0.0, 0.0, 0.0}, s1 = 0.0, s2 = 0.0;
+  if (fs < fe) {
+    const char* rec = reinterpret_cast<const char*>(J.seg) + (uint64_t)kRunBytes * i * J.J;
+    for (uint64_t c = fs >> 10; c <= (fe - 1) >> 10; c++, rec += kRunBytes) {
+      const v4f32 a = gload<v4f32>(rec);
+      const u32x4 b = gload<u32x4>(rec + 16);
+      for (int j = 0; j < 4; j++) d[j] += (double)a[j];
+      s1 += (double)__uint_as_float(b.x);
+      s2 += __longlong_as_double((long long)((uint64_t)b.w << 32 | b.z));
+    }
+  }
+  const float* R = reinterpret_cast<const float*>(J.r);
+  auto rest = [&](uint64_t b0, uint64_t b1) {  // payload bytes [b0, b1) of row i
+    for (uint64_t e = b0 / J.esz; e < b1 / J.esz; e++) {
+      const float x = J.esz == 2
+                          ? __uint_as_float((uint32_t)gload<uint16_t>(
+                                                reinterpret_cast<const uint16_t*>(J.p) + e)
+                                            << 16)
+                          : gload<float>(reinterpret_cast<const float*>(J.p) + e);
+      const uint64_t col = e - (uint64_t)i * J.w;
+      for (int j = 0; j < 4; j++) d[j] += (double)x * (double)gload<float>(R + col * 4 + j);
+      s1 += fabs((double)x);
+      s2 += (double)x * (double)x;
+    }
+  };
+  if (i == 0 && hc > H) rest(0, hc - H);
+  if (i + 1 == J.n && lf < L) rest(lf - H, L - H);
+  float* pdot = reinterpret_cast<float*>(J.pdot);
+  for (int j = 0; j < 4; j++) gstore<float>(pdot + (uint64_t)i * 4 + j, (float)d[j]);
+  gstore<float>(reinterpret_cast<float*>(J.pabs) + i, (float)s1);
+  gstore<double>(reinterpret_cast<double*>(J.psq) + i, s2);
+}
+
 // ---- the plan ---------------------------------------------------------------------------
 
 struct PassLaunch {
@@ -699,6 +766,20 @@ struct FvPlan {
   bool need_b3 = false, need_f4 = false;
   uint64_t bytes = 0;  // algorithmic bytes: A, B, P read once
   uint64_t r_floats = 0;
+  // Host copies kept for fusing with a leaf plan.
+  std::vector<pots_fv_product> h_prods;
+  std::vector<uint64_t> h_r_off;    // product i's R at d_r + h_r_off[i] floats
+  std::vector<PassJob> h_jobs;      // the ordered job array
+  std::vector<uint32_t> h_src;      // original job index of each ordered job
+  std::vector<uint32_t> h_blk;      // the block -> job table
+  std::vector<FinJob> h_fin;
+  std::unordered_map<uint64_t, int64_t> p_index;  // P address -> product (-1: shared)
+  // Fused products: their run records and fix-up jobs, one allocation.
+  bool fused = false;
+  char* fbase = nullptr;
+  FixJob* d_fix = nullptr;
+  uint32_t n_fix = 0;
+  uint64_t n_fix_rows = 0;
 };
 
 // Packed operands (R, B·R) hold whole 32-row groups, one bf16 K-step of the row pass; rows past
@@ -1065,9 +1146,160 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     delete P;
     return rc;
   }
+  P->h_prods.assign(prods, prods + n);
+  P->h_r_off.resize(n);
+  for (size_t i = 0; i < n; i++) {
+    P->h_r_off[i] = items[i].out_off;
+    const uint64_t a = reinterpret_cast<uint64_t>(prods[i].p);
+    auto it = P->p_index.find(a);
+    if (it == P->p_index.end()) P->p_index.emplace(a, (int64_t)i);
+    else it->second = -1;  // two products share this P: neither is fused
+  }
+  P->h_jobs = std::move(ordered);
+  P->h_src = std::move(ordered_src);
+  P->h_blk = std::move(blk_table);
+  P->h_fin = std::move(fin);
   *plan = P;
   return POTS_E_OK;
 }
+
+namespace pots {
+
+bool fv_fuse_candidate(void* fv, uint64_t payload, uint64_t len, uint32_t kind,
+                       FusedProduct* out) {
+  FvPlan* P = static_cast<FvPlan*>(fv);
+  if (!P || P->fused || P->k != 4) return false;
+  auto it = P->p_index.find(payload);
+  if (it == P->p_index.end() || it->second < 0) return false;
+  const uint32_t i = (uint32_t)it->second;
+  const pots_fv_product& p = P->h_prods[i];
+  const uint32_t esz = p.p_dtype == DT_BF16 ? 2 : 4;
+  const bool kind_ok = (p.p_dtype == DT_BF16 && kind == POTS_KIND_BF16) ||
+                       (p.p_dtype == DT_F32 && kind == POTS_KIND_F32);
+  const uint64_t row_bytes = (uint64_t)p.w * esz;
+  if (!kind_ok || p.ldp != p.w || len != (uint64_t)p.n * row_bytes || row_bytes < 1024 ||
+      row_bytes >= 0x80000000ull || p.n >= 0x80000000u)
+    return false;
+  out->r = reinterpret_cast<uint64_t>(P->d_r) + 4 * P->h_r_off[i];
+  out->n = p.n;
+  out->w = p.w;
+  out->esz = esz;
+  out->prod = i;
+  return true;
+}
+
+int fv_fuse_commit(void* fv, const std::vector<uint32_t>& prods,
+                   const std::vector<uint32_t>& head_len, std::vector<uint64_t>* seg_out) {
+  FvPlan* P = static_cast<FvPlan*>(fv);
+  if (!P || P->fused || prods.size() != head_len.size()) return POTS_E_ARG;
+  const size_t n = P->n;
+  std::vector<uint8_t> fused(n, 0);
+  for (uint32_t i : prods) {
+    if (i >= n || fused[i]) return POTS_E_ARG;
+    fused[i] = 1;
+  }
+  // Position of each original job in the ordered array.
+  std::vector<size_t> pos(3 * n);
+  for (size_t oi = 0; oi < P->h_src.size(); oi++) pos[P->h_src[oi]] = oi;
+
+  // One allocation: the fix-up jobs, then each product's records.
+  size_t at = 0;
+  auto place = [&](size_t bytes) {
+    size_t a = at;
+    at = align_up(at + std::max<size_t>(bytes, 16), 256);
+    return a;
+  };
+  const size_t o_fix = place(prods.size() * sizeof(FixJob));
+  std::vector<size_t> o_seg(prods.size());
+  for (size_t f = 0; f < prods.size(); f++) {
+    const pots_fv_product& p = P->h_prods[prods[f]];
+    const uint64_t rb = (uint64_t)p.w * (p.p_dtype == DT_BF16 ? 2 : 4);
+    o_seg[f] = place((uint64_t)p.n * ((rb + 1023) / 1024 + 1) * kRunBytes);
+  }
+  char* fbase = nullptr;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&fbase), at);
+  if (e != hipSuccess) {
+    note_hip_error(e, "hipMalloc(fused records)", __FILE__, __LINE__);
+    return e == hipErrorOutOfMemory ? POTS_E_NOMEM : POTS_E_HIP;
+  }
+  const uint64_t fb = reinterpret_cast<uint64_t>(fbase);
+  std::vector<FixJob> fix(prods.size());
+  uint64_t rows = 0;
+  seg_out->assign(prods.size(), 0);
+  for (size_t f = 0; f < prods.size(); f++) {
+    const uint32_t i = prods[f];
+    const pots_fv_product& p = P->h_prods[i];
+    const PassJob& J = P->h_jobs[pos[2 * n + i]];
+    FixJob& x = fix[f];
+    memset(&x, 0, sizeof x);
+    x.p = reinterpret_cast<uint64_t>(p.p);
+    x.r = reinterpret_cast<uint64_t>(P->d_r) + 4 * P->h_r_off[i];
+    x.seg = fb + o_seg[f];
+    x.pdot = J.pdot;
+    x.pabs = J.pabs;
+    x.psq = J.psq;
+    x.row_first = rows;
+    x.n = p.n;
+    x.w = p.w;
+    x.head = head_len[f];
+    x.esz = p.p_dtype == DT_BF16 ? 2 : 4;
+    x.J = (uint32_t)(((uint64_t)p.w * x.esz + 1023) / 1024 + 1);
+    rows += p.n;
+    (*seg_out)[f] = x.seg;
+  }
+  // The P pass without the fused products: each P launch keeps its other jobs, packed at the
+  // front of its ranges of the job array and the block table.
+  std::vector<PassLaunch> launches = P->pass_ap;
+  std::vector<PassJob> jobs = P->h_jobs;
+  std::vector<uint32_t> blk = P->h_blk;
+  for (PassLaunch& L : launches) {
+    if (L.weighted) continue;  // A pass
+    uint32_t kept = 0;
+    uint64_t blocks = 0;
+    for (uint32_t j = 0; j < L.n_jobs; j++) {
+      const size_t oi = L.job_off + j;
+      if (fused[P->h_src[oi] - 2 * n]) continue;
+      PassJob J = P->h_jobs[oi];
+      J.block_first = blocks;
+      const uint64_t nb = (uint64_t)J.n_rg * J.n_chunks * J.n_jt;
+      std::fill(blk.begin() + L.blk_off + blocks, blk.begin() + L.blk_off + blocks + nb, kept);
+      blocks += nb;
+      jobs[L.job_off + kept++] = J;
+    }
+    L.n_jobs = kept;
+    L.n_blocks = (uint32_t)blocks;
+  }
+  std::vector<FinJob> fin = P->h_fin;
+  for (uint32_t i : prods) fin[i].p_chunks = 1;
+  auto up = [&](void* dst, const void* src, size_t bytes) -> int {
+    if (!bytes) return POTS_E_OK;
+    POTS_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return POTS_E_OK;
+  };
+  int rc;
+  if ((rc = up(fbase + o_fix, fix.data(), fix.size() * sizeof(FixJob))) ||
+      (rc = up(P->d_jobs, jobs.data(), jobs.size() * sizeof(PassJob))) ||
+      (rc = up(P->d_blk, blk.data(), blk.size() * 4)) ||
+      (rc = up(P->d_fin, fin.data(), n * sizeof(FinJob)))) {
+    // The device tables may be half rewritten: the plan is unusable, and says so.
+    P->fused = true;
+    P->fbase = fbase;
+    P->n_fix = 0;
+    return rc;
+  }
+  P->pass_ap = launches;
+  P->h_jobs = std::move(jobs);
+  P->h_blk = std::move(blk);
+  P->h_fin = std::move(fin);
+  P->fused = true;
+  P->fbase = fbase;
+  P->d_fix = reinterpret_cast<FixJob*>(fbase + o_fix);
+  P->n_fix = (uint32_t)prods.size();
+  P->n_fix_rows = rows;
+  return POTS_E_OK;
+}
+
+}  // namespace pots
 
 template <uint32_t XT, bool W, bool S, uint32_t NJG>
 static void launch_pass(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
@@ -1140,6 +1372,12 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
       for (const PassLaunch& L : P->pass_ap)
         if ((L.weighted != 0) == (stage == 3) && (rc = run_pass(P, L, s)) != POTS_E_OK)
           return rc;
+      if (stage == 4 && P->fused) {
+        if (P->n_fix == 0) return POTS_E_HIP;  // a fusion that failed half way
+        hipLaunchKernelGGL(fused_rows, dim3((uint32_t)((P->n_fix_rows + 255) / 256)), dim3(256),
+                           0, s, P->d_fix, P->n_fix, P->n_fix_rows);
+        POTS_HIP(hipGetLastError());
+      }
       return POTS_E_OK;
     case 5:
       if (P->n_biased) {
@@ -1163,6 +1401,7 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
 extern "C" int pots_fv_plan_run(void* plan, const uint8_t* d_key, double* d_rows, void* stream) {
   if (!plan || !d_key || !d_rows) return POTS_E_ARG;
   FvPlan* P = static_cast<FvPlan*>(plan);
+  if (P->fused) return POTS_E_ARG;  // stage 4 needs the leaf plan's chunk stage first
   for (int stage = 0; stage < POTS_FV_STAGES; stage++) {
     const int rc = run_stage(P, stage, d_key, d_rows, static_cast<hipStream_t>(stream));
     if (rc != POTS_E_OK) return rc;
@@ -1193,5 +1432,6 @@ extern "C" void pots_fv_plan_destroy(void* plan) {
   FvPlan* P = static_cast<FvPlan*>(plan);
   if (!P) return;
   if (P->base) (void)hipFree(P->base);
+  if (P->fbase) (void)hipFree(P->fbase);
   delete P;
 }

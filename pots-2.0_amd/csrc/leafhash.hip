@@ -29,13 +29,17 @@
 
 #include <algorithm>
 #include <new>
+#include <unordered_set>
 #include <vector>
 
 #include "blake3_device.h"
 #include "common.h"
+#include "freivalds.h"
 #include "gmem.h"
 
 namespace pots {
+
+constexpr uint32_t kNoFuse = 0xFFFFFFFFu;
 
 struct LeafDesc {
   uint64_t payload;    // device address of payload byte 0 (word aligned)
@@ -44,8 +48,32 @@ struct LeafDesc {
   uint32_t head_len;   // bytes of 0x00 || header, a multiple of 4 (0 for a staged leaf)
   uint32_t kind;       // POTS_KIND_*
   uint32_t fin_from;   // message byte where the payload (the NaN/Inf-tested bytes) begins
+  uint64_t cv_first;   // where chunk 0's chaining value goes in the level-0 buffer
+  uint32_t n_chunks;   // 1 KiB chunks of the message (at least 1)
+  uint32_t fuse;       // index of its fused-product entry, or kNoFuse
 };
-static_assert(sizeof(LeafDesc) == 32, "LeafDesc layout");
+static_assert(sizeof(LeafDesc) == 48, "LeafDesc layout");
+
+// A leaf whose product's P-pass sums the chunk kernel takes (freivalds.h). Its first nf
+// chunks are hashed in class order: class kappa = c mod T holds the chunks whose payload
+// offset is the same modulo the row length, so the T classes of Q lanes each (Q a multiple of
+// 64, padding lanes idle) give every wave chunks at one common column offset: R is read with
+// scalar loads, one copy for the wave. A last chunk with fewer than 128 bytes has no interior
+// pair and no P-pass work; it is left out of the classes (nf = n_chunks - 1) and hashed by a
+// wave of its own after them, so that the header's few bytes do not pad every class.
+struct FuseDesc {
+  uint64_t r;          // R [m][4] fp32, row-major
+  uint64_t seg;        // run records [n_rows][J]
+  uint32_t row_bytes;  // m · esz
+  uint32_t n_rows;
+  uint32_t J;          // record slots per row
+  uint32_t T;          // classes
+  uint32_t Q;          // lanes per class
+  uint32_t esz;        // 2 (bf16) or 4 (fp32)
+  uint32_t nf;         // chunks in class order
+  uint32_t pad;
+};
+static_assert(sizeof(FuseDesc) == 48, "FuseDesc layout");
 
 struct LevelEntry {     // one leaf with >= 2 nodes at the input level of one fold
   uint64_t in_off;      // its first node in the level's input buffer
@@ -73,7 +101,7 @@ struct Fin {
   u16x2 acc = {0, 0};
   uint32_t mask;
   unsigned short thr;
-  __device__ explicit Fin(uint32_t kind)
+  __device__ __forceinline__ explicit Fin(uint32_t kind)
       : mask(kind == POTS_KIND_F32    ? 0x7F800000u
              : kind == POTS_KIND_BF16 ? 0x7F807F80u
              : kind == POTS_KIND_F16  ? 0x7C007C00u
@@ -86,6 +114,67 @@ struct Fin {
     return mask != 0u && (acc.x >= thr || acc.y >= thr);
   }
 };
+
+// ---- P-pass sums of a fused product leaf ---------------------------------------------------
+//
+// A lane keeps one run at a time: Σ x·R[col][j] (j < 4) and Σ|x| in fp32 over the run, Σx² in
+// fp32 over each 128-byte pair and in fp64 across pairs. A run ends where its row does (the
+// row boundary is at the same offset in every lane of the wave, so the branch is uniform) and
+// at the end of the chunk, and is written as one record.
+
+typedef float v4f32 __attribute__((ext_vector_type(4)));
+#define POTS_CONST __attribute__((address_space(4)))
+
+struct PRun {
+  float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f, s1 = 0.f;
+  double s2 = 0.0;
+  bool live = false;
+};
+
+// The elements t in [lo, hi) of a 128-byte pair (words w[0..31] of payload) into the run;
+// element t's column is R row rcol + t (rcol: wave-uniform address of R's row for t = 0).
+// Unmasked, every element of the pair is taken and the bounds are not read.
+template <int ESZ, bool MASKED>
+__device__ __forceinline__ void run_add(const uint32_t* w, uint64_t rcol, uint32_t lo,
+                                        uint32_t hi, PRun& a) {
+  constexpr int NE = 128 / ESZ;
+  const POTS_CONST v4f32* R = reinterpret_cast<const POTS_CONST v4f32*>(rcol);
+  float q = 0.f;
+#pragma unroll
+  for (int t = 0; t < NE; t++) {
+    if (MASKED && !((uint32_t)t >= lo && (uint32_t)t < hi)) continue;
+    float x;
+    if (ESZ == 2) x = __uint_as_float((t & 1) ? (w[t >> 1] & 0xFFFF0000u) : (w[t >> 1] << 16));
+    else x = __uint_as_float(w[t]);
+    const v4f32 r = R[t];
+    a.d0 = fmaf(x, r[0], a.d0);
+    a.d1 = fmaf(x, r[1], a.d1);
+    a.d2 = fmaf(x, r[2], a.d2);
+    a.d3 = fmaf(x, r[3], a.d3);
+    a.s1 += fabsf(x);
+    q = fmaf(x, x, q);
+  }
+  a.s2 += (double)q;
+  a.live = true;
+}
+
+// Write the run of `row` in chunk c (message offset of the payload H) as its record: slot
+// c − (chunk of the row's first element a chunk takes). Out-of-range indices are not written.
+__device__ __forceinline__ void run_flush(const FuseDesc& f, uint64_t H, uint32_t row,
+                                          uint64_t c, PRun& a) {
+  if (a.live) {
+    const uint64_t hc = (H + 127) & ~uint64_t(127);
+    const uint64_t fs = max<uint64_t>(H + (uint64_t)row * f.row_bytes, hc);
+    const uint64_t slot = c - (fs >> 10);
+    if (row < f.n_rows && slot < f.J) {
+      char* rec = reinterpret_cast<char*>(f.seg) + (uint64_t)kRunBytes * ((uint64_t)row * f.J + slot);
+      gstore<v4f32>(rec, v4f32{a.d0, a.d1, a.d2, a.d3});
+      const uint64_t sb = (uint64_t)__double_as_longlong(a.s2);
+      gstore<u32x4>(rec + 16, u32x4{__float_as_uint(a.s1), 0u, (uint32_t)sb, (uint32_t)(sb >> 32)});
+    }
+  }
+  a = PRun();
+}
 
 // Message block b of chunk c for the general case: blocks that touch the header, the end of
 // the payload or a partial word. Header words come from the head table (a staged leaf holds
@@ -130,9 +219,13 @@ __device__ __forceinline__ void edge_block(const LeafDesc& d, const uint32_t* __
 // go in pairs: a pair wholly inside the payload is read as one 144-byte aligned window (nine
 // 16-byte loads), so each 128-byte line a lane touches is used up by one group of loads
 // instead of being fetched again for the second half; other pairs take edge_block.
-template <int SH>
+//
+// ESZ != 0 (a fused product leaf, SH == 1): each interior pair's elements also go into the
+// lane's P-pass run.
+template <int SH, int ESZ>
 __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __restrict__ head,
-                                           uint64_t c, bool root, uint32_t cv[8], Fin& fin) {
+                                           uint64_t c, bool root, uint32_t cv[8], Fin& fin,
+                                           const FuseDesc& f) {
   const uint64_t H = d.head_len;
   const uint64_t L = H + d.len;
   const uint64_t cstart = c * 1024u;
@@ -145,6 +238,9 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
   // already streamed past is often an HBM refetch).
   u32x4 carry = u32x4{0, 0, 0, 0};
   bool have_carry = false;
+  PRun run;
+  uint32_t prow = 0, prb = 0;  // row of the next pair and its byte offset in the row
+  bool pinit = false;
 #pragma unroll 1
   for (uint32_t b = 0; b < nb; b += 2) {
     const uint64_t o = cstart + 64u * b;
@@ -180,6 +276,36 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
       }
 #pragma unroll
       for (int j = 0; j < 32; j++) fin.add(w[j + SH]);
+      if constexpr (ESZ != 0) {
+        if (!pinit) {  // the chunk's first interior pair
+          const uint64_t po = o - H;
+          prow = (uint32_t)(po / f.row_bytes);
+          prb = (uint32_t)(po - (uint64_t)prow * f.row_bytes);
+          pinit = true;
+        }
+        // Every active lane holds the same offset (the class order), so these are scalars.
+        // (readfirstlane returns int: each word goes through uint32_t before widening.)
+        const uint32_t rb = (uint32_t)__builtin_amdgcn_readfirstlane(prb);
+        const uint64_t rbase =
+            (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(f.r >> 32)) << 32 |
+            (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)f.r);
+        if (rb + 128 <= f.row_bytes) {
+          run_add<ESZ, false>(w + SH, rbase + (uint64_t)(rb / ESZ) * 16, 0, 128 / ESZ, run);
+          prb = rb + 128;
+          if (prb == f.row_bytes) {
+            run_flush(f, H, prow, c, run);
+            prow++;
+            prb = 0;
+          }
+        } else {  // the pair ends row prow at element tb and starts row prow + 1
+          const uint32_t tb = (f.row_bytes - rb) / ESZ;
+          run_add<ESZ, true>(w + SH, rbase + (uint64_t)(rb / ESZ) * 16, 0, tb, run);
+          run_flush(f, H, prow, c, run);
+          prow++;
+          run_add<ESZ, true>(w + SH, rbase - (uint64_t)tb * 16, tb, 128 / ESZ, run);
+          prb = rb + 128 - f.row_bytes;
+        }
+      }
       // Two whole 64-byte blocks of which the first never ends the chunk: the block lengths
       // are constant, and the chunk counter fits 32 bits (plan creation refuses a leaf of
       // 4 TiB or more).
@@ -201,53 +327,100 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
       b3_compress_cv(cv, m1, c, blen1, f1, cv);
     }
   }
+  if constexpr (ESZ != 0) run_flush(f, H, prow, c, run);
 }
 
-// One lane's chunk: global chunk index g, in block-table slot `blk` (every chunk of that slot
-// belongs to a leaf in blk_leaf[blk] .. blk_leaf[blk + 1]).
-__device__ __forceinline__ void chunk_one(
-    uint64_t g, uint32_t blk, const LeafDesc* __restrict__ leaves,
-    const uint64_t* __restrict__ chunk_first, const uint32_t* __restrict__ blk_leaf,
-    const uint32_t* __restrict__ head, uint32_t* __restrict__ cv_out,
-    uint32_t* __restrict__ digests, uint32_t* __restrict__ first_bad) {
-  uint32_t lo = blk_leaf[blk], hi = blk_leaf[blk + 1];
-  while (lo < hi) {  // the last leaf whose first chunk is <= g
+// A chunk order: entry e covers slots first[e] .. first[e + 1] of leaf leaf[e], and the
+// entries of block b's slots (kThreads of them) lie in blk_ent[b] .. blk_ent[b + 1].
+struct Order {
+  const uint64_t* __restrict__ first;
+  const uint32_t* __restrict__ leaf;
+  const uint32_t* __restrict__ blk_ent;
+  uint64_t n_slots;   // slots of the order
+  uint32_t n_blocks;  // ceil(n_slots / kThreads)
+};
+
+__device__ __forceinline__ uint32_t order_entry(const Order& od, uint64_t g, uint32_t blk) {
+  uint32_t lo = od.blk_ent[blk], hi = od.blk_ent[blk + 1];
+  while (lo < hi) {  // the last entry whose first slot is <= g
     const uint32_t mid = (lo + hi + 1) >> 1;
-    if (chunk_first[mid] <= g) lo = mid;
+    if (od.first[mid] <= g) lo = mid;
     else hi = mid - 1;
   }
-  const uint32_t i = lo;
-  const LeafDesc d = leaves[i];
-  const uint64_t c = g - chunk_first[i];
-  const bool root = chunk_first[i + 1] - chunk_first[i] == 1;
-  const uint32_t sh = (uint32_t)((d.payload - d.head_len) >> 2) & 3u;
-  uint32_t cv[8];
-  Fin fin(d.kind);
-  switch (sh) {
-    case 0: hash_chunk<0>(d, head, c, root, cv, fin); break;
-    case 1: hash_chunk<1>(d, head, c, root, cv, fin); break;
-    case 2: hash_chunk<2>(d, head, c, root, cv, fin); break;
-    default: hash_chunk<3>(d, head, c, root, cv, fin); break;
-  }
-  if (fin.bad()) atomicMin(first_bad, i);
-  u32x4* dst = reinterpret_cast<u32x4*>(root ? digests + 8ull * i : cv_out + 8ull * g);
+  return lo;
+}
+
+__device__ __forceinline__ void store_cv(uint32_t* p, const uint32_t cv[8]) {
+  u32x4* dst = reinterpret_cast<u32x4*>(p);
   gstore<u32x4>(dst, u32x4{cv[0], cv[1], cv[2], cv[3]});
   gstore<u32x4>(dst + 1, u32x4{cv[4], cv[5], cv[6], cv[7]});
 }
 
-// Every chunk's chaining value (or, for a one-chunk leaf, its digest). The chunks are cut
-// into n_slots slots of kThreads consecutive chunks; block b hashes slots b, b + gridDim.x,
-// ... so a grid smaller than n_slots holds a bounded share of the GPU and leaves the rest to
-// kernels on other streams.
+// Every chunk of the unfused leaves: slot g of the plain order is chunk g − first[e] of leaf
+// leaf[e] (slots past a leaf's chunks are idle). The chaining value goes to cv_out, or the
+// digest itself for a one-chunk leaf. Block b hashes slot blocks b, b + gridDim.x, ... so a
+// grid smaller than the order holds a bounded share of the GPU and leaves the rest to kernels
+// on other streams.
 __global__ __launch_bounds__(kThreads) void chunk_kernel(
-    const LeafDesc* __restrict__ leaves, const uint64_t* __restrict__ chunk_first,
-    const uint32_t* __restrict__ blk_leaf, uint64_t n_chunks, uint32_t n_slots,
-    const uint32_t* __restrict__ head, uint32_t* __restrict__ cv_out,
-    uint32_t* __restrict__ digests, uint32_t* __restrict__ first_bad) {
-  for (uint32_t blk = blockIdx.x; blk < n_slots; blk += gridDim.x) {
+    const LeafDesc* __restrict__ leaves, Order od, const uint32_t* __restrict__ head,
+    uint32_t* __restrict__ cv_out, uint32_t* __restrict__ digests,
+    uint32_t* __restrict__ first_bad) {
+  for (uint32_t blk = blockIdx.x; blk < od.n_blocks; blk += gridDim.x) {
     const uint64_t g = (uint64_t)blk * kThreads + threadIdx.x;
-    if (g < n_chunks)
-      chunk_one(g, blk, leaves, chunk_first, blk_leaf, head, cv_out, digests, first_bad);
+    if (g >= od.n_slots) continue;
+    const uint32_t e = order_entry(od, g, blk);
+    const uint32_t i = od.leaf[e];
+    const LeafDesc d = leaves[i];
+    const uint64_t c = g - od.first[e];
+    if (c >= d.n_chunks) continue;
+    uint32_t cv[8];
+    Fin fin(d.kind);
+    const FuseDesc none{};
+    const bool root = d.n_chunks == 1;
+    switch ((uint32_t)((d.payload - d.head_len) >> 2) & 3u) {
+      case 0: hash_chunk<0, 0>(d, head, c, root, cv, fin, none); break;
+      case 1: hash_chunk<1, 0>(d, head, c, root, cv, fin, none); break;
+      case 2: hash_chunk<2, 0>(d, head, c, root, cv, fin, none); break;
+      default: hash_chunk<3, 0>(d, head, c, root, cv, fin, none); break;
+    }
+    if (fin.bad()) atomicMin(first_bad, i);
+    store_cv(root ? digests + 8ull * i : cv_out + 8ull * (d.cv_first + c), cv);
+  }
+}
+
+// The fused leaves (FuseDesc), each starting at a multiple of 64 slots in the fused order and
+// holding a multiple of 64: a wave's slots are one leaf's and one class's, so the entry, the
+// leaf's descriptors and R's rows are wave-uniform and live in scalar registers. Local slot l
+// is chunk l / Q + T·(l mod Q) for l < T·Q, the short last chunk after that.
+__global__ __launch_bounds__(kThreads) void chunk_kernel_fused(
+    const LeafDesc* __restrict__ leaves, const FuseDesc* __restrict__ fuses, Order od,
+    const uint32_t* __restrict__ head, uint32_t* __restrict__ cv_out,
+    uint32_t* __restrict__ first_bad) {
+  const uint32_t wave_lane0 = threadIdx.x & ~63u;
+  for (uint32_t blk = blockIdx.x; blk < od.n_blocks; blk += gridDim.x) {
+    const uint64_t g0 = (uint64_t)blk * kThreads + wave_lane0;  // the wave's first slot
+    if (g0 >= od.n_slots) continue;  // n_slots is a multiple of 64: whole waves
+    const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane(order_entry(od, g0, blk));
+    const uint32_t i = od.leaf[e];
+    const LeafDesc d = leaves[i];
+    const FuseDesc f = fuses[d.fuse];
+    const uint32_t l32 = (uint32_t)(g0 - od.first[e]) + (threadIdx.x & 63u);  // < T·Q + 64
+    const uint32_t tq = f.T * f.Q;
+    uint32_t cv[8];
+    Fin fin(d.kind);
+    uint64_t c;
+    if (l32 < tq) {
+      c = (uint64_t)(l32 / f.Q) + (uint64_t)f.T * (l32 % f.Q);
+      if (c >= f.nf) continue;
+      if (f.esz == 2) hash_chunk<1, 2>(d, head, c, false, cv, fin, f);
+      else hash_chunk<1, 4>(d, head, c, false, cv, fin, f);
+    } else {  // the short last chunk, if any
+      c = (uint64_t)f.nf + (l32 - tq);
+      if (c >= d.n_chunks) continue;
+      hash_chunk<1, 0>(d, head, c, false, cv, fin, f);
+    }
+    if (fin.bad()) atomicMin(first_bad, i);
+    store_cv(cv_out + 8ull * (d.cv_first + c), cv);
   }
 }
 
@@ -334,28 +507,82 @@ struct LevelInfo {
 struct LeafPlan {
   size_t n = 0;
   uint64_t n_chunks = 0, bytes = 0;
+  uint32_t n_fused = 0;  // product leaves whose P-pass sums the chunk kernel takes
+  FuseDesc* d_fuse = nullptr;
+  Order plain{}, fused{};  // the two kernels' chunk orders (device tables)
   bool owned = false;
   char* base = nullptr;  // one device allocation: metadata, then workspace
   size_t total = 0;
   // device views
   LeafDesc* d_leaves = nullptr;
-  uint64_t* d_chunk_first = nullptr;
-  uint32_t* d_blk_leaf = nullptr;
   uint32_t* d_head = nullptr;
   LevelEntry* d_levels = nullptr;
   uint32_t* d_blk_ent = nullptr;
   uint32_t* d_cv[2] = {nullptr, nullptr};
-  uint32_t n_blocks = 0;  // chunk slots of kThreads chunks
   uint32_t max_grid = 0;  // chunk kernel's grid limit; 0 = one block per slot
   std::vector<LevelInfo> levels;
   std::vector<StageCopy> stages;
 };
 
 // Build the plan's host image and sizes. `device_only` refuses host payloads.
+// A chunk order on the host: entries (first slot, leaf) and the block -> entry table.
+struct OrderHost {
+  std::vector<uint64_t> first;  // n_ents + 1 (closing bound = n_slots)
+  std::vector<uint32_t> leaf;
+  std::vector<uint32_t> blk_ent;
+  uint64_t n_slots = 0;
+  uint32_t n_blocks = 0;
+  void add(uint32_t i, uint64_t slots) {
+    first.push_back(n_slots);
+    leaf.push_back(i);
+    n_slots += slots;
+  }
+  bool finish() {
+    first.push_back(n_slots);
+    const uint64_t nb = (n_slots + kThreads - 1) / kThreads;
+    if (nb >= 0x7FFFFFFFull || leaf.size() >= 0xFFFFFFFFull) return false;
+    n_blocks = (uint32_t)nb;
+    blk_ent.assign(n_blocks + 1, 0);
+    size_t e = 0;
+    for (uint32_t b = 0; b < n_blocks; b++) {
+      const uint64_t g = (uint64_t)b * kThreads;
+      while (first[e + 1] <= g) e++;
+      blk_ent[b] = (uint32_t)e;
+    }
+    blk_ent[n_blocks] = leaf.empty() ? 0 : (uint32_t)(leaf.size() - 1);
+    return true;
+  }
+};
+
+// A fused leaf's chunk order: T classes (chunk c in class c mod T, T = lcm(row bytes, 1024) /
+// 1024, so a class's chunks start at one offset in the row) of Q lanes each, Q the class size
+// rounded up to 64. Fusing is declined when the padding would exceed 1/16 of the chunks.
+static bool fuse_shape(uint64_t msg_bytes, uint32_t row_bytes, uint32_t* T, uint32_t* Q,
+                       uint32_t* nf, uint64_t* slots) {
+  const uint64_t n_chunks = (msg_bytes + 1023) / 1024;
+  const uint64_t f = msg_bytes % 1024 != 0 && msg_bytes % 1024 < 128 ? n_chunks - 1 : n_chunks;
+  uint64_t a = row_bytes, b = 1024;
+  while (b) {
+    const uint64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  const uint64_t t = (uint64_t)row_bytes / a;  // lcm / 1024
+  const uint64_t q = ((f + t - 1) / t + 63) / 64 * 64;
+  const uint64_t total = t * q + (f < n_chunks ? 64 : 0);
+  if (total >= 0xFFFFFFFFull || (t * q - f) * 16 > f) return false;
+  *T = (uint32_t)t;
+  *Q = (uint32_t)q;
+  *nf = (uint32_t)f;
+  *slots = total;
+  return true;
+}
+
 static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
                       const uint32_t* hdr_len, const uint32_t* hdr_idx,
                       const uint64_t* payload_ptr, const uint64_t* payload_len,
-                      const uint8_t* kind, bool device_only, bool owned, LeafPlan** out) {
+                      const uint8_t* kind, bool device_only, bool owned, void* fv,
+                      LeafPlan** out) {
   if (n == 0 || n >= 0xFFFFFFFFull) return POTS_E_ARG;
   for (size_t i = 0; i < n; i++)
     if (kind[i] > POTS_KIND_F16) return POTS_E_ARG;
@@ -367,10 +594,13 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
   // Per leaf: its head bytes (0x00 || header) and whether it must be staged.
   std::vector<LeafDesc> desc(n);
   std::vector<uint8_t> headbytes;  // word-aligned heads of direct leaves, then staged heads
-  std::vector<uint64_t> chunk_first(n + 1);
+  OrderHost plain, fused;
   std::vector<int64_t> stage_head_at(n, -1);
   uint64_t stage_bytes = 0;
   std::vector<uint64_t> stage_off(n, 0);
+  std::vector<FuseDesc> fdesc;                 // per fused leaf
+  std::vector<uint32_t> fprod, fhead;          // its product and head bytes
+  std::unordered_set<uint32_t> fused_prods;
   uint64_t nc = 0;
   for (size_t i = 0; i < n; i++) {
     const uint32_t u = hdr_idx[i];
@@ -411,44 +641,59 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
       delete P;
       return POTS_E_ARG;
     }
-    chunk_first[i] = nc;
-    nc += std::max<uint64_t>(1, (L + 1023) / 1024);
+    const uint64_t nck = std::max<uint64_t>(1, (L + 1023) / 1024);
+    d.cv_first = nc;
+    d.n_chunks = (uint32_t)nck;
+    d.fuse = kNoFuse;
+    FusedProduct fp;
+    uint32_t T = 0, Q = 0, nf = 0;
+    uint64_t slots = 0;
+    if (fv && !stage && (kind[i] == POTS_KIND_BF16 || kind[i] == POTS_KIND_F32) &&
+        (ptr - hl) % 16 == 4 && fv_fuse_candidate(fv, ptr, len, kind[i], &fp) &&
+        !fused_prods.count(fp.prod) && fuse_shape(L, fp.w * fp.esz, &T, &Q, &nf, &slots)) {
+      fused_prods.insert(fp.prod);
+      FuseDesc f;
+      memset(&f, 0, sizeof f);
+      f.r = fp.r;
+      f.row_bytes = fp.w * fp.esz;
+      f.n_rows = fp.n;
+      f.J = (f.row_bytes + 1023) / 1024 + 1;
+      f.T = T;
+      f.Q = Q;
+      f.esz = fp.esz;
+      f.nf = nf;
+      d.fuse = (uint32_t)fdesc.size();
+      fdesc.push_back(f);
+      fprod.push_back(fp.prod);
+      fhead.push_back((uint32_t)hl);
+      fused.add((uint32_t)i, slots);  // slots: a multiple of 64, so every entry is aligned
+    } else {
+      plain.add((uint32_t)i, nck);
+    }
+    nc += nck;
     P->bytes += L;
   }
-  chunk_first[n] = nc;
   P->n_chunks = nc;
+  P->n_fused = (uint32_t)fdesc.size();
   if (headbytes.size() / 4 >= 0xFFFFFFFFull) {
     delete P;
     return POTS_E_ARG;
   }
 
-  // Block -> first leaf table for the chunk kernel.
-  const uint64_t nblocks64 = (nc + kThreads - 1) / kThreads;
-  if (nblocks64 >= 0x7FFFFFFFull) {
+  if (!plain.finish() || !fused.finish()) {
     delete P;
     return POTS_E_ARG;
   }
-  P->n_blocks = (uint32_t)nblocks64;
-  std::vector<uint32_t> blk_leaf(P->n_blocks + 1);
-  {
-    size_t i = 0;
-    for (uint32_t b = 0; b < P->n_blocks; b++) {
-      const uint64_t g = (uint64_t)b * kThreads;
-      while (chunk_first[i + 1] <= g) i++;
-      blk_leaf[b] = (uint32_t)i;
-    }
-    blk_leaf[P->n_blocks] = (uint32_t)(n - 1);
-  }
 
-  // Reduction folds of kFold levels each. Level 0 nodes of leaf i sit at chunk_first[i] in
+  // Reduction folds of kFold levels each. Level 0 nodes of leaf i sit at desc[i].cv_first in
   // cv0; a fold takes a leaf's n nodes to ceil(n / 2^kFold) (BLAKE3's halving with a
   // promoted odd node, kFold times, composes to that ceiling).
   std::vector<LevelEntry> ents;
   std::vector<uint32_t> blk_ent;
   std::vector<uint64_t> n_nodes(n), off(n);
   for (size_t i = 0; i < n; i++) {
-    n_nodes[i] = chunk_first[i + 1] - chunk_first[i];
-    off[i] = chunk_first[i];
+    n_nodes[i] = desc[i].n_chunks;
+    off[i] = desc[i].cv_first;
   }
   uint64_t cv1_need = 0;
   int in_buf = 0;
@@ -495,8 +740,14 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
     return a;
   };
   const size_t o_leaves = place(n * sizeof(LeafDesc));
-  const size_t o_chunk = place((n + 1) * sizeof(uint64_t));
-  const size_t o_blk = place((P->n_blocks + 1) * sizeof(uint32_t));
+  const size_t o_fuse = place(std::max<size_t>(fdesc.size(), 1) * sizeof(FuseDesc));
+  size_t o_ord[2][3];
+  OrderHost* ords[2] = {&plain, &fused};
+  for (int k = 0; k < 2; k++) {
+    o_ord[k][0] = place(ords[k]->first.size() * sizeof(uint64_t));
+    o_ord[k][1] = place(std::max<size_t>(ords[k]->leaf.size(), 1) * sizeof(uint32_t));
+    o_ord[k][2] = place(ords[k]->blk_ent.size() * sizeof(uint32_t));
+  }
   const size_t o_head = place(std::max<size_t>(headbytes.size(), 4));
   const size_t o_lev = place(std::max<size_t>(ents.size(), 1) * sizeof(LevelEntry));
   const size_t o_blk_ent = place(std::max<size_t>(blk_ent.size(), 1) * sizeof(uint32_t));
@@ -532,19 +783,46 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
     }
   }
   P->d_leaves = reinterpret_cast<LeafDesc*>(P->base + o_leaves);
-  P->d_chunk_first = reinterpret_cast<uint64_t*>(P->base + o_chunk);
-  P->d_blk_leaf = reinterpret_cast<uint32_t*>(P->base + o_blk);
+  P->d_fuse = reinterpret_cast<FuseDesc*>(P->base + o_fuse);
+  Order* dords[2] = {&P->plain, &P->fused};
+  for (int k = 0; k < 2; k++) {
+    dords[k]->first = reinterpret_cast<const uint64_t*>(P->base + o_ord[k][0]);
+    dords[k]->leaf = reinterpret_cast<const uint32_t*>(P->base + o_ord[k][1]);
+    dords[k]->blk_ent = reinterpret_cast<const uint32_t*>(P->base + o_ord[k][2]);
+    dords[k]->n_slots = ords[k]->n_slots;
+    dords[k]->n_blocks = ords[k]->n_blocks;
+  }
   P->d_head = reinterpret_cast<uint32_t*>(P->base + o_head);
   P->d_levels = reinterpret_cast<LevelEntry*>(P->base + o_lev);
   P->d_blk_ent = reinterpret_cast<uint32_t*>(P->base + o_blk_ent);
   P->d_cv[0] = reinterpret_cast<uint32_t*>(P->base + o_cv0);
   P->d_cv[1] = reinterpret_cast<uint32_t*>(P->base + o_cv1);
 
+  // The fused products' run records, allocated by the Freivalds plan.
+  if (!fdesc.empty()) {
+    std::vector<uint64_t> segs;
+    const int frc = fv_fuse_commit(fv, fprod, fhead, &segs);
+    if (frc != POTS_E_OK) {
+      if (owned) (void)hipFree(P->base);
+      delete P;
+      return frc;
+    }
+    for (size_t f = 0; f < fdesc.size(); f++) fdesc[f].seg = segs[f];
+  }
+
   // Upload the metadata in one copy.
   std::vector<char> img(meta_bytes, 0);
   memcpy(img.data() + o_leaves, desc.data(), n * sizeof(LeafDesc));
-  memcpy(img.data() + o_chunk, chunk_first.data(), (n + 1) * sizeof(uint64_t));
-  memcpy(img.data() + o_blk, blk_leaf.data(), (P->n_blocks + 1) * sizeof(uint32_t));
+  if (!fdesc.empty()) memcpy(img.data() + o_fuse, fdesc.data(), fdesc.size() * sizeof(FuseDesc));
+  for (int k = 0; k < 2; k++) {
+    memcpy(img.data() + o_ord[k][0], ords[k]->first.data(),
+           ords[k]->first.size() * sizeof(uint64_t));
+    if (!ords[k]->leaf.empty())
+      memcpy(img.data() + o_ord[k][1], ords[k]->leaf.data(),
+             ords[k]->leaf.size() * sizeof(uint32_t));
+    memcpy(img.data() + o_ord[k][2], ords[k]->blk_ent.data(),
+           ords[k]->blk_ent.size() * sizeof(uint32_t));
+  }
   if (!headbytes.empty()) memcpy(img.data() + o_head, headbytes.data(), headbytes.size());
   if (!ents.empty()) memcpy(img.data() + o_lev, ents.data(), ents.size() * sizeof(LevelEntry));
   if (!blk_ent.empty())
@@ -580,12 +858,24 @@ static int plan_stage(LeafPlan* P, int stage, uint32_t* d_digests, uint32_t* d_f
       POTS_HIP(hipGetLastError());
       return POTS_E_OK;
     case 1:
-      hipLaunchKernelGGL(chunk_kernel,
-                         dim3(P->max_grid ? std::min(P->max_grid, P->n_blocks) : P->n_blocks),
-                         dim3(kThreads), 0, stream, P->d_leaves, P->d_chunk_first,
-                         P->d_blk_leaf, P->n_chunks, P->n_blocks, P->d_head, P->d_cv[0],
-                         d_digests, d_first_bad);
-      POTS_HIP(hipGetLastError());
+      // The fused leaves first: with the other kernel's blocks queued behind them, the two
+      // kernels' tails overlap.
+      if (P->fused.n_blocks) {
+        hipLaunchKernelGGL(chunk_kernel_fused,
+                           dim3(P->max_grid ? std::min(P->max_grid, P->fused.n_blocks)
+                                            : P->fused.n_blocks),
+                           dim3(kThreads), 0, stream, P->d_leaves, P->d_fuse, P->fused,
+                           P->d_head, P->d_cv[0], d_first_bad);
+        POTS_HIP(hipGetLastError());
+      }
+      if (P->plain.n_blocks) {
+        hipLaunchKernelGGL(chunk_kernel,
+                           dim3(P->max_grid ? std::min(P->max_grid, P->plain.n_blocks)
+                                            : P->plain.n_blocks),
+                           dim3(kThreads), 0, stream, P->d_leaves, P->plain, P->d_head,
+                           P->d_cv[0], d_digests, d_first_bad);
+        POTS_HIP(hipGetLastError());
+      }
       return POTS_E_OK;
     case 2:
       for (const LevelInfo& li : P->levels) {
@@ -628,7 +918,7 @@ extern "C" size_t pots_hash_leaves(size_t n, const uint8_t* hdr_buf, const uint6
   if (n == 0) return 0;
   LeafPlan* P = nullptr;
   if (plan_build(n, hdr_buf, hdr_off, hdr_len, hdr_idx, payload_ptr, payload_len, kind,
-                 /*device_only=*/false, /*owned=*/false, &P) != POTS_E_OK)
+                 /*device_only=*/false, /*owned=*/false, nullptr, &P) != POTS_E_OK)
     return SIZE_MAX;
   void* res = nullptr;
   size_t bad = SIZE_MAX;
@@ -654,9 +944,43 @@ extern "C" int pots_leaf_plan_create(size_t n, const uint8_t* hdr_buf, const uin
   if (!plan) return POTS_E_ARG;
   LeafPlan* P = nullptr;
   int rc = plan_build(n, hdr_buf, hdr_off, hdr_len, hdr_idx, payload_ptr, payload_len, kind,
-                      /*device_only=*/true, /*owned=*/true, &P);
+                      /*device_only=*/true, /*owned=*/true, nullptr, &P);
   if (rc == POTS_E_OK) *plan = P;
   return rc;
+}
+
+extern "C" int pots_leaf_plan_create_fused(size_t n, const uint8_t* hdr_buf,
+                                           const uint64_t* hdr_off, const uint32_t* hdr_len,
+                                           const uint32_t* hdr_idx, const uint64_t* payload_ptr,
+                                           const uint64_t* payload_len, const uint8_t* kind,
+                                           void* fv_plan, void** plan) {
+  if (!plan || !fv_plan) return POTS_E_ARG;
+  LeafPlan* P = nullptr;
+  int rc = plan_build(n, hdr_buf, hdr_off, hdr_len, hdr_idx, payload_ptr, payload_len, kind,
+                      /*device_only=*/true, /*owned=*/true, fv_plan, &P);
+  if (rc == POTS_E_OK) *plan = P;
+  return rc;
+}
+
+extern "C" uint32_t pots_leaf_plan_fused(const void* plan) {
+  return plan ? static_cast<const LeafPlan*>(plan)->n_fused : 0;
+}
+
+extern "C" int pots_step_run(void* leaf_plan, void* fv_plan, const uint8_t* d_key,
+                             uint8_t* d_digests, uint32_t* d_first_bad, double* d_rows,
+                             void* stream) {
+  if (!leaf_plan || !fv_plan || !d_key || !d_digests || !d_first_bad || !d_rows)
+    return POTS_E_ARG;
+  int rc;
+  if ((rc = pots_fv_plan_run_stage(fv_plan, 0, d_key, d_rows, stream)) != POTS_E_OK) return rc;
+  for (int st = 0; st < POTS_LEAF_STAGES; st++)
+    if ((rc = pots_leaf_plan_run_stage(leaf_plan, st, d_digests, d_first_bad, stream)) !=
+        POTS_E_OK)
+      return rc;
+  for (int st = 1; st < POTS_FV_STAGES; st++)
+    if ((rc = pots_fv_plan_run_stage(fv_plan, st, d_key, d_rows, stream)) != POTS_E_OK)
+      return rc;
+  return POTS_E_OK;
 }
 
 extern "C" int pots_leaf_plan_run(void* plan, uint8_t* d_out, uint32_t* d_first_bad,

@@ -300,7 +300,7 @@ class StepHasher:
     in HBM, then :meth:`digests` enqueues the whole step's hashing with no host work."""
 
     def __init__(self, c: DeclaredComputation, leaves: Sequence[Any],
-                 device: torch.device | None = None) -> None:
+                 device: torch.device | None = None, fuse: Any = None) -> None:
         if len(leaves) != c.n_leaves:
             raise ValueError(f"transcript has {len(leaves)} leaves, the computation declares "
                              f"{c.n_leaves}")
@@ -320,7 +320,9 @@ class StepHasher:
             payloads.append(t)
             kinds.append(native.FINITE_KIND[t.dtype])
         self.c = c
-        self.plan = native.get().leaf_plan(headers, payloads, kinds)
+        # With `fuse` (a native.FvPlan over this step's products), the product leaves' P-pass
+        # sums are taken while they are hashed.
+        self.plan = native.get().leaf_plan(headers, payloads, kinds, fuse)
         self.n = len(leaves)
         self.bytes = self.plan.bytes
 

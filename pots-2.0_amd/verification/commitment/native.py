@@ -21,6 +21,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+import weakref
 from collections.abc import Iterator, Sequence
 from contextlib import contextmanager
 from pathlib import Path
@@ -90,6 +91,10 @@ class Native:
             "pots_leaf_plan_chunks": ([_vp], _u64),
             "pots_leaf_plan_bytes": ([_vp], _u64),
             "pots_leaf_plan_destroy": ([_vp], None),
+            "pots_leaf_plan_create_fused": ([_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                             ctypes.POINTER(_vp)], _int),
+            "pots_leaf_plan_fused": ([_vp], _u32),
+            "pots_step_run": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp], _int),
             "pots_merkle_tree_async": ([_sz, _vp, _vp, _vp], _int),
             "pots_challenges": ([_vp, _u32, _sz, _vp, _vp, _vp, _vp, _u32], _int),
             "pots_fv_plan_create": ([_sz, _vp, _u32, _u32, ctypes.POINTER(_vp)], _int),
@@ -254,10 +259,24 @@ class Native:
         return UpdatePlan(self, weights, eta, eps_w)
 
     def leaf_plan(self, headers: Sequence[bytes], payloads: Sequence[torch.Tensor],
-                  kinds: Sequence[int]) -> LeafPlan:
+                  kinds: Sequence[int], fuse: FvPlan | None = None) -> LeafPlan:
         """A reusable hashing plan over GPU-resident payloads: leaf ``i`` is
-        ``BLAKE3(0x00 ‖ headers[i] ‖ payload bytes of payloads[i])``."""
-        return LeafPlan(self, headers, payloads, kinds)
+        ``BLAKE3(0x00 ‖ headers[i] ‖ payload bytes of payloads[i])``. With ``fuse``, the
+        leaves that are the P of a product of that Freivalds plan also have its P-pass sums
+        taken by the chunk stage (``pots_leaf_plan_create_fused``)."""
+        return LeafPlan(self, headers, payloads, kinds, fuse)
+
+    def step_run(self, leaf: LeafPlan, fv: FvPlan, key: torch.Tensor, digests: torch.Tensor,
+                 bad: torch.Tensor, rows: torch.Tensor,
+                 stream: torch.cuda.Stream | None = None) -> None:
+        """``pots_step_run``: fv stage 0, the leaf plan, fv stages 1-5, on one stream."""
+        if digests.shape != (leaf.n, 32) or digests.dtype != torch.uint8:
+            raise ValueError("digests must be uint8 [n, 32]")
+        if rows.shape != (fv.n, 5 + fv.k) or rows.dtype != torch.float64:
+            raise ValueError("rows must be fp64 [n, 5 + k]")
+        self._check(self._lib.pots_step_run(leaf._h, fv._h, key.data_ptr(), digests.data_ptr(),
+                                            bad.data_ptr(), rows.data_ptr(), _stream(stream)),
+                    "pots_step_run")
 
 
 class LeafPlan:
@@ -265,7 +284,7 @@ class LeafPlan:
     every leaf on a stream with no allocation and no host sync."""
 
     def __init__(self, lib: Native, headers: Sequence[bytes], payloads: Sequence[torch.Tensor],
-                 kinds: Sequence[int]) -> None:
+                 kinds: Sequence[int], fuse: FvPlan | None = None) -> None:
         n = len(payloads)
         if not (len(headers) == len(kinds) == n) or n == 0:
             raise ValueError("one header and one kind per payload, at least one leaf")
@@ -289,10 +308,22 @@ class LeafPlan:
             ptr[i], ln[i] = t.data_ptr(), t.nbytes
         kd = np.asarray(kinds, dtype=np.uint8)
         h = ctypes.c_void_p()
-        lib._check(lib._lib.pots_leaf_plan_create(n, _addr(hb), _addr(hdr_off), _addr(hdr_len),
-                                                  _addr(idx), _addr(ptr), _addr(ln), _addr(kd),
-                                                  ctypes.byref(h)), "pots_leaf_plan_create")
+        if fuse is None:
+            lib._check(lib._lib.pots_leaf_plan_create(
+                n, _addr(hb), _addr(hdr_off), _addr(hdr_len), _addr(idx), _addr(ptr), _addr(ln),
+                _addr(kd), ctypes.byref(h)), "pots_leaf_plan_create")
+        else:
+            if fuse._fused_leaf is not None:
+                raise ValueError("this Freivalds plan is already fused with a leaf plan")
+            lib._check(lib._lib.pots_leaf_plan_create_fused(
+                n, _addr(hb), _addr(hdr_off), _addr(hdr_len), _addr(idx), _addr(ptr), _addr(ln),
+                _addr(kd), fuse._h, ctypes.byref(h)), "pots_leaf_plan_create_fused")
+            fuse._fused_leaf = weakref.ref(self)
         self._h = h
+        # The chunk stage of a fused plan writes into the Freivalds plan's records and reads
+        # its challenges: the Freivalds plan lives at least as long.
+        self._fv = fuse
+        self.fused = int(lib._lib.pots_leaf_plan_fused(h))
         self.n = n
         self.chunks = int(lib._lib.pots_leaf_plan_chunks(h))
         self.bytes = int(lib._lib.pots_leaf_plan_bytes(h))
@@ -426,6 +457,7 @@ class FvPlan:
         lib._check(lib._lib.pots_fv_plan_create(n, ctypes.addressof(arr), k, int(bool(guard)),
                                                 ctypes.byref(h)), "pots_fv_plan_create")
         self._lib, self._h, self._keep = lib, h, keep
+        self._fused_leaf = None  # weak reference to the leaf plan fused with this one
         self.n, self.k = n, k
         self.widths = [pr.p.shape[1] for pr in products]
         self.device = products[0].a.device
@@ -474,6 +506,9 @@ class FvPlan:
         return out
 
     def close(self) -> None:
+        leaf = self._fused_leaf() if getattr(self, "_fused_leaf", None) is not None else None
+        if leaf is not None:  # its chunk stage writes into this plan's memory
+            leaf.close()
         if getattr(self, "_h", None) is not None and self._h.value:
             self._lib._lib.pots_fv_plan_destroy(self._h)
             self._h = ctypes.c_void_p()

@@ -9,11 +9,15 @@ as check 2 at the end (F15a: check 5 keys on the claimed root, so it need not wa
 recomputed one).
 
 What runs where. Check 2's hashing (leaf digests, then the Merkle tree) and check 5's
-measuring (challenges, the three Freivalds passes, rows) read disjoint work and both depend
-only on the leaves and the claimed root, so they run on two streams at once: hashing is
-integer-VALU bound and uses a fraction of HBM bandwidth, the Freivalds passes are memory bound
-and leave the VALUs mostly idle. The verdicts follow on the main stream. One host read at the
-end returns the root, the first non-finite leaf and the first rejected product.
+measuring (challenges, the three Freivalds passes, rows) depend only on the leaves and the
+claimed root, so they run on two streams at once: hashing is integer-VALU bound and uses a
+fraction of HBM bandwidth, the Freivalds passes are memory bound and leave the VALUs mostly
+idle. Each product's P is a leaf, so by default the leaf plan is fused with the Freivalds plan
+(``pots_leaf_plan_create_fused``): the chunk kernel takes the P-pass sums of the product leaves
+it streams and P is read once. The challenges then go first, the chunk kernel waits for them,
+and the P stage (which adds up the chunk kernel's run records) waits for the chunk kernel. The
+verdicts follow on the main stream. One host read at the end returns the root, the first
+non-finite leaf and the first rejected product.
 """
 
 from __future__ import annotations
@@ -52,11 +56,10 @@ class DeviceStepVerifier:
     :meth:`run` with the claimed root."""
 
     def __init__(self, c: DeclaredComputation, leaves: Sequence[Any], operands: Any, *, k: int,
-                 bands: Bands | None = None, guard: bool = True) -> None:
+                 bands: Bands | None = None, guard: bool = True, fuse: bool = True) -> None:
         self.c, self.k, self.guard = c, k, guard
         self.bands = bands or Bands.provisional()
         lib = self.lib = native.get()
-        self.hasher = StepHasher(c, leaves)
         prods = []
         for spec in c.products:
             a, b = operands(spec)
@@ -66,6 +69,10 @@ class DeviceStepVerifier:
                 bias = leaves[c.w_t_index(spec.bias)].to(c.operand_dtype).to(torch.float32)
             prods.append(native.FvProduct(a, b, p, spec.m, bias))
         self.plan = lib.fv_plan(prods, k, guard)
+        # Fused: the chunk kernel takes the P-pass sums of the product leaves it hashes, so
+        # each P is read from HBM once (pots_leaf_plan_create_fused).
+        self.hasher = StepHasher(c, leaves, fuse=self.plan if fuse else None)
+        self.fused = self.hasher.plan.fused
         self.specs = native.verdict_specs(
             [s.q for s in c.products], [s.a_shape[0] for s in c.products],
             [s.bias is not None for s in c.products],
@@ -93,8 +100,15 @@ class DeviceStepVerifier:
             self.key.copy_(torch.frombuffer(bytearray(claimed), dtype=torch.uint8))
         start = torch.cuda.Event(enable_timing=events is not None)
         start.record(main)
-        self.side.wait_event(start)
         timing = events is not None
+        plan = self.plan
+        if self.fused:  # the chunk kernel reads the challenges
+            plan.run_stage(0, self.key, self.rows, main)
+            ready = torch.cuda.Event()
+            ready.record(main)
+            self.side.wait_event(ready)
+        else:
+            self.side.wait_event(start)
         c_begin = torch.cuda.Event(enable_timing=timing)
         c_end = torch.cuda.Event(enable_timing=timing)
         with torch.cuda.stream(self.side):
@@ -107,7 +121,12 @@ class DeviceStepVerifier:
             nodes = self.lib.merkle_tree_device(self.digests, self.side)
         hashed = torch.cuda.Event(enable_timing=events is not None)
         hashed.record(self.side)
-        self.plan.rows(self.key, self.rows, main)
+        for st in range(1 if self.fused else 0, 4):
+            plan.run_stage(st, self.key, self.rows, main)
+        if self.fused:  # stage 4 adds up the chunk kernel's run records
+            main.wait_event(c_end)
+        for st in (4, 5):
+            plan.run_stage(st, self.key, self.rows, main)
         measured = torch.cuda.Event(enable_timing=events is not None)
         measured.record(main)
         main.wait_event(hashed)

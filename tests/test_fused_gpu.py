@@ -1,0 +1,216 @@
+"""P read once: the leaf hasher taking the Freivalds P pass of product leaves
+(``pots_leaf_plan_create_fused``), against the unfused plans and the CPU oracle.
+
+Each case is a small transcript of product leaves (2-D tensors, tag 0x03) with their A and B,
+hashed and measured twice: by an unfused leaf plan plus an unfused Freivalds plan, and by a
+Freivalds plan fused with the leaf plan and run through ``pots_step_run``. The shapes put row
+boundaries inside 128-byte pairs and at chunk boundaries, the leaf's first bytes after the
+header and its last bytes in the regions no chunk's interior pairs take, and include products
+that must not be fused (rows under 1 KiB, a class padding over 1/16, a payload at an offset,
+a P shared by two products, k != 4).
+
+Tolerances: digests, first-bad and verdict codes bit for bit; the rows' non-negative columns
+relative 1e-6 against the unfused plan and 1e-5 against the fp64 oracle; residuals against the
+fp64 oracle within 2 band units when honest and relative 1e-4 (floor 2 band units) when a P
+entry was changed, as the Freivalds tests do.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+BF16, FP32 = 2.0**-8, 2.0**-24
+KEY = bytes(range(32))
+
+
+def _product(n, q, w, dt, seed, tamper=()):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(n, q, generator=g).to(dt)
+    b = (torch.randn(q, w, generator=g) * q ** -0.5).to(dt)
+    p = (a.double() @ b.double()).to(dt)
+    for i, j, f in tamper:
+        p[i, j] = (p[i, j].double() * f).to(dt)
+    return a, b, p
+
+
+def _run_case(lib, prods_cpu, k=4, expect_fused=None, extra_leaves=()):
+    """prods_cpu: [(a, b, p)] on the CPU. Returns (rows_fused, rows_unfused, digests) after
+    checking digests and fusion counts."""
+    from verification.commitment import native
+    dev = [(a.cuda(), b.cuda(), p.cuda()) for a, b, p in prods_cpu]
+    leaves = [p for _, _, p in dev] + [t.cuda() for t in extra_leaves]
+    hdrs = [O.tensor_leaf_header(O.TAG_PRODUCT, t) for t in leaves]
+    kinds = [native.FINITE_KIND[t.dtype] for t in leaves]
+    fvp = [native.FvProduct(a, b, p, i + 1) for i, (a, b, p) in enumerate(dev)]
+    key = torch.tensor(list(KEY), dtype=torch.uint8, device="cuda")
+
+    fv_u = lib.fv_plan(fvp, k)
+    rows_u = fv_u.rows(key)
+    leaf_u = lib.leaf_plan(hdrs, leaves, kinds)
+    dig_u, bad_u = leaf_u.run()
+
+    fv_f = lib.fv_plan(fvp, k)
+    leaf_f = lib.leaf_plan(hdrs, leaves, kinds, fuse=fv_f)
+    if expect_fused is not None:
+        assert leaf_f.fused == expect_fused
+    dig_f = torch.empty_like(dig_u)
+    bad_f = torch.empty(1, dtype=torch.int32, device="cuda")
+    rows_f = torch.empty_like(rows_u)
+    for _ in range(2):  # a second run reuses the records
+        lib.step_run(leaf_f, fv_f, key, dig_f, bad_f, rows_f)
+    torch.cuda.synchronize()
+    assert torch.equal(dig_f, dig_u)
+    assert int(bad_f.item()) == int(bad_u.item()) == len(leaves)
+    want = [O.tensor_leaf_hash(O.TAG_PRODUCT, t.cpu()) for t in leaves]
+    assert [bytes(x) for x in dig_f.cpu().numpy()] == want
+    if leaf_f.fused:
+        with pytest.raises(ValueError):
+            fv_f.rows(key)  # a fused plan runs only beside its leaf plan
+    leaf_f.close()
+    fv_f.close()
+    return rows_f.cpu().tolist(), rows_u.cpu().tolist()
+
+
+def _check_rows(prods_cpu, rows_f, rows_u, k=4, tampered=()):
+    ms = list(range(1, len(prods_cpu) + 1))
+    for i, (a, b, p) in enumerate(prods_cpu):
+        r = O.challenge_matrices(KEY, [ms[i]], k, p.shape[1])[0]
+        ref = O.measure_row_f64(a, b, p, r, None)
+        eps_in = BF16 if p.dtype == torch.bfloat16 else FP32
+        unit = O.finish_row(ref, q=a.shape[1], n=a.shape[0], eps_in=eps_in,
+                            eps_acc=FP32)["unit"]
+        for col in range(5):
+            assert rows_f[i][col] == pytest.approx(rows_u[i][col], rel=1e-6, abs=1e-300), (i, col)
+            assert rows_f[i][col] == pytest.approx(ref[col], rel=1e-5, abs=1e-300), (i, col)
+        for x, y in zip(rows_f[i][5:], ref[5:]):
+            if i in tampered:
+                assert x == pytest.approx(y, rel=1e-4, abs=2 * unit), i
+            else:
+                assert abs(x - y) <= 2 * unit, (i, x, y, unit)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_fused_rows_equal_unfused_and_oracle(lib, dt):
+    esz = 2 if dt == torch.bfloat16 else 4
+    shapes = [(64, 96, 1024 // esz),    # 1 KiB rows: one class
+              (128, 64, 2560 // esz),   # 2.5 KiB rows: 5 classes, rows end mid-pair
+              (256, 80, 4096 // esz),   # 4 KiB rows
+              (64, 48, 3072 // esz)]    # 3 KiB rows
+    prods = [_product(n, q, w, dt, seed=s) for s, (n, q, w) in enumerate(shapes)]
+    rows_f, rows_u = _run_case(lib, prods, expect_fused=len(prods))
+    _check_rows(prods, rows_f, rows_u)
+
+
+def test_fused_large_rows_and_many_classes(lib):
+    # 17.5 KiB rows (35 classes) and a header-only last chunk
+    prods = [_product(128, 64, 8960, torch.bfloat16, seed=7)]
+    rows_f, rows_u = _run_case(lib, prods, expect_fused=1)
+    _check_rows(prods, rows_f, rows_u)
+
+
+def test_fused_changed_entries_in_every_region(lib):
+    n, q, w = 128, 64, 1280  # 2560-byte rows
+    # row 0's first elements lie before the first 128-byte boundary (12-byte header), the last
+    # row's last ones after the last boundary, others at row ends inside pairs and at chunk
+    # boundaries
+    tamper = [(0, 0, 1.5), (0, 57, -2.0), (n - 1, w - 1, 3.0), (n - 1, w - 5, 0.5),
+              (5, w - 1, 1.25), (6, 0, 1.25), (40, 506, -1.0), (77, 640, 2.0)]
+    prods = [_product(n, q, w, torch.bfloat16, seed=11, tamper=tamper),
+             _product(n, q, w, torch.bfloat16, seed=12, tamper=[(0, 0, 1.0 + 2**-7)]),
+             _product(n, q, w, torch.bfloat16, seed=13)]
+    rows_f, rows_u = _run_case(lib, prods, expect_fused=3)
+    _check_rows(prods, rows_f, rows_u, tampered=(0, 1))
+    # eight changed entries stand well above the bf16 rounding of an honest P
+    assert max(rows_f[0][5:]) > 2 * max(rows_f[2][5:])
+
+
+def test_products_that_are_not_fused(lib):
+    dt = torch.bfloat16
+    small = _product(64, 32, 256, dt, seed=1)        # 512-byte rows
+    padded = _product(100, 32, 1000, dt, seed=2)     # 125 classes for 196 chunks
+    shared = _product(64, 32, 512, dt, seed=3)
+    prods = [small, padded, shared, (shared[0], shared[1], shared[2]),
+             _product(64, 32, 512, dt, seed=4)]      # only this one qualifies
+    from verification.commitment import native
+    dev = [(a.cuda(), b.cuda(), p.cuda()) for a, b, p in prods]
+    dev[3] = (dev[3][0], dev[3][1], dev[2][2])  # the same P tensor as product 3
+    leaves = [dev[0][2], dev[1][2], dev[2][2], dev[4][2]]
+    hdrs = [O.tensor_leaf_header(O.TAG_PRODUCT, t) for t in leaves]
+    kinds = [native.FINITE_KIND[dt]] * 4
+    fvp = [native.FvProduct(a, b, p, i + 1) for i, (a, b, p) in enumerate(dev)]
+    key = torch.tensor(list(KEY), dtype=torch.uint8, device="cuda")
+    rows_u = lib.fv_plan(fvp, 4).rows(key).cpu().tolist()
+    fv_f = lib.fv_plan(fvp, 4)
+    leaf_f = lib.leaf_plan(hdrs, leaves, kinds, fuse=fv_f)
+    assert leaf_f.fused == 1
+    dig = torch.empty(4, 32, dtype=torch.uint8, device="cuda")
+    bad = torch.empty(1, dtype=torch.int32, device="cuda")
+    rows = torch.empty(5, 9, dtype=torch.float64, device="cuda")
+    lib.step_run(leaf_f, fv_f, key, dig, bad, rows)
+    rows = rows.cpu().tolist()
+    assert [bytes(x) for x in dig.cpu().numpy()] == [
+        O.tensor_leaf_hash(O.TAG_PRODUCT, t.cpu()) for t in leaves]
+    for i in range(4):  # unfused products: the same kernels, the same bits
+        assert rows[i] == rows_u[i]
+    assert rows[4][:5] == pytest.approx(rows_u[4][:5], rel=1e-6)
+    # k != 4: nothing is fused
+    fv3 = lib.fv_plan(fvp, 3)
+    assert lib.leaf_plan(hdrs, leaves, kinds, fuse=fv3).fused == 0
+    # a plan is fused once
+    with pytest.raises(ValueError):
+        lib.leaf_plan(hdrs, leaves, kinds, fuse=fv_f)
+
+
+def test_payload_at_an_offset_is_not_fused(lib):
+    from verification.commitment import native
+    a, b, p = _product(64, 32, 256, torch.float32, seed=5)
+    buf = torch.zeros(p.numel() + 1, dtype=torch.float32, device="cuda")
+    buf[1:] = p.reshape(-1).cuda()
+    pv = buf[1:].view(64, 256)  # 4 bytes past a 16-byte boundary
+    fvp = [native.FvProduct(a.cuda(), b.cuda(), pv, 1)]
+    hdr = [O.tensor_leaf_header(O.TAG_PRODUCT, pv)]
+    fv = lib.fv_plan(fvp, 4)
+    assert lib.leaf_plan(hdr, [pv], [native.FINITE_KIND[torch.float32]], fuse=fv).fused == 0
+
+
+def test_non_finite_product_leaf_is_still_reported(lib):
+    from verification.commitment import native
+    prods = [_product(64, 32, 512, torch.bfloat16, seed=s) for s in range(3)]
+    dev = [(a.cuda(), b.cuda(), p.cuda()) for a, b, p in prods]
+    dev[1][2][30, 100] = float("nan")
+    leaves = [p for _, _, p in dev]
+    hdrs = [O.tensor_leaf_header(O.TAG_PRODUCT, t) for t in leaves]
+    fv = lib.fv_plan([native.FvProduct(a, b, p, i + 1) for i, (a, b, p) in enumerate(dev)], 4)
+    leaf = lib.leaf_plan(hdrs, leaves, [native.FINITE_KIND[torch.bfloat16]] * 3, fuse=fv)
+    assert leaf.fused == 3
+    key = torch.tensor(list(KEY), dtype=torch.uint8, device="cuda")
+    dig = torch.empty(3, 32, dtype=torch.uint8, device="cuda")
+    bad = torch.empty(1, dtype=torch.int32, device="cuda")
+    rows = torch.empty(3, 9, dtype=torch.float64, device="cuda")
+    lib.step_run(leaf, fv, key, dig, bad, rows)
+    assert int(bad.item()) == 1
+
+
+def test_device_step_verifier_fused_equals_unfused(lib):
+    from verification.computation.instances.decoder import DecoderComputation
+    from verification.prover.synthetic import synthetic_step
+    from verification.verifier.step import DeviceStepVerifier
+    c = DecoderComputation(L=1, d=512, d_f=1024, n_h=4, n_kv=2, n_v=1024, n_s=2, n=256,
+                           qkv_bias=True, compute_dtype=torch.bfloat16)
+    step = synthetic_step(c, seed=3, operands=True)
+    fused = DeviceStepVerifier(c, step.leaves, lambda s: step.operands[s.m], k=4)
+    plain = DeviceStepVerifier(c, step.leaves, lambda s: step.operands[s.m], k=4, fuse=False)
+    assert fused.fused > 0 and plain.fused == 0
+    d, _ = plain.hasher.digests()
+    claimed = bytes(lib.merkle_tree_device(d)[0].cpu().numpy())
+    for _ in range(2):
+        a, b = fused.run(claimed), plain.run(claimed)
+        assert a.root == b.root == claimed
+        assert (a.first_bad, a.first_fail, a.check) == (b.first_bad, b.first_fail, b.check)
+        assert torch.equal(a.codes, b.codes)
+        ra, rb = a.rows.cpu(), b.rows.cpu()
+        assert torch.allclose(ra[:, :5], rb[:, :5], rtol=1e-6, atol=0)
