@@ -8,10 +8,13 @@ hash every leaf (BLAKE3 chunks, per-leaf trees, NaN/Inf test fused) and build th
 root; expand the claimed root into every product's challenge matrix; run the three
 Freivalds passes over every product's B, A and P; reduce to one fp64 row per product; judge
 every product. One host read at the end of the step (root, first non-finite leaf, first
-rejected product).
+rejected product). Each product's P is a leaf, and the hashing kernel takes the P pass of the
+product leaves it streams (pots_leaf_plan_create_fused), so those P are read from HBM once.
 
 Prints one JSON line (the driver's contract): `value` is the step's verified throughput,
-(bytes hashed + bytes Freivalds-checked) / step time, in GB/s; `parts` splits it by stage;
+(bytes hashed + bytes Freivalds-checked) / step time, in GB/s, every P counted in both (it is
+hashed and Freivalds-checked) though the fused kernel reads it once; `parts` splits it by
+stage and gives the HBM bytes the step actually reads;
 `roofline` is the dominant kernel against MI355X's 8 TB/s; `cpu_baseline` times the CPU
 oracle on a bounded sample of the same transcript on the host's cores.
 
@@ -194,11 +197,13 @@ def trace_summary(d: Path, steps: int, warmup: int) -> int:
         if k.startswith("pots::") or k.startswith("__amd"):
             print(f"| `{k}` | {len(ds)} | {sum(ds) / len(ds):.3f} | {min(ds):.3f} | "
                   f"{max(ds):.3f} |")
-    ck = by.get("pots::chunk_kernel", [])
+    name = "pots::chunk_kernel_fused" if "pots::chunk_kernel_fused" in by else \
+        "pots::chunk_kernel"
+    ck = by.get(name, [])
     n_pre = 1 + warmup
     timed, leg = ck[n_pre:n_pre + steps], ck[n_pre + steps:]
     if timed and leg:
-        print(f"\nchunk_kernel: {len(timed)} launches in the timed steps, mean "
+        print(f"\n{name[6:]}: {len(timed)} launches in the timed steps, mean "
               f"{sum(timed) / len(timed):.3f} ms (beside the Freivalds passes); {len(leg)} "
               f"launches in the serialised stage leg, mean {sum(leg) / len(leg):.3f} ms")
     return 0
@@ -225,6 +230,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--hash-first", action="store_true",
+                    help="start the fused chunk kernel after the challenges, not the B pass")
+    ap.add_argument("--plain-early", action="store_true",
+                    help="hash the unfused leaves while the B pass runs")
+    ap.add_argument("--b-grid", type=int, default=0,
+                    help="blocks of the B pass (0: one per tile)")
+    ap.add_argument("--a-grid", type=int, default=None,
+                    help="blocks of the A pass (default: one per CU when fused, else one per "
+                         "tile); see pots_fv_plan_set_grid")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="copy this many MiB device to device twice before timing, so a "
                          "counter run sees a plain copy kernel of known size")
@@ -271,7 +285,9 @@ def main() -> int:
 
     stream = torch.cuda.current_stream()
     items = product_inputs(step)
-    v = DeviceStepVerifier(c, step.leaves, lambda spec: step.operands[spec.m], k=k)
+    v = DeviceStepVerifier(c, step.leaves, lambda spec: step.operands[spec.m], k=k,
+                           a_grid=args.a_grid, b_grid=args.b_grid,
+                           hash_after_b=not args.hash_first, plain_early=args.plain_early)
     # The claimed root: the honest root of this transcript, as the prover would send it.
     v.hasher.digests(v.digests, v.bad, stream)
     claimed = lib.merkle_tree_device(v.digests, stream)[0].clone()
@@ -311,8 +327,11 @@ def main() -> int:
     # Stage leg: the same work serialised on one stream, every stage bracketed by events on
     # that stream, for the per-kernel figures and the roofline.
     # (The challenges come first: a fused chunk kernel reads them.)
+    # The chunk stage's two kernels are timed apart: the fused leaves' and the others'.
     fv_stages = native.FvPlan.STAGES
-    names = ([f"freivalds.{fv_stages[0]}"] + [f"hash.{s}" for s in native.LeafPlan.STAGES] +
+    leaf_stages = [(0, "hash.stage"), (native.LeafPlan.FUSED_CHUNKS, "hash.chunks_fused"),
+                   (native.LeafPlan.PLAIN_CHUNKS, "hash.chunks"), (2, "hash.levels")]
+    names = ([f"freivalds.{fv_stages[0]}"] + [nm for _, nm in leaf_stages] +
              ["tree"] + [f"freivalds.{s}" for s in fv_stages[1:]] + ["verdicts"])
 
     def staged(ev):
@@ -322,7 +341,7 @@ def main() -> int:
         v.plan.run_stage(0, v.key, v.rows, stream)
         i += 1
         ev[i].record(stream)
-        for st in range(len(native.LeafPlan.STAGES)):
+        for st, _ in leaf_stages:
             v.hasher.plan.run_stage(st, v.digests, v.bad, stream)
             i += 1
             ev[i].record(stream)
@@ -382,20 +401,30 @@ def main() -> int:
     a_bytes = sum(a.nbytes for a, _, _, _, _ in items)
     b_bytes = sum(b.nbytes for _, b, _, _, _ in items)
     p_bytes = sum(p.nbytes for _, _, p, _, _ in items)
+    hp = v.hasher.plan
     kernels = {
-        "hash.chunks": ("chunk_kernel", hash_bytes + 32 * v.hasher.plan.chunks),
+        "hash.chunks": ("chunk_kernel", hash_bytes - hp.fused_bytes +
+                        32 * (hp.chunks - hp.fused_chunks)),
         "freivalds.a_pass": ("row_pass<bf16, weighted> (A pass)", a_bytes),
         "freivalds.b_pass": ("row_pass<bf16> (B pass)", b_bytes),
     }
-    if not v.fused:  # fused, the P pass reads only the products the chunk kernel did not take
+    if v.fused:  # message bytes read, chaining values and run records written
+        kernels["hash.chunks_fused"] = ("chunk_kernel_fused", hp.fused_bytes +
+                                        32 * hp.fused_chunks + 32 * hp.fused_records)
+    else:  # fused, the P pass reads only the products the chunk kernel did not take
         kernels["freivalds.p_pass"] = ("row_pass<bf16, fp64 squares> (P pass)", p_bytes)
     dom = max(kernels, key=lambda nm: stage_ms[nm])
+    # the kernel the step's chunk events bracket
+    in_step_kernel = "hash.chunks_fused" if v.fused else "hash.chunks"
     dom_name, dom_bytes = kernels[dom]
     achieved = dom_bytes / (stage_ms[dom] * 1e-3) / 1e9
-    hash_ms = sum(stage_ms[f"hash.{s}"] for s in native.LeafPlan.STAGES)
+    hash_ms = sum(stage_ms[nm] for _, nm in leaf_stages)
     fv_ms = sum(stage_ms[f"freivalds.{s}"] for s in native.FvPlan.STAGES)
     total = hash_bytes + fv_bytes
     value = total / (ms * 1e-3) / 1e9
+    # P of a fused product is read once, by the hashing kernel (its leaf message is the
+    # 12-byte 0x00 || header of a 2-D tensor, then P)
+    read_bytes = hash_bytes + a_bytes + b_bytes + p_bytes - (hp.fused_bytes - 12 * v.fused)
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
@@ -406,9 +435,14 @@ def main() -> int:
                                "Merkle root, check 5 challenges + Freivalds + verdicts) on a "
                                "transcript resident in HBM",
                    "leaves": c.n_leaves, "products": c.M, "k": k,
-                   "hash_bytes": hash_bytes, "freivalds_bytes": fv_bytes},
+                   "hash_bytes": hash_bytes, "freivalds_bytes": fv_bytes,
+                   "p_pass_fused_products": v.fused,
+                   "a_pass_blocks": v.a_grid},
         "parts": {"step_verify_ms": round(ms, 3),
                   "step_frac_hbm": round(value / HBM_PEAK_GBPS, 4),
+                  # bytes the step reads once each: every leaf, and the A and B operands
+                  "step_read_bytes": read_bytes,
+                  "step_read_gbps": round(read_bytes / (ms * 1e-3) / 1e9, 1),
                   "overlap": {"hashed_at_ms": round(hashed_ms, 3),
                               "rows_at_ms": round(measured_ms, 3),
                               "serial_ms": round(serial_ms, 3)},
@@ -421,11 +455,11 @@ def main() -> int:
                   "check_6a": check_6a},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_from_profile(dom_name) if dom == "hash.chunks" else None,
+                     "traffic": traffic_from_profile(dom_name),
                      "kernel": dom_name,
                      "algorithmic_bytes": dom_bytes, "launch_ms": round(stage_ms[dom], 4),
                      "launch_ms_in_step": (round(chunks_in_step_ms, 4)
-                                           if dom == "hash.chunks" else None)},
+                                           if dom == in_step_kernel else None)},
     }
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")

@@ -97,6 +97,11 @@ int pots_leaf_plan_run(void *plan, uint8_t *d_out, uint32_t *d_first_bad, void *
  * per-leaf BLAKE3 trees above the chunks. Enqueued on `stream` one at a time, so a caller can
  * time each stage; the caller keeps the order. No counterpart in the reference. */
 #define POTS_LEAF_STAGES 3
+/* Stage 1 is two kernels, which a caller may also enqueue apart (each once, both before
+ * stage 2): the chunks of the leaves fused with a Freivalds plan's products
+ * (pots_leaf_plan_create_fused; it reads the challenges), and the chunks of the others. */
+#define POTS_LEAF_STAGE_FUSED_CHUNKS 3
+#define POTS_LEAF_STAGE_PLAIN_CHUNKS 4
 int pots_leaf_plan_run_stage(void *plan, int stage, uint8_t *d_out, uint32_t *d_first_bad,
                              void *stream);
 
@@ -127,6 +132,12 @@ int pots_leaf_plan_create_fused(size_t n, const uint8_t *hdr_buf, const uint64_t
 /* Leaves of the plan whose product's P-pass sums its chunk stage takes (0 for an unfused
  * plan). */
 uint32_t pots_leaf_plan_fused(const void *plan);
+
+/* What one run of the fused chunk kernel moves: the fused leaves' message bytes (read), their
+ * 1 KiB chunks (a 32-byte chaining value written each) and the run records it writes (32 bytes
+ * each). Returns POTS_E_*. */
+int pots_leaf_plan_fused_stats(const void *plan, uint64_t *msg_bytes, uint64_t *chunks,
+                               uint64_t *records);
 
 /* One step on one stream: fv stage 0, the leaf plan's stages, fv stages 1-5 (digests and
  * first-bad as pots_leaf_plan_run, rows as pots_fv_plan_run). For a fused pair of plans and
@@ -182,6 +193,13 @@ int pots_fv_plan_run(void *plan, const uint8_t *d_key, double *d_rows, void *str
 #define POTS_FV_STAGES 6
 int pots_fv_plan_run_stage(void *plan, int stage, const uint8_t *d_key, double *d_rows,
                            void *stream);
+
+/* Limit the row-pass grid of stage 1 (B pass), 3 (A pass) or 4 (P pass) to max_blocks blocks
+ * of 256 lanes (0: no limit, one block per tile). Each block then takes several tiles in turn
+ * and the pass holds at most that many blocks' worth of the GPU, so that a kernel on another
+ * stream (the leaf hasher, which needs every SIMD's VALUs) can share the CUs. Results do not
+ * depend on it. No counterpart in the reference. */
+int pots_fv_plan_set_grid(void *plan, int stage, uint32_t max_blocks);
 
 /* Copy the last run's row-major challenge matrices (fp32; product i's [w_i, k] block follows
  * product i-1's) to d_out (device, Σ w_i·k floats), enqueued on `stream`. */

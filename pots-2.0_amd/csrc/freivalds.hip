@@ -252,21 +252,21 @@ __device__ __forceinline__ void compute_stage(const StageRegs<NJG>& r, v4f32 acc
   }
 }
 
-// One block: job blk_job[blockIdx.x], 64-row group, column chunk and column-group block
-// decoded from its index within the job (row group fastest).
+// One tile: job blk_job[bidx], 64-row group, column chunk and column-group block decoded
+// from its index within the job (row group fastest). Every wave of the block calls it with the
+// same tile and reaches its barrier.
 template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
-__global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
-                                                const uint32_t* __restrict__ blk_job,
-                                                uint32_t k) {
+__device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
+                                         const uint32_t* __restrict__ blk_job, uint32_t k,
+                                         uint32_t bidx, float* s_u, float* s_w) {
   using G = Geo<XT>;
   constexpr uint32_t SSTEP = G::KSTEP * KU;
-  __shared__ float s_u[WEIGHTED ? G::CHUNK : 4], s_w[WEIGHTED ? G::CHUNK : 4];
   // The wave index is uniform; readfirstlane lets the compiler keep everything derived from
   // it in scalar registers, so the loop has no divergent branches.
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63;
-  const PassJob J = jobs[blk_job[blockIdx.x]];
-  uint32_t local = blockIdx.x - (uint32_t)J.block_first;
+  const PassJob J = jobs[blk_job[bidx]];
+  uint32_t local = bidx - (uint32_t)J.block_first;
   const uint32_t rg = local % J.n_rg;
   local /= J.n_rg;
   const uint32_t chunk = local % J.n_chunks;
@@ -384,6 +384,21 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
       gstore<float>(pabs + cbase + row, a);
       gstore<double>(psq + cbase + row, q);
     }
+  }
+}
+
+// The row pass over n_tiles tiles: block b takes tiles b, b + gridDim.x, ... A grid smaller
+// than the tile count keeps the pass to a bounded share of each CU (a block holds 4 waves and
+// 32 KiB of LDS), so that a kernel on another stream (the leaf hasher) keeps the rest.
+template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
+__global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
+                                                const uint32_t* __restrict__ blk_job,
+                                                uint32_t k, uint32_t n_tiles) {
+  using G = Geo<XT>;
+  __shared__ float s_u[WEIGHTED ? G::CHUNK : 4], s_w[WEIGHTED ? G::CHUNK : 4];
+  for (uint32_t b = blockIdx.x; b < n_tiles; b += gridDim.x) {
+    row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, b, s_u, s_w);
+    if (WEIGHTED) __syncthreads();  // the next tile restages the weights
   }
 }
 
@@ -775,6 +790,7 @@ struct FvPlan {
   std::vector<FinJob> h_fin;
   std::unordered_map<uint64_t, int64_t> p_index;  // P address -> product (-1: shared)
   // Fused products: their run records and fix-up jobs, one allocation.
+  uint32_t max_grid[POTS_FV_STAGES] = {};  // row-pass grid limits (0: a block per tile)
   bool fused = false;
   char* fbase = nullptr;
   FixJob* d_fix = nullptr;
@@ -1302,33 +1318,35 @@ int fv_fuse_commit(void* fv, const std::vector<uint32_t>& prods,
 }  // namespace pots
 
 template <uint32_t XT, bool W, bool S, uint32_t NJG>
-static void launch_pass(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
-  hipLaunchKernelGGL((row_pass<XT, W, S, NJG>), dim3(L.n_blocks), dim3(256), 0, s,
-                     P->d_jobs + L.job_off, P->d_blk + L.blk_off, P->k);
+static void launch_pass(const FvPlan* P, const PassLaunch& L, uint32_t max_grid,
+                        hipStream_t s) {
+  const uint32_t grid = max_grid ? std::min(max_grid, L.n_blocks) : L.n_blocks;
+  hipLaunchKernelGGL((row_pass<XT, W, S, NJG>), dim3(grid), dim3(256), 0, s,
+                     P->d_jobs + L.job_off, P->d_blk + L.blk_off, P->k, L.n_blocks);
 }
 
 template <uint32_t XT, bool W, bool S>
-static int launch_njg(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
+static int launch_njg(const FvPlan* P, const PassLaunch& L, uint32_t g, hipStream_t s) {
   switch (L.njg) {
-    case 1: launch_pass<XT, W, S, 1>(P, L, s); return POTS_E_OK;
-    case 2: launch_pass<XT, W, S, 2>(P, L, s); return POTS_E_OK;
-    case 3: launch_pass<XT, W, S, 3>(P, L, s); return POTS_E_OK;
-    case 4: launch_pass<XT, W, S, 4>(P, L, s); return POTS_E_OK;
+    case 1: launch_pass<XT, W, S, 1>(P, L, g, s); return POTS_E_OK;
+    case 2: launch_pass<XT, W, S, 2>(P, L, g, s); return POTS_E_OK;
+    case 3: launch_pass<XT, W, S, 3>(P, L, g, s); return POTS_E_OK;
+    case 4: launch_pass<XT, W, S, 4>(P, L, g, s); return POTS_E_OK;
     default: return POTS_E_ARG;
   }
 }
 
-static int run_pass(const FvPlan* P, const PassLaunch& L, hipStream_t s) {
+static int run_pass(const FvPlan* P, const PassLaunch& L, uint32_t g, hipStream_t s) {
   if (L.n_blocks == 0) return POTS_E_OK;
   const uint32_t key = L.xt * 4 + L.weighted * 2 + L.sq64;
   int rc;
   switch (key) {
-    case 0: rc = launch_njg<DT_F32, false, false>(P, L, s); break;
-    case 1: rc = launch_njg<DT_F32, false, true>(P, L, s); break;
-    case 2: rc = launch_njg<DT_F32, true, false>(P, L, s); break;
-    case 4: rc = launch_njg<DT_BF16, false, false>(P, L, s); break;
-    case 5: rc = launch_njg<DT_BF16, false, true>(P, L, s); break;
-    case 6: rc = launch_njg<DT_BF16, true, false>(P, L, s); break;
+    case 0: rc = launch_njg<DT_F32, false, false>(P, L, g, s); break;
+    case 1: rc = launch_njg<DT_F32, false, true>(P, L, g, s); break;
+    case 2: rc = launch_njg<DT_F32, true, false>(P, L, g, s); break;
+    case 4: rc = launch_njg<DT_BF16, false, false>(P, L, g, s); break;
+    case 5: rc = launch_njg<DT_BF16, false, true>(P, L, g, s); break;
+    case 6: rc = launch_njg<DT_BF16, true, false>(P, L, g, s); break;
     default: return POTS_E_ARG;
   }
   if (rc != POTS_E_OK) return rc;
@@ -1357,7 +1375,7 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
       return POTS_E_OK;
     case 1:
       for (const PassLaunch& L : P->pass_b)
-        if ((rc = run_pass(P, L, s)) != POTS_E_OK) return rc;
+        if ((rc = run_pass(P, L, P->max_grid[1], s)) != POTS_E_OK) return rc;
       return POTS_E_OK;
     case 2: {
       const uint64_t blocks = (P->n_red_threads + 255) / 256;
@@ -1370,7 +1388,8 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
     case 3:
     case 4:
       for (const PassLaunch& L : P->pass_ap)
-        if ((L.weighted != 0) == (stage == 3) && (rc = run_pass(P, L, s)) != POTS_E_OK)
+        if ((L.weighted != 0) == (stage == 3) &&
+            (rc = run_pass(P, L, P->max_grid[stage], s)) != POTS_E_OK)
           return rc;
       if (stage == 4 && P->fused) {
         if (P->n_fix == 0) return POTS_E_HIP;  // a fusion that failed half way
@@ -1414,6 +1433,12 @@ extern "C" int pots_fv_plan_run_stage(void* plan, int stage, const uint8_t* d_ke
   if (!plan || !d_key || !d_rows || stage < 0 || stage >= POTS_FV_STAGES) return POTS_E_ARG;
   return run_stage(static_cast<FvPlan*>(plan), stage, d_key, d_rows,
                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pots_fv_plan_set_grid(void* plan, int stage, uint32_t max_blocks) {
+  if (!plan || (stage != 1 && stage != 3 && stage != 4)) return POTS_E_ARG;
+  static_cast<FvPlan*>(plan)->max_grid[stage] = max_blocks;
+  return POTS_E_OK;
 }
 
 extern "C" int pots_fv_plan_copy_challenges(const void* plan, float* d_out, void* stream) {

@@ -508,6 +508,7 @@ struct LeafPlan {
   size_t n = 0;
   uint64_t n_chunks = 0, bytes = 0;
   uint32_t n_fused = 0;  // product leaves whose P-pass sums the chunk kernel takes
+  uint64_t fused_msg = 0, fused_chunks = 0, fused_records = 0;  // per run of the fused kernel
   FuseDesc* d_fuse = nullptr;
   Order plain{}, fused{};  // the two kernels' chunk orders (device tables)
   bool owned = false;
@@ -667,6 +668,16 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
       fprod.push_back(fp.prod);
       fhead.push_back((uint32_t)hl);
       fused.add((uint32_t)i, slots);  // slots: a multiple of 64, so every entry is aligned
+      P->fused_msg += L;
+      P->fused_chunks += nck;
+      {  // run records: one per (row, chunk) with elements of the row in the chunk's pairs
+        const uint64_t hc = (hl + 127) & ~uint64_t(127), lf = L & ~uint64_t(127);
+        for (uint64_t r = 0; r < fp.n; r++) {
+          const uint64_t fs = std::max<uint64_t>(hl + r * f.row_bytes, hc);
+          const uint64_t fe = std::min<uint64_t>(hl + (r + 1) * f.row_bytes, lf);
+          if (fs < fe) P->fused_records += ((fe - 1) >> 10) - (fs >> 10) + 1;
+        }
+      }
     } else {
       plain.add((uint32_t)i, nck);
     }
@@ -842,6 +853,7 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
 // 2 the per-leaf tree levels.
 static int plan_stage(LeafPlan* P, int stage, uint32_t* d_digests, uint32_t* d_first_bad,
                       hipStream_t stream) {
+  int rc;
   switch (stage) {
     case 0:
       for (const StageCopy& s : P->stages) {
@@ -857,9 +869,12 @@ static int plan_stage(LeafPlan* P, int stage, uint32_t* d_digests, uint32_t* d_f
       hipLaunchKernelGGL(fill_u32, dim3(1), dim3(1), 0, stream, d_first_bad, (uint32_t)P->n);
       POTS_HIP(hipGetLastError());
       return POTS_E_OK;
-    case 1:
-      // The fused leaves first: with the other kernel's blocks queued behind them, the two
-      // kernels' tails overlap.
+    case 1:  // both chunk kernels: the fused leaves' (3), then the others' (4)
+      if ((rc = plan_stage(P, POTS_LEAF_STAGE_FUSED_CHUNKS, d_digests, d_first_bad, stream)) !=
+          POTS_E_OK)
+        return rc;
+      return plan_stage(P, POTS_LEAF_STAGE_PLAIN_CHUNKS, d_digests, d_first_bad, stream);
+    case POTS_LEAF_STAGE_FUSED_CHUNKS:
       if (P->fused.n_blocks) {
         hipLaunchKernelGGL(chunk_kernel_fused,
                            dim3(P->max_grid ? std::min(P->max_grid, P->fused.n_blocks)
@@ -868,6 +883,8 @@ static int plan_stage(LeafPlan* P, int stage, uint32_t* d_digests, uint32_t* d_f
                            P->d_head, P->d_cv[0], d_first_bad);
         POTS_HIP(hipGetLastError());
       }
+      return POTS_E_OK;
+    case POTS_LEAF_STAGE_PLAIN_CHUNKS:
       if (P->plain.n_blocks) {
         hipLaunchKernelGGL(chunk_kernel,
                            dim3(P->max_grid ? std::min(P->max_grid, P->plain.n_blocks)
@@ -966,6 +983,16 @@ extern "C" uint32_t pots_leaf_plan_fused(const void* plan) {
   return plan ? static_cast<const LeafPlan*>(plan)->n_fused : 0;
 }
 
+extern "C" int pots_leaf_plan_fused_stats(const void* plan, uint64_t* msg_bytes,
+                                          uint64_t* chunks, uint64_t* records) {
+  if (!plan || !msg_bytes || !chunks || !records) return POTS_E_ARG;
+  const LeafPlan* P = static_cast<const LeafPlan*>(plan);
+  *msg_bytes = P->fused_msg;
+  *chunks = P->fused_chunks;
+  *records = P->fused_records;
+  return POTS_E_OK;
+}
+
 extern "C" int pots_step_run(void* leaf_plan, void* fv_plan, const uint8_t* d_key,
                              uint8_t* d_digests, uint32_t* d_first_bad, double* d_rows,
                              void* stream) {
@@ -992,7 +1019,8 @@ extern "C" int pots_leaf_plan_run(void* plan, uint8_t* d_out, uint32_t* d_first_
 
 extern "C" int pots_leaf_plan_run_stage(void* plan, int stage, uint8_t* d_out,
                                         uint32_t* d_first_bad, void* stream) {
-  if (!plan || !d_out || !d_first_bad || stage < 0 || stage >= POTS_LEAF_STAGES)
+  if (!plan || !d_out || !d_first_bad || stage < 0 ||
+      stage > POTS_LEAF_STAGE_PLAIN_CHUNKS)
     return POTS_E_ARG;
   return plan_stage(static_cast<LeafPlan*>(plan), stage, reinterpret_cast<uint32_t*>(d_out),
                     d_first_bad, static_cast<hipStream_t>(stream));

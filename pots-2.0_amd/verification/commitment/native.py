@@ -94,6 +94,7 @@ class Native:
             "pots_leaf_plan_create_fused": ([_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                              ctypes.POINTER(_vp)], _int),
             "pots_leaf_plan_fused": ([_vp], _u32),
+            "pots_leaf_plan_fused_stats": ([_vp, _vp, _vp, _vp], _int),
             "pots_step_run": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp], _int),
             "pots_merkle_tree_async": ([_sz, _vp, _vp, _vp], _int),
             "pots_challenges": ([_vp, _u32, _sz, _vp, _vp, _vp, _vp, _u32], _int),
@@ -101,6 +102,7 @@ class Native:
             "pots_fv_plan_run": ([_vp, _vp, _vp, _vp], _int),
             "pots_fv_plan_run_stage": ([_vp, _int, _vp, _vp, _vp], _int),
             "pots_fv_plan_copy_challenges": ([_vp, _vp, _vp], _int),
+            "pots_fv_plan_set_grid": ([_vp, _int, _u32], _int),
             "pots_fv_plan_bytes": ([_vp], _u64),
             "pots_fv_plan_destroy": ([_vp], None),
             "pots_verdicts_async": ([_sz, _vp, _u32, _vp, ctypes.c_double, ctypes.c_double,
@@ -324,6 +326,13 @@ class LeafPlan:
         # its challenges: the Freivalds plan lives at least as long.
         self._fv = fuse
         self.fused = int(lib._lib.pots_leaf_plan_fused(h))
+        st = (ctypes.c_uint64 * 3)()
+        lib._check(lib._lib.pots_leaf_plan_fused_stats(h, ctypes.byref(st, 0),
+                                                       ctypes.byref(st, 8),
+                                                       ctypes.byref(st, 16)),
+                   "pots_leaf_plan_fused_stats")
+        # the fused chunk kernel's message bytes, chunks and run records per run
+        self.fused_bytes, self.fused_chunks, self.fused_records = (int(x) for x in st)
         self.n = n
         self.chunks = int(lib._lib.pots_leaf_plan_chunks(h))
         self.bytes = int(lib._lib.pots_leaf_plan_bytes(h))
@@ -344,6 +353,9 @@ class LeafPlan:
         return out, bad
 
     STAGES = ("stage", "chunks", "levels")
+    # Stage 1's two kernels on their own (pots_leaf_plan_run_stage): the fused leaves' chunks
+    # and the other leaves' chunks.
+    FUSED_CHUNKS, PLAIN_CHUNKS = 3, 4
 
     def set_grid(self, max_blocks: int) -> None:
         """Limit the chunk kernel to ``max_blocks`` blocks (0: no limit); results are the same,
@@ -492,6 +504,15 @@ class FvPlan:
         self._lib._check(self._lib._lib.pots_fv_plan_run_stage(
             self._h, stage, key.data_ptr(), out.data_ptr(), _stream(stream)),
             "pots_fv_plan_run_stage")
+
+    def set_grid(self, stage: int, max_blocks: int) -> None:
+        """Limit the row pass of ``stage`` (1 B, 3 A, 4 P) to ``max_blocks`` blocks (0: no
+        limit); results are the same, the pass just leaves the rest of each CU to other
+        streams."""
+        if not 0 <= max_blocks < 1 << 32:
+            raise ValueError(f"max_blocks must be in [0, 2^32), got {max_blocks}")
+        self._lib._check(self._lib._lib.pots_fv_plan_set_grid(self._h, stage, max_blocks),
+                         "pots_fv_plan_set_grid")
 
     def challenges(self) -> list[torch.Tensor]:
         """The last run's challenge matrices, fp32 ``[w_i, k]`` per product (GPU views)."""

@@ -56,7 +56,9 @@ class DeviceStepVerifier:
     :meth:`run` with the claimed root."""
 
     def __init__(self, c: DeclaredComputation, leaves: Sequence[Any], operands: Any, *, k: int,
-                 bands: Bands | None = None, guard: bool = True, fuse: bool = True) -> None:
+                 bands: Bands | None = None, guard: bool = True, fuse: bool = True,
+                 a_grid: int | None = None, b_grid: int = 0, hash_after_b: bool = True,
+                 plain_early: bool = False) -> None:
         self.c, self.k, self.guard = c, k, guard
         self.bands = bands or Bands.provisional()
         lib = self.lib = native.get()
@@ -69,10 +71,19 @@ class DeviceStepVerifier:
                 bias = leaves[c.w_t_index(spec.bias)].to(c.operand_dtype).to(torch.float32)
             prods.append(native.FvProduct(a, b, p, spec.m, bias))
         self.plan = lib.fv_plan(prods, k, guard)
+        # A bounded A pass (``a_grid`` blocks, 0: one per tile) leaves room on every CU for the
+        # hashing kernels beside it.
+        self.hash_after_b, self.plain_early = hash_after_b, plain_early
         # Fused: the chunk kernel takes the P-pass sums of the product leaves it hashes, so
         # each P is read from HBM once (pots_leaf_plan_create_fused).
         self.hasher = StepHasher(c, leaves, fuse=self.plan if fuse else None)
         self.fused = self.hasher.plan.fused
+        if a_grid is None:  # fused: one A-pass block per CU beside the chunk kernel
+            a_grid = torch.cuda.get_device_properties(leaves[-1].device).multi_processor_count \
+                if self.fused else 0
+        self.plan.set_grid(3, a_grid)
+        self.plan.set_grid(1, b_grid)
+        self.a_grid = a_grid
         self.specs = native.verdict_specs(
             [s.q for s in c.products], [s.a_shape[0] for s in c.products],
             [s.bias is not None for s in c.products],
@@ -101,32 +112,46 @@ class DeviceStepVerifier:
         start = torch.cuda.Event(enable_timing=events is not None)
         start.record(main)
         timing = events is not None
-        plan = self.plan
-        if self.fused:  # the chunk kernel reads the challenges
-            plan.run_stage(0, self.key, self.rows, main)
-            ready = torch.cuda.Event()
-            ready.record(main)
-            self.side.wait_event(ready)
-        else:
-            self.side.wait_event(start)
+        plan, hp, side = self.plan, self.hasher.plan, self.side
         c_begin = torch.cuda.Event(enable_timing=timing)
         c_end = torch.cuda.Event(enable_timing=timing)
-        with torch.cuda.stream(self.side):
-            hp = self.hasher.plan
-            hp.run_stage(0, self.digests, self.bad, self.side)
-            c_begin.record(self.side)
-            hp.run_stage(1, self.digests, self.bad, self.side)
-            c_end.record(self.side)
-            hp.run_stage(2, self.digests, self.bad, self.side)
-            nodes = self.lib.merkle_tree_device(self.digests, self.side)
+        side.wait_event(start)
+        if not self.fused:
+            with torch.cuda.stream(side):
+                hp.run_stage(0, self.digests, self.bad, side)
+                c_begin.record(side)
+                hp.run_stage(1, self.digests, self.bad, side)
+                c_end.record(side)
+            for st in range(5):
+                plan.run_stage(st, self.key, self.rows, main)
+        else:
+            # The fused chunk kernel reads the challenges and, started after the B pass,
+            # shares the CUs with a bounded A pass; the other leaves' chunks go first.
+            with torch.cuda.stream(side):
+                hp.run_stage(0, self.digests, self.bad, side)
+                if self.plain_early:
+                    hp.run_stage(native.LeafPlan.PLAIN_CHUNKS, self.digests, self.bad, side)
+            for st in range(3 if self.hash_after_b else 1):
+                plan.run_stage(st, self.key, self.rows, main)
+            ready = torch.cuda.Event()
+            ready.record(main)
+            side.wait_event(ready)
+            with torch.cuda.stream(side):
+                c_begin.record(side)
+                hp.run_stage(native.LeafPlan.FUSED_CHUNKS, self.digests, self.bad, side)
+                c_end.record(side)
+                if not self.plain_early:
+                    hp.run_stage(native.LeafPlan.PLAIN_CHUNKS, self.digests, self.bad, side)
+            for st in range(3 if self.hash_after_b else 1, 4):
+                plan.run_stage(st, self.key, self.rows, main)
+            main.wait_event(c_end)  # the P stage adds up the fused kernel's run records
+            plan.run_stage(4, self.key, self.rows, main)
+        with torch.cuda.stream(side):
+            hp.run_stage(2, self.digests, self.bad, side)
+            nodes = self.lib.merkle_tree_device(self.digests, side)
         hashed = torch.cuda.Event(enable_timing=events is not None)
-        hashed.record(self.side)
-        for st in range(1 if self.fused else 0, 4):
-            plan.run_stage(st, self.key, self.rows, main)
-        if self.fused:  # stage 4 adds up the chunk kernel's run records
-            main.wait_event(c_end)
-        for st in (4, 5):
-            plan.run_stage(st, self.key, self.rows, main)
+        hashed.record(side)
+        plan.run_stage(5, self.key, self.rows, main)
         measured = torch.cuda.Event(enable_timing=events is not None)
         measured.record(main)
         main.wait_event(hashed)
