@@ -709,6 +709,7 @@ __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ job
   const uint64_t hc = (H + 127) & ~uint64_t(127), lf = L & ~uint64_t(127);
   const uint64_t fs = max<uint64_t>(H + i * rb, hc), fe = min<uint64_t>(H + (i + 1) * rb, lf);
   double d[4] = {0.0, 0.0, 0.0, 0.0}, s1 = 0.0, s2 = 0.0;
+  bool exact = false;
   if (fs < fe) {
     const char* rec = reinterpret_cast<const char*>(J.seg) + (uint64_t)kRunBytes * i * J.J;
     for (uint64_t c = fs >> 10; c <= (fe - 1) >> 10; c++, rec += kRunBytes) {
@@ -716,17 +717,20 @@ __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ job
       const u32x4 b = gload<u32x4>(rec + 16);
       for (int j = 0; j < 4; j++) d[j] += (double)a[j];
       s1 += (double)__uint_as_float(b.x);
+      exact |= b.y != 0u;
       s2 += __longlong_as_double((long long)((uint64_t)b.w << 32 | b.z));
     }
   }
   const float* R = reinterpret_cast<const float*>(J.r);
+  auto elem = [&](uint64_t e) {
+    return J.esz == 2 ? __uint_as_float((uint32_t)gload<uint16_t>(
+                                            reinterpret_cast<const uint16_t*>(J.p) + e)
+                                        << 16)
+                      : gload<float>(reinterpret_cast<const float*>(J.p) + e);
+  };
   auto rest = [&](uint64_t b0, uint64_t b1) {  // payload bytes [b0, b1) of row i
     for (uint64_t e = b0 / J.esz; e < b1 / J.esz; e++) {
-      const float x = J.esz == 2
-                          ? __uint_as_float((uint32_t)gload<uint16_t>(
-                                                reinterpret_cast<const uint16_t*>(J.p) + e)
-                                            << 16)
-                          : gload<float>(reinterpret_cast<const float*>(J.p) + e);
+      const float x = elem(e);
       const uint64_t col = e - (uint64_t)i * J.w;
       for (int j = 0; j < 4; j++) d[j] += (double)x * (double)gload<float>(R + col * 4 + j);
       s1 += fabs((double)x);
@@ -735,6 +739,13 @@ __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ job
   };
   if (i == 0 && hc > H) rest(0, hc - H);
   if (i + 1 == J.n && lf < L) rest(lf - H, L - H);
+  if (exact) {  // a run met exponents out of fp32 squares' range: the row's squares in fp64
+    s2 = 0.0;
+    for (uint64_t e = (uint64_t)i * J.w; e < (uint64_t)(i + 1) * J.w; e++) {
+      const double x = elem(e);
+      s2 += x * x;
+    }
+  }
   float* pdot = reinterpret_cast<float*>(J.pdot);
   for (int j = 0; j < 4; j++) gstore<float>(pdot + (uint64_t)i * 4 + j, (float)d[j]);
   gstore<float>(reinterpret_cast<float*>(J.pabs) + i, (float)s1);

@@ -121,6 +121,13 @@ struct Fin {
 // fp32 over each 128-byte pair and in fp64 across pairs. A run ends where its row does (the
 // row boundary is at the same offset in every lane of the wave, so the branch is uniform) and
 // at the end of the chunk, and is written as one record.
+//
+// Σx² in fp32 is exact to rounding only while the squares are normal and their sum finite: a
+// run with a pair whose largest biased exponent (from the NaN/Inf test's per-pair maximum) is
+// outside [kSqLo, kSqHi] (|x| below 2^-50 or from 2^63 on) is marked in its record, and the
+// P stage then takes that row's squares in fp64 from P, as the unfused P pass does.
+
+constexpr uint32_t kSqLo = 127 - 50, kSqHi = 127 + 62;
 
 typedef float v4f32 __attribute__((ext_vector_type(4)));
 #define POTS_CONST __attribute__((address_space(4)))
@@ -129,14 +136,19 @@ struct PRun {
   float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f, s1 = 0.f;
   double s2 = 0.0;
   bool live = false;
+  bool exact = false;  // a pair's exponents leave fp32 squares' range: the row is redone in fp64
 };
 
 // The elements t in [lo, hi) of a 128-byte pair (words w[0..31] of payload) into the run;
 // element t's column is R row rcol + t (rcol: wave-uniform address of R's row for t = 0).
 // Unmasked, every element of the pair is taken and the bounds are not read.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Elements t in [lo, hi) of a pair (its 32 payload words w) into the run. `emax`: the pair's
+// largest biased exponent; outside [kSqLo, kSqHi] the run is marked for the exact squares.
 template <int ESZ, bool MASKED>
 __device__ __forceinline__ void run_add(const uint32_t* w, uint64_t rcol, uint32_t lo,
-                                        uint32_t hi, PRun& a) {
+                                        uint32_t hi, uint32_t emax, PRun& a) {
   constexpr int NE = 128 / ESZ;
   const POTS_CONST v4f32* R = reinterpret_cast<const POTS_CONST v4f32*>(rcol);
   float q = 0.f;
@@ -152,9 +164,17 @@ __device__ __forceinline__ void run_add(const uint32_t* w, uint64_t rcol, uint32
     a.d2 = fmaf(x, r[2], a.d2);
     a.d3 = fmaf(x, r[3], a.d3);
     a.s1 += fabsf(x);
-    q = fmaf(x, x, q);
+    if (MASKED || ESZ == 4) q = fmaf(x, x, q);
+  }
+  if (!MASKED && ESZ == 2) {  // lo² + hi² per word; products of bf16 values are exact in fp32
+#pragma unroll
+    for (int u = 0; u < 32; u++) {
+      const bf16x2 v = __builtin_bit_cast(bf16x2, w[u]);
+      q = __builtin_amdgcn_fdot2_f32_bf16(v, v, q, false);
+    }
   }
   a.s2 += (double)q;
+  a.exact |= emax < kSqLo || emax > kSqHi;
   a.live = true;
 }
 
@@ -170,7 +190,8 @@ __device__ __forceinline__ void run_flush(const FuseDesc& f, uint64_t H, uint32_
       char* rec = reinterpret_cast<char*>(f.seg) + (uint64_t)kRunBytes * ((uint64_t)row * f.J + slot);
       gstore<v4f32>(rec, v4f32{a.d0, a.d1, a.d2, a.d3});
       const uint64_t sb = (uint64_t)__double_as_longlong(a.s2);
-      gstore<u32x4>(rec + 16, u32x4{__float_as_uint(a.s1), 0u, (uint32_t)sb, (uint32_t)(sb >> 32)});
+      gstore<u32x4>(rec + 16, u32x4{__float_as_uint(a.s1), a.exact ? 1u : 0u, (uint32_t)sb,
+                                    (uint32_t)(sb >> 32)});
     }
   }
   a = PRun();
@@ -274,9 +295,25 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
         m0[j] = w[j + SH];
         m1[j] = w[16 + j + SH];
       }
+      // The NaN/Inf test's per-pair maximum (a tree, then one merge into the running one).
+      u16x2 pm[8];
 #pragma unroll
-      for (int j = 0; j < 32; j++) fin.add(w[j + SH]);
+      for (int j = 0; j < 8; j++) {
+        pm[j] = __builtin_elementwise_max(
+            __builtin_elementwise_max(__builtin_bit_cast(u16x2, w[4 * j + SH] & fin.mask),
+                                      __builtin_bit_cast(u16x2, w[4 * j + 1 + SH] & fin.mask)),
+            __builtin_elementwise_max(__builtin_bit_cast(u16x2, w[4 * j + 2 + SH] & fin.mask),
+                                      __builtin_bit_cast(u16x2, w[4 * j + 3 + SH] & fin.mask)));
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) pm[j] = __builtin_elementwise_max(pm[j], pm[j + 4]);
+      pm[0] = __builtin_elementwise_max(__builtin_elementwise_max(pm[0], pm[1]),
+                                        __builtin_elementwise_max(pm[2], pm[3]));
+      fin.acc = __builtin_elementwise_max(fin.acc, pm[0]);
       if constexpr (ESZ != 0) {
+        // the pair's largest biased exponent: bf16 halves hold it at bit 7, fp32 at bit 23
+        const uint32_t emax = ESZ == 2 ? (uint32_t)max(pm[0].x, pm[0].y) >> 7
+                                       : (uint32_t)pm[0].y >> 7;
         if (!pinit) {  // the chunk's first interior pair
           const uint64_t po = o - H;
           prow = (uint32_t)(po / f.row_bytes);
@@ -290,7 +327,8 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
             (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(f.r >> 32)) << 32 |
             (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)f.r);
         if (rb + 128 <= f.row_bytes) {
-          run_add<ESZ, false>(w + SH, rbase + (uint64_t)(rb / ESZ) * 16, 0, 128 / ESZ, run);
+          run_add<ESZ, false>(w + SH, rbase + (uint64_t)(rb / ESZ) * 16, 0, 128 / ESZ, emax,
+                              run);
           prb = rb + 128;
           if (prb == f.row_bytes) {
             run_flush(f, H, prow, c, run);
@@ -299,10 +337,10 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
           }
         } else {  // the pair ends row prow at element tb and starts row prow + 1
           const uint32_t tb = (f.row_bytes - rb) / ESZ;
-          run_add<ESZ, true>(w + SH, rbase + (uint64_t)(rb / ESZ) * 16, 0, tb, run);
+          run_add<ESZ, true>(w + SH, rbase + (uint64_t)(rb / ESZ) * 16, 0, tb, emax, run);
           run_flush(f, H, prow, c, run);
           prow++;
-          run_add<ESZ, true>(w + SH, rbase - (uint64_t)tb * 16, tb, 128 / ESZ, run);
+          run_add<ESZ, true>(w + SH, rbase - (uint64_t)tb * 16, tb, 128 / ESZ, emax, run);
           prb = rb + 128 - f.row_bytes;
         }
       }

@@ -128,6 +128,28 @@ def test_fused_changed_entries_in_every_region(lib):
     assert max(rows_f[0][5:]) > 2 * max(rows_f[2][5:])
 
 
+def test_fused_squares_of_tiny_and_huge_entries(lib):
+    """Rows whose squares leave fp32's normal range (entries near 1e-22, or 1e25 whose squares
+    overflow fp32) are marked by the chunk kernel and their Σx² taken in fp64 from P; the
+    norms equal the unfused pass's and the fp64 oracle's."""
+    n, q, w = 64, 32, 1024
+    base = [_product(n, q, w, torch.bfloat16, seed=s) for s in (21, 22, 23)]
+    tiny = (base[0][0], base[0][1], (base[0][2].float() * 1e-22).to(torch.bfloat16))
+    huge = (base[1][0], base[1][1], (base[1][2].float() * 1e25).to(torch.bfloat16))
+    mixed_p = base[2][2].clone()
+    mixed_p[10] = (mixed_p[10].float() * 1e-30).to(torch.bfloat16)  # one row of tiny entries
+    mixed = (base[2][0], base[2][1], mixed_p)
+    prods = [tiny, huge, mixed]
+    rows_f, rows_u = _run_case(lib, prods, expect_fused=3)
+    ms = [1, 2, 3]
+    for i, (a, b, p) in enumerate(prods):
+        r = O.challenge_matrices(KEY, [ms[i]], 4, w)[0]
+        ref = O.measure_row_f64(a, b, p, r, None)
+        for col in (1, 2):  # ‖|P|1‖ and ‖P‖_F
+            assert rows_f[i][col] == pytest.approx(rows_u[i][col], rel=1e-6), (i, col)
+            assert rows_f[i][col] == pytest.approx(ref[col], rel=1e-5), (i, col)
+
+
 def test_products_that_are_not_fused(lib):
     dt = torch.bfloat16
     small = _product(64, 32, 256, dt, seed=1)        # 512-byte rows
