@@ -160,15 +160,16 @@ def counter_summary(d: Path, copy_mib: int) -> int:
     if copy_mib:
         for cn in sorted({cn for _, cn in sums}):
             copy_kib = sum(v for (k, c2), v in sums.items() if c2 == cn and "copyBuffer" in k)
-            chunk = [(v, len(disp[(k, c2)])) for (k, c2), v in sums.items()
-                     if c2 == cn and k.endswith("chunk_kernel")]
-            if not copy_kib or not chunk:
+            if not copy_kib:
                 continue
             factor = 2 * copy_mib * 1024 / copy_kib  # true KiB per reported KiB
-            v, n = chunk[0]
             print(f"\n{cn}: calibration copy reports {copy_kib:.0f} KiB for "
-                  f"{2 * copy_mib * 1024} KiB moved, factor {factor:.3f}; chunk_kernel "
-                  f"{v / n * factor * 1024 / 1e9:.3f} GB per launch")
+                  f"{2 * copy_mib * 1024} KiB moved, factor {factor:.3f}")
+            for (k, c2), v in sorted(sums.items()):
+                if c2 == cn and k.split("::")[-1] in ("chunk_kernel", "chunk_kernel_fused"):
+                    n = len(disp[(k, c2)])
+                    print(f"  {k}: {v / n * factor * 1024:.0f} bytes "
+                          f"({v / n * factor * 1024 / 1e9:.3f} GB) per launch")
     return 0
 
 

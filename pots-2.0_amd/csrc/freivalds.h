@@ -37,12 +37,13 @@ int challenges_enqueue(const uint32_t* d_key, const ChallengeItem* d_items, uint
 // A product whose P is a leaf of the transcript has its P-pass sums (P·R_j, Σ|p|, Σp² per
 // row) taken by the leaf hasher while it streams that leaf, so P is read from HBM once for
 // both checks. The hasher cuts each row into runs (the elements of one row inside one 1 KiB
-// chunk) and writes one record per run: [n][J] records of kRunBytes, J = ceil(w·esz / 1024)
-// + 1 slots per row, slot s of row i for the s-th chunk its elements fall in. The Freivalds
-// plan then adds each row's records and the few elements no chunk took (the leaf's first
-// bytes up to a 128-byte boundary and its last bytes after one) in a fixed order.
+// chunk) and writes one record per run: [J][n] records of kRunBytes, J = ceil(w·esz / 1024)
+// + 1 slots per row, slot s of row i (at s·n + i) for the s-th chunk its elements fall in; a
+// wave's lanes hold one class of chunks, which puts their records side by side. The
+// Freivalds plan then adds each row's records and the few elements no chunk took (the leaf's
+// first bytes up to a 128-byte boundary and its last bytes after one) in a fixed order.
 
-constexpr uint32_t kRunBytes = 32;  // float d[4], float s1, pad, double s2
+constexpr uint32_t kRunBytes = 32;  // float d[4], float s1, exact flag, double s2
 
 // What the leaf plan needs of a product it fuses.
 struct FusedProduct {

@@ -680,7 +680,7 @@ __global__ __launch_bounds__(256) void finish_final(const FinJob* __restrict__ j
 // One fused product (freivalds.h): its P is a leaf whose message is 0x00 || header (head
 // bytes) || P, and the chunk kernel wrote one record per run of a row.
 struct FixJob {
-  uint64_t p, r, seg;        // P, R [w][4], run records [n][J]
+  uint64_t p, r, seg;        // P, R [w][4], run records [J][n]
   uint64_t pdot, pabs, psq;  // the P job's partials: column chunk 0 of [rows_pad]
   uint64_t row_first;        // prefix of rows over the jobs before it
   uint32_t n, w;
@@ -711,8 +711,9 @@ __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ job
   double d[4] = {0.0, 0.0, 0.0, 0.0}, s1 = 0.0, s2 = 0.0;
   bool exact = false;
   if (fs < fe) {
-    const char* rec = reinterpret_cast<const char*>(J.seg) + (uint64_t)kRunBytes * i * J.J;
-    for (uint64_t c = fs >> 10; c <= (fe - 1) >> 10; c++, rec += kRunBytes) {
+    const char* rec = reinterpret_cast<const char*>(J.seg) + (uint64_t)kRunBytes * i;
+    const uint64_t stride = (uint64_t)kRunBytes * J.n;
+    for (uint64_t c = fs >> 10; c <= (fe - 1) >> 10; c++, rec += stride) {
       const v4f32 a = gload<v4f32>(rec);
       const u32x4 b = gload<u32x4>(rec + 16);
       for (int j = 0; j < 4; j++) d[j] += (double)a[j];

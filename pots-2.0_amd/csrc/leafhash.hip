@@ -63,7 +63,7 @@ static_assert(sizeof(LeafDesc) == 48, "LeafDesc layout");
 // wave of its own after them, so that the header's few bytes do not pad every class.
 struct FuseDesc {
   uint64_t r;          // R [m][4] fp32, row-major
-  uint64_t seg;        // run records [n_rows][J]
+  uint64_t seg;        // run records [J][n_rows]
   uint32_t row_bytes;  // m · esz
   uint32_t n_rows;
   uint32_t J;          // record slots per row
@@ -187,7 +187,8 @@ __device__ __forceinline__ void run_flush(const FuseDesc& f, uint64_t H, uint32_
     const uint64_t fs = max<uint64_t>(H + (uint64_t)row * f.row_bytes, hc);
     const uint64_t slot = c - (fs >> 10);
     if (row < f.n_rows && slot < f.J) {
-      char* rec = reinterpret_cast<char*>(f.seg) + (uint64_t)kRunBytes * ((uint64_t)row * f.J + slot);
+      char* rec = reinterpret_cast<char*>(f.seg) +
+                  (uint64_t)kRunBytes * (slot * f.n_rows + row);
       gstore<v4f32>(rec, v4f32{a.d0, a.d1, a.d2, a.d3});
       const uint64_t sb = (uint64_t)__double_as_longlong(a.s2);
       gstore<u32x4>(rec + 16, u32x4{__float_as_uint(a.s1), a.exact ? 1u : 0u, (uint32_t)sb,
