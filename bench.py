@@ -438,6 +438,8 @@ def main() -> int:
                    "leaves": c.n_leaves, "products": c.M, "k": k,
                    "hash_bytes": hash_bytes, "freivalds_bytes": fv_bytes,
                    "p_pass_fused_products": v.fused,
+                   "p_pass_fused_leaf_bytes": v.hasher.plan.fused_bytes,
+                   "p_pass_fused_records": v.hasher.plan.fused_records,
                    "a_pass_blocks": v.a_grid},
         "parts": {"step_verify_ms": round(ms, 3),
                   "step_frac_hbm": round(value / HBM_PEAK_GBPS, 4),
