@@ -191,6 +191,11 @@ int pots_fv_plan_run(void *plan, const uint8_t *d_key, double *d_rows, void *str
  * so a caller can time each stage; the caller keeps the order. No counterpart in the
  * reference. */
 #define POTS_FV_STAGES 6
+/* Stage 4 is two parts, which a caller may also enqueue apart (each once, both after stage 2
+ * and before stage 5): the P pass over the products not fused with a leaf plan, and the fused
+ * products' sums from the records the leaf plan's chunk stage wrote (nothing when unfused). */
+#define POTS_FV_STAGE_P_PASS 6
+#define POTS_FV_STAGE_P_FUSED 7
 int pots_fv_plan_run_stage(void *plan, int stage, const uint8_t *d_key, double *d_rows,
                            void *stream);
 

@@ -1398,12 +1398,17 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
       return POTS_E_OK;
     }
     case 3:
-    case 4:
+    case POTS_FV_STAGE_P_PASS:
       for (const PassLaunch& L : P->pass_ap)
         if ((L.weighted != 0) == (stage == 3) &&
-            (rc = run_pass(P, L, P->max_grid[stage], s)) != POTS_E_OK)
+            (rc = run_pass(P, L, P->max_grid[stage == 3 ? 3 : 4], s)) != POTS_E_OK)
           return rc;
-      if (stage == 4 && P->fused) {
+      return POTS_E_OK;
+    case 4:  // the P pass, then the fused products' records
+      if ((rc = run_stage(P, POTS_FV_STAGE_P_PASS, d_key, d_rows, s)) != POTS_E_OK) return rc;
+      return run_stage(P, POTS_FV_STAGE_P_FUSED, d_key, d_rows, s);
+    case POTS_FV_STAGE_P_FUSED:
+      if (P->fused) {
         if (P->n_fix == 0) return POTS_E_HIP;  // a fusion that failed half way
         hipLaunchKernelGGL(fused_rows, dim3((uint32_t)((P->n_fix_rows + 255) / 256)), dim3(256),
                            0, s, P->d_fix, P->n_fix, P->n_fix_rows);
@@ -1442,7 +1447,7 @@ extern "C" int pots_fv_plan_run(void* plan, const uint8_t* d_key, double* d_rows
 
 extern "C" int pots_fv_plan_run_stage(void* plan, int stage, const uint8_t* d_key,
                                       double* d_rows, void* stream) {
-  if (!plan || !d_key || !d_rows || stage < 0 || stage >= POTS_FV_STAGES) return POTS_E_ARG;
+  if (!plan || !d_key || !d_rows || stage < 0 || stage > POTS_FV_STAGE_P_FUSED) return POTS_E_ARG;
   return run_stage(static_cast<FvPlan*>(plan), stage, d_key, d_rows,
                    static_cast<hipStream_t>(stream));
 }

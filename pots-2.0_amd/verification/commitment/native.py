@@ -494,6 +494,9 @@ class FvPlan:
         return out
 
     STAGES = ("challenges", "b_pass", "reduce", "a_pass", "p_pass", "rows")
+    # Stage 4's two parts on their own: the row pass over the unfused products' P, and the
+    # fused products' sums from the leaf plan's run records.
+    P_PASS, P_FUSED = 6, 7
 
     def run_stage(self, stage: int, key: torch.Tensor, out: torch.Tensor,
                   stream: torch.cuda.Stream | None = None) -> None:
