@@ -236,3 +236,68 @@ def test_device_step_verifier_fused_equals_unfused(lib):
         assert torch.equal(a.codes, b.codes)
         ra, rb = a.rows.cpu(), b.rows.cpu()
         assert torch.allclose(ra[:, :5], rb[:, :5], rtol=1e-6, atol=0)
+
+
+def test_stages_apart_and_grid_limits_equal_one_call(lib):
+    """The fused pair's stages enqueued one at a time (the leaf plan's two chunk kernels and
+    the P stage's two parts apart) and row passes limited to a few blocks give the rows and
+    digests of pots_step_run bit for bit."""
+    from verification.commitment import native
+    prods = [_product(128, 64, 1280, torch.bfloat16, seed=31),
+             _product(64, 32, 256, torch.bfloat16, seed=32),      # not fused (512-byte rows)
+             _product(64, 48, 768, torch.float32, seed=33)]
+    dev = [(a.cuda(), b.cuda(), p.cuda()) for a, b, p in prods]
+    leaves = [p for _, _, p in dev]
+    hdrs = [O.tensor_leaf_header(O.TAG_PRODUCT, t) for t in leaves]
+    kinds = [native.FINITE_KIND[t.dtype] for t in leaves]
+    fvp = [native.FvProduct(a, b, p, i + 1) for i, (a, b, p) in enumerate(dev)]
+    key = torch.tensor(list(KEY), dtype=torch.uint8, device="cuda")
+
+    def fresh():
+        fv = lib.fv_plan(fvp, 4)
+        leaf = lib.leaf_plan(hdrs, leaves, kinds, fuse=fv)
+        assert leaf.fused == 2
+        return fv, leaf, (torch.empty(3, 32, dtype=torch.uint8, device="cuda"),
+                          torch.empty(1, dtype=torch.int32, device="cuda"),
+                          torch.empty(3, 9, dtype=torch.float64, device="cuda"))
+
+    fv, leaf, (dig1, bad1, rows1) = fresh()
+    lib.step_run(leaf, fv, key, dig1, bad1, rows1)
+    fv2, leaf2, (dig2, bad2, rows2) = fresh()
+    for st, n in ((1, 3), (3, 5), (4, 2)):
+        fv2.set_grid(st, n)
+    LP, FP = native.LeafPlan, native.FvPlan
+    fv2.run_stage(0, key, rows2)
+    for st in (0, LP.PLAIN_CHUNKS, LP.FUSED_CHUNKS, 2):
+        leaf2.run_stage(st, dig2, bad2)
+    for st in (1, 2, FP.P_PASS, 3, FP.P_FUSED, 5):
+        fv2.run_stage(st, key, rows2)
+    torch.cuda.synchronize()
+    assert torch.equal(dig1, dig2) and int(bad2.item()) == 3
+    assert torch.equal(rows1.view(torch.int64), rows2.view(torch.int64))
+    with pytest.raises(ValueError):
+        fv2.run_stage(FP.P_FUSED + 1, key, rows2)
+    with pytest.raises(ValueError):
+        fv2.set_grid(2, 4)  # only the row passes take a grid limit
+    with pytest.raises(ValueError):
+        leaf2.run_stage(LP.PLAIN_CHUNKS + 1, dig2, bad2)
+
+
+def test_fused_stats_count_what_the_kernel_moves(lib):
+    """pots_leaf_plan_fused_stats: the fused leaves' message bytes, chunks, and one record per
+    (row, chunk) pair whose 128-byte interior windows hold elements of the row."""
+    from verification.commitment import native
+    n, w = 128, 1280
+    a, b, p = (t.cuda() for t in _product(n, 32, w, torch.bfloat16, seed=41))
+    fv = lib.fv_plan([native.FvProduct(a, b, p, 1)], 4)
+    hdr = O.tensor_leaf_header(O.TAG_PRODUCT, p)
+    leaf = lib.leaf_plan([hdr], [p], [native.FINITE_KIND[torch.bfloat16]], fuse=fv)
+    H, rb = 1 + len(hdr), 2 * w
+    L = H + n * rb
+    hc, lf = -(-H // 128) * 128, L // 128 * 128
+    records = 0
+    for i in range(n):  # chunks each row's interior bytes fall in
+        fs, fe = max(H + i * rb, hc), min(H + (i + 1) * rb, lf)
+        records += (fe - 1) // 1024 - fs // 1024 + 1
+    assert (leaf.fused_bytes, leaf.fused_chunks, leaf.fused_records) == (L, -(-L // 1024),
+                                                                         records)
