@@ -134,7 +134,7 @@ def cpu_baseline(step, items, fv_budget_s: float = 3.0, runs: int = 3) -> dict:
                       f"challenges included)"}
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "chunk_kernel_c4_traffic.md"
+TRAFFIC_FILE = ROOT / "profiles" / "chunk_kernels_c4_traffic.md"
 
 
 def counter_summary(d: Path, copy_mib: int) -> int:
@@ -212,16 +212,18 @@ def trace_summary(d: Path, steps: int, warmup: int) -> int:
 
 def traffic_from_profile(kernel: str) -> int | None:
     """HBM bytes per launch of ``kernel`` from the committed counter summary (the fenced
-    JSON block of TRAFFIC_FILE), or None when it holds no figure for that kernel."""
+    JSON block of TRAFFIC_FILE: one object per kernel), or None when it holds no figure for
+    that kernel."""
     try:
         text = TRAFFIC_FILE.read_text()
         block = text.split("```json", 1)[1].split("```", 1)[0]
         d = json.loads(block)
     except (OSError, IndexError, ValueError):
         return None
-    if d.get("kernel") != kernel:
-        return None
-    return int(d["fetch_bytes_per_launch"]) + int(d["write_bytes_per_launch"])
+    for e in d if isinstance(d, list) else [d]:
+        if e.get("kernel") == kernel:
+            return int(e["fetch_bytes_per_launch"]) + int(e["write_bytes_per_launch"])
+    return None
 
 
 def main() -> int:
