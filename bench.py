@@ -226,6 +226,78 @@ def traffic_from_profile(kernel: str) -> int | None:
     return None
 
 
+def disk_leg(root: Path, c, step, k: int, claimed: bytes, v) -> dict:
+    """The stored-step path: write the transcript as the on-disk store does (one torch.save
+    file per leaf, meta.json, leaf_hashes.bin; plus the captured operands), then bring it back
+    into HBM twice with the native loader (pread into pinned staging, DMA into one arena), and
+    once with the reference's reader (torch.load of each leaf, then a copy to the GPU); verify
+    the loaded copy with the device step verifier. The files were just written, so the reads
+    come from the host's page cache: this measures the loader, not a disk."""
+    import shutil
+
+    import torch
+
+    from verification.commitment import native
+    from verification.commitment.merkle import MerkleTree
+    from verification.transcript.loader import StepLoader, write_operands
+    from verification.transcript.store import DiskStore
+    from verification.verifier.step import DeviceStepVerifier
+
+    d = root / "step"
+    nodes = native.get().merkle_tree_device(v.digests)
+    tree = MerkleTree.from_nodes(nodes.cpu().numpy().tobytes(), c.n_leaves)
+    t0 = time.perf_counter()
+    disk = DiskStore.write(d, c, step.leaves, tree)
+    write_operands(d, step.operands)
+    write_s = time.perf_counter() - t0
+    files = sum(1 for _ in d.rglob("*.pt"))
+    log(f"[bench] disk leg: {files} files written under {d} in {write_s:.1f} s")
+    loader = StepLoader(threads=8, staging_mib=256)
+    ms = [s.m for s in c.products]
+    loads = []
+    res = None
+    try:
+        for _ in range(2):
+            res = None
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            res = loader.load(disk, c.n_leaves, ms)
+            loads.append((time.perf_counter() - t0, dict(res.times)))
+        best_s, times = min(loads, key=lambda x: x[0])
+        moved, fallback = res.bytes, res.fallback
+        log(f"[bench] disk leg: {moved / 1e9:.2f} GB in {best_s:.2f} s "
+            f"({moved / best_s / 1e9:.1f} GB/s); " +
+            ", ".join(f"{key} {t:.2f} s" for key, t in times.items()))
+        out = DeviceStepVerifier(c, res.leaves, lambda s: res.operands[s.m], k=k).run(disk.root)
+        assert out.root == claimed and out.check is None, out.detail
+        # the reference's reader over the same leaves: torch.load, then a copy to the GPU
+        dev = torch.device("cuda", torch.cuda.current_device())
+        t0 = time.perf_counter()
+        n_ref = 0
+        for i in range(c.n_leaves):
+            obj = disk.leaf(i)
+            if isinstance(obj, torch.Tensor):
+                obj.to(dev)
+                n_ref += obj.nbytes
+        torch.cuda.synchronize()
+        ref_s = time.perf_counter() - t0
+        log(f"[bench] disk leg: the reference's reader took {ref_s:.2f} s for the leaves "
+            f"({n_ref / ref_s / 1e9:.2f} GB/s)")
+    finally:
+        res = None
+        shutil.rmtree(d, ignore_errors=True)
+    return {"files": files, "fallback_files": fallback, "bytes": moved,
+            "write_s": round(write_s, 2),
+            "load_s": [round(x[0], 3) for x in loads],
+            "load_parts_s": {key: round(t, 3) for key, t in times.items()},
+            "gbps": round(moved / best_s / 1e9, 2),
+            "native_copy_gbps": round(moved / times["load"] / 1e9, 2),
+            "threads": loader.threads, "staging_mib": 256,
+            "reference_reader_s": round(ref_s, 3),
+            "reference_reader_gbps": round(n_ref / ref_s / 1e9, 2),
+            "verified": True, "source": "page cache (files written just before)"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -245,6 +317,10 @@ def main() -> int:
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="copy this many MiB device to device twice before timing, so a "
                          "counter run sees a plain copy kernel of known size")
+    ap.add_argument("--disk-leg", metavar="DIR",
+                    help="also write the transcript under DIR in the on-disk store's format "
+                         "(with the captured operands), load it back into HBM with the native "
+                         "loader, verify the loaded copy, report parts.disk_load, and delete it")
     ap.add_argument("--counter-summary", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSV output under DIR and exit")
     ap.add_argument("--trace-summary", metavar="DIR",
@@ -466,6 +542,8 @@ def main() -> int:
                      "launch_ms_in_step": (round(chunks_in_step_ms, 4)
                                            if dom == in_step_kernel else None)},
     }
+    if args.disk_leg:
+        out["parts"]["disk_load"] = disk_leg(Path(args.disk_leg), c, step, k, claimed_b, v)
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")
         out["cpu_baseline"] = cpu_baseline(step, items)

@@ -274,6 +274,83 @@ int pots_update_plan_run(void *plan, pots_update_result *d_out, void *stream);
 uint64_t pots_update_plan_bytes(void *plan);
 void pots_update_plan_destroy(void *plan);
 
+/* ---- Stored steps: leaf files to device memory ------------------------------------------
+ *
+ * The on-disk transcript store (verification/transcript/store.py:285-380, DiskStore) writes
+ * one torch.save file per leaf. Its reader (store.py:347-357, DiskStore.leaf) unpickles each
+ * file into pageable host memory with torch.load; the checks then copy the tensors to the GPU
+ * one by one. These two entry points replace that read for a whole step: a parallel scan of
+ * the files' ZIP directories and pickles (no Python, nothing executed), then parallel reads
+ * of the storage bytes into pinned staging and DMA into one device buffer. */
+
+#define POTS_E_IO (-5) /* a file could not be opened or read; see pots_last_error() */
+
+/* Element types of a stored tensor, from its pickled storage class (torch.FloatStorage ...). */
+#define POTS_STORE_F32 1
+#define POTS_STORE_F64 2
+#define POTS_STORE_F16 3
+#define POTS_STORE_BF16 4
+#define POTS_STORE_I64 5
+#define POTS_STORE_I32 6
+#define POTS_STORE_I16 7
+#define POTS_STORE_I8 8
+#define POTS_STORE_U8 9
+#define POTS_STORE_BOOL 10
+
+/* Scan status of one file. */
+#define POTS_STORE_OK 0     /* one plain tensor, described below */
+#define POTS_STORE_OTHER 1  /* anything else (a record's dict, a tensor that needs grad, a
+                               big-endian or compressed archive, ...): read it with torch.load */
+#define POTS_STORE_UNREADABLE 2 /* not a ZIP archive that can be read; torch.load fails too */
+
+#define POTS_STORE_MAX_DIM 8
+
+/* What pots_store_scan found in one file: a tensor of `ndim` dims with these sizes and
+ * strides (elements) at `storage_offset` elements into a storage of `storage_bytes` bytes,
+ * stored uncompressed at `data_offset` in the file. Fields other than status are meaningful
+ * only for POTS_STORE_OK. */
+typedef struct pots_stored_tensor {
+  uint64_t data_offset;
+  uint64_t storage_bytes;
+  uint64_t storage_offset;
+  int64_t size[POTS_STORE_MAX_DIM];
+  int64_t stride[POTS_STORE_MAX_DIM];
+  uint32_t ndim;
+  uint32_t dtype; /* POTS_STORE_F32 ... */
+  int32_t status; /* POTS_STORE_OK ... */
+  uint32_t pad;
+} pots_stored_tensor;
+
+/* Scan n_files files on n_threads host threads (0: 8). Accepts exactly the pickle torch.save
+ * writes for one tensor that does not require grad, torch._utils._rebuild_tensor_v2(storage,
+ * offset, size, stride, False, OrderedDict()), with a little-endian byte order record and the
+ * storage's record stored; its opcodes are walked, never executed. Returns POTS_E_OK (each
+ * file's own outcome is in its status) or POTS_E_ARG. Host only: needs no GPU. */
+int pots_store_scan(uint32_t n_files, const char *const *paths, pots_stored_tensor *out,
+                    uint32_t n_threads);
+
+/* One piece of a file for pots_store_load: `bytes` bytes at `file_offset` of file `file` go
+ * to `dst_offset` bytes into the destination. */
+typedef struct pots_store_segment {
+  uint32_t file;
+  uint32_t pad;
+  uint64_t file_offset;
+  uint64_t bytes;
+  uint64_t dst_offset;
+} pots_store_segment;
+
+/* Copy the segments (sorted by dst_offset, not overlapping) into `dst`. With dst_device >= 0,
+ * dst is memory of that device: n_threads host threads (0: 8) each read their share of the
+ * spans into two slots of the pinned host `staging` (staging_bytes, at least 2·n_threads·64
+ * KiB, from hipHostMalloc) and send each slot with one hipMemcpyAsync on a stream of their
+ * own. With dst_device < 0, dst is host memory read into directly (staging unused). Bytes
+ * between segments that fall inside one span are written with unspecified values. Returns
+ * after every copy has completed: POTS_E_OK, POTS_E_IO (a short or failed read), POTS_E_HIP
+ * or POTS_E_ARG. */
+int pots_store_load(uint32_t n_files, const char *const *paths, uint32_t n_segs,
+                    const pots_store_segment *segs, void *dst, int dst_device, void *staging,
+                    uint64_t staging_bytes, uint32_t n_threads);
+
 #ifdef __cplusplus
 }
 #endif

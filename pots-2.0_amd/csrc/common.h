@@ -7,6 +7,7 @@
 #include <stdio.h>
 
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include "../../include/pots_mi355x.h"
@@ -24,6 +25,9 @@ namespace pots {
   } while (0)
 
 void note_hip_error(hipError_t e, const char* what, const char* file, int line);
+
+// Set the calling thread's pots_last_error() text.
+void note_error(const std::string& msg);
 
 // A device buffer that only grows, one per (device, slot), kept for the life of the process.
 // The synchronous entry points use it for metadata and intermediate chaining values; the

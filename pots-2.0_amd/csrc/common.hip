@@ -16,6 +16,8 @@ void note_hip_error(hipError_t e, const char* what, const char* file, int line) 
   g_last_error = buf;
 }
 
+void note_error(const std::string& msg) { g_last_error = msg; }
+
 namespace {
 constexpr int kMaxDevices = 64;
 constexpr int kSlots = 8;

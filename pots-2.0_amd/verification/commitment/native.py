@@ -38,7 +38,7 @@ FINITE_KIND: dict[torch.dtype, int] = {
     torch.int32: KIND_NONE,
 }
 
-E_OK, E_NOMEM, E_HIP, E_ARG = 0, -1, -3, -4
+E_OK, E_NOMEM, E_HIP, E_ARG, E_IO = 0, -1, -3, -4, -5
 _SIZE_MAX = (1 << (8 * ctypes.sizeof(ctypes.c_size_t))) - 1
 
 

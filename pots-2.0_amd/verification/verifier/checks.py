@@ -197,14 +197,17 @@ def check_6a_linear_update(store: TranscriptStore, c: DeclaredComputation, ctx: 
 def _products(c: DeclaredComputation, leaves: CommittedLeaves, replay: Any
               ) -> list[native.FvProduct]:
     """Every product's ``A``, ``B`` (from the replay), committed ``P`` and, for a biased
-    product, its committed ``W_t`` bias in the operand format (as ``[A | 1]·[B ; bᵀ]``)."""
+    product, its committed ``W_t`` bias in the operand format (as ``[A | 1]·[B ; bᵀ]``), on
+    the current GPU (a store may serve host tensors, as the on-disk one does)."""
+    dev = torch.device("cuda", torch.cuda.current_device())
     out = []
     for spec in c.products:
-        a, b = replay.operands(spec.m)
-        p = leaves.leaf(c.product_index(spec.m))
+        a, b = (x.to(dev) for x in replay.operands(spec.m))
+        p = leaves.leaf(c.product_index(spec.m)).to(dev)
         bias = None
         if spec.bias is not None:
-            bias = leaves.leaf(c.w_t_index(spec.bias)).to(c.operand_dtype).to(torch.float32)
+            bias = leaves.leaf(c.w_t_index(spec.bias)).to(dev).to(c.operand_dtype) \
+                .to(torch.float32)
         out.append(native.FvProduct(a, b, p, spec.m, bias))
     return out
 
