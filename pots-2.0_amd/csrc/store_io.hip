@@ -70,6 +70,36 @@ inline uint32_t le32(const uint8_t* p) {
 }
 inline uint64_t le64(const uint8_t* p) { return le32(p) | (uint64_t)le32(p + 4) << 32; }
 
+// A file being scanned. Its first and last few KiB are read once and reads inside them are
+// served from memory: a torch.save archive keeps its small records, their local headers and
+// the central directory there, so a scan costs two reads.
+struct ScanFile {
+  static constexpr uint64_t kWindow = 4096;
+  int fd = -1;
+  uint64_t size = 0;
+  std::vector<uint8_t> head, tail;
+  uint64_t tail_off = 0;
+
+  bool open_windows() {
+    head.resize(std::min(size, kWindow));
+    tail_off = size - std::min(size, kWindow);
+    tail.resize(size - tail_off);
+    return read_at(fd, head.data(), head.size(), 0) &&
+           read_at(fd, tail.data(), tail.size(), tail_off);
+  }
+  bool read(void* dst, uint64_t n, uint64_t off) const {
+    if (n <= head.size() && off <= head.size() - n) {
+      memcpy(dst, head.data() + off, n);
+      return true;
+    }
+    if (off >= tail_off && n <= tail.size() && off - tail_off <= tail.size() - n) {
+      memcpy(dst, tail.data() + (off - tail_off), n);
+      return true;
+    }
+    return read_at(fd, dst, n, off);
+  }
+};
+
 // ---- the ZIP directory ---------------------------------------------------------------------
 
 struct Entry {
@@ -81,19 +111,29 @@ struct Entry {
 
 // The central directory's entries (APPNOTE 4.3.12 and 4.3.16, with the ZIP64 end records of
 // 4.3.14-4.3.15 and the ZIP64 extended information extra field of 4.5.3).
-bool directory(int fd, uint64_t fsize, std::vector<Entry>* out) {
-  if (fsize < 22) return false;
-  const uint64_t tail_n = std::min<uint64_t>(fsize, 65535 + 22);
-  std::vector<uint8_t> tail(tail_n);
-  if (!read_at(fd, tail.data(), tail_n, fsize - tail_n)) return false;
+bool directory(const ScanFile& f, std::vector<Entry>* out) {
+  if (f.size < 22) return false;
+  // The end record sits in the last 22 bytes unless a comment (up to 64 KiB) follows it.
+  std::vector<uint8_t> big;
+  const std::vector<uint8_t>* tailp = &f.tail;
   int64_t e = -1;
-  for (int64_t i = (int64_t)tail_n - 22; i >= 0; --i) {
-    if (le32(&tail[i]) == 0x06054b50u) {
-      e = i;
-      break;
+  for (int pass = 0; pass < 2 && e < 0; ++pass) {
+    if (pass == 1) {
+      const uint64_t n = std::min<uint64_t>(f.size, 65535 + 22);
+      if (n <= f.tail.size()) break;
+      big.resize(n);
+      if (!read_at(f.fd, big.data(), n, f.size - n)) return false;
+      tailp = &big;
+    }
+    for (int64_t i = (int64_t)tailp->size() - 22; i >= 0; --i) {
+      if (le32(&(*tailp)[i]) == 0x06054b50u) {
+        e = i;
+        break;
+      }
     }
   }
   if (e < 0) return false;
+  const std::vector<uint8_t>& tail = *tailp;
   const uint8_t* eo = &tail[e];
   uint64_t n_entries = le16(eo + 10), on_disk = le16(eo + 8), cd_size = le32(eo + 12),
            cd_off = le32(eo + 16), disk = le16(eo + 4), cd_disk = le16(eo + 6);
@@ -104,7 +144,7 @@ bool directory(int fd, uint64_t fsize, std::vector<Entry>* out) {
     const uint8_t* loc = eo - 20;
     const uint64_t z_off = le64(loc + 8);
     uint8_t z[56];
-    if (fsize < 56 || z_off > fsize - 56 || !read_at(fd, z, 56, z_off) ||
+    if (f.size < 56 || z_off > f.size - 56 || !f.read(z, 56, z_off) ||
         le32(z) != 0x06064b50u || le64(z + 4) < 44 || le32(loc + 16) != 1)
       return false;
     disk = le32(z + 16);
@@ -118,11 +158,11 @@ bool directory(int fd, uint64_t fsize, std::vector<Entry>* out) {
   }
   // One disk only, as torch's ZIP reader requires.
   if (disk != 0 || cd_disk != 0 || on_disk != n_entries || n_entries > 0xFFFFFFFFu) return false;
-  if (cd_size > kMaxDirectory || cd_off > fsize || cd_size > fsize - cd_off ||
+  if (cd_size > kMaxDirectory || cd_off > f.size || cd_size > f.size - cd_off ||
       cd_size < n_entries * 46)
     return false;
   std::vector<uint8_t> cd(cd_size);
-  if (cd_size && !read_at(fd, cd.data(), cd_size, cd_off)) return false;
+  if (cd_size && !f.read(cd.data(), cd_size, cd_off)) return false;
   out->clear();
   uint64_t p = 0;
   for (uint64_t k = 0; k < n_entries; ++k) {
@@ -162,8 +202,8 @@ bool directory(int fd, uint64_t fsize, std::vector<Entry>* out) {
     // and 13), sizes that agree for a stored
     // record, no data without compressed bytes, the first disk, a local header inside the file.
     if ((en.flags & 0x2061) || (en.method == 0 && en.usize != en.csize) ||
-        (en.usize && !en.csize) || le16(h + 34) != 0 || en.local > fsize ||
-        en.csize > fsize - en.local || fsize - en.local - en.csize < 30)
+        (en.usize && !en.csize) || le16(h + 34) != 0 || en.local > f.size ||
+        en.csize > f.size - en.local || f.size - en.local - en.csize < 30)
       return false;
     out->push_back(std::move(en));
     p += 46 + (uint64_t)nl + xl + cl;
@@ -172,13 +212,13 @@ bool directory(int fd, uint64_t fsize, std::vector<Entry>* out) {
 }
 
 // Where a stored (uncompressed, unencrypted) record's bytes start; false if it is not one.
-bool record_data(int fd, uint64_t fsize, const Entry& en, uint64_t* data) {
+bool record_data(const ScanFile& f, const Entry& en, uint64_t* data) {
   if (en.dir || en.method != 0 || (en.flags & 1) || en.csize != en.usize) return false;
   uint8_t h[30];
-  if (en.local > fsize || fsize - en.local < 30 || !read_at(fd, h, 30, en.local)) return false;
+  if (en.local > f.size || f.size - en.local < 30 || !f.read(h, 30, en.local)) return false;
   if (le32(h) != 0x04034b50u) return false;
   const uint64_t start = en.local + 30 + le16(h + 26) + le16(h + 28);
-  if (start > fsize || en.usize > fsize - start) return false;
+  if (start > f.size || en.usize > f.size - start) return false;
   *data = start;
   return true;
 }
@@ -299,13 +339,9 @@ bool parse_pickle(const uint8_t* p, uint64_t n, Val* result) {
         st.push_back(std::move(g));
         break;
       }
-      case 'q':  // BINPUT
-        if (!need(1)) return false;
-        i += 1;
-        break;
-      case 'r':  // LONG_BINPUT
-        if (!need(4)) return false;
-        i += 4;
+      case 'q': case 'r':  // BINPUT, LONG_BINPUT: memoize the top (not through a MARK)
+        if (!need(op == 'q' ? 1 : 4) || st.empty() || st.back().kind == Val::MARK) return false;
+        i += op == 'q' ? 1 : 4;
         break;
       case '(':  // MARK
         st.emplace_back(Val::MARK);
@@ -432,22 +468,25 @@ bool parse_pickle(const uint8_t* p, uint64_t n, Val* result) {
 // ---- one file -------------------------------------------------------------------------------
 
 // The whole of a small stored record equals `want`; false if absent, different or unreadable.
-bool record_is(int fd, uint64_t fsize, const Entry* e, const char* want) {
+bool record_is(const ScanFile& f, const Entry* e, const char* want) {
   const size_t n = strlen(want);
   uint64_t at = 0;
-  if (!e || e->usize != n || !record_data(fd, fsize, *e, &at)) return false;
+  if (!e || e->usize != n || !record_data(f, *e, &at)) return false;
   char buf[16];
-  return n <= sizeof buf && read_at(fd, buf, n, at) && memcmp(buf, want, n) == 0;
+  return n <= sizeof buf && f.read(buf, n, at) && memcmp(buf, want, n) == 0;
 }
 
 int32_t scan_one(const char* path, pots_stored_tensor* out) {
-  Fd f(path);
-  if (f.fd < 0) return POTS_STORE_UNREADABLE;
+  Fd fd(path);
+  if (fd.fd < 0) return POTS_STORE_UNREADABLE;
   struct stat sb;
-  if (fstat(f.fd, &sb) != 0 || !S_ISREG(sb.st_mode)) return POTS_STORE_UNREADABLE;
-  const uint64_t fsize = (uint64_t)sb.st_size;
+  if (fstat(fd.fd, &sb) != 0 || !S_ISREG(sb.st_mode)) return POTS_STORE_UNREADABLE;
+  ScanFile f;
+  f.fd = fd.fd;
+  f.size = (uint64_t)sb.st_size;
   std::vector<Entry> entries;
-  if (!directory(f.fd, fsize, &entries) || entries.empty()) return POTS_STORE_UNREADABLE;
+  if (!f.open_windows() || !directory(f, &entries) || entries.empty())
+    return POTS_STORE_UNREADABLE;
   // torch's reader takes the archive's folder from its first entry, and every record name
   // must lie in that folder and decode as UTF-8.
   const size_t slash = entries[0].name.find('/');
@@ -474,30 +513,30 @@ int32_t scan_one(const char* path, pots_stored_tensor* out) {
   // torch.load, which decides.
   uint64_t at = 0;
   const std::string ver = has(prefix + ".data/version") ? ".data/version" : "version";
-  if (!record_is(f.fd, fsize, find(prefix + ver), "3\n")) return POTS_STORE_OTHER;
-  if (!record_is(f.fd, fsize, find(prefix + "byteorder"), "little")) return POTS_STORE_OTHER;
+  if (!record_is(f, find(prefix + ver), "3\n")) return POTS_STORE_OTHER;
+  if (!record_is(f, find(prefix + "byteorder"), "little")) return POTS_STORE_OTHER;
   if (has(prefix + ".format_version") &&
-      !record_is(f.fd, fsize, find(prefix + ".format_version"), "1"))
+      !record_is(f, find(prefix + ".format_version"), "1"))
     return POTS_STORE_OTHER;
   if (has(prefix + ".storage_alignment") &&
-      !record_is(f.fd, fsize, find(prefix + ".storage_alignment"), "64"))
+      !record_is(f, find(prefix + ".storage_alignment"), "64"))
     return POTS_STORE_OTHER;
   if (has(prefix + ".data/serialization_id")) {  // torch reads it as text
     const Entry* id = find(prefix + ".data/serialization_id");
     char buf[256];
-    if (!id || id->usize > sizeof buf || !record_data(f.fd, fsize, *id, &at) ||
-        !read_at(f.fd, buf, id->usize, at) || !utf8(std::string(buf, id->usize)))
+    if (!id || id->usize > sizeof buf || !record_data(f, *id, &at) ||
+        !f.read(buf, id->usize, at) || !utf8(std::string(buf, id->usize)))
       return POTS_STORE_OTHER;
   }
   const Entry* pkl = find(prefix + "data.pkl");
   if (!pkl) return POTS_STORE_OTHER;
-  if (pkl->usize > kMaxPickle || !record_data(f.fd, fsize, *pkl, &at)) return POTS_STORE_OTHER;
+  if (pkl->usize > kMaxPickle || !record_data(f, *pkl, &at)) return POTS_STORE_OTHER;
   std::vector<uint8_t> pk(pkl->usize);
-  if (!pk.empty() && !read_at(f.fd, pk.data(), pk.size(), at)) return POTS_STORE_UNREADABLE;
+  if (!pk.empty() && !f.read(pk.data(), pk.size(), at)) return POTS_STORE_UNREADABLE;
   Val t(Val::INT);
   if (!parse_pickle(pk.data(), pk.size(), &t)) return POTS_STORE_OTHER;
   const Entry* data = find(prefix + "data/" + t.a);
-  if (!data || !record_data(f.fd, fsize, *data, &at)) return POTS_STORE_OTHER;
+  if (!data || !record_data(f, *data, &at)) return POTS_STORE_OTHER;
 
   const uint32_t esz = elem_size(t.dtype);
   const auto& size = t.items[0].items;

@@ -47,7 +47,8 @@ import torch
 
 from verification.commitment import native
 from verification.transcript.errors import LeafReadError, StoreMutationError
-from verification.transcript.store import DiskStore, TranscriptStore, _versions, savable
+from verification.transcript.store import (LEAF_FILE, DiskStore, TranscriptStore, _versions,
+                                           savable)
 
 __all__ = ["ALIGN", "OPERAND_DIR", "OPERAND_FILE", "STORE_DTYPES", "StoredStep",
            "ResidentStore", "StepLoader", "load_step", "scan_files", "write_operands"]
@@ -105,19 +106,39 @@ def _check(rc: int, what: str) -> None:
     raise native.NativeError(f"{what} failed with {rc}: {msg}")
 
 
-def _path_array(paths: Sequence[Path]) -> tuple[ctypes.Array, list[bytes]]:
-    raw = [os.fsencode(p) for p in paths]
-    arr = (ctypes.c_char_p * max(1, len(raw)))(*raw)
-    return arr, raw
+class _PathTable:
+    """File names as the C ABI takes them: an array of pointers to NUL-terminated bytes, built
+    with numpy (a step has tens of thousands of files)."""
+
+    def __init__(self, paths: Sequence[str | bytes | os.PathLike]) -> None:
+        raw = [p if isinstance(p, bytes) else os.fsencode(p) for p in paths]
+        self.raw = raw
+        self.buf = np.frombuffer(b"\0".join(raw) + b"\0", dtype=np.uint8)
+        lens = np.fromiter((len(r) + 1 for r in raw), dtype=np.uint64, count=len(raw))
+        starts = np.zeros(len(raw), dtype=np.uint64)
+        if len(raw) > 1:
+            np.cumsum(lens[:-1], out=starts[1:])
+        self.ptrs = starts + np.uint64(self.buf.ctypes.data)
+
+    def __len__(self) -> int:
+        return len(self.raw)
+
+    @property
+    def address(self) -> int:
+        return self.ptrs.ctypes.data
+
+    def path(self, k: int) -> Path:
+        return Path(os.fsdecode(self.raw[k]))
 
 
-def scan_files(paths: Sequence[Path], threads: int = 0) -> np.ndarray:
+def scan_files(paths: Sequence[str | bytes | os.PathLike] | _PathTable, threads: int = 0
+               ) -> np.ndarray:
     """``pots_store_scan`` over ``paths``: one structured record per file."""
-    out = np.zeros(len(paths), dtype=_STORED)
-    if not paths:
+    table = paths if isinstance(paths, _PathTable) else _PathTable(paths)
+    out = np.zeros(len(table), dtype=_STORED)
+    if not len(table):
         return out
-    arr, _keep = _path_array(paths)
-    _check(_lib().pots_store_scan(len(paths), ctypes.addressof(arr), out.ctypes.data, threads),
+    _check(_lib().pots_store_scan(len(table), table.address, out.ctypes.data, threads),
            "pots_store_scan")
     return out
 
@@ -180,13 +201,26 @@ def _aligned(n: int) -> int:
     return (n + ALIGN - 1) // ALIGN * ALIGN
 
 
-def _over(arena: torch.Tensor, off: int, dtype: torch.dtype, size: Sequence[int],
-          stride: Sequence[int], storage_offset: int) -> torch.Tensor:
-    """A tensor over ``arena`` bytes from ``off``, with its own version counter."""
-    esz = torch.empty(0, dtype=dtype).element_size()
-    t = torch.empty(0, dtype=dtype, device=arena.device)
-    return t.set_(arena.untyped_storage(), arena.storage_offset() + off // esz + storage_offset,
-                  tuple(size), tuple(stride))
+_ESZ = {dt: torch.empty(0, dtype=dt).element_size() for dt in STORE_DTYPES.values()}
+
+
+class _Views:
+    """Tensors over one arena, each with a version counter of its own (``Tensor.set_`` on a
+    fresh tensor, not a view of the arena)."""
+
+    def __init__(self, arena: torch.Tensor) -> None:
+        self.storage = arena.untyped_storage()
+        self.base = arena.storage_offset()
+        self.device = arena.device
+        self.empty = {dt: torch.empty(0, dtype=dt, device=arena.device)
+                      for dt in STORE_DTYPES.values()}
+
+    def __call__(self, off: int, dtype: torch.dtype, size: Sequence[int],
+                 stride: Sequence[int], storage_offset: int) -> torch.Tensor:
+        t = self.empty[dtype].new_empty(0) if dtype in self.empty else \
+            torch.empty(0, dtype=dtype, device=self.device)
+        esz = t.element_size()
+        return t.set_(self.storage, (self.base + off) // esz + storage_offset, size, stride)
 
 
 def _bytes_of(t: torch.Tensor) -> torch.Tensor:
@@ -218,21 +252,22 @@ class StepLoader:
         the store) and the captured operands of products ``operand_ms``."""
         times: dict[str, float] = {}
         t0 = time.perf_counter()
-        leaf_paths = [store.leaf_path(i) for i in range(n_leaves)]
-        op_dir = store.directory / OPERAND_DIR
-        op_paths = [op_dir / OPERAND_FILE.format(m, w) for m in operand_ms for w in "ab"]
-        paths = leaf_paths + op_paths
+        d = os.fsencode(store.directory)
+        leaf_name = os.fsencode(LEAF_FILE).replace(b"{:05d}", b"%05d")
+        op_name = os.fsencode(f"{OPERAND_DIR}/{OPERAND_FILE}").replace(b"{:05d}_{}", b"%05d_%s")
+        paths = _PathTable([d + b"/" + leaf_name % i for i in range(n_leaves)] +
+                           [d + b"/" + op_name % (m, w) for m in operand_ms for w in (b"a", b"b")])
         info = scan_files(paths, self.threads)
         times["scan"] = time.perf_counter() - t0
 
         # Layout: every scanned storage, then every fallback tensor's storage.
         t1 = time.perf_counter()
-        off = 0
         offsets = np.zeros(len(paths), dtype=np.int64)
         ok = info["status"] == STORE_OK
-        for k in np.flatnonzero(ok):
-            offsets[k] = off
-            off += _aligned(int(info["storage_bytes"][k]))
+        aligned = (info["storage_bytes"][ok].astype(np.int64) + ALIGN - 1) // ALIGN * ALIGN
+        ends = np.cumsum(aligned)
+        offsets[ok] = ends - aligned
+        off = int(ends[-1]) if len(ends) else 0
         objs: dict[int, Any] = {}
         fb_tensors: list[tuple[int, torch.Tensor]] = []
         for k in np.flatnonzero(~ok):
@@ -242,12 +277,14 @@ class StepLoader:
                     obj = store.leaf(k)
                 else:
                     try:
-                        obj = torch.load(paths[k], map_location="cpu", weights_only=True)
+                        obj = torch.load(paths.path(k), map_location="cpu",
+                                         weights_only=True)
                     except Exception as e:
-                        raise LeafReadError(f"operand file {paths[k].name} unreadable: "
+                        raise LeafReadError(f"operand file {paths.path(k).name} unreadable: "
                                             f"{type(e).__name__}: {e}") from e
                     if not isinstance(obj, torch.Tensor):
-                        raise LeafReadError(f"operand file {paths[k].name} holds no tensor")
+                        raise LeafReadError(f"operand file {paths.path(k).name} holds no "
+                                            "tensor")
             except Exception as e:  # kept, and raised when the leaf is read
                 if k >= n_leaves:
                     raise
@@ -269,45 +306,60 @@ class StepLoader:
         segs["bytes"] = info["storage_bytes"][idx]
         segs["dst_offset"] = offsets[idx]
         moved = int(segs["bytes"].sum())
-        if len(segs):
-            arr, _keep = _path_array(paths)
-            host = self.device.type != "cuda"
-            staging = 0 if host else self.staging.data_ptr()
-            staging_bytes = 0 if host else self.staging.numel()
-            _check(_lib().pots_store_load(
-                len(paths), ctypes.addressof(arr), len(segs), segs.ctypes.data,
-                arena.data_ptr(), -1 if host else self.device.index, staging, staging_bytes,
-                self.threads), "pots_store_load")
-        times["load"] = time.perf_counter() - t2
+        # The native load runs on a thread of its own (ctypes lets go of the GIL), while this
+        # thread lays the leaves' tensors over the arena: they need only the offsets.
+        failure: list[BaseException] = []
+        native_s = [0.0]
 
+        def native_load() -> None:
+            t = time.perf_counter()
+            try:
+                host = self.device.type != "cuda"
+                staging = 0 if host else self.staging.data_ptr()
+                staging_bytes = 0 if host else self.staging.numel()
+                _check(_lib().pots_store_load(
+                    len(paths), paths.address, len(segs), segs.ctypes.data,
+                    arena.data_ptr(), -1 if host else self.device.index, staging,
+                    staging_bytes, self.threads), "pots_store_load")
+            except BaseException as e:  # raised on the caller's thread below
+                failure.append(e)
+            native_s[0] = time.perf_counter() - t
+
+        worker = threading.Thread(target=native_load, name="pots-store-load")
+        if len(segs):
+            worker.start()
+        t3 = time.perf_counter()
+        view = _Views(arena)
+        out: list[Any] = []
+        cols = (ok.tolist(), offsets.tolist(), info["dtype"].tolist(), info["ndim"].tolist(),
+                info["size"].tolist(), info["stride"].tolist(), info["storage_offset"].tolist())
+        for k, (good, o, dt, nd, size, stride, so) in enumerate(zip(*cols)):
+            if good:
+                v = view(o, STORE_DTYPES[dt], size[:nd], stride[:nd], so)
+            else:
+                v = objs[k]
+                if isinstance(v, torch.Tensor):
+                    t = v
+                    v = view(o, t.dtype, t.shape, t.stride(), t.storage_offset())
+                    if t.requires_grad:
+                        v.requires_grad_(True)
+            out.append(v)
+        times["build"] = time.perf_counter() - t3
+        if len(segs):
+            worker.join()
+        times["load"] = native_s[0]
+        times["load_and_build"] = time.perf_counter() - t2
+        if failure:
+            raise failure[0]
         # Fallback tensors after the native load: its spans may write the bytes between
         # segments.
-        t3 = time.perf_counter()
         for k, t in fb_tensors:
             nb = t.untyped_storage().nbytes()
             if nb:
                 o = int(offsets[k])
                 arena[o:o + nb].copy_(_bytes_of(t))
-        out: list[Any] = []
-        for k in range(len(paths)):
-            if ok[k]:
-                r = info[k]
-                nd = int(r["ndim"])
-                v = _over(arena, int(offsets[k]), STORE_DTYPES[int(r["dtype"])],
-                          r["size"][:nd].tolist(), r["stride"][:nd].tolist(),
-                          int(r["storage_offset"]))
-            else:
-                v = objs[k]
-                if isinstance(v, torch.Tensor):
-                    t = v
-                    v = _over(arena, int(offsets[k]), t.dtype, t.shape, t.stride(),
-                              t.storage_offset())
-                    if t.requires_grad:
-                        v.requires_grad_(True)
-            out.append(v)
         if self.device.type == "cuda":
             torch.cuda.current_stream(self.device).synchronize()
-        times["build"] = time.perf_counter() - t3
         leaves = out[:n_leaves]
         ops = {m: (out[n_leaves + 2 * j], out[n_leaves + 2 * j + 1])
                for j, m in enumerate(operand_ms)}

@@ -303,24 +303,36 @@ def test_scan_refuses_big_endian_and_compressed_archives(tmp_path):
     assert info["status"].tolist() == [L.STORE_OTHER, L.STORE_OTHER]
 
 
-def test_scan_never_takes_a_damaged_file_torch_load_reads_otherwise(tmp_path):
-    """Bytes flipped anywhere in the archive: whenever the scan still takes the file,
-    torch.load reads it to exactly what the scan describes."""
-    t = torch.arange(60, dtype=torch.float32).reshape(6, 10)
+def _record_span(raw: bytes, info: zipfile.ZipInfo) -> tuple[int, int]:
+    nl, xl = struct.unpack("<HH", raw[info.header_offset + 26:info.header_offset + 30])
+    lo = info.header_offset + 30 + nl + xl
+    return lo, lo + info.file_size
+
+
+@pytest.mark.filterwarnings("ignore:Detected pickle protocol")
+@pytest.mark.parametrize("region", ["archive", "pickle"])
+@pytest.mark.parametrize("tensor", ["f32", "bf16_permuted"])
+def test_scan_never_takes_a_damaged_file_torch_load_reads_otherwise(tmp_path, region, tensor):
+    """Bytes changed anywhere in the archive (or only in the pickle): whenever the scan still
+    takes the file, torch.load reads it to exactly what the scan describes."""
+    t = (torch.arange(60, dtype=torch.float32).reshape(6, 10) if tensor == "f32" else
+         torch.randn(3, 4, 50, generator=torch.Generator().manual_seed(0))
+         .to(torch.bfloat16).permute(2, 0, 1))
     torch.save(t, tmp_path / "a.pt")
     raw = (tmp_path / "a.pt").read_bytes()
     with zipfile.ZipFile(tmp_path / "a.pt") as zf:
-        data_info = next(i for i in zf.infolist() if "/data/" in i.filename)
-    nl, xl = struct.unpack("<HH", raw[data_info.header_offset + 26:data_info.header_offset + 30])
-    data_lo = data_info.header_offset + 30 + nl + xl
-    data_hi = data_lo + data_info.file_size
-    rng = random.Random(7)
+        data_lo, data_hi = _record_span(raw, next(i for i in zf.infolist()
+                                                  if "/data/" in i.filename))
+        pk_lo, pk_hi = _record_span(raw, next(i for i in zf.infolist()
+                                              if i.filename.endswith("/data.pkl")))
+    rng = random.Random({"archive": 7, "pickle": 11}[region] + 100 * (tensor == "f32"))
     paths = []
-    for k in range(400):
+    for k in range(300):
         b = bytearray(raw)
-        for _ in range(rng.choice((1, 1, 2, 3))):
+        for _ in range(rng.choice((1, 1, 2, 3, 5))):
             while True:
-                pos = rng.randrange(len(b))
+                pos = rng.randrange(pk_lo, pk_hi) if region == "pickle" else \
+                    rng.randrange(len(b))
                 if not data_lo <= pos < data_hi:  # the values themselves are free bytes
                     break
             b[pos] = rng.randrange(256)
@@ -334,6 +346,22 @@ def test_scan_never_takes_a_damaged_file_torch_load_reads_otherwise(tmp_path):
             taken += 1
             _agrees(p, r)
     assert 0 < taken < len(paths)
+
+
+def test_scan_refuses_a_memo_put_with_nothing_to_memoize(tmp_path):
+    """A pickle that opens with BINPUT: torch.load fails on it (the unpickler's stack is
+    empty), so the scan must not take it."""
+    torch.save(torch.zeros(4), tmp_path / "a.pt")
+    raw = bytearray((tmp_path / "a.pt").read_bytes())
+    with zipfile.ZipFile(tmp_path / "a.pt") as zf:
+        lo, _ = _record_span(bytes(raw), next(i for i in zf.infolist()
+                                              if i.filename.endswith("/data.pkl")))
+    assert raw[lo] == 0x80  # PROTO
+    raw[lo] = ord("q")      # BINPUT 2
+    (tmp_path / "b.pt").write_bytes(bytes(raw))
+    with pytest.raises(Exception):
+        torch.load(tmp_path / "b.pt", weights_only=True)
+    assert L.scan_files([tmp_path / "b.pt"])["status"][0] == L.STORE_OTHER
 
 
 # ---- pots_store_load and the loader on the host ------------------------------------------
@@ -408,13 +436,13 @@ def test_loader_brings_captured_operands(tmp_path):
 def test_store_load_rejects_bad_segments_and_short_files(tmp_path):
     p = tmp_path / "x.bin"
     p.write_bytes(bytes(range(256)) * 16)
-    arr, _keep = L._path_array([p])
+    table = L._PathTable([p])
     dst = np.zeros(8192, dtype=np.uint8)
 
     def run(segs):
         s = np.array(segs, dtype=L._SEGMENT)
-        return L._lib().pots_store_load(1, __import__("ctypes").addressof(arr), len(s),
-                                        s.ctypes.data, dst.ctypes.data, -1, None, 0, 2)
+        return L._lib().pots_store_load(1, table.address, len(s), s.ctypes.data,
+                                        dst.ctypes.data, -1, None, 0, 2)
 
     assert run([(0, 0, 100, 50, 0), (0, 0, 0, 64, 4096)]) == 0
     assert bytes(dst[:50]) == (bytes(range(256)) * 16)[100:150]
