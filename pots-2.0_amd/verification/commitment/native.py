@@ -400,8 +400,10 @@ class _FvProductC(ctypes.Structure):
 
 class FvProduct:
     """One checked product for :class:`FvPlan`: GPU tensors ``a`` [n, q], ``b`` [q, w], ``p``
-    [n, w] (fp32 or bf16, unit column stride), an optional fp32 ``bias`` [w], and the
-    challenge label ``m``."""
+    [n, w] (fp32 or bf16), an optional fp32 ``bias`` [w], and the challenge label ``m``.
+    The kernels stream rows with unit column stride; an operand in another layout (a
+    transposed view such as a linear layer's ``W.t()``, as captured operands are) is copied
+    to that layout by the plan, once, when the plan is built."""
 
     __slots__ = ("a", "b", "p", "bias", "m")
 
@@ -425,6 +427,14 @@ def verdict_specs(qs: Sequence[int], ns: Sequence[int], biased: Sequence[bool],
     return torch.from_numpy(rec.view(np.uint8).copy()).to(device)
 
 
+def _row_major(t: torch.Tensor) -> torch.Tensor:
+    """``t`` if its rows are contiguous and do not overlap, else a row-major copy."""
+    if isinstance(t, torch.Tensor) and t.dim() == 2 and t.numel() and \
+            (t.stride(1) != 1 or t.stride(0) < t.shape[1]):
+        return t.contiguous()
+    return t
+
+
 class FvPlan:
     """``pots_fv_plan_*``: operand layout and workspace fixed once; :meth:`rows` enqueues the
     challenges, the three streaming passes and the reduction for every product."""
@@ -439,11 +449,11 @@ class FvPlan:
         arr = (_FvProductC * n)()
         keep = []
         for i, pr in enumerate(products):
-            a, b, p = pr.a, pr.b, pr.p
+            a, b, p = (_row_major(t) for t in (pr.a, pr.b, pr.p))
             for name, t in (("a", a), ("b", b), ("p", p)):
                 if not t.is_cuda or t.dim() != 2 or t.stride(1) != 1 or t.dtype not in _DT:
                     raise ValueError(f"product {i}: {name} must be a 2-D GPU tensor in fp32 or "
-                                     f"bf16 with unit column stride")
+                                     f"bf16")
             nn, q = a.shape
             q2, w = b.shape
             if q2 != q or tuple(p.shape) != (nn, w):

@@ -201,6 +201,29 @@ def test_strided_rows_and_views(lib):
     _check_row(rows[0].tolist(), a, b, p, r, None, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_transposed_operands(lib, dtype):
+    """Captured operands come as transposed views (a linear layer's ``B = W.t()``, a weight
+    gradient's ``A = δYᵀ``): the rows equal those of row-major copies bit for bit."""
+    from verification.commitment import native
+    a, b, p, bv = _operands(96, 130, 70, 5, dtype, bias=True)
+    a_t = a.t().contiguous().to(DEV).t()   # [n, q] with strides (1, n)
+    b_t = b.t().contiguous().to(DEV).t()   # [q, w] with strides (1, q)
+    assert a_t.stride() == (1, 96) and b_t.stride() == (1, 130)
+
+    def rows(x, y):
+        plan = lib.fv_plan([native.FvProduct(x, y, p.to(DEV), 9, bv.to(DEV))], 4, True)
+        try:
+            return plan.rows(H).cpu()
+        finally:
+            plan.close()
+
+    got = rows(a_t, b_t)
+    assert torch.equal(got, rows(a.to(DEV), b.to(DEV)))
+    r = O.challenge_matrices(H, [9], 4, 70)[0]
+    _check_row(got[0].tolist(), a, b, p, r, bv, dtype)
+
+
 def test_plan_challenges_equal_oracle(lib):
     from verification.commitment import native
     a, b, p, _ = _operands(32, 16, 40, 2, torch.bfloat16)
