@@ -4,15 +4,20 @@ Reference: verification/computation/interface.py:60-330. Only the layout contrac
 path needs is kept: ``ProductSpec`` (which leaf is ``P_m``, its shapes, its challenge width),
 the leaf order ``[records n_s | W_t n_w | P_1..P_M | W_{t+1} n_w]``, the index helpers, and
 check 6a's declaration (the step size ``eta``, ``linear_weights``, ``chain_gradient``).
-The model replay that rebuilds operands is not part of this build; check 5 takes its
-operands from a :class:`Replay` the caller supplies.
+A computation serves check 5's operands through :meth:`DeclaredComputation.replay`: the
+decoder takes the captured operands it is given (its model replay is not part of this build),
+the MLP instance replays its glue from the committed leaves. The prover's side
+(:meth:`~DeclaredComputation.build_model`, :meth:`~DeclaredComputation.loss`,
+:meth:`~DeclaredComputation.forward_backward`, :meth:`~DeclaredComputation.label`;
+reference interface.py:362-413) drives ``verification.prover.step.prove_step``.
 """
 
 from __future__ import annotations
 
 import abc
+import contextlib
 import enum
-from collections.abc import Iterable, Sequence
+from collections.abc import Callable, Iterable, Mapping, Sequence
 from dataclasses import dataclass
 from functools import cached_property
 from typing import Any
@@ -87,6 +92,37 @@ class Replay(abc.ABC):
         if dtype is not None:
             a, b = a.to(dtype), b.to(dtype)
         return a, b
+
+
+class LabelingError(RuntimeError):
+    """Captured matmuls do not map one to one onto the declared product slots."""
+
+
+def load_weights(computation: DeclaredComputation, model: torch.nn.Module,
+                 weights: Mapping[str, torch.Tensor]) -> None:
+    """Copy ``weights`` into ``model``; both hold exactly the declared weights (reference
+    interface.py:183-198)."""
+    params = dict(model.named_parameters())
+    names = set(computation.weight_names)
+    if set(params) != names:
+        raise ValueError(f"model parameters {sorted(params)} differ from the declared weights")
+    if set(weights) != names:
+        raise ValueError(f"weights {sorted(weights)} differ from the declared weights")
+    with torch.no_grad():
+        for name in computation.weight_names:
+            w, p = weights[name], params[name]
+            if w.shape != p.shape or w.dtype != p.dtype:
+                raise ValueError(f"{name}: got {w.dtype} {tuple(w.shape)}, the model holds "
+                                 f"{p.dtype} {tuple(p.shape)}")
+            p.copy_(w)
+
+
+def snapshot_weights(computation: DeclaredComputation,
+                     model: torch.nn.Module) -> dict[str, torch.Tensor]:
+    """Copies of the model's declared weights, in ``weight_names`` order, on the device the
+    model is on (reference interface.py:201-212 copies them to the host; here a step's
+    ``W_{t+1}`` leaves stay in HBM for the device commit)."""
+    return {n: model.get_parameter(n).detach().clone() for n in computation.weight_names}
 
 
 def chain_gradient(parts: Iterable[torch.Tensor], dtype: torch.dtype) -> torch.Tensor:
@@ -174,6 +210,32 @@ class DeclaredComputation(abc.ABC):
     def encode_record(self, record: Any) -> bytes:
         from setup.records import encode_record
         return encode_record(record)
+
+    # ---- prover side (reference interface.py:362-413; the verifier never calls these) ----
+
+    def build_model(self) -> torch.nn.Module:
+        """A fresh model whose parameters are exactly :attr:`weight_names`."""
+        raise NotImplementedError(f"{type(self).__name__} builds no model in this build")
+
+    def loss(self, model: torch.nn.Module, records: Sequence[Any]) -> torch.Tensor:
+        """Assemble the batch and run the forward pass to the scalar loss."""
+        raise NotImplementedError(f"{type(self).__name__} has no training loss in this build")
+
+    def forward_backward(self, model: torch.nn.Module, records: Sequence[Any],
+                         stage: Callable[[str], contextlib.AbstractContextManager[Any]]
+                         ) -> torch.Tensor:
+        """One training pass: the forward pass to the loss inside ``stage("forward")``, then
+        ``loss.backward()`` inside ``stage("backward")``; returns the loss."""
+        with stage("forward"):
+            loss = self.loss(model, records)
+        with stage("backward"):
+            loss.backward()
+        return loss
+
+    def label(self, capture: Any, model: torch.nn.Module) -> list[torch.Tensor]:
+        """The captured outputs in canonical order ``P_1..P_M``, mapped by operand identity;
+        :class:`LabelingError` unless every slot is filled once with its declared shape."""
+        raise NotImplementedError(f"{type(self).__name__} labels no capture in this build")
 
     def product_class(self, spec: ProductSpec) -> str:
         """The κ class of a product; by default its kind and role with layer digits masked."""

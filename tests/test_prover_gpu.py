@@ -1,0 +1,110 @@
+"""The prover on the GPU and the MLP step verified with its replay (reference
+tests/verification/test_m1_smoke.py: an honest MLP step accepts, a perturbed product rejects).
+
+The products stay in HBM (the capture keeps each op's own output) and the commit hashes every
+leaf there; the root must equal the CPU oracle's over the same leaves. The verifier then
+rebuilds every operand from the committed leaves (``MLPReplay``, no captured operands) and
+must accept the honest step through ``Verifier`` and ``DeviceStepVerifier`` alike, and reject
+a step whose committed product was changed at check 5, and one whose ``W_{t+1}`` was changed
+at check 6a.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+WIDTHS = (48, 96, 80, 24)
+
+
+def _prove(seed=0, n_s=32, perturb=None, widths=WIDTHS):
+    from verification.computation.instances.mlp import (MLPComputation, init_weights,
+                                                        synthetic_dataset)
+    from verification.prover.step import commit, prove_step
+    c = MLPComputation(widths, n_s=n_s, eta=0.05)
+    model = c.build_model().cuda()
+    w0 = init_weights(widths, seed, "cuda")
+    records = synthetic_dataset(widths, n_s, seed + 7)
+    step = prove_step(c, model, w0, records, perturb=perturb)
+    return c, step, commit(c, step)
+
+
+def _oracle_root(c, leaves):
+    hashes = []
+    for i, obj in enumerate(leaves):
+        if i < c.n_s:
+            hashes.append(O.tensor_leaf_hash(0x04, obj.cpu()))
+        else:
+            tag = O.TAG_PRODUCT if c.n_s + c.n_w <= i < c.n_s + c.n_w + c.M else O.TAG_WEIGHT
+            hashes.append(O.tensor_leaf_hash(tag, obj.cpu()))
+    return O.merkle_root(hashes)
+
+
+def test_products_stay_in_hbm_and_commit_matches_the_oracle(lib):
+    c, step, tree = _prove(seed=1)
+    assert step.capture["device_resident"] and step.capture["n_products"] == c.M
+    assert all(p.is_cuda for p in step.products)
+    assert all(w.is_cuda for w in step.w_next.values())
+    assert tree.root == _oracle_root(c, step.leaves())
+
+
+def test_honest_step_accepts_with_the_replay(lib):
+    from verification.transcript.store import InMemoryStore
+    from verification.verifier.driver import Verifier
+    c, step, tree = _prove(seed=2)
+    v = Verifier(c, k=2)
+    assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
+    assert [s.m for s in v.stats[1].products] == [p.m for p in c.products]
+    assert v.stats[1].max_normalized() <= 8.0
+
+
+def test_device_step_verifier_with_the_replay(lib):
+    from verification.computation.instances.mlp import MLPReplay
+    from verification.verifier.step import DeviceStepVerifier
+    c, step, tree = _prove(seed=3)
+    replay = MLPReplay(c, step.leaves())
+    out = DeviceStepVerifier(c, step.leaves(), lambda s: replay.operands(s.m), k=2).run(
+        tree.root)
+    assert out.check is None, out.detail
+    assert out.root == tree.root and out.first_fail == c.M
+
+
+def test_perturbed_product_rejects_at_check_5(lib):
+    from verification.transcript.store import InMemoryStore
+    from verification.verifier.driver import Verifier
+    m = 2  # Y_2, a forward product: check 6a does not read it
+    c, step, tree = _prove(seed=4, perturb={m: lambda p: p.index_add_(
+        0, torch.tensor([3], device=p.device), torch.full_like(p[:1], 0.25))})
+    rej = Verifier(c, k=2).verify_step(1, InMemoryStore(step.leaves(), tree))
+    assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
+    assert rej.detail.startswith(f"P_{m} (Y_2)")
+
+
+def test_changed_update_rejects_at_check_6a(lib):
+    from verification.commitment.leaves import commit_leaves_device
+    from verification.transcript.store import InMemoryStore
+    from verification.verifier.driver import Verifier
+    c, step, _ = _prove(seed=5)
+    leaves = step.leaves()
+    i = c.w_next_index(c.weight(2))
+    leaves[i] = leaves[i].clone()
+    leaves[i][0, 0] += 1e-2
+    tree = commit_leaves_device(c, leaves)
+    rej = Verifier(c, k=2).verify_step(1, InMemoryStore(leaves, tree))
+    assert rej is not None and rej.check_id == "6a", rej
+
+
+def test_stored_mlp_step_verifies_from_disk(lib, tmp_path):
+    from verification.transcript.loader import ResidentStore, load_step
+    from verification.transcript.store import DiskStore
+    from verification.verifier.driver import Verifier
+    c, step, tree = _prove(seed=6)
+    disk = DiskStore.write(tmp_path / "step", c, step.leaves(), tree)
+    res = load_step(disk, c.n_leaves)
+    assert res.fallback == 0  # records are plain tensor leaves here
+    for store in (disk, ResidentStore(disk, res)):
+        assert Verifier(c, k=2).verify_step(1, store) is None

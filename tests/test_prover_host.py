@@ -1,0 +1,174 @@
+"""The prover side on the host: the matmul capture's recording rules (reference
+tests/verification/prover/test_capture.py), the MLP computation's inventory, labeling and SGD
+step (reference instances/mlp.py, prover/step.py), and the MLP replay's operands, which must
+reproduce every committed product bit for bit on the same device.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from verification.computation.instances.mlp import (MLPComputation, MLPReplay, init_weights,
+                                                    synthetic_dataset)
+from verification.computation.interface import ProductKind
+from verification.computation.matmul_ops import HANDLED_OPS, REJECTED_OPS, param_storage_map
+from verification.prover.capture import (BiasedMatmulError, MatmulCapture,
+                                         MutatedCaptureError, PhaseError,
+                                         UnsupportedMatmulError)
+from verification.prover.step import prove_step
+
+WIDTHS = (6, 9, 7, 5)
+
+
+def test_op_lists_name_real_aten_ops():
+    missing = [n for n in sorted(HANDLED_OPS | REJECTED_OPS)
+               if not hasattr(torch.ops.aten, n)]
+    # a few names exist only on some builds (MPS, CUDA-only kernels); the rest must resolve
+    assert len(missing) < 15, missing
+    assert not HANDLED_OPS & REJECTED_OPS
+
+
+def test_capture_records_products_with_their_operands():
+    a, b = torch.randn(4, 3), torch.randn(3, 5)
+    bias = torch.randn(5)
+    x, y = torch.randn(2, 4, 3), torch.randn(2, 3, 6)
+    cap = MatmulCapture()
+    with cap, cap.phase("forward"):
+        p1 = torch.mm(a, b)
+        p2 = torch.addmm(bias, a, b)                        # the bias rule: a vector added once
+        p3 = torch.bmm(x, y)
+        p4 = torch.addmm(torch.zeros(4, 5), a, b)           # an inert bias
+        p5 = torch.baddbmm(torch.zeros(2, 4, 6), x, y, beta=0)
+    assert [r.op for r in cap.records] == ["aten.mm.default", "aten.addmm.default",
+                                           "aten.bmm.default", "aten.addmm.default",
+                                           "aten.baddbmm.default"]
+    assert all(r.out is p for r, p in zip(cap.records, (p1, p2, p3, p4, p5)))
+    assert cap.records[1].bias is bias and cap.records[0].bias is None
+    assert cap.records[2].batch == 2 and cap.n_products == 1 + 1 + 2 + 1 + 2
+    assert [m[2].shape for m in cap.records[2].members()] == [(4, 6), (4, 6)]
+    assert all(r.q == 3 for r in cap.records) and not cap.glue_outer
+    s = cap.summary()
+    assert s["n_calls"] == 5 and s["n_products"] == 7 and s["products_by_phase"] == {
+        "forward": 7}
+
+
+def test_capture_rules_refuse_what_the_inventory_cannot_hold():
+    a, b = torch.randn(4, 3), torch.randn(3, 5)
+    cap = MatmulCapture()
+    with cap:
+        with pytest.raises(PhaseError):
+            torch.mm(a, b)                                  # outside a phase
+        with cap.phase("forward"):
+            with pytest.raises(PhaseError):
+                with cap.phase("backward"):
+                    pass
+            with pytest.raises(BiasedMatmulError):
+                torch.addmm(torch.ones(4, 5), a, b)         # a matrix bias
+            with pytest.raises(BiasedMatmulError):
+                torch.addmm(torch.ones(5), a, b, alpha=2)
+            with pytest.raises(BiasedMatmulError):
+                torch.baddbmm(torch.ones(5), a[None], b[None])  # a batched product's bias
+            with pytest.raises(UnsupportedMatmulError):
+                torch.mv(a, torch.randn(3))
+            with pytest.raises(UnsupportedMatmulError):
+                torch.ops.aten.mm.out(a, b, out=torch.empty(4, 5))
+            torch.mm(torch.randn(4, 1), torch.randn(1, 5))  # q = 1: an outer product, glue
+    with pytest.raises(PhaseError):
+        with cap.phase("sideways"):
+            pass
+    assert len(cap.glue_outer) == 1 and not cap.records
+
+
+def test_capture_tracks_producers_parameter_copies_and_mutation():
+    lin = torch.nn.Linear(3, 4, bias=False)
+    names = param_storage_map(lin)
+    x = torch.randn(5, 3)
+    cap = MatmulCapture(param_names=names)
+    with cap:
+        with cap.phase("forward"):
+            y = lin(x)
+            w16 = lin.weight.to(torch.float64)              # a copy of a parameter
+            z = torch.mm(y, torch.randn(4, 2))
+            torch.mm(x.double(), w16.t())
+    fwd, second, third = cap.records
+    assert fwd.b_info.param_name == "weight"
+    assert second.a_info.producer_index == fwd.index       # z's A is y, fwd's output
+    assert third.b_info.param_copy == "weight" and third.b_info.param_name is None
+    assert any(c.param == "weight" for c in cap.copies)
+    cap.assert_unmodified()
+    z.add_(1.0)
+    with pytest.raises(MutatedCaptureError):
+        cap.assert_unmodified()
+    cap.release_operands()
+    assert all(r.a is None and r.b is None for r in cap.records)
+
+
+def test_mlp_inventory_matches_the_reference_layout():
+    c = MLPComputation(WIDTHS, n_s=4, eta=0.05)
+    assert c.M == 3 * c.L - 1 == 8
+    assert [p.name for p in c.products] == ["Y_1", "Y_2", "Y_3", "dX_3", "G_3", "dX_2", "G_2",
+                                            "G_1"]
+    g3 = c.product(c.m_of("G_3"))
+    assert (g3.kind, g3.a_shape, g3.b_shape) == (ProductKind.WEIGHT_GRAD, (5, 4), (4, 7))
+    assert c.linear_weights == {"layers.0.weight": (8,), "layers.1.weight": (7,),
+                                "layers.2.weight": (5,)}
+    assert c.n_leaves == 4 + 2 * 3 + 8
+    with pytest.raises(ValueError):
+        MLPComputation(WIDTHS, n_s=1, eta=0.05)
+    with pytest.raises(ValueError):
+        c.encode_record(torch.zeros(10))
+
+
+def _step(seed=0, n_s=4, perturb=None):
+    c = MLPComputation(WIDTHS, n_s=n_s, eta=0.05)
+    model = c.build_model()
+    w0 = init_weights(WIDTHS, seed)
+    records = synthetic_dataset(WIDTHS, n_s, seed + 7)
+    return c, w0, prove_step(c, model, w0, records, perturb=perturb), model
+
+
+def test_prove_step_labels_products_and_steps_sgd():
+    c, w0, step, model = _step()
+    assert len(step.leaves()) == c.n_leaves
+    x1, targets = c.assemble(step.records)
+    ws = [w0[n] for n in c.weight_names]
+    y1 = x1 @ ws[0].t()
+    assert torch.allclose(step.products[c.m_of("Y_1") - 1], y1, rtol=1e-6, atol=1e-6)
+    y2 = torch.tanh(y1) @ ws[1].t()
+    assert torch.allclose(step.products[c.m_of("Y_2") - 1], y2, rtol=1e-5, atol=1e-6)
+    # W_{t+1} = W_t − η·G_ℓ, G_ℓ the committed weight-gradient product
+    for l in range(1, c.L + 1):
+        g = step.products[c.m_of(f"G_{l}") - 1]
+        assert torch.allclose(step.w_next[c.weight(l)], w0[c.weight(l)] - c.eta * g,
+                              rtol=0, atol=1e-7)
+    assert step.capture["n_products"] == c.M
+    step.assert_unmodified()
+    step.products[0].add_(1.0)
+    with pytest.raises(MutatedCaptureError):
+        step.assert_unmodified()
+
+
+def test_prove_step_perturbation_changes_only_the_committed_leaf():
+    m = 2
+    c, _, honest, _ = _step()
+    _, _, cheat, _ = _step(perturb={m: lambda p: p + 1.0})
+    assert torch.equal(cheat.products[m - 1], honest.products[m - 1] + 1.0)
+    for k in range(c.M):
+        if k != m - 1:
+            assert torch.equal(cheat.products[k], honest.products[k])
+
+
+def test_replay_operands_reproduce_every_product():
+    c, _, step, _ = _step(seed=3)
+    replay = MLPReplay(c, step.leaves(), device="cpu")
+    for spec in c.products:
+        a, b = replay.operands(spec.m)
+        assert (tuple(a.shape), tuple(b.shape)) == (spec.a_shape, spec.b_shape)
+        assert torch.equal(torch.mm(a, b), step.products[spec.m - 1]), spec.name
+    assert replay.glue_gradients() == {}
+    # any order gives the same operands
+    again = MLPReplay(c, step.leaves(), device="cpu")
+    for spec in reversed(c.products):
+        a, b = again.operands(spec.m)
+        assert torch.equal(torch.mm(a, b), step.products[spec.m - 1]), spec.name
