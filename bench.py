@@ -298,6 +298,77 @@ def disk_leg(root: Path, c, step, k: int, claimed: bytes, v) -> dict:
             "verified": True, "source": "page cache (files written just before)"}
 
 
+def prover_leg(widths=(4096, 8192, 8192, 4096), n_s: int = 2048, k: int = 2) -> dict:
+    """The device-resident prover on an MLP step: the training pass with and without the
+    capture, the labeling and SGD step, the commit of every leaf in HBM (the reference copies
+    each product to the host as it is produced and hashes there: the bytes it would move are
+    timed as a device-to-host copy into pinned memory), and the verify step with every operand
+    rebuilt from the committed leaves by the replay."""
+    import torch
+
+    from verification.computation.instances.mlp import (MLPComputation, MLPReplay,
+                                                        init_weights, synthetic_dataset)
+    from verification.prover.step import commit, prove_step
+    from verification.verifier.step import DeviceStepVerifier
+
+    c = MLPComputation(widths, n_s=n_s, eta=1e-3)
+    with torch.device("cuda"):
+        model = c.build_model()
+    w0 = init_weights(widths, 0, "cuda")
+    records = synthetic_dataset(widths, n_s, 7)
+
+    def timed(fn, reps=3):
+        best, out = math.inf, None
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = fn()
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+        return best * 1e3, out
+
+    def plain():
+        from verification.computation.interface import load_weights
+        load_weights(c, model, w0)
+        model.zero_grad(set_to_none=True)
+        c.loss(model, records).backward()
+
+    plain_ms, _ = timed(plain)
+    prove_ms, step = timed(lambda: prove_step(c, model, w0, records))
+    commit_ms, tree = timed(lambda: commit(c, step))
+    leaves = step.leaves()
+    leaf_bytes = sum(x.nbytes for x in leaves)
+    moved = [*step.products, *step.w_next.values()]
+    host = [torch.empty(x.shape, dtype=x.dtype, pin_memory=True) for x in moved]
+
+    def offload():
+        for h, x in zip(host, moved):
+            h.copy_(x, non_blocking=True)
+
+    d2h_ms, _ = timed(offload)
+    d2h_bytes = sum(x.nbytes for x in moved)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    replay = MLPReplay(c, leaves)
+    v = DeviceStepVerifier(c, leaves, lambda s: replay.operands(s.m), k=k)
+    torch.cuda.synchronize()
+    setup_ms = (time.perf_counter() - t0) * 1e3
+    verify_ms, verdict = timed(lambda: v.run(tree.root))
+    assert verdict.check is None and verdict.root == tree.root, verdict.detail
+    log(f"[bench] prover leg: MLP {widths} x {n_s}: training pass {plain_ms:.1f} ms, under "
+        f"capture with labeling and SGD {prove_ms:.1f} ms; commit of {leaf_bytes / 1e9:.2f} GB "
+        f"in HBM {commit_ms:.2f} ms; the host copy it avoids: {d2h_bytes / 1e9:.2f} GB in "
+        f"{d2h_ms:.1f} ms; replay and plans {setup_ms:.1f} ms, verify {verify_ms:.1f} ms")
+    return {"model": f"MLP widths {list(widths)}, {n_s} records, fp32", "k": k,
+            "products": c.M, "leaf_bytes": leaf_bytes,
+            "training_pass_ms": round(plain_ms, 2), "prove_step_ms": round(prove_ms, 2),
+            "commit_ms": round(commit_ms, 3),
+            "commit_gbps": round(leaf_bytes / (commit_ms * 1e-3) / 1e9, 1),
+            "avoided_d2h_bytes": d2h_bytes, "avoided_d2h_ms": round(d2h_ms, 2),
+            "replay_and_plans_ms": round(setup_ms, 2), "verify_ms": round(verify_ms, 2),
+            "verified": True}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -321,6 +392,9 @@ def main() -> int:
                     help="also write the transcript under DIR in the on-disk store's format "
                          "(with the captured operands), load it back into HBM with the native "
                          "loader, verify the loaded copy, report parts.disk_load, and delete it")
+    ap.add_argument("--prover-leg", action="store_true",
+                    help="also prove one MLP step on the GPU (capture, labeling, SGD), commit "
+                         "it in HBM, verify it with the replay, and report parts.prover")
     ap.add_argument("--counter-summary", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSV output under DIR and exit")
     ap.add_argument("--trace-summary", metavar="DIR",
@@ -544,6 +618,8 @@ def main() -> int:
     }
     if args.disk_leg:
         out["parts"]["disk_load"] = disk_leg(Path(args.disk_leg), c, step, k, claimed_b, v)
+    if args.prover_leg:
+        out["parts"]["prover"] = prover_leg()
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")
         out["cpu_baseline"] = cpu_baseline(step, items)

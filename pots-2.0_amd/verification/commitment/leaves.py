@@ -193,13 +193,14 @@ def _until_error(c: DeclaredComputation, items: Iterable[tuple[int, Any]],
                 stats.read_s += perf_counter() - t0
                 stats.leaves += 1
             try:
-                if 0 <= i < c.n_s:
+                as_tensor = c.record_leaf(obj) if 0 <= i < c.n_s else None
+                if 0 <= i < c.n_s and as_tensor is None:
                     batch.headers.append(c.encode_record(obj))
                     batch.ptr.append(0)
                     batch.nbytes.append(0)
                     batch.kind.append(0)
                 else:
-                    tag, t = _checked_tensor(c, i, obj)
+                    tag, t = as_tensor if as_tensor is not None else _checked_tensor(c, i, obj)
                     key = (tag, t.dtype, tuple(t.shape))
                     h = hdr_cache.get(key)
                     if h is None:
@@ -306,8 +307,22 @@ class StepHasher:
                              f"{c.n_leaves}")
         dev = device or next(t.device for t in leaves[c.n_s:] if isinstance(t, torch.Tensor))
         headers, payloads, kinds = [], [], []
+        host_records: list[tuple[int, torch.Tensor]] = []
+        record_headers: dict[tuple[int, torch.dtype, tuple[int, ...]], bytes] = {}
         for i, obj in enumerate(leaves):
             if i < c.n_s:
+                as_tensor = c.record_leaf(obj)
+                if as_tensor is not None:  # a tensor leaf: hashed where it lies
+                    tag, t = as_tensor
+                    key = (tag, t.dtype, tuple(t.shape))
+                    if key not in record_headers:
+                        record_headers[key] = tensor_leaf_header(tag, t)
+                    headers.append(record_headers[key])
+                    kinds.append(native.FINITE_KIND[t.dtype])
+                    payloads.append(t if t.is_cuda else None)
+                    if not t.is_cuda:
+                        host_records.append((i, t))
+                    continue
                 rec = np.frombuffer(c.encode_record(obj), dtype=np.uint8).copy()
                 headers.append(b"")
                 payloads.append(torch.from_numpy(rec).to(dev))
@@ -319,6 +334,15 @@ class StepHasher:
             headers.append(tensor_leaf_header(tag, t))
             payloads.append(t)
             kinds.append(native.FINITE_KIND[t.dtype])
+        if host_records:  # one copy to the device for every host record tensor
+            flat = torch.cat([t.contiguous().view(-1).view(torch.uint8)
+                              for _, t in host_records]).to(dev)
+            self._records = flat
+            o = 0
+            for i, t in host_records:
+                n = t.numel() * t.element_size()
+                payloads[i] = flat[o:o + n].view(t.dtype).view(t.shape)
+                o += n
         self.c = c
         # With `fuse` (a native.FvPlan over this step's products), the product leaves' P-pass
         # sums are taken while they are hashed.

@@ -183,6 +183,10 @@ class MLPComputation(DeclaredComputation):
         self._check_record(record)
         return encode_tensor_leaf(TAG_MLP_RECORD, record)
 
+    def record_leaf(self, record: torch.Tensor) -> tuple[int, torch.Tensor]:
+        self._check_record(record)
+        return TAG_MLP_RECORD, record
+
     def _check_record(self, record: Any) -> None:
         if (not isinstance(record, torch.Tensor) or record.dtype != torch.float32
                 or tuple(record.shape) != (self.d_in + self.d_out,)):
@@ -289,7 +293,8 @@ class MLPReplay(Replay):
             device = torch.device("cuda", torch.cuda.current_device()) \
                 if torch.cuda.is_available() else torch.device("cpu")
         self.device = torch.device(device)
-        self.model = computation.build_model().to(self.device)
+        with self.device:  # the parameters are created (and initialised) on the device
+            self.model = computation.build_model()
         load_weights(computation, self.model,
                      {n: self.w_t(n) for n in computation.weight_names})
         self._x: dict[int, torch.Tensor] = {}

@@ -211,6 +211,13 @@ class DeclaredComputation(abc.ABC):
         from setup.records import encode_record
         return encode_record(record)
 
+    def record_leaf(self, record: Any) -> tuple[int, torch.Tensor] | None:
+        """``(tag, tensor)`` when a record's leaf is a tensor leaf (its encoding is
+        ``encode_tensor_leaf(tag, tensor)``), so a hasher can read its payload where it lies;
+        ``None`` (the default) when only :meth:`encode_record` gives its bytes. Validates the
+        record as :meth:`encode_record` does."""
+        return None
+
     # ---- prover side (reference interface.py:362-413; the verifier never calls these) ----
 
     def build_model(self) -> torch.nn.Module:
