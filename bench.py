@@ -407,7 +407,7 @@ def main() -> int:
         return trace_summary(Path(args.trace_summary), args.steps, args.warmup)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
-              "sharding is a design in DESIGN.md, not a measured path.", file=sys.stderr)
+              "sharding across GPUs is designed but not built or measured.", file=sys.stderr)
         return 2
 
     import torch

@@ -1,6 +1,6 @@
 """Parity of the gfx950 challenge, Freivalds and verdict kernels with the CPU oracle.
 
-Tolerances (stated per column, see DESIGN.md "Parity"):
+Tolerances, per column:
 - challenges: bit for bit;
 - ν, ‖|P|·1‖, ‖P‖_F, ΣA²(B²1), ‖b‖² (sums of non-negative terms): relative 1e-5;
 - residuals dominated by a planted error, and residuals of bf16 products (dominated by the
