@@ -406,8 +406,8 @@ def main() -> int:
     if args.trace_summary:
         return trace_summary(Path(args.trace_summary), args.steps, args.warmup)
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
-              "sharding across GPUs is designed but not built or measured.", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); sharding "
+              "across GPUs is designed but not built or measured.", file=sys.stderr)
         return 2
 
     import torch
