@@ -398,6 +398,14 @@ class _FvProductC(ctypes.Structure):
                 ("pad", _u32)]
 
 
+# _FvProductC as a numpy record, so a plan's table is filled column by column
+_FV_RECORD = np.dtype([("a", "<u8"), ("b", "<u8"), ("p", "<u8"), ("bias", "<u8"),
+                       ("lda", "<u8"), ("ldb", "<u8"), ("ldp", "<u8"), ("n", "<u4"),
+                       ("q", "<u4"), ("w", "<u4"), ("m", "<u4"), ("a_dtype", "<u4"),
+                       ("b_dtype", "<u4"), ("p_dtype", "<u4"), ("pad", "<u4")])
+assert _FV_RECORD.itemsize == ctypes.sizeof(_FvProductC)
+
+
 class FvProduct:
     """One checked product for :class:`FvPlan`: GPU tensors ``a`` [n, q], ``b`` [q, w], ``p``
     [n, w] (fp32 or bf16), an optional fp32 ``bias`` [w], and the challenge label ``m``.
@@ -429,9 +437,10 @@ def verdict_specs(qs: Sequence[int], ns: Sequence[int], biased: Sequence[bool],
 
 def _row_major(t: torch.Tensor) -> torch.Tensor:
     """``t`` if its rows are contiguous and do not overlap, else a row-major copy."""
-    if isinstance(t, torch.Tensor) and t.dim() == 2 and t.numel() and \
-            (t.stride(1) != 1 or t.stride(0) < t.shape[1]):
-        return t.contiguous()
+    if isinstance(t, torch.Tensor) and t.dim() == 2:
+        s0, s1 = t.stride()
+        if (s1 != 1 or s0 < t.shape[1]) and t.numel():
+            return t.contiguous()
     return t
 
 
@@ -446,7 +455,7 @@ class FvPlan:
             raise ValueError("a Freivalds plan needs at least one product")
         if not 1 <= k <= 255:
             raise ValueError(f"k must be in [1, 255], got {k}")
-        arr = (_FvProductC * n)()
+        table = []
         keep = []
         for i, pr in enumerate(products):
             a, b, p = (_row_major(t) for t in (pr.a, pr.b, pr.p))
@@ -468,15 +477,14 @@ class FvPlan:
                     raise ValueError(f"product {i}: bias of shape {tuple(bias.shape)}, "
                                      f"expected ({w},)")
                 keep.append(bias)
-            c = arr[i]
-            c.a, c.b, c.p = a.data_ptr(), b.data_ptr(), p.data_ptr()
-            c.bias = bias.data_ptr() if bias is not None else None
-            c.lda, c.ldb, c.ldp = a.stride(0), b.stride(0), p.stride(0)
-            c.n, c.q, c.w, c.m = nn, q, w, pr.m
-            c.a_dtype, c.b_dtype, c.p_dtype = _DT[a.dtype], _DT[b.dtype], _DT[p.dtype]
+            table.append((a.data_ptr(), b.data_ptr(), p.data_ptr(),
+                          bias.data_ptr() if bias is not None else 0, a.stride(0), b.stride(0),
+                          p.stride(0), nn, q, w, pr.m, _DT[a.dtype], _DT[b.dtype],
+                          _DT[p.dtype], 0))
             keep += [a, b, p]
+        arr = np.array(table, dtype=_FV_RECORD)
         h = ctypes.c_void_p()
-        lib._check(lib._lib.pots_fv_plan_create(n, ctypes.addressof(arr), k, int(bool(guard)),
+        lib._check(lib._lib.pots_fv_plan_create(n, arr.ctypes.data, k, int(bool(guard)),
                                                 ctypes.byref(h)), "pots_fv_plan_create")
         self._lib, self._h, self._keep = lib, h, keep
         self._fused_leaf = None  # weak reference to the leaf plan fused with this one

@@ -55,7 +55,7 @@ from verification.verifier.context import (
     _guard,
     _is_digest,
 )
-from verification.verifier.matmul_check.freivalds import ProductMeasure, finish_row
+from verification.verifier.matmul_check.freivalds import ProductMeasure, finish_rows
 
 __all__ = ["DEFAULT_ORDER", "ROOT_SLOT", "CHECKS", "protocol_id", "check_2_commitment",
            "check_2_root", "check_6a_linear_update", "check_5_matmuls"]
@@ -200,13 +200,17 @@ def _products(c: DeclaredComputation, leaves: CommittedLeaves, replay: Any
     product, its committed ``W_t`` bias in the operand format (as ``[A | 1]·[B ; bᵀ]``), on
     the current GPU (a store may serve host tensors, as the on-disk one does)."""
     dev = torch.device("cuda", torch.cuda.current_device())
+
+    def on_gpu(x: torch.Tensor) -> torch.Tensor:
+        return x if x.is_cuda else x.to(dev)
+
     out = []
     for spec in c.products:
-        a, b = (x.to(dev) for x in replay.operands(spec.m))
-        p = leaves.leaf(c.product_index(spec.m)).to(dev)
+        a, b = (on_gpu(x) for x in replay.operands(spec.m))
+        p = on_gpu(leaves.leaf(c.product_index(spec.m)))
         bias = None
         if spec.bias is not None:
-            bias = leaves.leaf(c.w_t_index(spec.bias)).to(dev).to(c.operand_dtype) \
+            bias = on_gpu(leaves.leaf(c.w_t_index(spec.bias))).to(c.operand_dtype) \
                 .to(torch.float32)
         out.append(native.FvProduct(a, b, p, spec.m, bias))
     return out
@@ -243,15 +247,17 @@ def check_5_matmuls(store: TranscriptStore, c: DeclaredComputation, ctx: StepCon
             _, _, first = lib.verdicts(rows, specs, k=ctx.k, eps_in=ctx.eps_in,
                                        eps_acc=ctx.eps_acc, tau=bands.tau,
                                        guard=ctx.kappa_guard, judge=ctx.judge)
-            host = rows.cpu().tolist()
+            host = rows.cpu().numpy()
             device_first = int(first.item())
         finally:
             plan.close()
     with ctx.timed("5.judge"):
-        done = [(spec, finish_row(row, q=spec.q, n=spec.a_shape[0], eps_in=ctx.eps_in,
-                                  eps_acc=ctx.eps_acc, guard=ctx.kappa_guard,
-                                  biased=spec.bias is not None))
-                for spec, row in zip(c.products, host)]
+        # finish_row on every row at once (the same fp64 operations, bit for bit)
+        mps = finish_rows(host, q=[s.q for s in c.products],
+                          n=[s.a_shape[0] for s in c.products], eps_in=ctx.eps_in,
+                          eps_acc=ctx.eps_acc, guard=ctx.kappa_guard,
+                          biased=[s.bias is not None for s in c.products])
+        done = list(zip(c.products, mps))
         for i, (spec, mp) in enumerate(done):
             rej = _judge_product(c, spec, mp, ctx, bands)
             if rej is not None:

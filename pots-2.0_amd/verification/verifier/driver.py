@@ -10,7 +10,10 @@ checks 0, 1, 4, 6b, 7 and 8, the record pass after a rejection) is not part of t
 
 from __future__ import annotations
 
+import contextlib
+import gc
 import time
+from collections.abc import Iterator
 from typing import Any
 
 from verification.computation.interface import DeclaredComputation
@@ -20,6 +23,21 @@ from verification.verifier.checks import CHECKS, DEFAULT_ORDER
 from verification.verifier.context import Rejection, StepContext, StepStats
 
 __all__ = ["Verifier"]
+
+
+@contextlib.contextmanager
+def _collector_paused() -> Iterator[None]:
+    """Python's cyclic collector off for one step: the step allocates tens of thousands of
+    small objects (a row per product, a stat per leaf), and each collection it would trigger
+    scans the whole heap of transcript objects. Reference counting still frees everything;
+    cycles wait for the next collection."""
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
 
 
 class Verifier:
@@ -50,12 +68,13 @@ class Verifier:
             kappa_guard=self.kappa_guard)
         timings = self.timings[t] = {}
         self.stats[t] = ctx.stats
-        for slot in DEFAULT_ORDER:
-            t0 = time.perf_counter()
-            rej = CHECKS[slot](store, self.c, ctx, bands)
-            timings[slot] = time.perf_counter() - t0
-            if rej is not None:
-                self.rejection = rej
-                return rej
+        with _collector_paused():
+            for slot in DEFAULT_ORDER:
+                t0 = time.perf_counter()
+                rej = CHECKS[slot](store, self.c, ctx, bands)
+                timings[slot] = time.perf_counter() - t0
+                if rej is not None:
+                    self.rejection = rej
+                    return rej
         self._last_step = t
         return None

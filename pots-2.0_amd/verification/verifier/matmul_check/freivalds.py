@@ -25,13 +25,14 @@ import math
 from collections.abc import Sequence
 from dataclasses import dataclass, replace
 
+import numpy as np
 import torch
 
 from verification.commitment import native
 from verification.verifier.matmul_check.challenges import SIGMA_R
 from verification.verifier.matmul_check.sizing import product_e_m
 
-__all__ = ["ROW", "MeasureScratch", "ProductMeasure", "band_unit", "finish_row",
+__all__ = ["ROW", "MeasureScratch", "ProductMeasure", "band_unit", "finish_row", "finish_rows",
            "measure_product", "measure_product_row", "measure_products",
            "measure_products_rows", "row_width", "term_scale", "term_scales",
            "measure_batch_rows"]
@@ -165,6 +166,40 @@ def finish_row(row: Sequence[float], *, q: int, n: int, eps_in: float, eps_acc: 
         u2 += n * bias_sq
     mp = _measure(nu, p_abs1, tuple(res), p_norm, q, eps_in, eps_acc, math.sqrt(u2))
     return mp if guard else replace(mp, kappa=math.nan)
+
+
+def finish_rows(rows: np.ndarray, *, q: Sequence[int], n: Sequence[int], eps_in: float,
+                eps_acc: float, guard: bool = True,
+                biased: Sequence[bool] | None = None) -> list[ProductMeasure]:
+    """:func:`finish_row` for every row of ``rows`` (fp64 ``[M, 5 + k]``) at once, with the
+    same IEEE operations in the same order on arrays, so every field equals
+    :func:`finish_row`'s bit for bit; one array pass instead of a Python loop per product."""
+    rows = np.asarray(rows, dtype=np.float64)
+    m = rows.shape[0]
+    qf = np.asarray(q, dtype=np.float64)
+    nf = np.asarray(n, dtype=np.float64)
+    nu, p_abs1, p_norm, u2, bias_sq = (rows[:, c] for c in range(5))
+    res = rows[:, 5:]
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        if biased is not None:
+            u2 = np.where(np.asarray(biased, dtype=bool), u2 + nf * bias_sq, u2)
+        u = np.sqrt(u2)
+        kappa = np.where(p_abs1 > 0, nu / p_abs1, np.where(nu == 0, 1.0, np.inf))
+        if not guard:
+            kappa = np.full(m, np.nan)
+        zero = p_norm == 0
+        # term_ratio: U/‖P‖_F, 1 when both are 0, inf when only ‖P‖_F is (NaN below 0)
+        ratio = np.where(zero, np.where(u == 0, 1.0, np.where(u > 0, np.inf, np.nan)),
+                         u / p_norm)
+        e = math.sqrt(2.0) * eps_in + np.sqrt(qf) * eps_acc * np.maximum(1.0, ratio)
+        e = np.where(np.isnan(ratio), np.nan, e)
+        unit = np.where(zero, SIGMA_R * np.sqrt(qf) * eps_acc * u, SIGMA_R * e * p_norm)
+        normalized = np.where(unit[:, None] > 0, res / unit[:, None],
+                              np.where(res == 0, 0.0, np.inf))
+    cols = (nu.tolist(), p_abs1.tolist(), kappa.tolist(), res.tolist(), p_norm.tolist(),
+            unit.tolist(), normalized.tolist(), u.tolist())
+    return [ProductMeasure(a, b, kp, tuple(r), pn, un, tuple(nz), uu)
+            for a, b, kp, r, pn, un, nz, uu in zip(*cols)]
 
 
 def band_unit(q: int, eps_in: float, eps_acc: float, p_norm: float, u: float) -> float:

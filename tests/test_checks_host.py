@@ -143,3 +143,40 @@ def test_nan_never_passes_a_band():
                     eps_acc=2.0**-24)
     rej = _judge_product(_C(), SPEC, mp, ctx, Bands.provisional())
     assert rej is not None and rej.check_id == "5" and "challenge j=2" in rej.detail
+
+
+def test_finish_rows_equals_finish_row_bit_for_bit():
+    """Check 5 finishes every row at once; each field must equal the per-row closed form,
+    including zeros of either sign, NaN, infinities and the biased and unguarded cases."""
+    import random
+
+    import numpy as np
+
+    from verification.verifier.matmul_check.freivalds import finish_row, finish_rows
+    rng = random.Random(0)
+    specials = [0.0, -0.0, 1e-300, 1e300, math.inf, math.nan, 1.0, 3.5e-8]
+
+    def val():
+        if rng.random() < 0.3:
+            return rng.choice(specials)
+        return rng.uniform(0, 10) * 10 ** rng.randint(-12, 6)
+
+    def same(a, b):
+        return (math.isnan(a) and math.isnan(b)) or \
+            (a == b and math.copysign(1, a) == math.copysign(1, b))
+
+    for k in (1, 4):
+        rows = [[val() for _ in range(5 + k)] for _ in range(600)]
+        q = [rng.randint(2, 20000) for _ in rows]
+        n = [rng.randint(1, 9000) for _ in rows]
+        biased = [rng.random() < 0.3 for _ in rows]
+        for guard in (True, False):
+            got = finish_rows(np.array(rows), q=q, n=n, eps_in=2.0**-8, eps_acc=2.0**-24,
+                              guard=guard, biased=biased)
+            for r, qq, nn, b, g in zip(rows, q, n, biased, got):
+                w = finish_row(r, q=qq, n=nn, eps_in=2.0**-8, eps_acc=2.0**-24, guard=guard,
+                               biased=b)
+                for f in ("nu", "p_abs1", "kappa", "p_norm", "unit", "u"):
+                    assert same(getattr(w, f), getattr(g, f)), (f, r, qq, nn, b)
+                assert all(same(x, y) for x, y in zip(w.residuals, g.residuals))
+                assert all(same(x, y) for x, y in zip(w.normalized, g.normalized))
