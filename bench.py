@@ -369,6 +369,111 @@ def prover_leg(widths=(4096, 8192, 8192, 4096), n_s: int = 2048, k: int = 2) -> 
             "verified": True}
 
 
+def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14) -> dict:
+    """A real training step of a Qwen2-1.5B-shaped model (transformers' Qwen2ForCausalLM,
+    random init, eager attention; ``layers`` of the 28 decoder layers) under the
+    device-resident capture: every matmul's output stays in HBM, and all of them are hashed
+    there as product leaves with the verifier's kernels. The model runs in fp32: the eager
+    attention's batched products and their backward take transposed right operands, which
+    bf16 batched products must not get on these GPUs. The reference copies each product to pinned host memory as it is made
+    (``_offload``) and hashes on the host; that copy is timed on a sample. The decoder's
+    labeling into canonical slots is not built, so the products are hashed in capture order:
+    this measures the capture and the in-place hashing, not a committed root."""
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from verification.commitment import native
+    from verification.commitment.encoding import TAG_PRODUCT, tensor_leaf_header
+    from verification.computation.matmul_ops import param_storage_map
+    from verification.prover.capture import MatmulCapture
+
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
+                      num_hidden_layers=layers, num_attention_heads=12, num_key_value_heads=2,
+                      max_position_embeddings=seq, tie_word_embeddings=True)
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = Qwen2ForCausalLM(cfg)
+    ids = torch.randint(0, cfg.vocab_size, (batch, seq), device="cuda")
+
+    def train(cap=None):
+        model.zero_grad(set_to_none=True)
+        if cap is None:
+            model(input_ids=ids, labels=ids).loss.backward()
+            return None
+        with cap:
+            with cap.phase("forward"):
+                loss = model(input_ids=ids, labels=ids).loss
+            with cap.phase("backward"):
+                loss.backward()
+        return cap
+
+    train()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    train()
+    torch.cuda.synchronize()
+    plain_ms = (time.perf_counter() - t0) * 1e3
+    cap = MatmulCapture(param_names=param_storage_map(model))
+    t0 = time.perf_counter()
+    train(cap)
+    torch.cuda.synchronize()
+    captured_ms = (time.perf_counter() - t0) * 1e3
+    cap.release_operands()
+    outs = [p for rec in cap.records for _, _, p in _members_of(rec)]
+    out_bytes = sum(p.numel() * p.element_size() for p in outs)
+    lib = native.get()
+    headers = [tensor_leaf_header(TAG_PRODUCT, p) for p in outs]
+    kinds = [native.FINITE_KIND[p.dtype] for p in outs]
+    plan = lib.leaf_plan(headers, [p.contiguous() for p in outs], kinds)
+    d, bad = plan.run()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(3):
+        d, bad = plan.run()
+    ev[1].record()
+    torch.cuda.synchronize()
+    hash_ms = ev[0].elapsed_time(ev[1]) / 3
+    assert int(bad.item()) == len(outs), "a captured product holds NaN or Inf"
+    # the reference's per-product copy to pinned host memory, on every 8th product
+    sample = outs[::8]
+    host = [torch.empty(p.shape, dtype=p.dtype, pin_memory=True) for p in sample]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for h, p in zip(host, sample):
+        h.copy_(p, non_blocking=True)
+    torch.cuda.synchronize()
+    d2h_s = time.perf_counter() - t0
+    d2h_gbps = sum(p.numel() * p.element_size() for p in sample) / d2h_s / 1e9
+    summary = cap.summary()
+    log(f"[bench] qwen2 capture leg: step {plain_ms:.0f} ms, under capture {captured_ms:.0f} "
+        f"ms; {len(outs)} products ({summary['n_calls']} calls), {out_bytes / 1e9:.2f} GB in "
+        f"HBM, hashed in {hash_ms:.2f} ms ({out_bytes / (hash_ms * 1e-3) / 1e9:.0f} GB/s); the "
+        f"host copy it avoids runs at {d2h_gbps:.1f} GB/s ({out_bytes / d2h_gbps / 1e9:.2f} s "
+        f"for all of them)")
+    return {"model": f"Qwen2-1.5B-shaped, {layers} of 28 layers (transformers "
+                     f"Qwen2ForCausalLM, random init, fp32, eager attention), {batch}x{seq} "
+                     "tokens",
+            "training_step_ms": round(plain_ms, 1), "captured_step_ms": round(captured_ms, 1),
+            "products": len(outs), "calls": summary["n_calls"],
+            "glue_outer_products": summary["n_glue_outer_products"],
+            "product_bytes": out_bytes, "hash_ms": round(hash_ms, 3),
+            "hash_gbps": round(out_bytes / (hash_ms * 1e-3) / 1e9, 1),
+            "avoided_d2h_gbps": round(d2h_gbps, 1),
+            "avoided_d2h_s": round(out_bytes / d2h_gbps / 1e9, 3),
+            "note": "capture order; the decoder's labeling is not built"}
+
+
+def _members_of(rec):
+    """``(A_i, B_i, P_i)`` of a record after its operands were released: the outputs only."""
+    if rec.batch is None:
+        yield None, None, rec.out
+    else:
+        for i in range(rec.batch):
+            yield None, None, rec.out[i]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -392,9 +497,12 @@ def main() -> int:
                     help="also write the transcript under DIR in the on-disk store's format "
                          "(with the captured operands), load it back into HBM with the native "
                          "loader, verify the loaded copy, report parts.disk_load, and delete it")
-    ap.add_argument("--prover-leg", action="store_true",
-                    help="also prove one MLP step on the GPU (capture, labeling, SGD), commit "
-                         "it in HBM, verify it with the replay, and report parts.prover")
+    ap.add_argument("--prover-leg", nargs="?", const="mlp", choices=("mlp", "qwen2"),
+                    help="also run the device-resident prover and report parts.prover: 'mlp' "
+                         "proves an MLP step (capture, labeling, SGD), commits it in HBM and "
+                         "verifies it with the replay; 'qwen2' captures a Qwen2-1.5B-shaped "
+                         "training step (random init, fp32, 14 of 28 layers, 4x2048 tokens) "
+                         "and hashes every captured product in HBM")
     ap.add_argument("--counter-summary", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSV output under DIR and exit")
     ap.add_argument("--trace-summary", metavar="DIR",
@@ -618,8 +726,10 @@ def main() -> int:
     }
     if args.disk_leg:
         out["parts"]["disk_load"] = disk_leg(Path(args.disk_leg), c, step, k, claimed_b, v)
-    if args.prover_leg:
+    if args.prover_leg == "mlp":
         out["parts"]["prover"] = prover_leg()
+    elif args.prover_leg == "qwen2":
+        out["parts"]["prover"] = capture_leg_qwen2()
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")
         out["cpu_baseline"] = cpu_baseline(step, items)
