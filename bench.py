@@ -420,7 +420,7 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14) -> dict
     torch.cuda.synchronize()
     captured_ms = (time.perf_counter() - t0) * 1e3
     cap.release_operands()
-    outs = [p for rec in cap.records for _, _, p in _members_of(rec)]
+    outs = [p for rec in cap.records for p in _outputs_of(rec)]
     out_bytes = sum(p.numel() * p.element_size() for p in outs)
     lib = native.get()
     headers = [tensor_leaf_header(TAG_PRODUCT, p) for p in outs]
@@ -465,13 +465,9 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14) -> dict
             "note": "capture order; the decoder's labeling is not built"}
 
 
-def _members_of(rec):
-    """``(A_i, B_i, P_i)`` of a record after its operands were released: the outputs only."""
-    if rec.batch is None:
-        yield None, None, rec.out
-    else:
-        for i in range(rec.batch):
-            yield None, None, rec.out[i]
+def _outputs_of(rec) -> list:
+    """The checked products of a capture record: its output, or each batch member's."""
+    return [rec.out] if rec.batch is None else [rec.out[i] for i in range(rec.batch)]
 
 
 def main() -> int:
