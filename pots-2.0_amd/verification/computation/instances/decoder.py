@@ -10,6 +10,13 @@ Per layer: the q/k/v projections (with biases for Qwen2), ``n_s·n_h`` members e
 ``S = Q·Kᵀ`` and ``O = A·V``, then o/gate/up/down; the head ``Λ = X·W_outᵀ`` in ``B`` row
 blocks; then backward, layers in reverse: input and weight gradients of down/gate/up/o, the
 members' ``dA, dV`` and ``dQ, dK``, and the input and weight gradients of q/k/v.
+
+The prover side (:meth:`DecoderComputation.build_model`, :meth:`~DecoderComputation.loss`,
+:meth:`~DecoderComputation.label_with_operands`) runs transformers' Llama/Qwen2 causal LM with
+eager attention, one head block, in the computation's dtype, and maps the captured records onto
+the slots above by operand identity (reference decoder.py:774-1100, for the cases this build
+takes: one head block, no autocast). The replay that rebuilds the operands from the leaves is
+not built: the labeler returns the captured operands with the products.
 """
 
 from __future__ import annotations
@@ -18,7 +25,8 @@ from functools import cached_property
 
 import torch
 
-from verification.computation.interface import DeclaredComputation, ProductKind, ProductSpec
+from verification.computation.interface import (DeclaredComputation, LabelingError,
+                                               ProductKind, ProductSpec)
 
 LINEARS = ("q", "k", "v", "o", "gate", "up", "down")
 _LINEAR_PATH = {
@@ -212,6 +220,170 @@ class DecoderComputation(DeclaredComputation):
 
     def product_class(self, spec: ProductSpec) -> str:
         return self._inventory[1][spec.m - 1]
+
+    # ---- prover side ----------------------------------------------------------------------
+
+    def build_model(self) -> torch.nn.Module:
+        """transformers' causal LM of this shape (Qwen2 with q/k/v biases, else Llama), eager
+        attention, random init, in the computation's dtype on the current default device."""
+        from transformers import LlamaConfig, LlamaForCausalLM, Qwen2Config, Qwen2ForCausalLM
+        cfg_cls, model_cls = (Qwen2Config, Qwen2ForCausalLM) if self.qkv_bias else \
+            (LlamaConfig, LlamaForCausalLM)
+        cfg = cfg_cls(vocab_size=self.n_v, hidden_size=self.d, intermediate_size=self.d_f,
+                      num_hidden_layers=self.L, num_attention_heads=self.n_h,
+                      num_key_value_heads=self.n_kv, head_dim=self.d_h,
+                      max_position_embeddings=max(self.n, 16), tie_word_embeddings=self.tied)
+        if not self.qkv_bias:
+            cfg.attention_bias = False
+            cfg.mlp_bias = False
+        cfg._attn_implementation = "eager"
+        if self.head_blocks != 1:
+            raise NotImplementedError("the prover side takes one head block")
+        return model_cls(cfg).to(self.compute_dtype)
+
+    def loss(self, model: torch.nn.Module, records) -> torch.Tensor:
+        """Mean cross-entropy of the targets over the masked tokens."""
+        dev = next(model.parameters()).device
+        ids = torch.stack([r.ids for r in records]).to(device=dev, dtype=torch.long)
+        targets = torch.stack([r.targets for r in records]).to(device=dev, dtype=torch.long)
+        mask = torch.stack([r.mask for r in records]).to(device=dev, dtype=torch.float32)
+        logits = model(input_ids=ids).logits.float()
+        ce = torch.nn.functional.cross_entropy(logits.reshape(-1, self.n_v),
+                                               targets.reshape(-1), reduction="none")
+        return (ce * mask.reshape(-1)).sum() / mask.sum()
+
+    def label(self, capture, model: torch.nn.Module) -> list[torch.Tensor]:
+        return self.label_with_operands(capture, model)[0]
+
+    def label_with_operands(self, capture, model: torch.nn.Module
+                            ) -> tuple[list[torch.Tensor], dict[int, tuple[torch.Tensor,
+                                                                           torch.Tensor]]]:
+        """``(P_1..P_M, {m: (A_m, B_m)})`` from the capture, mapped by operand identity.
+
+        Forward: a linear's ``B`` views its weight; the two batched products after layer
+        ``ℓ``'s v projection are ``S`` then ``O``; the head's ``B`` views ``W_out``. Backward:
+        an input gradient's ``B`` is the weight itself; a weight gradient's output is the
+        weight's ``.grad`` (the tied head's, whose ``.grad`` also holds the embedding's share,
+        is the product whose ``B`` is the head's input); ``dA`` reads ``O``'s ``B``, ``dV``
+        ``O``'s ``A``, ``dQ`` ``S``'s ``B``, and the batched product reading ``S``'s ``A`` is
+        ``K̃``'s gradient ``Q̃ᵀ·δS``, whose transpose is the ``dK`` leaf with operands
+        ``(δSᵀ, Q̃)``.
+        """
+        if len(capture.glue_outer) > 1:
+            raise LabelingError(f"{len(capture.glue_outer)} q=1 products; only the rotary "
+                                f"table's is expected")
+        by_weight = {self.w(l, x): (l, x) for l in range(1, self.L + 1) for x in LINEARS}
+        slots: dict[str, tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = {}
+        spec_by_name = {s.name: s for s in self.products}
+
+        def fill(name, a, b, p):
+            if name in slots:
+                raise LabelingError(f"slot {name} filled twice")
+            spec = spec_by_name.get(name)
+            if spec is None:
+                raise LabelingError(f"no declared slot {name}")
+            got = (tuple(a.shape), tuple(b.shape), tuple(p.shape))
+            want = (spec.a_shape, spec.b_shape, spec.p_shape)
+            if got != want:
+                raise LabelingError(f"{name}: shapes {got} != declared {want}")
+            slots[name] = (a, b, p)
+
+        def members(role, l, rec, transpose_out=False):
+            if rec.batch != self.n_s * self.n_h:
+                raise LabelingError(f"L{l}.{role}: a batch of {rec.batch}, expected "
+                                    f"{self.n_s * self.n_h}")
+            for i in range(rec.batch):
+                s_, h = divmod(i, self.n_h)
+                a, b, p = rec.a[i], rec.b[i], rec.out[i]
+                if transpose_out:  # K̃'s gradient Q̃ᵀ·δS: the leaf is (δSᵀ·Q̃)
+                    a, b, p = rec.b[i].transpose(0, 1), rec.a[i].transpose(0, 1), \
+                        rec.out[i].transpose(0, 1).contiguous()
+                fill(f"L{l}.{role}[{s_},{h}]", a, b, p)
+
+        fwd = [r for r in capture.records if r.phase == "forward"]
+        bwd = [r for r in capture.records if r.phase == "backward"]
+        if any(r.a is None for r in capture.records):
+            raise LabelingError("the capture's operands were released before labeling")
+        s_rec: dict[int, object] = {}
+        o_rec: dict[int, object] = {}
+        head_in = None
+        layer = None
+        pending = []
+        for rec in fwd:
+            name = rec.b_info.param_name
+            if rec.batch is not None:
+                if layer is None:
+                    raise LabelingError(f"batched record #{rec.index} before any layer")
+                pending.append(rec)
+                if len(pending) == 1:
+                    s_rec[layer] = rec
+                elif len(pending) == 2:
+                    o_rec[layer] = rec
+                else:
+                    raise LabelingError(f"layer {layer}: more than two forward batched products")
+                continue
+            if name in by_weight:
+                l, x = by_weight[name]
+                if x == "q":
+                    layer, pending = l, []
+                fill(f"L{l}.Y_{x}", rec.a, rec.b, rec.out)
+            elif name == self.w_out and rec.out.shape[-1] == self.n_v:
+                head_in = rec.a
+                fill(self.head_name("Lambda", 0), rec.a, rec.b, rec.out)
+            else:
+                raise LabelingError(f"forward record #{rec.index} matches no slot")
+        for l in range(1, self.L + 1):
+            if l not in s_rec or l not in o_rec:
+                raise LabelingError(f"layer {l}: the attention products were not seen")
+            members("S", l, s_rec[l])
+            members("O", l, o_rec[l])
+
+        def storage(t):
+            return t.untyped_storage().data_ptr()
+
+        s_a = {storage(s_rec[l].a): l for l in s_rec}
+        s_b = {storage(s_rec[l].b): l for l in s_rec}
+        o_a = {storage(o_rec[l].a): l for l in o_rec}
+        o_b = {storage(o_rec[l].b): l for l in o_rec}
+        grad_owner = {prm.grad.untyped_storage().data_ptr(): n
+                      for n, prm in model.named_parameters() if prm.grad is not None}
+        for rec in bwd:
+            name = rec.b_info.param_name
+            if rec.batch is not None:
+                a_st, b_st = storage(rec.a), storage(rec.b)
+                if b_st in o_b:
+                    members("dA", o_b[b_st], rec)
+                elif a_st in o_a:
+                    members("dV", o_a[a_st], rec)
+                elif b_st in s_b:
+                    members("dQ", s_b[b_st], rec)
+                elif a_st in s_a:
+                    members("dK", s_a[a_st], rec, transpose_out=True)
+                else:
+                    raise LabelingError(f"backward batched record #{rec.index} matches no slot")
+                continue
+            if name in by_weight:
+                l, x = by_weight[name]
+                fill(f"L{l}.dX_{x}", rec.a, rec.b, rec.out)
+            elif name == self.w_out:
+                fill(self.head_name("dF", 0), rec.a, rec.b, rec.out)
+            else:
+                owner = grad_owner.get(rec.out_info.storage_ptr)
+                if owner in by_weight and capture.is_output_of(
+                        model.get_parameter(owner).grad, rec):
+                    l, x = by_weight[owner]
+                    fill(f"L{l}.G_{x}", rec.a, rec.b, rec.out)
+                elif head_in is not None and storage(rec.b) == storage(head_in) and \
+                        rec.out.shape == (self.n_v, self.d):
+                    fill(self.head_name("G", 0), rec.a, rec.b, rec.out)
+                else:
+                    raise LabelingError(f"backward record #{rec.index} matches no slot")
+        missing = [s.name for s in self.products if s.name not in slots]
+        if missing:
+            raise LabelingError(f"{len(missing)} slots never filled, e.g. {missing[:3]}")
+        products = [slots[s.name][2] for s in self.products]
+        operands = {s.m: slots[s.name][:2] for s in self.products}
+        return products, operands
 
 
 # The configurations the benchmark and the tests use (BASELINE.json's configs).

@@ -56,6 +56,13 @@ class StepOutput:
     loss: float
     versions: tuple[int, ...] = field(repr=False)
     capture: dict = field(default_factory=dict, repr=False)
+    # {m: (A_m, B_m)} as captured, when prove_step was asked to keep them
+    operands: dict = field(default_factory=dict, repr=False)
+
+    def replay(self):
+        """The kept operands as check 5's operand source."""
+        from verification.prover.synthetic import CapturedReplay
+        return CapturedReplay(self.operands)
 
     def leaves(self) -> list[Any]:
         return [*self.records, *self.w_t.values(), *self.products, *self.w_next.values()]
@@ -85,13 +92,15 @@ def _w_t_leaves(c: DeclaredComputation, model: torch.nn.Module,
 
 
 def prove_step(c: DeclaredComputation, model: torch.nn.Module, w_t: Mapping[str, torch.Tensor],
-               records: Sequence[Any], *, perturb: Mapping[int, Perturbation] | None = None
-               ) -> StepOutput:
+               records: Sequence[Any], *, perturb: Mapping[int, Perturbation] | None = None,
+               keep_operands: bool = False) -> StepOutput:
     """Run ``C(b, W_t)`` on ``model`` and emit the step's leaves.
 
     ``model`` is loaded with ``w_t`` and left holding ``W_{t+1}`` with its gradients cleared.
     ``perturb`` (``{m: fn}``) replaces committed product ``P_m`` by ``fn(copy of P_m)`` after
     the capture, a prover-side cheat for tests; training uses the true gradients.
+    ``keep_operands`` keeps every product's captured ``(A_m, B_m)`` (the computation's
+    ``label_with_operands``), for a computation whose replay is not built.
     """
     if len(records) != c.n_s:
         raise ValueError(f"batch has {len(records)} records, the computation declares {c.n_s}")
@@ -113,7 +122,22 @@ def prove_step(c: DeclaredComputation, model: torch.nn.Module, w_t: Mapping[str,
 
     with cap:
         loss = c.forward_backward(model, records, stage)
-    products = [p.detach() for p in c.label(cap, model)]
+    operands: dict = {}
+    if keep_operands:
+        labeled, captured = c.label_with_operands(cap, model)
+
+        def held(t: torch.Tensor) -> torch.Tensor:
+            # An operand that views a parameter (a linear's W.t(), an input gradient's W)
+            # would see the SGD step: it is served from the committed W_t leaf instead.
+            name = cap.param_of(t)
+            if name is not None and name in w_t_leaves:
+                return w_t_leaves[name].as_strided(t.shape, t.stride(), t.storage_offset())
+            return t.detach()
+
+        operands = {m: (held(a), held(b)) for m, (a, b) in captured.items()}
+    else:
+        labeled = c.label(cap, model)
+    products = [p.detach() for p in labeled]
     if len(products) != c.M:
         raise RuntimeError(f"label returned {len(products)} products, M = {c.M}")
     cap.assert_unmodified()
@@ -138,7 +162,7 @@ def prove_step(c: DeclaredComputation, model: torch.nn.Module, w_t: Mapping[str,
         loss=float(loss.detach()),
         versions=(record_versions + w_t_versions + tuple(product_versions)
                   + _versions(list(w_next.values()))),
-        capture=summary)
+        capture=summary, operands=operands)
 
 
 def commit(c: DeclaredComputation, step: StepOutput):

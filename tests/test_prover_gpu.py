@@ -108,3 +108,65 @@ def test_stored_mlp_step_verifies_from_disk(lib, tmp_path):
     assert res.fallback == 0  # records are plain tensor leaves here
     for store in (disk, ResidentStore(disk, res)):
         assert Verifier(c, k=2).verify_step(1, store) is None
+
+
+def _decoder_prove(seed=0, qkv_bias=True, n_kv=2, perturb=None):
+    from setup.records import Record
+    from verification.computation.instances.decoder import DecoderComputation
+    from verification.computation.interface import snapshot_weights
+    from verification.prover.step import commit, prove_step
+    c = DecoderComputation(L=2, d=128, d_f=256, n_h=4, n_kv=n_kv, n_v=320, n_s=2, n=64,
+                           qkv_bias=qkv_bias, compute_dtype=torch.float32)
+    torch.manual_seed(seed)
+    with torch.device("cuda"):
+        model = c.build_model()
+    w0 = snapshot_weights(c, model)
+    g = torch.Generator().manual_seed(seed + 1)
+    records = []
+    for _ in range(c.n_s):
+        ids = torch.randint(0, c.n_v, (c.n,), generator=g, dtype=torch.int32)
+        records.append(Record(ids, torch.roll(ids, -1), torch.ones(c.n, dtype=torch.int32)))
+    step = prove_step(c, model, w0, records, keep_operands=True, perturb=perturb)
+    c.use_operands(step.replay())
+    return c, step, commit(c, step)
+
+
+def _decoder_oracle_root(c, leaves):
+    hashes = []
+    for i, obj in enumerate(leaves):
+        if i < c.n_s:
+            hashes.append(O.hash_leaf(O.encode_record(obj.ids, obj.targets, obj.mask)))
+        else:
+            tag = O.TAG_PRODUCT if c.n_s + c.n_w <= i < c.n_s + c.n_w + c.M else O.TAG_WEIGHT
+            hashes.append(O.tensor_leaf_hash(tag, obj.cpu()))
+    return O.merkle_root(hashes)
+
+
+@pytest.mark.parametrize("qkv_bias,n_kv", [(True, 2), (False, 4)])
+def test_real_decoder_step_commits_and_verifies(lib, qkv_bias, n_kv):
+    """A transformers Qwen2/Llama training step proved on the GPU: the products stay in HBM,
+    the device commit equals the CPU oracle's root, and the verifier accepts the step with the
+    captured operands through the check-level API and the device step alike."""
+    from verification.transcript.store import InMemoryStore
+    from verification.verifier.driver import Verifier
+    from verification.verifier.step import DeviceStepVerifier
+    c, step, tree = _decoder_prove(seed=7, qkv_bias=qkv_bias, n_kv=n_kv)
+    assert step.capture["device_resident"]
+    assert tree.root == _decoder_oracle_root(c, step.leaves())
+    v = Verifier(c, k=2)
+    assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
+    assert len(v.stats[1].products) == c.M
+    out = DeviceStepVerifier(c, step.leaves(), lambda s: step.operands[s.m], k=2).run(tree.root)
+    assert out.check is None and out.root == tree.root, out.detail
+
+
+def test_real_decoder_step_with_a_changed_member_rejects_at_check_5(lib):
+    from verification.transcript.store import InMemoryStore
+    from verification.verifier.driver import Verifier
+    c0, _, _ = _decoder_prove(seed=8)
+    spec = next(s for s in c0.products if s.name == "L2.O[1,3]")
+    c, step, tree = _decoder_prove(seed=8, perturb={spec.m: lambda p: p.index_add_(
+        0, torch.tensor([5], device=p.device), torch.full_like(p[:1], 0.5))})
+    rej = Verifier(c, k=2).verify_step(1, InMemoryStore(step.leaves(), tree))
+    assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
+    assert rej.detail.startswith(f"P_{spec.m} (L2.O[1,3])")

@@ -172,3 +172,45 @@ def test_replay_operands_reproduce_every_product():
     for spec in reversed(c.products):
         a, b = again.operands(spec.m)
         assert torch.equal(torch.mm(a, b), step.products[spec.m - 1]), spec.name
+
+
+def _decoder_step(qkv_bias=True, n_kv=2):
+    from setup.records import Record
+    from verification.computation.instances.decoder import DecoderComputation
+    from verification.computation.interface import snapshot_weights
+    c = DecoderComputation(L=2, d=64, d_f=128, n_h=4, n_kv=n_kv, n_v=160, n_s=2, n=16,
+                           qkv_bias=qkv_bias, compute_dtype=torch.float32)
+    torch.manual_seed(0)
+    model = c.build_model()
+    w0 = snapshot_weights(c, model)
+    g = torch.Generator().manual_seed(1)
+    records = []
+    for _ in range(c.n_s):
+        ids = torch.randint(0, c.n_v, (c.n,), generator=g, dtype=torch.int32)
+        records.append(Record(ids, torch.roll(ids, -1), torch.ones(c.n, dtype=torch.int32)))
+    return c, w0, prove_step(c, model, w0, records, keep_operands=True)
+
+
+@pytest.mark.parametrize("qkv_bias,n_kv", [(True, 2), (False, 4)])
+def test_decoder_labeling_fills_every_slot_with_its_own_product(qkv_bias, n_kv):
+    """A transformers Qwen2 (biased q/k/v, grouped KV heads) or Llama step under the capture:
+    every declared slot is filled, and each product equals its captured operands' product
+    (bit for bit where the op itself computed it, 1e-5 for the transposed dK leaves and the
+    biased forward linears)."""
+    c, w0, step = _decoder_step(qkv_bias, n_kv)
+    assert len(step.products) == c.M and step.capture["n_glue_outer_calls"] == 1
+    for spec in c.products:
+        a, b = step.operands[spec.m]
+        p = step.products[spec.m - 1]
+        assert (tuple(a.shape), tuple(b.shape)) == (spec.a_shape, spec.b_shape), spec.name
+        q = torch.mm(a, b)
+        if spec.bias is not None:
+            q = q + w0[spec.bias]
+        if ".dK[" in spec.name or spec.bias is not None:
+            assert torch.allclose(q, p, rtol=1e-5, atol=1e-6), spec.name
+        else:
+            assert torch.equal(q, p), spec.name
+    # a linear weight's update is its committed weight gradient's SGD step
+    name = c.w(1, "up")
+    g = step.products[c.product_index(c.linear_weights[name][0]) - c.n_s - c.n_w]
+    assert torch.allclose(step.w_next[name], w0[name] - c.eta * g, rtol=0, atol=1e-7)
