@@ -369,105 +369,98 @@ def prover_leg(widths=(4096, 8192, 8192, 4096), n_s: int = 2048, k: int = 2) -> 
             "verified": True}
 
 
-def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14) -> dict:
-    """A real training step of a Qwen2-1.5B-shaped model (transformers' Qwen2ForCausalLM,
-    random init, eager attention; ``layers`` of the 28 decoder layers) under the
-    device-resident capture: every matmul's output stays in HBM, and all of them are hashed
-    there as product leaves with the verifier's kernels. The model runs in fp32: the eager
-    attention's batched products and their backward take transposed right operands, which
-    bf16 batched products must not get on these GPUs. The reference copies each product to pinned host memory as it is made
-    (``_offload``) and hashes on the host; that copy is timed on a sample. The decoder's
-    labeling into canonical slots is not built, so the products are hashed in capture order:
-    this measures the capture and the in-place hashing, not a committed root."""
+def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int = 4) -> dict:
+    """A real training step of a Qwen2-1.5B-shaped model, proved, committed and verified on
+    the GPU: transformers' Qwen2ForCausalLM at C4's shapes (``layers`` of the 28 decoder
+    layers, random init, eager attention) runs under the device-resident capture; the products
+    are labeled into the declared computation's canonical slots, SGD steps the weights, every
+    leaf is hashed in HBM, and the device step verifier checks the step with the captured
+    operands. The model runs in fp32: the eager attention's batched products and their
+    backward take transposed right operands, which bf16 batched products must not get on
+    these GPUs. The reference copies each product to pinned host memory as it is made
+    (``_offload``) and hashes on the host; that copy is timed on a sample."""
     import torch
-    from transformers import Qwen2Config, Qwen2ForCausalLM
 
-    from verification.commitment import native
-    from verification.commitment.encoding import TAG_PRODUCT, tensor_leaf_header
-    from verification.computation.matmul_ops import param_storage_map
-    from verification.prover.capture import MatmulCapture
+    from setup.records import Record
+    from verification.computation.instances.decoder import DecoderComputation
+    from verification.computation.interface import snapshot_weights
+    from verification.prover.step import commit, prove_step
+    from verification.verifier.step import DeviceStepVerifier
 
-    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
-                      num_hidden_layers=layers, num_attention_heads=12, num_key_value_heads=2,
-                      max_position_embeddings=seq, tie_word_embeddings=True)
-    cfg._attn_implementation = "eager"
+    c = DecoderComputation(L=layers, d=1536, d_f=8960, n_h=12, n_kv=2, n_v=151936, n_s=batch,
+                           n=seq, d_h=128, tied=True, qkv_bias=True,
+                           compute_dtype=torch.float32)
     torch.manual_seed(0)
     with torch.device("cuda"):
-        model = Qwen2ForCausalLM(cfg)
-    ids = torch.randint(0, cfg.vocab_size, (batch, seq), device="cuda")
+        model = c.build_model()
+    w0 = snapshot_weights(c, model)
+    g = torch.Generator().manual_seed(1)
+    records = []
+    for _ in range(batch):
+        ids = torch.randint(0, c.n_v, (seq,), generator=g, dtype=torch.int32)
+        records.append(Record(ids, torch.roll(ids, -1), torch.ones(seq, dtype=torch.int32)))
 
-    def train(cap=None):
+    def plain():
+        from verification.computation.interface import load_weights
+        load_weights(c, model, w0)
         model.zero_grad(set_to_none=True)
-        if cap is None:
-            model(input_ids=ids, labels=ids).loss.backward()
-            return None
-        with cap:
-            with cap.phase("forward"):
-                loss = model(input_ids=ids, labels=ids).loss
-            with cap.phase("backward"):
-                loss.backward()
-        return cap
+        c.loss(model, records).backward()
 
-    train()
+    for _ in range(2):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        plain()
+        torch.cuda.synchronize()
+        plain_ms = (time.perf_counter() - t0) * 1e3
+    model.zero_grad(set_to_none=True)
+    t0 = time.perf_counter()
+    step = prove_step(c, model, w0, records, keep_operands=True)
+    torch.cuda.synchronize()
+    prove_ms = (time.perf_counter() - t0) * 1e3
+    t0 = time.perf_counter()
+    tree = commit(c, step)
+    torch.cuda.synchronize()
+    commit_ms = (time.perf_counter() - t0) * 1e3
+    leaves = step.leaves()
+    leaf_bytes = sum(x.nbytes for x in leaves[c.n_s:])
+    product_bytes = sum(p.nbytes for p in step.products)
+    t0 = time.perf_counter()
+    v = DeviceStepVerifier(c, leaves, lambda s: step.operands[s.m], k=k)
+    torch.cuda.synchronize()
+    setup_ms = (time.perf_counter() - t0) * 1e3
+    verdict = v.run(tree.root)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    train()
+    verdict = v.run(tree.root)
     torch.cuda.synchronize()
-    plain_ms = (time.perf_counter() - t0) * 1e3
-    cap = MatmulCapture(param_names=param_storage_map(model))
-    t0 = time.perf_counter()
-    train(cap)
-    torch.cuda.synchronize()
-    captured_ms = (time.perf_counter() - t0) * 1e3
-    cap.release_operands()
-    outs = [p for rec in cap.records for p in _outputs_of(rec)]
-    out_bytes = sum(p.numel() * p.element_size() for p in outs)
-    lib = native.get()
-    headers = [tensor_leaf_header(TAG_PRODUCT, p) for p in outs]
-    kinds = [native.FINITE_KIND[p.dtype] for p in outs]
-    plan = lib.leaf_plan(headers, [p.contiguous() for p in outs], kinds)
-    d, bad = plan.run()
-    torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-    ev[0].record()
-    for _ in range(3):
-        d, bad = plan.run()
-    ev[1].record()
-    torch.cuda.synchronize()
-    hash_ms = ev[0].elapsed_time(ev[1]) / 3
-    assert int(bad.item()) == len(outs), "a captured product holds NaN or Inf"
+    verify_ms = (time.perf_counter() - t0) * 1e3
+    assert verdict.check is None and verdict.root == tree.root, verdict.detail
     # the reference's per-product copy to pinned host memory, on every 8th product
-    sample = outs[::8]
+    sample = list(step.products[::8])
     host = [torch.empty(p.shape, dtype=p.dtype, pin_memory=True) for p in sample]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for h, p in zip(host, sample):
         h.copy_(p, non_blocking=True)
     torch.cuda.synchronize()
-    d2h_s = time.perf_counter() - t0
-    d2h_gbps = sum(p.numel() * p.element_size() for p in sample) / d2h_s / 1e9
-    summary = cap.summary()
-    log(f"[bench] qwen2 capture leg: step {plain_ms:.0f} ms, under capture {captured_ms:.0f} "
-        f"ms; {len(outs)} products ({summary['n_calls']} calls), {out_bytes / 1e9:.2f} GB in "
-        f"HBM, hashed in {hash_ms:.2f} ms ({out_bytes / (hash_ms * 1e-3) / 1e9:.0f} GB/s); the "
-        f"host copy it avoids runs at {d2h_gbps:.1f} GB/s ({out_bytes / d2h_gbps / 1e9:.2f} s "
-        f"for all of them)")
+    d2h_gbps = sum(p.nbytes for p in sample) / (time.perf_counter() - t0) / 1e9
+    summary = step.capture
+    log(f"[bench] qwen2 prover leg: training step {plain_ms:.0f} ms, proved (capture, "
+        f"labeling, SGD) {prove_ms:.0f} ms; {c.M} products ({summary['n_calls']} calls), "
+        f"{product_bytes / 1e9:.2f} GB in HBM; commit of {leaf_bytes / 1e9:.2f} GB "
+        f"{commit_ms:.0f} ms (root {tree.root.hex()[:16]}…); verifier plans {setup_ms:.0f} ms, "
+        f"verify {verify_ms:.1f} ms (accepted); the host copy it avoids runs at "
+        f"{d2h_gbps:.1f} GB/s ({product_bytes / d2h_gbps / 1e9:.2f} s for the products)")
     return {"model": f"Qwen2-1.5B-shaped, {layers} of 28 layers (transformers "
                      f"Qwen2ForCausalLM, random init, fp32, eager attention), {batch}x{seq} "
                      "tokens",
-            "training_step_ms": round(plain_ms, 1), "captured_step_ms": round(captured_ms, 1),
-            "products": len(outs), "calls": summary["n_calls"],
-            "glue_outer_products": summary["n_glue_outer_products"],
-            "product_bytes": out_bytes, "hash_ms": round(hash_ms, 3),
-            "hash_gbps": round(out_bytes / (hash_ms * 1e-3) / 1e9, 1),
+            "k": k, "products": c.M, "calls": summary["n_calls"],
+            "product_bytes": product_bytes, "leaf_bytes": leaf_bytes,
+            "training_step_ms": round(plain_ms, 1), "prove_step_ms": round(prove_ms, 1),
+            "commit_ms": round(commit_ms, 1), "verifier_setup_ms": round(setup_ms, 1),
+            "verify_ms": round(verify_ms, 2), "verified": True,
             "avoided_d2h_gbps": round(d2h_gbps, 1),
-            "avoided_d2h_s": round(out_bytes / d2h_gbps / 1e9, 3),
-            "note": "capture order; the decoder's labeling is not built"}
-
-
-def _outputs_of(rec) -> list:
-    """The checked products of a capture record: its output, or each batch member's."""
-    return [rec.out] if rec.batch is None else [rec.out[i] for i in range(rec.batch)]
+            "avoided_d2h_s": round(product_bytes / d2h_gbps / 1e9, 3)}
 
 
 def main() -> int:
@@ -496,9 +489,9 @@ def main() -> int:
     ap.add_argument("--prover-leg", nargs="?", const="mlp", choices=("mlp", "qwen2"),
                     help="also run the device-resident prover and report parts.prover: 'mlp' "
                          "proves an MLP step (capture, labeling, SGD), commits it in HBM and "
-                         "verifies it with the replay; 'qwen2' captures a Qwen2-1.5B-shaped "
-                         "training step (random init, fp32, 14 of 28 layers, 4x2048 tokens) "
-                         "and hashes every captured product in HBM")
+                         "verifies it with the replay; 'qwen2' proves a Qwen2-1.5B-shaped "
+                         "training step (transformers, random init, fp32, 14 of 28 layers, "
+                         "4x2048 tokens), commits it in HBM and verifies it")
     ap.add_argument("--counter-summary", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSV output under DIR and exit")
     ap.add_argument("--trace-summary", metavar="DIR",
