@@ -170,3 +170,34 @@ def test_real_decoder_step_with_a_changed_member_rejects_at_check_5(lib):
     rej = Verifier(c, k=2).verify_step(1, InMemoryStore(step.leaves(), tree))
     assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
     assert rej.detail.startswith(f"P_{spec.m} (L2.O[1,3])")
+
+
+def test_c1_real_smollm2_step_proves_commits_and_verifies(lib):
+    """BASELINE config 0 as specified: a SmolLM2-135M-shaped Llama (30 layers, d 576, 9/3
+    heads of dim 64, MLP 1536, vocab 49152, tied; random-init fp32), one plain-SGD step at lr
+    1e-4 on 4 x 256 random token ids, every matmul captured, the transcript committed (root
+    checked against the CPU oracle) and verified with k = 1."""
+    from setup.records import Record
+    from verification.computation.instances.decoder import smollm2_135m
+    from verification.computation.interface import snapshot_weights
+    from verification.prover.step import commit, prove_step
+    from verification.transcript.store import InMemoryStore
+    from verification.verifier.driver import Verifier
+    c = smollm2_135m()
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = c.build_model()
+    w0 = snapshot_weights(c, model)
+    g = torch.Generator().manual_seed(0)
+    records = []
+    for _ in range(c.n_s):
+        ids = torch.randint(0, c.n_v, (c.n,), generator=g, dtype=torch.int32)
+        records.append(Record(ids, torch.roll(ids, -1), torch.ones(c.n, dtype=torch.int32)))
+    step = prove_step(c, model, w0, records, keep_operands=True)
+    assert len(step.products) == c.M == 7113
+    tree = commit(c, step)
+    assert tree.root == _decoder_oracle_root(c, step.leaves())
+    c.use_operands(step.replay())
+    v = Verifier(c, k=1)
+    assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
+    assert len(v.stats[1].products) == c.M and v.stats[1].max_normalized() <= 8.0
