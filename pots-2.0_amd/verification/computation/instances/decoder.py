@@ -1,10 +1,11 @@
-"""The Llama/Qwen2 decoder's declared computation: leaf layout and product inventory only.
+"""The Llama/Qwen2 decoder's declared computation: leaf layout, product inventory and the
+prover's labeling.
 
 Reference: verification/computation/instances/decoder.py:154-160 (``matmul_count_decoder``),
 :320-400 (weight names and shapes) and :416-471 (``_inventory``). The order of weights and
 products, their shapes and their κ classes follow the reference exactly, since they fix which
-leaf is which and what challenge width each product gets. The model itself (HF modules,
-autocast, the replay that rebuilds operands) is outside this build.
+leaf is which and what challenge width each product gets. Autocast, head blocks on the prover
+side and the replay that rebuilds operands from the leaves are outside this build.
 
 Per layer: the q/k/v projections (with biases for Qwen2), ``n_s·n_h`` members each of
 ``S = Q·Kᵀ`` and ``O = A·V``, then o/gate/up/down; the head ``Λ = X·W_outᵀ`` in ``B`` row

@@ -192,10 +192,9 @@ class DeclaredComputation(abc.ABC):
     def replay(self, leaves: Any) -> Replay:
         """Check 5's operands for the committed ``leaves`` (reference interface.py:380).
 
-        Rebuilding ``A_m, B_m`` by replaying the model from the committed leaves is not part of
-        this build: a computation serves operands it was given with :meth:`use_operands` (the
-        exact operands the prover used, as a capture records them), or a subclass overrides
-        this method."""
+        By default a computation serves operands it was given with :meth:`use_operands` (the
+        exact operands the prover used, as a capture records them); a subclass that replays
+        its glue from the leaves (the MLP instance) overrides this method."""
         r = getattr(self, "_operands", None)
         if r is None:
             raise NotImplementedError(
