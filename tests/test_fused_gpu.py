@@ -112,6 +112,19 @@ def test_fused_large_rows_and_many_classes(lib):
     _check_rows(prods, rows_f, rows_u)
 
 
+def test_fused_head_shaped_rows(lib):
+    """The tied head's row length: 151,936 bf16 columns, 303,872-byte rows, 1,187 chunk
+    classes with no class padding (the C4 logits and dF leaves have it), with changed
+    entries on a row end and deep inside a row. At this width two changed entries sit below
+    the honest rounding noise, so the rows are compared, not the verdicts."""
+    w = 151936
+    a, b, p = _product(256, 64, w, torch.bfloat16, seed=31)
+    tampered = _product(256, 64, w, torch.bfloat16, seed=32,
+                        tamper=[(3, w - 1, 2.0), (200, 77777, -1.0)])
+    rows_f, rows_u = _run_case(lib, [(a, b, p), tampered], expect_fused=2)
+    _check_rows([(a, b, p), tampered], rows_f, rows_u, tampered=(1,))
+
+
 def test_fused_changed_entries_in_every_region(lib):
     n, q, w = 128, 64, 1280  # 2560-byte rows
     # row 0's first elements lie before the first 128-byte boundary (12-byte header), the last
