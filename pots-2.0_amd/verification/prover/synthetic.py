@@ -44,7 +44,11 @@ class SyntheticStep:
 
 
 class CapturedReplay(Replay):
-    """Check 5's operands as the prover used them: ``operands[m] = (A_m, B_m)``."""
+    """Check 5's operands as the prover used them: ``operands[m] = (A_m, B_m)``. They come
+    from the prover, not from the committed leaves, so a verifier takes them only when told
+    to trust them (``prover_supplied``)."""
+
+    prover_supplied = True
 
     def __init__(self, operands: dict[int, tuple[torch.Tensor, torch.Tensor]]) -> None:
         self._ops = operands

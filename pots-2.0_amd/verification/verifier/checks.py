@@ -6,9 +6,13 @@ Reference: verification/verifier/checks.py:204-251 (``check_2_commitment``), :25
 the reference's check ids, rejection kinds and detail strings.
 
 Of the reference's order ``4 → 7 → 2 → 6a → 5 → 6b → 2.root`` this build runs
-:data:`DEFAULT_ORDER` = ``2 → 6a → 5 → 2.root``. Checks 4 (batch anchor), 7 (chaining) and 6b
-(the glue weights' update identity, which needs the model replay's glue gradients) are not
-part of it.
+:data:`DEFAULT_ORDER` = ``7 → 2 → 6a → 5 → 2.root``. Check 4 (the batch anchor into ``h_D`` at
+the schedule's indices) and 6b (the glue weights' update identity, which needs the model
+replay's glue gradients) are not part of it.
+
+- **Check 7** (check 0 on the first step) hashes the ``W_t`` leaves on the GPU and compares
+  them with the hashes the verifier kept: the agreed ``W_0``'s, or step ``t−1``'s
+  ``W_{t+1}``.
 
 - **Check 2's read** reads every leaf once, in order, hashes them on the GPU (through
   ``leaf_hashes_of``, which keeps the first-error-in-order semantics: a malformed or
@@ -24,9 +28,10 @@ part of it.
 - **Check 2's root comparison** runs last and compares the Merkle root over check 2's hashes
   (built on the GPU) with the claimed root.
 
-Operands come from ``c.replay(leaves)``. Rebuilding them by replaying the model is not part of
-this build; a computation serves captured operands instead (``DeclaredComputation.
-use_operands``).
+Operands come from ``c.replay(leaves)``: the MLP instance rebuilds them from the committed
+leaves; a computation given the prover's captured operands (``DeclaredComputation.
+use_operands``) serves those, which the verifier takes only when trusted, and check 5 marks
+the step's statistics with it.
 """
 
 from __future__ import annotations
@@ -38,7 +43,7 @@ from typing import Any
 import torch
 
 from verification.commitment import native
-from verification.commitment.leaves import leaf_hashes_of
+from verification.commitment.leaves import leaf_hashes_of, leaf_hashes_until_error
 from verification.commitment.merkle import DIGEST_SIZE, merkle_root
 from verification.computation.interface import (DeclaredComputation, ProductSpec,
                                                  chain_gradient)
@@ -57,8 +62,8 @@ from verification.verifier.context import (
 )
 from verification.verifier.matmul_check.freivalds import ProductMeasure, finish_rows
 
-__all__ = ["DEFAULT_ORDER", "ROOT_SLOT", "CHECKS", "protocol_id", "check_2_commitment",
-           "check_2_root", "check_6a_linear_update", "check_5_matmuls"]
+__all__ = ["DEFAULT_ORDER", "ROOT_SLOT", "CHECKS", "protocol_id", "check_7_chaining",
+           "check_2_commitment", "check_2_root", "check_6a_linear_update", "check_5_matmuls"]
 
 ROOT_SLOT = "2.root"
 
@@ -66,6 +71,48 @@ ROOT_SLOT = "2.root"
 def protocol_id(slot: str) -> str:
     """The protocol check id of a slot: ``"2.root"`` rejects as ``"2"``."""
     return slot.split(".", 1)[0]
+
+
+# ---- check 7: chaining (check 0 on the first step) ---------------------------------------
+
+
+@_checked
+def check_7_chaining(store: TranscriptStore, c: DeclaredComputation, ctx: StepContext,
+                     bands: Bands) -> Rejection | None:
+    """The ``W_t`` leaves hash to the digests the verifier kept: step ``t−1``'s ``W_{t+1}``
+    hashes from its check 2, or on the first step the agreed ``W_0``'s, where a mismatch is
+    check 0 (reference checks.py:159-197).
+
+    The leaves are read and validated in order and hashed on the GPU, then judged in order:
+    the first leaf that fails to read, validate or hash, or that hashes to another digest,
+    decides, so an error after a mismatch never shows. Each digest is kept for check 2, which
+    must see the same bytes.
+    """
+    cid = ctx.chain_check_id
+    if len(ctx.prev_w_hashes) != c.n_w:
+        raise RuntimeError(f"{len(ctx.prev_w_hashes)} chained hashes for {c.n_w} weights")
+    read_at = CommittedLeaves()  # versions at read time: a later read may write in place
+    slots = [c.w_t_index(name) for name in c.weight_names]
+
+    def read() -> Iterator[tuple[int, Any]]:
+        for i in slots:
+            obj = store.leaf(i)
+            read_at.add(obj)
+            yield i, obj
+
+    hashes, error = leaf_hashes_until_error(c, read())
+    for pos, got in enumerate(hashes):
+        i, name = slots[pos], c.weight_names[pos]
+        if read_at.changed(pos):
+            return ctx.reject(cid, f"leaf {i} changed in place during check {cid}", "malformed")
+        ctx.state.early_hashes[i] = got
+        if got != ctx.prev_w_hashes[pos]:
+            prior = "the agreed W_0" if cid == "0" else f"W_{{t+1}} of step {ctx.step - 1}"
+            return ctx.reject(cid, f"W_t[{name}] differs from {prior}")
+    if error is not None:
+        with _guard(ctx, cid):
+            raise error
+    return None
 
 
 # ---- check 2: commitment ----------------------------------------------------------------
@@ -194,57 +241,62 @@ def check_6a_linear_update(store: TranscriptStore, c: DeclaredComputation, ctx: 
 # ---- check 5: matmuls -------------------------------------------------------------------
 
 
-def _products(c: DeclaredComputation, leaves: CommittedLeaves, replay: Any
-              ) -> list[native.FvProduct]:
-    """Every product's ``A``, ``B`` (from the replay), committed ``P`` and, for a biased
+def _served(c: DeclaredComputation, spec: ProductSpec, ctx: StepContext, leaves: CommittedLeaves,
+            replay: Any) -> native.FvProduct:
+    """Product ``spec.m``'s ``A``, ``B`` (from the replay), committed ``P`` and, for a biased
     product, its committed ``W_t`` bias in the operand format (as ``[A | 1]·[B ; bᵀ]``), on
-    the current GPU (a store may serve host tensors, as the on-disk one does)."""
-    dev = torch.device("cuda", torch.cuda.current_device())
+    the current GPU (a store may serve host tensors, as the on-disk one does). A prover-data
+    error while serving is a malformed rejection at check 5; operands of the wrong shape are a
+    verifier error (reference checks.py:805-833)."""
 
     def on_gpu(x: torch.Tensor) -> torch.Tensor:
-        return x if x.is_cuda else x.to(dev)
+        return x if x.is_cuda else x.to(torch.device("cuda", torch.cuda.current_device()))
 
-    out = []
-    for spec in c.products:
-        a, b = (on_gpu(x) for x in replay.operands(spec.m))
-        p = on_gpu(leaves.leaf(c.product_index(spec.m)))
-        bias = None
+    bias = None
+    with _guard(ctx, "5", _AFTER_COMMIT):
+        with ctx.timed("5.glue"):
+            a, b = replay.operands(spec.m)
+        p = leaves.leaf(c.product_index(spec.m))
         if spec.bias is not None:
             bias = on_gpu(leaves.leaf(c.w_t_index(spec.bias))).to(c.operand_dtype) \
                 .to(torch.float32)
-        out.append(native.FvProduct(a, b, p, spec.m, bias))
-    return out
+    if (tuple(a.shape), tuple(b.shape)) != (spec.a_shape, spec.b_shape):
+        raise RuntimeError(f"{spec.name}: replay operands {tuple(a.shape)}·{tuple(b.shape)} "
+                           f"!= declared {spec.a_shape}·{spec.b_shape}")
+    return native.FvProduct(on_gpu(a), on_gpu(b), on_gpu(p), spec.m, bias)
 
 
-def check_5_matmuls(store: TranscriptStore, c: DeclaredComputation, ctx: StepContext,
-                    bands: Bands) -> Rejection | None:
-    """Both tests of check 5 on every product, in canonical order; stop at the first failure.
+def _serve_until_error(c: DeclaredComputation, ctx: StepContext, leaves: CommittedLeaves,
+                       replay: Any) -> tuple[list[native.FvProduct], Exception | None]:
+    """Every product served in canonical order, up to the first whose serving raises: the
+    products before it and that error (``None`` when all are served)."""
+    out: list[native.FvProduct] = []
+    for spec in c.products:
+        try:
+            out.append(_served(c, spec, ctx, leaves, replay))
+        except Exception as e:  # judged after the products before it
+            return out, e
+    return out, None
 
-    The challenges are keyed on ``ctx.state.claimed_root`` (check 2's read validated it).
-    Every product is measured at once on the GPU; the rows come back in one read and are
-    recorded and judged in canonical order. At a rejection, the products after the failing
-    one go to ``StepState.run_rest``, measured and not judged.
-    """
-    root = ctx.state.claimed_root
-    if root is None:
-        raise RuntimeError("check 5 needs the claimed root that check 2's read validated")
-    leaves = ctx.state.committed()
-    with _guard(ctx, "5", _AFTER_COMMIT), ctx.timed("5.glue"):
-        replay = c.replay(leaves)
-    ctx.state.replay = replay
-    if c.M == 0:
+
+def _measure_and_judge(c: DeclaredComputation, prods: list[native.FvProduct], root: bytes,
+                       ctx: StepContext, bands: Bands) -> Rejection | None:
+    """Measure ``prods`` (the first ``len(prods)`` products in canonical order) in one
+    Freivalds plan, read the rows back once, then record and judge them in order; the device
+    verdict kernel judges the same rows and must agree on the first failure."""
+    specs = c.products[:len(prods)]
+    if not specs:
         return None
     lib = native.get()
-    with _guard(ctx, "5", _AFTER_COMMIT), ctx.timed("5.measure"):
-        prods = _products(c, leaves, replay)
+    with ctx.timed("5.measure"):
         plan = lib.fv_plan(prods, ctx.k, ctx.kappa_guard)
         try:
             rows = plan.rows(root)
-            specs = native.verdict_specs(
-                [s.q for s in c.products], [s.a_shape[0] for s in c.products],
-                [s.bias is not None for s in c.products],
-                [bands.kappa_for(product_class(c, s)) for s in c.products], device=rows.device)
-            _, _, first = lib.verdicts(rows, specs, k=ctx.k, eps_in=ctx.eps_in,
+            vspecs = native.verdict_specs(
+                [s.q for s in specs], [s.a_shape[0] for s in specs],
+                [s.bias is not None for s in specs],
+                [bands.kappa_for(product_class(c, s)) for s in specs], device=rows.device)
+            _, _, first = lib.verdicts(rows, vspecs, k=ctx.k, eps_in=ctx.eps_in,
                                        eps_acc=ctx.eps_acc, tau=bands.tau,
                                        guard=ctx.kappa_guard, judge=ctx.judge)
             host = rows.cpu().numpy()
@@ -253,11 +305,10 @@ def check_5_matmuls(store: TranscriptStore, c: DeclaredComputation, ctx: StepCon
             plan.close()
     with ctx.timed("5.judge"):
         # finish_row on every row at once (the same fp64 operations, bit for bit)
-        mps = finish_rows(host, q=[s.q for s in c.products],
-                          n=[s.a_shape[0] for s in c.products], eps_in=ctx.eps_in,
-                          eps_acc=ctx.eps_acc, guard=ctx.kappa_guard,
-                          biased=[s.bias is not None for s in c.products])
-        done = list(zip(c.products, mps))
+        mps = finish_rows(host, q=[s.q for s in specs], n=[s.a_shape[0] for s in specs],
+                          eps_in=ctx.eps_in, eps_acc=ctx.eps_acc, guard=ctx.kappa_guard,
+                          biased=[s.bias is not None for s in specs])
+        done = list(zip(specs, mps))
         for i, (spec, mp) in enumerate(done):
             rej = _judge_product(c, spec, mp, ctx, bands)
             if rej is not None:
@@ -266,10 +317,51 @@ def check_5_matmuls(store: TranscriptStore, c: DeclaredComputation, ctx: StepCon
                                        f"{device_first}, the host closed form {i}")
                 ctx.state.run_rest = done[i + 1:]
                 return rej
-    if device_first != c.M:
+    if device_first != len(specs):
         raise RuntimeError(f"check 5: the device verdicts reject product index {device_first}, "
                            f"the host closed form accepts every product")
     return None
+
+
+@_checked
+def check_5_matmuls(store: TranscriptStore, c: DeclaredComputation, ctx: StepContext,
+                    bands: Bands) -> Rejection | None:
+    """Both tests of check 5 on every product, in canonical order; stop at the first failure.
+
+    The challenges are keyed on ``ctx.state.claimed_root`` (check 2's read validated it).
+    The products are served in canonical order, every one measured at once on the GPU; the
+    rows come back in one read and are recorded and judged in canonical order. At a
+    rejection, the products after the failing one go to ``StepState.run_rest``, measured and
+    not judged.
+
+    An error while serving product ``m`` is raised only after the products before ``m`` are
+    judged, as it would be one product at a time (reference checks.py:613-650): if one of them
+    rejects, that rejection is returned and the error goes to ``StepState.run_rest_error``;
+    otherwise the error is raised, and a prover-data error becomes check 5's malformed
+    rejection.
+    """
+    root = ctx.state.claimed_root
+    if root is None:
+        raise RuntimeError("check 5 needs the claimed root that check 2's read validated")
+    leaves = ctx.state.committed()
+    with _guard(ctx, "5", _AFTER_COMMIT), ctx.timed("5.glue"):
+        replay = c.replay(leaves)
+    ctx.state.replay = replay
+    if getattr(replay, "prover_supplied", False):
+        if not ctx.trust_prover_operands:
+            raise RuntimeError("check 5 was given the prover's captured operands without "
+                               "trust_prover_operands")
+        ctx.stats.operands_from_prover = True
+    if c.M == 0:
+        return None
+    prods, error = _serve_until_error(c, ctx, leaves, replay)
+    rej = _measure_and_judge(c, prods, root, ctx, bands)
+    if error is None:
+        return rej
+    if rej is None:
+        raise error
+    ctx.state.run_rest_error = error
+    return rej
 
 
 def _judge_product(c: DeclaredComputation, spec: ProductSpec, mp: ProductMeasure,
@@ -301,9 +393,10 @@ def _judge_product(c: DeclaredComputation, spec: ProductSpec, mp: ProductMeasure
 
 
 CHECKS: dict[str, Callable[..., Rejection | None]] = {
+    "7": check_7_chaining,
     "2": check_2_commitment,
     "6a": check_6a_linear_update,
     "5": check_5_matmuls,
     ROOT_SLOT: check_2_root,
 }
-DEFAULT_ORDER: tuple[str, ...] = ("2", "6a", "5", ROOT_SLOT)
+DEFAULT_ORDER: tuple[str, ...] = ("7", "2", "6a", "5", ROOT_SLOT)

@@ -98,6 +98,8 @@ class TensorStat:
 class StepStats:
     products: list[ProductStat] = field(default_factory=list)
     tensors: list[TensorStat] = field(default_factory=list)
+    # check 5 measured the prover's captured operands, not a replay of the committed leaves
+    operands_from_prover: bool = False
 
     def max_normalized(self) -> float:
         return max((max(p.normalized) for p in self.products), default=0.0)
@@ -191,6 +193,7 @@ class StepContext:
     eps_w: float
     judge: bool = True
     kappa_guard: bool = True
+    trust_prover_operands: bool = False
     state: StepState = field(default_factory=StepState)
     stats: StepStats = field(default_factory=StepStats)
     section: Section | None = None

@@ -42,10 +42,10 @@ def _root(c, leaves):
     return O.merkle_root(want)
 
 
-def _verify(c, leaves, claimed, k=2):
+def _verify(c, leaves, claimed, k=2, w0_leaves=None):
+    from conftest import started_verifier
     from verification.transcript.store import InMemoryStore
-    from verification.verifier.driver import Verifier
-    v = Verifier(c, k=k)
+    v = started_verifier(c, w0_leaves if w0_leaves is not None else leaves, k=k)
     rej = v.verify_step(1, InMemoryStore(leaves, claimed_root=claimed))
     return v, rej
 
@@ -58,7 +58,8 @@ def test_honest_step_accepts_with_stats(lib):
     stats = v.stats[1].products
     assert [s.m for s in stats] == [s.m for s in c.products]
     assert all(max(s.normalized) <= 8.0 for s in stats)
-    assert set(v.timings[1]) == {"2", "6a", "5", "2.root"}
+    assert set(v.timings[1]) == {"7", "2", "6a", "5", "2.root"}
+    assert v.stats[1].operands_from_prover
 
 
 def test_forged_product_rejects_at_check_5(lib):
@@ -85,7 +86,7 @@ def test_wrong_shape_leaf_is_malformed_at_check_2(lib):
     c, step = _step(14)
     leaves = list(step.leaves)
     name = next(n for n in c.weight_names if len(c.weight_shapes[n]) == 2)
-    i = c.w_t_index(name)
+    i = c.w_next_index(name)
     leaves[i] = leaves[i].reshape(-1)
     _, rej = _verify(c, leaves, bytes(32))
     assert rej is not None and (rej.check_id, rej.kind) == ("2", "malformed")
@@ -110,24 +111,115 @@ def test_claimed_root_not_a_digest_is_malformed(lib):
 
 
 def test_mutation_after_handoff_is_malformed(lib):
+    from conftest import started_verifier
     from verification.transcript.store import InMemoryStore
-    from verification.verifier.driver import Verifier
     c, step = _step(17)
+    v = started_verifier(c, step.leaves, k=2)
+    store = InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves))
+    step.leaves[c.product_index(1)].add_(1.0)
+    rej = v.verify_step(1, store)
+    assert rej is not None and (rej.check_id, rej.kind) == ("2", "malformed")
+    assert "StoreMutationError" in rej.detail
+    # a W_t leaf is read first by check 0 on the first step
+    c, step = _step(17)
+    v = started_verifier(c, step.leaves, k=2)
     store = InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves))
     step.leaves[c.n_s].add_(1.0)
-    rej = Verifier(c, k=2).verify_step(1, store)
-    assert rej is not None and (rej.check_id, rej.kind) == ("2", "malformed")
+    rej = v.verify_step(1, store)
+    assert rej is not None and (rej.check_id, rej.kind) == ("0", "malformed")
     assert "StoreMutationError" in rej.detail
 
 
-def test_check_5_agrees_with_the_device_step_verifier(lib):
-    from verification.verifier.step import DeviceStepVerifier
-    c, step = _step(18, k=3)
-    spec = c.products[5]
-    step.product(spec.m)[0, 0] += 64.0  # well above a bf16 product's band
-    claimed = _root(c, step.leaves)
-    _, rej = _verify(c, step.leaves, claimed, k=3)
-    out = DeviceStepVerifier(c, step.leaves, lambda s: step.operands[s.m], k=3).run(claimed)
-    assert rej is not None and rej.check_id == "5" and out.check == "5"
-    assert out.first_fail == spec.m - 1
-    assert rej.detail.startswith(f"P_{spec.m} ({spec.name})")
+def test_w_t_other_than_w0_rejects_at_check_0(lib):
+    c, step = _step(19)
+    w0 = list(step.leaves)
+    name = c.weight_names[3]
+    w0[c.w_t_index(name)] = w0[c.w_t_index(name)] + 1.0
+    _, rej = _verify(c, step.leaves, _root(c, step.leaves), w0_leaves=w0)
+    assert rej is not None and (rej.step, rej.check_id, rej.kind) == (1, "0", "failed")
+    assert rej.detail == f"W_t[{name}] differs from the agreed W_0"
+
+
+def test_two_steps_chain_and_end_run(lib):
+    """Step 2 starts from step 1's W_{t+1} (check 7); check 8 compares the last W_{t+1} with
+    the agreed final weights and counts the steps."""
+    from conftest import started_verifier
+    from verification.computation.interface import chain_gradient
+    from verification.transcript.store import InMemoryStore
+    c, step = _step(20)
+    nxt = list(step.leaves)
+    for name in c.weight_names:  # same products; W_t moves on, W_{t+1} follows check 6a
+        w_t = step.leaves[c.w_next_index(name)]
+        nxt[c.w_t_index(name)] = w_t
+        if name in c.linear_weights:
+            g = chain_gradient((step.leaves[c.product_index(m)]
+                                for m in c.linear_weights[name]), torch.float32)
+            nxt[c.w_next_index(name)] = torch.add(w_t, g, alpha=-c.eta)
+        else:
+            nxt[c.w_next_index(name)] = w_t - 1e-4
+    final = {n: nxt[c.w_next_index(n)].clone() for n in c.weight_names}
+    v = started_verifier(c, step.leaves, k=2, n_steps=2)
+    for t, leaves in ((1, step.leaves), (2, nxt)):
+        assert v.verify_step(t, InMemoryStore(leaves, claimed_root=_root(c, leaves))) is None
+    verdict = v.end_run(final)
+    assert verdict.accepted and verdict.steps_verified == 2 and verdict.rejection is None
+    # a second step that does not start from step 1's W_{t+1} fails check 7
+    v = started_verifier(c, step.leaves, k=2, n_steps=2)
+    assert v.verify_step(1, InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves))) \
+        is None
+    rej = v.verify_step(2, InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves)))
+    assert rej is not None and (rej.step, rej.check_id, rej.kind) == (2, "7", "failed")
+    assert rej.detail == f"W_t[{c.weight_names[0]}] differs from W_{{t+1}} of step 1"
+    # a run that stops early, or ends on other weights, fails check 8
+    v = started_verifier(c, step.leaves, k=2, n_steps=2)
+    assert v.verify_step(1, InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves))) \
+        is None
+    verdict = v.end_run(final)
+    assert not verdict.accepted and verdict.rejection.check_id == "8"
+    assert verdict.rejection.detail == "1 steps verified, the run declares T = 2"
+    v = started_verifier(c, step.leaves, k=2, n_steps=1)
+    assert v.verify_step(1, InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves))) \
+        is None
+    verdict = v.end_run(final)
+    assert verdict.rejection.detail == \
+        f"final W_T[{c.weight_names[0]}] differs from the agreed weights"
+
+
+def test_serving_error_after_a_forged_product(lib):
+    """A serving error at product m is raised only after the products before m are judged
+    (reference checks.py:613-650): with a forged product k < m the step rejects at k as
+    "failed" and keeps the error for the record; without it the error is check 5's malformed
+    rejection."""
+    from verification.transcript.errors import TranscriptFormatError
+    from verification.transcript.store import InMemoryStore
+
+    class Failing:
+        prover_supplied = True
+
+        def __init__(self, inner, m):
+            self.inner, self.m = inner, m
+
+        def operands(self, m):
+            if m == self.m:
+                raise TranscriptFormatError(f"operands of product {m} unreadable")
+            return self.inner.operands(m)
+
+    for forged in (True, False):
+        c, step = _step(21)
+        k_spec, m_spec = c.products[10], c.products[40]
+        if forged:
+            step.product(k_spec.m)[1, 2] += 8.0
+        c.use_operands(Failing(step.replay(), m_spec.m))
+        from conftest import started_verifier
+        v = started_verifier(c, step.leaves, k=2, trust_prover_operands=True)
+        store = InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves))
+        rej = v.verify_step(1, store)
+        assert rej is not None and rej.check_id == "5"
+        if forged:
+            assert rej.kind == "failed" and rej.detail.startswith(f"P_{k_spec.m} ")
+            assert [s.m for s in v.stats[1].products][-1] == k_spec.m
+        else:
+            assert rej.kind == "malformed"
+            assert rej.detail == (f"malformed prover data: TranscriptFormatError: operands of "
+                                  f"product {m_spec.m} unreadable")
+            assert [s.m for s in v.stats[1].products] == [s.m for s in c.products[:40]]

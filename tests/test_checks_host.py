@@ -47,7 +47,7 @@ def _mp(nu=1.0, p_abs1=1.0, res=(0.0, 0.0), p_norm=1.0, unit=1e-3, u=1.0):
 
 
 def test_slot_order_and_ids():
-    assert DEFAULT_ORDER == ("2", "6a", "5", "2.root")
+    assert DEFAULT_ORDER == ("7", "2", "6a", "5", "2.root")
     assert protocol_id("2.root") == "2" and protocol_id("5") == "5"
 
 
@@ -180,3 +180,106 @@ def test_finish_rows_equals_finish_row_bit_for_bit():
                     assert same(getattr(w, f), getattr(g, f)), (f, r, qq, nn, b)
                 assert all(same(x, y) for x, y in zip(w.residuals, g.residuals))
                 assert all(same(x, y) for x, y in zip(w.normalized, g.normalized))
+
+
+def _tiny_decoder():
+    from verification.computation.instances.decoder import DecoderComputation
+    return DecoderComputation(L=1, d=16, d_f=32, n_h=2, n_kv=1, n_v=40, n_s=1, n=8)
+
+
+class _RaisingReplay:
+    """Operands from a table; product ``bad`` fails to serve with ``error``."""
+
+    def __init__(self, table, bad, error):
+        self.table, self.bad, self.error = table, bad, error
+
+    def operands(self, m):
+        if m == self.bad:
+            raise self.error
+        return self.table[m]
+
+
+def _ctx_after_check_2(c, leaves, **kw):
+    ctx = _ctx(**kw)
+    committed = CommittedLeaves()
+    for obj in leaves:
+        committed.add(obj)
+    ctx.state.claimed_root, ctx.state.leaves = bytes(32), committed
+    return ctx
+
+
+def _leaves(c):
+    from setup.records import Record
+    out = [Record(torch.zeros(c.n, dtype=torch.int32), torch.zeros(c.n, dtype=torch.int32),
+                  torch.ones(c.n, dtype=torch.int32))]
+    out += [torch.zeros(c.weight_shapes[n]) for n in c.weight_names]
+    out += [torch.zeros(s.p_shape, dtype=c.product_dtype) for s in c.products]
+    out += [torch.zeros(c.weight_shapes[n]) for n in c.weight_names]
+    return out
+
+
+def test_check_5_serving_error_at_the_first_product_is_malformed():
+    """A prover-data error while serving product 1 (nothing measured before it) is check 5's
+    malformed rejection, returned, not raised (reference checks.py:574,613-650)."""
+    from verification.transcript.errors import TranscriptFormatError
+    from verification.verifier.checks import check_5_matmuls
+    c = _tiny_decoder()
+    leaves = _leaves(c)
+    c.use_operands(_RaisingReplay({}, 1, TranscriptFormatError("operand file truncated")))
+    ctx = _ctx_after_check_2(c, leaves)
+    rej = check_5_matmuls(None, c, ctx, Bands.provisional())
+    assert rej == Rejection(3, "5", "malformed prover data: TranscriptFormatError: operand "
+                                    "file truncated", "malformed")
+    assert ctx.state.run_rest_error is None
+
+
+def test_check_5_leaf_mutated_after_check_2_is_malformed():
+    from verification.verifier.checks import check_5_matmuls
+    c = _tiny_decoder()
+    leaves = _leaves(c)
+    table = {s.m: (torch.zeros(s.a_shape), torch.zeros(s.b_shape)) for s in c.products}
+    c.use_operands(_RaisingReplay(table, None, None))
+    ctx = _ctx_after_check_2(c, leaves)
+    leaves[c.product_index(1)].add_(1)  # after check 2 hashed it
+    rej = check_5_matmuls(None, c, ctx, Bands.provisional())
+    assert rej is not None and (rej.check_id, rej.kind) == ("5", "malformed")
+    assert rej.detail.startswith("malformed prover data: StoreMutationError: leaf "
+                                 f"{c.product_index(1)} changed in place")
+
+
+def test_check_5_refuses_untrusted_prover_operands():
+    from verification.prover.synthetic import CapturedReplay
+    from verification.verifier.checks import check_5_matmuls
+    c = _tiny_decoder()
+    c.use_operands(CapturedReplay({}))
+    with pytest.raises(RuntimeError, match="trust_prover_operands"):
+        check_5_matmuls(None, c, _ctx_after_check_2(c, _leaves(c)), Bands.provisional())
+
+
+def test_verifier_constructor_refuses_what_the_reference_refuses():
+    from verification.prover.synthetic import CapturedReplay
+    from verification.verifier.driver import Verifier
+    c = _tiny_decoder()
+    w0 = {n: torch.zeros(c.weight_shapes[n]) for n in c.weight_names}
+    base = dict(h_D=bytes(32), n_records=4, k=2, n_steps=3, bands=Bands.provisional(),
+                seed=0, w0=w0, allow_provisional=True)
+
+    def refused(match, **kw):
+        with pytest.raises(ValueError, match=match):
+            Verifier(c, **{**base, **kw})
+
+    refused("exactly one of w0 and w0_hashes", w0_hashes=[bytes(32)] * c.n_w)
+    refused("h_D must be a 32-byte digest", h_D=b"x")
+    refused("k must be in 1..255", k=0)
+    refused("n_steps", n_steps=0)
+    refused("bands are required", bands=None)
+    refused("allow_provisional", allow_provisional=False)
+    refused("κ guard", calibrate=True, kappa_guard=False)
+    refused("match no product", bands=Bands(tau=8.0, kappa_max=1e4,
+                                            kappa_classes={"no such class": 2.0}))
+    c.use_operands(CapturedReplay({}))
+    refused("trust_prover_operands")
+    v = Verifier(c, **base, trust_prover_operands=True)
+    with pytest.raises(RuntimeError, match="start_run"):
+        v.verify_step(1, None)
+    assert v.band_source == "provisional"

@@ -54,9 +54,9 @@ def test_products_stay_in_hbm_and_commit_matches_the_oracle(lib):
 
 def test_honest_step_accepts_with_the_replay(lib):
     from verification.transcript.store import InMemoryStore
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     c, step, tree = _prove(seed=2)
-    v = Verifier(c, k=2)
+    v = started_verifier(c, step.leaves(), k=2)
     assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
     assert [s.m for s in v.stats[1].products] == [p.m for p in c.products]
     assert v.stats[1].max_normalized() <= 8.0
@@ -75,11 +75,12 @@ def test_device_step_verifier_with_the_replay(lib):
 
 def test_perturbed_product_rejects_at_check_5(lib):
     from verification.transcript.store import InMemoryStore
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     m = 2  # Y_2, a forward product: check 6a does not read it
     c, step, tree = _prove(seed=4, perturb={m: lambda p: p.index_add_(
         0, torch.tensor([3], device=p.device), torch.full_like(p[:1], 0.25))})
-    rej = Verifier(c, k=2).verify_step(1, InMemoryStore(step.leaves(), tree))
+    rej = started_verifier(c, step.leaves(), k=2).verify_step(
+        1, InMemoryStore(step.leaves(), tree))
     assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
     assert rej.detail.startswith(f"P_{m} (Y_2)")
 
@@ -87,27 +88,27 @@ def test_perturbed_product_rejects_at_check_5(lib):
 def test_changed_update_rejects_at_check_6a(lib):
     from verification.commitment.leaves import commit_leaves_device
     from verification.transcript.store import InMemoryStore
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     c, step, _ = _prove(seed=5)
     leaves = step.leaves()
     i = c.w_next_index(c.weight(2))
     leaves[i] = leaves[i].clone()
     leaves[i][0, 0] += 1e-2
     tree = commit_leaves_device(c, leaves)
-    rej = Verifier(c, k=2).verify_step(1, InMemoryStore(leaves, tree))
+    rej = started_verifier(c, leaves, k=2).verify_step(1, InMemoryStore(leaves, tree))
     assert rej is not None and rej.check_id == "6a", rej
 
 
 def test_stored_mlp_step_verifies_from_disk(lib, tmp_path):
     from verification.transcript.loader import ResidentStore, load_step
     from verification.transcript.store import DiskStore
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     c, step, tree = _prove(seed=6)
     disk = DiskStore.write(tmp_path / "step", c, step.leaves(), tree)
     res = load_step(disk, c.n_leaves)
     assert res.fallback == 0  # records are plain tensor leaves here
     for store in (disk, ResidentStore(disk, res)):
-        assert Verifier(c, k=2).verify_step(1, store) is None
+        assert started_verifier(c, step.leaves(), k=2).verify_step(1, store) is None
 
 
 def _decoder_prove(seed=0, qkv_bias=True, n_kv=2, perturb=None):
@@ -148,12 +149,12 @@ def test_real_decoder_step_commits_and_verifies(lib, qkv_bias, n_kv):
     the device commit equals the CPU oracle's root, and the verifier accepts the step with the
     captured operands through the check-level API and the device step alike."""
     from verification.transcript.store import InMemoryStore
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     from verification.verifier.step import DeviceStepVerifier
     c, step, tree = _decoder_prove(seed=7, qkv_bias=qkv_bias, n_kv=n_kv)
     assert step.capture["device_resident"]
     assert tree.root == _decoder_oracle_root(c, step.leaves())
-    v = Verifier(c, k=2)
+    v = started_verifier(c, step.leaves(), k=2)
     assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
     assert len(v.stats[1].products) == c.M
     out = DeviceStepVerifier(c, step.leaves(), lambda s: step.operands[s.m], k=2).run(tree.root)
@@ -162,12 +163,13 @@ def test_real_decoder_step_commits_and_verifies(lib, qkv_bias, n_kv):
 
 def test_real_decoder_step_with_a_changed_member_rejects_at_check_5(lib):
     from verification.transcript.store import InMemoryStore
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     c0, _, _ = _decoder_prove(seed=8)
     spec = next(s for s in c0.products if s.name == "L2.O[1,3]")
     c, step, tree = _decoder_prove(seed=8, perturb={spec.m: lambda p: p.index_add_(
         0, torch.tensor([5], device=p.device), torch.full_like(p[:1], 0.5))})
-    rej = Verifier(c, k=2).verify_step(1, InMemoryStore(step.leaves(), tree))
+    rej = started_verifier(c, step.leaves(), k=2).verify_step(
+        1, InMemoryStore(step.leaves(), tree))
     assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
     assert rej.detail.startswith(f"P_{spec.m} (L2.O[1,3])")
 
@@ -182,7 +184,7 @@ def test_c1_real_smollm2_step_proves_commits_and_verifies(lib):
     from verification.computation.interface import snapshot_weights
     from verification.prover.step import commit, prove_step
     from verification.transcript.store import InMemoryStore
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     c = smollm2_135m()
     torch.manual_seed(0)
     with torch.device("cuda"):
@@ -198,6 +200,6 @@ def test_c1_real_smollm2_step_proves_commits_and_verifies(lib):
     tree = commit(c, step)
     assert tree.root == _decoder_oracle_root(c, step.leaves())
     c.use_operands(step.replay())
-    v = Verifier(c, k=1)
+    v = started_verifier(c, step.leaves(), k=1)
     assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
     assert len(v.stats[1].products) == c.M and v.stats[1].max_normalized() <= 8.0

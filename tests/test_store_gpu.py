@@ -82,12 +82,12 @@ def test_stored_step_reads_back_bit_for_bit(lib, tmp_path):
 def test_verifier_decides_a_stored_step_as_in_memory(lib, tmp_path):
     from verification.transcript.loader import ResidentStore, load_step
     from verification.transcript.store import InMemoryStore
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     c, step, tree, disk = _stored(tmp_path, 22)
     res = load_step(disk, c.n_leaves)
     stats = []
     for store in (InMemoryStore(step.leaves, tree), disk, ResidentStore(disk, res)):
-        v = Verifier(c, k=2)
+        v = started_verifier(c, step.leaves, k=2)
         assert v.verify_step(1, store) is None
         stats.append([(s.m, s.normalized, s.kappa, s.p_norm, s.p_abs1)
                       for s in v.stats[1].products])
@@ -111,12 +111,12 @@ def test_device_step_verifier_on_a_loaded_step(lib, tmp_path):
 def test_corrupt_leaf_file_rejects_as_malformed(lib, tmp_path):
     from verification.transcript.loader import ResidentStore, load_step
     from verification.transcript.store import LEAF_FILE
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     c, step, tree, disk = _stored(tmp_path, 24)
     (disk.directory / LEAF_FILE.format(c.product_index(2))).write_bytes(b"\0" * 10)
     res = load_step(disk, c.n_leaves)
     for store in (disk, ResidentStore(disk, res)):
-        rej = Verifier(c, k=2).verify_step(1, store)
+        rej = started_verifier(c, step.leaves, k=2).verify_step(1, store)
         assert rej is not None and (rej.step, rej.check_id, rej.kind) == (1, "2", "malformed")
         assert "LeafReadError" in rej.detail
 
@@ -124,7 +124,7 @@ def test_corrupt_leaf_file_rejects_as_malformed(lib, tmp_path):
 def test_changed_product_file_rejects_at_check_5(lib, tmp_path):
     from verification.transcript.loader import ResidentStore, load_step
     from verification.transcript.store import LEAF_FILE
-    from verification.verifier.driver import Verifier
+    from conftest import started_verifier
     c, step, tree, disk = _stored(tmp_path, 25)
     spec = c.products[len(c.products) // 3]
     p = step.product(spec.m).clone()
@@ -133,7 +133,7 @@ def test_changed_product_file_rejects_at_check_5(lib, tmp_path):
     res = load_step(disk, c.n_leaves)
     details = []
     for store in (disk, ResidentStore(disk, res)):
-        rej = Verifier(c, k=2).verify_step(1, store)
+        rej = started_verifier(c, step.leaves, k=2).verify_step(1, store)
         assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed")
         assert rej.detail.startswith(f"P_{spec.m} ({spec.name})")
         details.append(rej.detail)
