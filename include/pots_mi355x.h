@@ -63,6 +63,21 @@ size_t pots_hash_leaves(size_t n, const uint8_t *hdr_buf, const uint64_t *hdr_of
                         const uint64_t *payload_ptr, const uint64_t *payload_len,
                         const uint8_t *kind, uint8_t *out, uint32_t n_threads);
 
+/* No counterpart in the reference: pots_hash_leaves for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, results and return values, bit for bit; it calls no hipMalloc,
+ * hipFree or other allocating routine. Its workspace (the plan's descriptors and chaining
+ * values, staged host payloads, the digests before their copy out) lives in a static 64 MiB
+ * device array, one per GPU, held until the process ends: about 2 M chunks of 1 KiB, i.e.
+ * some 2 GiB of leaf bytes in device memory (host payloads also take their size in it). A
+ * larger request returns SIZE_MAX with the reason in pots_last_error(), before any GPU work.
+ * Calls in one process are serialised, since they share the array; calls from two processes
+ * on one GPU use separate arrays. Synchronous, on the null stream. */
+size_t pots_hash_leaves_noalloc(size_t n, const uint8_t *hdr_buf, const uint64_t *hdr_off,
+                                const uint32_t *hdr_len, const uint32_t *hdr_idx,
+                                const uint64_t *payload_ptr, const uint64_t *payload_len,
+                                const uint8_t *kind, uint8_t *out, uint32_t n_threads);
+
 /* Replaces native.c:299 pots_all_finite: 1 when every value of the nbytes bytes at p (host
  * or device) is finite under `kind` (kind 0: always 1), 0 when one is NaN or Inf, a negative
  * POTS_E_* on failure. Synchronous. */

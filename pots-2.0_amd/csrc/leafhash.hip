@@ -28,6 +28,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
+#include <string>
 #include <new>
 #include <unordered_set>
 #include <vector>
@@ -622,7 +624,7 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
                       const uint32_t* hdr_len, const uint32_t* hdr_idx,
                       const uint64_t* payload_ptr, const uint64_t* payload_len,
                       const uint8_t* kind, bool device_only, bool owned, void* fv,
-                      LeafPlan** out) {
+                      LeafPlan** out, char* ext_base = nullptr, size_t ext_cap = 0) {
   if (n == 0 || n >= 0xFFFFFFFFull) return POTS_E_ARG;
   for (size_t i = 0; i < n; i++)
     if (kind[i] > POTS_KIND_F16) return POTS_E_ARG;
@@ -808,7 +810,17 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
   P->total = at;
 
   int rc;
-  if (owned) {
+  if (ext_base) {  // memory the caller holds (the allocation-free entry point's scratch)
+    if (P->total > ext_cap) {
+      note_error("leaf hashing needs " + std::to_string(P->total) + " bytes of device scratch "
+                 "for these leaves; the allocation-free entry point holds " +
+                 std::to_string(ext_cap));
+      delete P;
+      return POTS_E_ARG;
+    }
+    P->owned = false;
+    P->base = ext_base;
+  } else if (owned) {
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&P->base), P->total);
     if (e != hipSuccess) {
       note_hip_error(e, "hipMalloc(leaf plan)", __FILE__, __LINE__);
@@ -990,6 +1002,74 @@ extern "C" size_t pots_hash_leaves(size_t n, const uint8_t* hdr_buf, const uint6
     }
   }
   plan_free(P);
+  return bad;
+}
+
+// ---- the allocation-free variant of pots_hash_leaves ----------------------------------------
+
+// Device scratch of pots_hash_leaves_noalloc: the results (32 B per leaf and the first-bad
+// word), then the plan (leaf descriptors, chaining values, staged messages). Each GPU the
+// library runs on holds its own copy until the process ends.
+constexpr size_t kNoallocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;  // one call at a time per process: every call shares the array
+char* g_scratch_ptr[64] = {};
+
+// The array's device address on the current GPU, looked up once per device with that device
+// current. Host code passes this address, never the symbol itself.
+int scratch_address(char** out) {
+  int dev = 0;
+  POTS_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return POTS_E_ARG;
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      note_hip_error(e, "hipGetSymbolAddress(scratch)", __FILE__, __LINE__);
+      return POTS_E_HIP;
+    }
+    g_scratch_ptr[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return POTS_E_OK;
+}
+}  // namespace
+
+extern "C" size_t pots_hash_leaves_noalloc(size_t n, const uint8_t* hdr_buf,
+                                           const uint64_t* hdr_off, const uint32_t* hdr_len,
+                                           const uint32_t* hdr_idx, const uint64_t* payload_ptr,
+                                           const uint64_t* payload_len, const uint8_t* kind,
+                                           uint8_t* out, uint32_t n_threads) {
+  (void)n_threads;
+  if (n == 0) return 0;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  char* base = nullptr;
+  if (scratch_address(&base) != POTS_E_OK) return SIZE_MAX;
+  const size_t res_bytes = align_up(32 * n + 16, 256);
+  if (res_bytes >= kNoallocScratchBytes) {
+    note_error(std::to_string(n) + " leaves need " + std::to_string(res_bytes) + " bytes of "
+               "results; the allocation-free entry point's scratch holds " +
+               std::to_string(kNoallocScratchBytes));
+    return SIZE_MAX;
+  }
+  LeafPlan* P = nullptr;
+  if (plan_build(n, hdr_buf, hdr_off, hdr_len, hdr_idx, payload_ptr, payload_len, kind,
+                 /*device_only=*/false, /*owned=*/false, nullptr, &P, base + res_bytes,
+                 kNoallocScratchBytes - res_bytes) != POTS_E_OK)
+    return SIZE_MAX;
+  uint32_t* d_dig = reinterpret_cast<uint32_t*>(base);
+  uint32_t* d_bad = reinterpret_cast<uint32_t*>(base + 32 * n);
+  size_t bad = SIZE_MAX;
+  uint32_t h_bad = 0;
+  if (plan_run(P, d_dig, d_bad, 0) == POTS_E_OK) {
+    hipError_t e = hipMemcpy(out, d_dig, 32 * n, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(&h_bad, d_bad, 4, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) bad = h_bad;
+    else note_hip_error(e, "hipMemcpy(digests)", __FILE__, __LINE__);
+  }
+  plan_free(P);  // host bookkeeping only: the plan's memory is the scratch
   return bad;
 }
 

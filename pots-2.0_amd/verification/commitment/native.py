@@ -81,6 +81,8 @@ class Native:
             "pots_simd_degree": ([], _sz),
             "pots_blake3_version": ([], ctypes.c_char_p),
             "pots_hash_leaves": ([_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32], _sz),
+            "pots_hash_leaves_noalloc": ([_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32],
+                                         _sz),
             "pots_all_finite": ([_vp, _u64, _u8, _u32], _int),
             "pots_merkle_tree": ([_sz, _vp, _vp], _int),
             "pots_leaf_plan_create": ([_sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -137,11 +139,14 @@ class Native:
 
     def hash_leaves(self, hdr_buf: bytes, hdr_off: np.ndarray, hdr_len: np.ndarray,
                     hdr_idx: np.ndarray, payload_ptr: np.ndarray, payload_len: np.ndarray,
-                    kind: np.ndarray, *, threads: int = 1) -> tuple[np.ndarray, int]:
+                    kind: np.ndarray, *, threads: int = 1,
+                    noalloc: bool = False) -> tuple[np.ndarray, int]:
         """``(digests, first_bad)`` of native.py:286-311: leaf ``i``'s digest is
         ``BLAKE3(0x00 ‖ header ‖ payload)``, uint8 ``[n, 32]``; ``first_bad`` is the first leaf
         whose payload holds NaN or Inf, or ``n``. Payload addresses may be host or device
-        memory; the caller keeps them alive until the call returns."""
+        memory; the caller keeps them alive until the call returns. ``noalloc`` takes the
+        entry point that allocates no device memory (``pots_hash_leaves_noalloc``, bounded
+        by its static scratch)."""
         n = len(payload_ptr)
         if not len(payload_len) == len(kind) == len(hdr_idx) == n:
             raise ValueError("payload_ptr, payload_len, kind and hdr_idx must have one length")
@@ -158,11 +163,10 @@ class Native:
         arrs = [np.ascontiguousarray(x, dtype=t) for x, t in (
             (hdr_off, np.uint64), (hdr_len, np.uint32), (hdr_idx, np.uint32),
             (payload_ptr, np.uint64), (payload_len, np.uint64), (kind, np.uint8))]
-        bad = self._lib.pots_hash_leaves(n, _addr(hb), *map(_addr, arrs), _addr(out),
-                                         max(1, int(threads)))
+        fn = self._lib.pots_hash_leaves_noalloc if noalloc else self._lib.pots_hash_leaves
+        bad = fn(n, _addr(hb), *map(_addr, arrs), _addr(out), max(1, int(threads)))
         if bad == _SIZE_MAX:
-            raise NativeError("pots_hash_leaves failed: "
-                              + self._lib.pots_last_error().decode())
+            raise NativeError(f"{fn.__name__} failed: " + self._lib.pots_last_error().decode())
         return out, int(bad)
 
     def all_finite(self, ptr: int, nbytes: int, kind: int, *, threads: int = 1) -> bool:
