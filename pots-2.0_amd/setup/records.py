@@ -74,17 +74,3 @@ def encode_record(rec: Record) -> bytes:
     """The record's leaf bytes."""
     return (struct.pack(">BBI", TAG_RECORD, INT32_CODE, len(rec))
             + _raw(rec.ids) + _raw(rec.targets) + _raw(rec.mask))
-
-
-def decode_record(b: bytes) -> Record:
-    """The record of canonical leaf bytes; anything else raises ``RecordError``."""
-    b = bytes(b)
-    if len(b) < 6:
-        raise RecordError("record too short")
-    tag, code, n = struct.unpack(">BBI", b[:6])
-    if tag != TAG_RECORD or code != INT32_CODE:
-        raise RecordError(f"bad record header tag={tag:#x} dtype={code:#x}")
-    if len(b) != 6 + 12 * n:
-        raise RecordError(f"record length field {n} does not match {len(b)} bytes")
-    arr = torch.frombuffer(bytearray(b[6:]), dtype=torch.int32)
-    return Record(ids=arr[:n].clone(), targets=arr[n:2 * n].clone(), mask=arr[2 * n:].clone())

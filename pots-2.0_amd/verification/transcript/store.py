@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import abc
 import json
+import os
 import shutil
 from collections.abc import Sequence
 from pathlib import Path
@@ -142,7 +143,7 @@ class InMemoryStore(TranscriptStore):
         return list(self._dataset_paths[i])
 
 
-# ---- on disk (reference store.py:244-380) -------------------------------------------------
+# ---- on disk (the reference's files, store.py:244-380) -----------------------------------
 
 LEAF_FILE = "leaf_{:05d}.pt"
 META_FILE = "meta.json"
@@ -152,50 +153,61 @@ RECORD_KEYS = ("ids", "mask", "targets")  # the dict a record leaf is saved as, 
 
 
 def savable(t: torch.Tensor) -> torch.Tensor:
-    """``t`` detached, copied if it does not own exactly its storage: ``torch.save`` writes a
-    tensor's whole storage, so a view would carry its base's bytes into the file."""
+    """A detached tensor that ``torch.save`` writes without foreign bytes: ``torch.save``
+    writes a tensor's whole storage, so a view (an attention member of a batched output, a
+    record sliced out of ``D``) is copied into a storage of its own first."""
     t = t.detach()
-    owns = t.storage_offset() == 0 and \
-        t.untyped_storage().nbytes() == t.numel() * t.element_size()
-    return t if owns else t.clone()
+    if t.storage_offset() != 0 or t.untyped_storage().nbytes() != t.nbytes:
+        return t.clone()
+    return t
 
 
 def disk_object(obj: Any) -> Any:
-    """What ``torch.save`` writes for one leaf: the tensor, or a record's three tensors."""
+    """The object one leaf file holds: the tensor itself, or a record's three tensors as a
+    dict keyed by :data:`RECORD_KEYS`."""
+    if isinstance(obj, Record):
+        return {"ids": savable(obj.ids), "mask": savable(obj.mask),
+                "targets": savable(obj.targets)}
     if isinstance(obj, torch.Tensor):
         return savable(obj)
-    if isinstance(obj, Record):
-        return {k: savable(getattr(obj, k)) for k in RECORD_KEYS}
     raise TypeError(f"unsupported leaf object {type(obj).__name__}")
 
 
 def leaf_object(index: int, obj: Any) -> Any:
-    """The leaf a loaded file holds; anything but a tensor or a record's dict is
-    :class:`LeafReadError`, and a dict that is no valid record raises ``RecordError``."""
+    """The leaf a loaded file holds. A tensor is served as it is; a dict with exactly the
+    record keys becomes a :class:`Record` (whose own checks raise ``RecordError``); anything
+    else is :class:`LeafReadError`."""
     if isinstance(obj, torch.Tensor):
         return obj
-    if isinstance(obj, dict) and tuple(sorted(obj)) == RECORD_KEYS:
-        return Record(**obj)
-    raise LeafReadError(f"leaf {index}: the stored object is a {type(obj).__name__}, not a leaf")
+    if isinstance(obj, dict) and set(obj) == set(RECORD_KEYS):
+        return Record(ids=obj["ids"], targets=obj["targets"], mask=obj["mask"])
+    raise LeafReadError(f"leaf {index} holds a {type(obj).__name__}, which is not a leaf")
 
 
-def _hex_digests(value: Any, what: str) -> list[bytes]:
+def _hexes(value: Any, what: str) -> list[bytes]:
+    """A JSON list of hex strings as digests' bytes; anything else is :class:`LeafReadError`."""
     if not isinstance(value, list):
-        raise LeafReadError(f"{what} is not a list")
-    try:
-        return [bytes.fromhex(x) for x in value]
-    except (TypeError, ValueError) as e:
-        raise LeafReadError(f"{what} is not a list of hex digests") from e
+        raise LeafReadError(f"{what}: expected a list of hex digests, got "
+                            f"{type(value).__name__}")
+    out = []
+    for x in value:
+        if not isinstance(x, str):
+            raise LeafReadError(f"{what}: a {type(x).__name__} where a hex digest belongs")
+        try:
+            out.append(bytes.fromhex(x))
+        except ValueError as e:
+            raise LeafReadError(f"{what}: {x[:20]!r} is not hex") from e
+    return out
 
 
 class DiskStore(TranscriptStore):
-    """One committed step in its directory, read back file by file.
+    """One committed step in its own directory, read back file by file.
 
-    :meth:`write` stores a step and opens it; ``DiskStore(directory)`` opens a written one and
-    reads nothing yet. :meth:`leaf`, :attr:`root` and the paths read their files on every
-    call: a file that is missing (``IndexError`` for a leaf) or cannot be read
-    (:class:`LeafReadError`) is bad prover data at the check that reads it. Leaves load with
-    ``weights_only=True``, which rebuilds tensors and plain containers and runs nothing else.
+    :meth:`write` stores a step and opens it; ``DiskStore(directory)`` opens a stored one
+    without reading anything. Every :meth:`leaf`, :attr:`root` and path reads its file again,
+    so a file that is missing (``IndexError`` for a leaf) or unreadable (:class:`LeafReadError`)
+    is prover data that fails at the check reading it. Leaves load with ``weights_only=True``,
+    which rebuilds tensors and plain containers and runs nothing else.
     """
 
     def __init__(self, directory: str | Path) -> None:
@@ -204,29 +216,36 @@ class DiskStore(TranscriptStore):
     @classmethod
     def write(cls, directory: str | Path, c: Any, leaves: Sequence[Any], tree: MerkleTree,
               dataset_paths: Sequence[Sequence[bytes]] | None = None) -> DiskStore:
-        """Store ``leaves`` and their ``tree`` (and each record's path into ``h_D``) in
-        ``directory``, replacing what it held. ``meta.json`` goes last, so a directory without
-        it is an unfinished write; a write that fails removes the directory."""
+        """Store the committed ``leaves``, their ``tree`` and each record's path into ``h_D``
+        as ``directory``, replacing what it held, and open it. The files go into a sibling
+        staging directory, the metadata last, which is renamed to ``directory`` only when
+        complete: ``directory`` never holds a partial step, and after a failed write it does
+        not exist."""
         if dataset_paths is not None and len(dataset_paths) != c.n_s:
             raise ValueError(f"{len(dataset_paths)} dataset paths for {c.n_s} records")
         if len(leaves) != tree.n_leaves:
             raise ValueError(f"{len(leaves)} leaves for a tree of {tree.n_leaves}")
-        d = Path(directory)
-        if d.exists():
-            shutil.rmtree(d)
-        d.mkdir(parents=True)
+        target = Path(directory)
+        staging = target.with_name(f".{target.name}.partial-{os.getpid()}")
+        for old in (target, staging):
+            if old.exists():
+                shutil.rmtree(old)
+        staging.mkdir(parents=True)
         try:
             for i, obj in enumerate(leaves):
-                torch.save(disk_object(obj), d / LEAF_FILE.format(i))
-            (d / HASHES_FILE).write_bytes(b"".join(tree.leaf(i) for i in range(tree.n_leaves)))
-            paths = None if dataset_paths is None else \
-                [[bytes(h).hex() for h in p] for p in dataset_paths]
-            (d / META_FILE).write_text(json.dumps(
-                {"format": DISK_FORMAT, "root": tree.root.hex(), "dataset_paths": paths}))
+                torch.save(disk_object(obj), staging / LEAF_FILE.format(i))
+            with open(staging / HASHES_FILE, "wb") as f:
+                for i in range(tree.n_leaves):
+                    f.write(tree.leaf(i))
+            meta = {"format": DISK_FORMAT, "root": tree.root.hex(), "dataset_paths": None}
+            if dataset_paths is not None:
+                meta["dataset_paths"] = [[bytes(h).hex() for h in p] for p in dataset_paths]
+            (staging / META_FILE).write_text(json.dumps(meta))
+            staging.rename(target)
         except BaseException:
-            shutil.rmtree(d, ignore_errors=True)
+            shutil.rmtree(staging, ignore_errors=True)
             raise
-        return cls(d)
+        return cls(target)
 
     def leaf_path(self, index: int) -> Path:
         return self.directory / LEAF_FILE.format(index)
@@ -235,41 +254,41 @@ class DiskStore(TranscriptStore):
         try:
             meta = json.loads((self.directory / META_FILE).read_text())
         except (OSError, ValueError) as e:
-            raise LeafReadError(f"store metadata unreadable: {type(e).__name__}: {e}") from e
+            raise LeafReadError(f"cannot read {META_FILE}: {type(e).__name__}: {e}") from e
         if not isinstance(meta, dict) or meta.get("format") != DISK_FORMAT:
-            raise LeafReadError("store metadata has an unknown format")
+            raise LeafReadError(f"{META_FILE} is not in store format {DISK_FORMAT}")
         return meta
 
     def leaf(self, index: int) -> Any:
-        if not isinstance(index, int) or index < 0:
-            raise IndexError(f"leaf index {index!r} out of range")
-        path = self.leaf_path(index)
-        if not path.is_file():
-            raise IndexError(f"leaf index {index} out of range (no file {path.name})")
+        path = self.leaf_path(index) if isinstance(index, int) and index >= 0 else None
+        if path is None or not path.is_file():
+            raise IndexError(f"no leaf {index!r} in {self.directory.name}")
         try:
             obj = torch.load(path, map_location="cpu", weights_only=True)
-        except Exception as e:  # an unloadable file is bad prover data, not a verifier bug
-            raise LeafReadError(f"leaf {index} unreadable: {type(e).__name__}: {e}") from e
+        except Exception as e:  # a file that does not load is bad prover data
+            raise LeafReadError(f"leaf {index}: {path.name} does not load "
+                                f"({type(e).__name__}: {e})") from e
         return leaf_object(index, obj)
 
     @property
     def root(self) -> bytes:
-        return _hex_digests([self._meta().get("root")], "the root")[0]
+        return _hexes([self._meta().get("root")], "the root")[0]
 
     def leaf_hashes(self) -> list[bytes]:
         """The stored leaf hashes (what the prover claims; the verifier rehashes leaves)."""
         try:
             raw = (self.directory / HASHES_FILE).read_bytes()
         except OSError as e:
-            raise LeafReadError(f"leaf hashes unreadable: {e}") from e
-        if not raw or len(raw) % DIGEST_SIZE:
-            raise LeafReadError(f"a leaf-hash file of {len(raw)} bytes")
-        return [raw[i:i + DIGEST_SIZE] for i in range(0, len(raw), DIGEST_SIZE)]
+            raise LeafReadError(f"cannot read {HASHES_FILE}: {e}") from e
+        n, rest = divmod(len(raw), DIGEST_SIZE)
+        if n == 0 or rest:
+            raise LeafReadError(f"{HASHES_FILE} holds {len(raw)} bytes, not whole digests")
+        return [raw[DIGEST_SIZE * i:DIGEST_SIZE * (i + 1)] for i in range(n)]
 
     def path(self, index: int) -> list[bytes]:
         hashes = self.leaf_hashes()
-        if not 0 <= index < len(hashes):
-            raise IndexError(f"leaf index {index} out of range")
+        if not (isinstance(index, int) and 0 <= index < len(hashes)):
+            raise IndexError(f"no leaf {index!r} among {len(hashes)}")
         return MerkleTree(hashes).path(index)
 
     def dataset_path(self, i: int) -> list[bytes]:
@@ -278,7 +297,7 @@ class DiskStore(TranscriptStore):
             raise LookupError("this store was written without dataset paths")
         if not isinstance(paths, list):
             raise LeafReadError("the dataset paths are not a list")
-        return _hex_digests(paths[i], f"dataset path {i}")
+        return _hexes(paths[i], f"dataset path {i}")
 
     def remove(self) -> None:
         """Delete the step's directory."""
@@ -289,20 +308,21 @@ class DiskStore(TranscriptStore):
 
 
 class StoreHandoff(abc.ABC):
-    """How a run loop gives step ``t``'s committed leaves to the verifier, and discards the
-    store once the step is verified."""
+    """How a run loop passes step ``t``'s committed leaves to the verifier, and drops the store
+    once the step is verified."""
 
     @abc.abstractmethod
     def hold(self, c: Any, t: int, leaves: list[Any], tree: MerkleTree,
              dataset_paths: Sequence[Sequence[bytes]] | None = None) -> TranscriptStore:
         """The store over the committed ``leaves``."""
 
-    def release(self, store: TranscriptStore) -> None:  # noqa: B027 (nothing to free in memory)
-        """Discard ``store``."""
+    def release(self, store: TranscriptStore) -> None:
+        """Drop ``store``. A hand-off that keeps nothing of its own has nothing to do."""
+        return None
 
 
 class InMemoryHandoff(StoreHandoff):
-    """Keep references to the leaves (:meth:`InMemoryStore.hold`)."""
+    """The leaves stay where they are; the store keeps references (:meth:`InMemoryStore.hold`)."""
 
     def hold(self, c: Any, t: int, leaves: list[Any], tree: MerkleTree,
              dataset_paths: Sequence[Sequence[bytes]] | None = None) -> InMemoryStore:
@@ -313,17 +333,19 @@ IN_MEMORY = InMemoryHandoff()
 
 
 class DiskHandoff(StoreHandoff):
-    """Write each step to ``directory/step_<t>/`` and serve it as a :class:`DiskStore`;
-    :meth:`release` deletes the step's directory unless ``keep``."""
+    """Each step is written to ``directory/step_<t>/`` and served as a :class:`DiskStore`;
+    releasing it deletes that directory unless ``keep``, so a run holds one step on disk."""
 
     def __init__(self, directory: str | Path, *, keep: bool = False) -> None:
-        self.directory = Path(directory)
-        self.keep = keep
+        self.directory, self.keep = Path(directory), keep
+
+    def step_directory(self, t: int) -> Path:
+        return self.directory / f"step_{t}"
 
     def hold(self, c: Any, t: int, leaves: list[Any], tree: MerkleTree,
              dataset_paths: Sequence[Sequence[bytes]] | None = None) -> DiskStore:
-        return DiskStore.write(self.directory / f"step_{t}", c, leaves, tree, dataset_paths)
+        return DiskStore.write(self.step_directory(t), c, leaves, tree, dataset_paths)
 
     def release(self, store: TranscriptStore) -> None:
-        if not self.keep and isinstance(store, DiskStore):
+        if isinstance(store, DiskStore) and not self.keep:
             store.remove()
