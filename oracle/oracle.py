@@ -32,8 +32,11 @@ known-answer tests (``tests/verification/verifier/matmul_check/test_challenges.p
 ``tests/verification/commitment/test_merkle.py:27-34``, ``test_encoding.py:22-30``,
 ``test_sizing.py:20-25``), BLAKE3's published test vectors for the unkeyed empty and
 short inputs, agreement with the independent recursive BLAKE3 of ``blake3_tree.py`` on
-multi-chunk inputs, brute-force tree shapes, and the closed-form invariants of the Freivalds
-rows (a forged entry stands out, bias as a ones column, U <= nu, scale invariance), and the
+multi-chunk inputs, brute-force tree shapes, the closed forms of every Freivalds column
+(all-ones operands: nu = ||(|P|1)|| = sqrt(n) q w, ||P||_F = q sqrt(n w), U^2 = n q w;
+non-negative operands: kappa = 1; integer operands with one planted entry: residual j equals
+|delta r[col, j]| exactly in fp64), their invariants (a forged entry stands out, bias as a
+ones column, U <= nu, scale invariance), and the
 update identity's exact small cases (R = 0 for an exactly rounded step, closed-form ρ for
 power-of-two entries, 0/0 and r/0, an fp32 quotient that underflows) together with the
 outcomes the reference's own update-identity tests state; see ``tests/test_oracle.py``.

@@ -307,6 +307,67 @@ def test_u_is_the_term_frobenius_norm_and_below_nu():
     assert math.sqrt(row[3]) <= row[0] * (1 + 1e-6)
 
 
+@pytest.mark.parametrize("row_fn", [O.measure_product_row, O.measure_row_f64])
+@pytest.mark.parametrize("n,q,w", [(5, 7, 3), (16, 64, 40), (33, 9, 128)])
+def test_all_ones_operands_give_the_closed_forms(row_fn, n, q, w):
+    """A = 1[n,q], B = 1[q,w], P = A·B = q·1[n,w]: every row of |A|(|B|1) and of |P|·1 is
+    q·w, so ν = ‖|P|·1‖ = √n·q·w; ‖P‖_F = q·√(n·w); U² = Σ A²(B²1) = n·q·w; the residuals
+    are 0: exactly in fp64, and within fp32 rounding (below one fp32 band unit) in the fp32
+    formulas. The other columns are small integers' sums: exact in both."""
+    a, b = torch.ones(n, q), torch.ones(q, w)
+    p = torch.full((n, w), float(q))
+    r = O.challenge_matrices(bytes(32), [9], 3, w)[0]
+    nu, p_abs1, p_norm, u2, bias_sq, *res = row_fn(a, b, p, r)
+    assert nu == pytest.approx(math.sqrt(n) * q * w, rel=1e-7)
+    assert p_abs1 == pytest.approx(math.sqrt(n) * q * w, rel=1e-7)
+    assert p_norm == pytest.approx(q * math.sqrt(n * w), rel=1e-7)
+    assert u2 == n * q * w and bias_sq == 0.0
+    if row_fn is O.measure_row_f64:
+        assert res == [0.0, 0.0, 0.0]
+    else:
+        unit = O.finish_row([nu, p_abs1, p_norm, u2, bias_sq, *res], q=q, n=n,
+                            eps_in=2**-24, eps_acc=2**-24)["unit"]
+        assert max(res) <= unit
+
+
+def test_non_negative_operands_have_no_cancellation():
+    """With A, B ≥ 0, |A|(|B|1) = A(B1) = P·1 = |P|·1, so κ = ν/‖|P|·1‖ = 1 to rounding; a
+    sign flip in one entry of A lowers ‖|P|·1‖ below ν."""
+    g = torch.Generator().manual_seed(4)
+    a, b = torch.rand(24, 16, generator=g), torch.rand(16, 30, generator=g)
+    p = (a.double() @ b.double()).float()
+    r = O.challenge_matrices(bytes(32), [2], 1, 30)[0]
+    for row_fn in (O.measure_product_row, O.measure_row_f64):
+        mp = O.finish_row(row_fn(a, b, p, r), q=16, n=24, eps_in=2**-24, eps_acc=2**-24)
+        assert mp["kappa"] == pytest.approx(1.0, abs=1e-6)
+    a2 = a.clone()
+    a2[:, 3] = -a2[:, 3]
+    p2 = (a2.double() @ b.double()).float()
+    mp = O.finish_row(O.measure_row_f64(a2, b, p2, r), q=16, n=24, eps_in=2**-24,
+                      eps_acc=2**-24)
+    assert mp["kappa"] > 1.0 + 1e-3
+
+
+def test_planted_residual_is_delta_times_its_challenge_entry():
+    """Integer operands make A·(B·r) − P·r exact in fp64, so an honest P has residual 0 and
+    P + δ·e_i·e_jᵀ has residual |δ·r[j, col]| in column ``col``: a swapped column or a wrong
+    sign fails it."""
+    g = torch.Generator().manual_seed(6)
+    a = torch.randint(-3, 4, (12, 10), generator=g).float()
+    b = torch.randint(-3, 4, (10, 14), generator=g).float()
+    p = a @ b
+    r = O.challenge_matrices(bytes(range(32)), [11], 4, 14)[0]
+    assert O.measure_row_f64(a, b, p, r)[5:] == [0.0] * 4
+    p2 = p.clone()
+    p2[7, 5] += 0.5
+    res = O.measure_row_f64(a, b, p2, r)[5:]
+    assert res == [abs(0.5 * float(r[5, col])) for col in range(4)]
+    # the fp32 formulas agree to within their own rounding (one fp32 band unit)
+    row32 = O.measure_product_row(a, b, p2, r)
+    unit = O.finish_row(row32, q=10, n=12, eps_in=2**-24, eps_acc=2**-24)["unit"]
+    assert row32[5:] == pytest.approx(res, rel=0, abs=unit)
+
+
 def test_safe_norm_large_and_zero():
     x = torch.tensor([3e19, -3e19, 1.0])
     assert math.isfinite(float(O.safe_norm(x)))

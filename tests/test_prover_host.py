@@ -214,3 +214,37 @@ def test_decoder_labeling_fills_every_slot_with_its_own_product(qkv_bias, n_kv):
     name = c.w(1, "up")
     g = step.products[c.product_index(c.linear_weights[name][0]) - c.n_s - c.n_w]
     assert torch.allclose(step.w_next[name], w0[name] - c.eta * g, rtol=0, atol=1e-7)
+
+
+def test_reference_inventory_literals():
+    """The reference's declaration numbers (tests/verification/computation/test_decoder.py
+    :167-184 at SmolLM2-135M, 4×128 tokens; test_sizing.py:45-48 and test_decoder.py:163-165
+    for the product count)."""
+    import math
+    from collections import Counter
+
+    from verification.computation.instances.decoder import matmul_count_decoder, smollm2_135m
+    from verification.computation.interface import ProductKind as K
+    c = smollm2_135m(n_s=4, n=128)
+    assert (c.M, c.n_w, c.n_leaves) == (7113, 272, 7661)
+    assert sum(math.prod(s) for s in c.weight_shapes.values()) == 134_515_008
+    assert Counter(p.kind for p in c.products) == {K.FORWARD: 2371, K.INPUT_GRAD: 211,
+                                                   K.WEIGHT_GRAD: 211, K.OPERAND_GRAD: 4320}
+    linears = ("q", "k", "v", "o", "gate", "up", "down")
+    q = {c.product_class(p): p.q for p in c.products}
+    assert q == {"Y_q": 576, "Y_k": 576, "Y_v": 576, "Y_o": 576, "Y_gate": 576, "Y_up": 576,
+                 "Y_down": 1536, "S": 64, "O": 128, "Lambda": 576,
+                 "dF": 49152, "G_E_head": 512,
+                 "dX_q": 576, "dX_k": 192, "dX_v": 192, "dX_o": 576, "dX_gate": 1536,
+                 "dX_up": 1536, "dX_down": 576,
+                 **{f"G_{x}": 512 for x in linears},
+                 "dA": 64, "dV": 128, "dQ": 128, "dK": 128}
+    per_member = c.L * c.n_s * c.n_h
+    assert Counter(c.product_class(p) for p in c.products) == Counter(
+        {**{f"{r}_{x}": c.L for r in ("Y", "dX", "G") for x in linears},
+         **{r: per_member for r in ("S", "O", "dA", "dV", "dQ", "dK")},
+         "Lambda": 1, "dF": 1, "G_E_head": 1})
+    assert all(p.width == p.p_shape[1] for p in c.products)
+    assert matmul_count_decoder(30, 4, 9) == 7_113
+    assert matmul_count_decoder(30, 128, 9) == 207_993
+    assert matmul_count_decoder(16, 128, 32) == 393_555
