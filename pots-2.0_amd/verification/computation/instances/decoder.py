@@ -226,7 +226,16 @@ class DecoderComputation(DeclaredComputation):
 
     def build_model(self) -> torch.nn.Module:
         """transformers' causal LM of this shape (Qwen2 with q/k/v biases, else Llama), eager
-        attention, random init, in the computation's dtype on the current default device."""
+        attention, random init, fp32, in eval mode (no dropout), on the current default device.
+
+        The weights are the fp32 masters the layout declares. A bf16 computation would run
+        under autocast over those masters (reference decoder.py:568-598), which the prover side
+        of this build does not do: it refuses such a computation rather than commit bf16
+        weight leaves where fp32 ones are declared."""
+        if self.compute_dtype != self.weight_dtype:
+            raise NotImplementedError(
+                f"the prover side runs the decoder in its weight dtype ({self.weight_dtype}); "
+                f"{self.compute_dtype} compute over fp32 masters (autocast) is not built")
         from transformers import LlamaConfig, LlamaForCausalLM, Qwen2Config, Qwen2ForCausalLM
         cfg_cls, model_cls = (Qwen2Config, Qwen2ForCausalLM) if self.qkv_bias else \
             (LlamaConfig, LlamaForCausalLM)
@@ -240,7 +249,13 @@ class DecoderComputation(DeclaredComputation):
         cfg._attn_implementation = "eager"
         if self.head_blocks != 1:
             raise NotImplementedError("the prover side takes one head block")
-        return model_cls(cfg).to(self.compute_dtype)
+        cfg.attention_dropout = 0.0
+        model = model_cls(cfg).to(self.weight_dtype).eval()
+        active = [name for name, mod in model.named_modules()
+                  if isinstance(mod, torch.nn.Dropout) and mod.p > 0]
+        if active:
+            raise ValueError(f"dropout is active in {active[:3]}: a step must be deterministic")
+        return model
 
     def loss(self, model: torch.nn.Module, records) -> torch.Tensor:
         """Mean cross-entropy of the targets over the masked tokens."""

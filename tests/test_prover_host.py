@@ -248,3 +248,17 @@ def test_reference_inventory_literals():
     assert matmul_count_decoder(30, 4, 9) == 7_113
     assert matmul_count_decoder(30, 128, 9) == 207_993
     assert matmul_count_decoder(16, 128, 32) == 393_555
+
+
+def test_decoder_prover_refuses_bf16_compute_over_fp32_masters():
+    """A bf16 decoder would need autocast over fp32 masters on the prover side; rather than
+    commit bf16 weight leaves where fp32 ones are declared, building its model refuses."""
+    from verification.computation.instances.decoder import DecoderComputation
+    c = DecoderComputation(L=1, d=16, d_f=32, n_h=2, n_kv=1, n_v=40, n_s=1, n=8,
+                           compute_dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="autocast"):
+        c.build_model()
+    fp32 = DecoderComputation(L=1, d=16, d_f=32, n_h=2, n_kv=1, n_v=40, n_s=1, n=8)
+    model = fp32.build_model()
+    assert not model.training
+    assert all(p.dtype == torch.float32 for p in model.parameters())
