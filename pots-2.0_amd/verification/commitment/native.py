@@ -18,6 +18,7 @@ runtime instead of a second copy.
 
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
 import threading
@@ -31,6 +32,24 @@ import torch
 
 PACKAGE_ROOT = Path(__file__).resolve().parents[2]
 LIB_PATH = Path(os.environ.get("POTS_MI355X_LIB", PACKAGE_ROOT / "libpots_mi355x.so"))
+
+# Every live plan, so that the process frees their device memory at exit while the HIP runtime
+# is certainly up: an atexit handler runs before the interpreter tears its objects down, and
+# the runtime's own destructors run after that. A plan closed earlier leaves the set by itself.
+_LIVE_PLANS: weakref.WeakSet = weakref.WeakSet()
+
+
+@atexit.register
+def _close_live_plans() -> None:
+    # leaf plans first: a fused leaf plan writes into its Freivalds plan's memory
+    plans = sorted(list(_LIVE_PLANS), key=lambda p: not isinstance(p, LeafPlan))
+    if plans and torch.cuda.is_available():
+        torch.cuda.synchronize()
+    for plan in plans:
+        try:
+            plan.close()
+        except Exception:
+            pass
 
 KIND_NONE, KIND_F32, KIND_BF16, KIND_F16 = 0, 1, 2, 3
 FINITE_KIND: dict[torch.dtype, int] = {
@@ -326,6 +345,7 @@ class LeafPlan:
                 _addr(kd), fuse._h, ctypes.byref(h)), "pots_leaf_plan_create_fused")
             fuse._fused_leaf = weakref.ref(self)
         self._h = h
+        _LIVE_PLANS.add(self)
         # The chunk stage of a fused plan writes into the Freivalds plan's records and reads
         # its challenges: the Freivalds plan lives at least as long.
         self._fv = fuse
@@ -491,6 +511,7 @@ class FvPlan:
         lib._check(lib._lib.pots_fv_plan_create(n, arr.ctypes.data, k, int(bool(guard)),
                                                 ctypes.byref(h)), "pots_fv_plan_create")
         self._lib, self._h, self._keep = lib, h, keep
+        _LIVE_PLANS.add(self)
         self._fused_leaf = None  # weak reference to the leaf plan fused with this one
         self.n, self.k = n, k
         self.widths = [pr.p.shape[1] for pr in products]
@@ -630,6 +651,7 @@ class UpdatePlan:
                                                     float(np.float32(eps_w)), ctypes.byref(h)),
                    "pots_update_plan_create")
         self._lib, self._h, self._keep = lib, h, keep
+        _LIVE_PLANS.add(self)
         self.n = n
         self.device = weights[0].w_t.device
         self.bytes = int(lib._lib.pots_update_plan_bytes(h))
