@@ -22,12 +22,16 @@ not built: the labeler returns the captured operands with the products.
 
 from __future__ import annotations
 
+from collections.abc import Sequence
 from functools import cached_property
+from typing import Any
 
 import torch
 
 from verification.computation.interface import (DeclaredComputation, LabelingError,
-                                               ProductKind, ProductSpec)
+                                               ProductKind, ProductSpec, Replay, load_weights)
+from verification.computation.substitution import (CallPlan, CommittedProducts, ReplayError,
+                                                   plan_calls)
 
 LINEARS = ("q", "k", "v", "o", "gate", "up", "down")
 _LINEAR_PATH = {
@@ -271,7 +275,25 @@ class DecoderComputation(DeclaredComputation):
     def label(self, capture, model: torch.nn.Module) -> list[torch.Tensor]:
         return self.label_with_operands(capture, model)[0]
 
-    def label_with_operands(self, capture, model: torch.nn.Module
+    # ---- verifier side --------------------------------------------------------------------
+
+    def replay(self, leaves: Any) -> Replay:
+        """Check 5's operands: the prover's captured ones when given (``use_operands``), else
+        the replay of the committed leaves (:class:`DecoderReplay`)."""
+        given = getattr(self, "_operands", None)
+        return given if given is not None else DecoderReplay(self, leaves)
+
+    def call_plan(self, model: torch.nn.Module, records: Sequence[Any]) -> CallPlan:
+        """Which call of a training pass fills which slot; the same for every step of this
+        computation, so it is planned once (``substitution.plan_calls``)."""
+        plan = getattr(self, "_call_plan", None)
+        if plan is None:
+            plan = self._call_plan = plan_calls(self, model, records)
+        return plan
+
+    def label_with_operands(self, capture, model: torch.nn.Module,
+                            call_slots: dict[int, list[tuple[int | None, str, bool]]] | None
+                            = None
                             ) -> tuple[list[torch.Tensor], dict[int, tuple[torch.Tensor,
                                                                            torch.Tensor]]]:
         """``(P_1..P_M, {m: (A_m, B_m)})`` from the capture, mapped by operand identity.
@@ -284,6 +306,10 @@ class DecoderComputation(DeclaredComputation):
         ``O``'s ``A``, ``dQ`` ``S``'s ``B``, and the batched product reading ``S``'s ``A`` is
         ``K̃``'s gradient ``Q̃ᵀ·δS``, whose transpose is the ``dK`` leaf with operands
         ``(δSᵀ, Q̃)``.
+
+        ``call_slots``, when given, receives for each labeled call (by capture index) the slots
+        its output fills: ``(member index or None, slot name, transposed)``, ``transposed``
+        when the slot holds the member's output transposed (the ``dK`` leaves).
         """
         if len(capture.glue_outer) > 1:
             raise LabelingError(f"{len(capture.glue_outer)} q=1 products; only the rotary "
@@ -292,7 +318,9 @@ class DecoderComputation(DeclaredComputation):
         slots: dict[str, tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = {}
         spec_by_name = {s.name: s for s in self.products}
 
-        def fill(name, a, b, p):
+        def fill(name, a, b, p, rec=None, member=None, transposed=False):
+            if call_slots is not None and rec is not None:
+                call_slots.setdefault(rec.index, []).append((member, name, transposed))
             if name in slots:
                 raise LabelingError(f"slot {name} filled twice")
             spec = spec_by_name.get(name)
@@ -314,7 +342,7 @@ class DecoderComputation(DeclaredComputation):
                 if transpose_out:  # K̃'s gradient Q̃ᵀ·δS: the leaf is (δSᵀ·Q̃)
                     a, b, p = rec.b[i].transpose(0, 1), rec.a[i].transpose(0, 1), \
                         rec.out[i].transpose(0, 1).contiguous()
-                fill(f"L{l}.{role}[{s_},{h}]", a, b, p)
+                fill(f"L{l}.{role}[{s_},{h}]", a, b, p, rec, i, transpose_out)
 
         fwd = [r for r in capture.records if r.phase == "forward"]
         bwd = [r for r in capture.records if r.phase == "backward"]
@@ -342,10 +370,10 @@ class DecoderComputation(DeclaredComputation):
                 l, x = by_weight[name]
                 if x == "q":
                     layer, pending = l, []
-                fill(f"L{l}.Y_{x}", rec.a, rec.b, rec.out)
+                fill(f"L{l}.Y_{x}", rec.a, rec.b, rec.out, rec)
             elif name == self.w_out and rec.out.shape[-1] == self.n_v:
                 head_in = rec.a
-                fill(self.head_name("Lambda", 0), rec.a, rec.b, rec.out)
+                fill(self.head_name("Lambda", 0), rec.a, rec.b, rec.out, rec)
             else:
                 raise LabelingError(f"forward record #{rec.index} matches no slot")
         for l in range(1, self.L + 1):
@@ -380,18 +408,18 @@ class DecoderComputation(DeclaredComputation):
                 continue
             if name in by_weight:
                 l, x = by_weight[name]
-                fill(f"L{l}.dX_{x}", rec.a, rec.b, rec.out)
+                fill(f"L{l}.dX_{x}", rec.a, rec.b, rec.out, rec)
             elif name == self.w_out:
-                fill(self.head_name("dF", 0), rec.a, rec.b, rec.out)
+                fill(self.head_name("dF", 0), rec.a, rec.b, rec.out, rec)
             else:
                 owner = grad_owner.get(rec.out_info.storage_ptr)
                 if owner in by_weight and capture.is_output_of(
                         model.get_parameter(owner).grad, rec):
                     l, x = by_weight[owner]
-                    fill(f"L{l}.G_{x}", rec.a, rec.b, rec.out)
+                    fill(f"L{l}.G_{x}", rec.a, rec.b, rec.out, rec)
                 elif head_in is not None and storage(rec.b) == storage(head_in) and \
                         rec.out.shape == (self.n_v, self.d):
-                    fill(self.head_name("G", 0), rec.a, rec.b, rec.out)
+                    fill(self.head_name("G", 0), rec.a, rec.b, rec.out, rec)
                 else:
                     raise LabelingError(f"backward record #{rec.index} matches no slot")
         missing = [s.name for s in self.products if s.name not in slots]
@@ -400,6 +428,68 @@ class DecoderComputation(DeclaredComputation):
         products = [slots[s.name][2] for s in self.products]
         operands = {s.m: slots[s.name][:2] for s in self.products}
         return products, operands
+
+
+class DecoderReplay(Replay):
+    """The verifier's glue replay of one decoder step, from the committed leaves only
+    (reference decoder.py:1142-1751, checks 3, 5 and 6b).
+
+    The model is built at the computation's shape and loaded with the committed ``W_t``; one
+    training pass on the committed batch runs with every checked product replaced by its
+    committed leaf (``substitution.CommittedProducts``), so every operand a product receives
+    (``X·`` after RMSNorm, ``Q̃, K̃`` after RoPE and ``repeat_kv``, the attention
+    probabilities, ``δY`` through SiLU and softmax, …) is glue recomputed from committed
+    values. The operands are kept as the ops received them and served in any order, each
+    checked unchanged since; the backward leaves each glue weight's full gradient (the norms'
+    γ, the biases and, tied, the embedding: its own backward plus the committed ``G_E_head``)
+    for check 6b. A pass that departs from the plan is :class:`ReplayError`, a verifier bug;
+    a leaf that fails to read raises its own error, which check 5 maps to a rejection.
+    """
+
+    def __init__(self, computation: DecoderComputation, leaves: Any,
+                 device: torch.device | str | None = None) -> None:
+        c = self.c = computation
+        self.leaves = leaves
+        if device is None:
+            device = torch.device("cuda", torch.cuda.current_device()) \
+                if torch.cuda.is_available() else "cpu"
+        self.device = torch.device(device)
+        records = [self._get(c.record_index(i)) for i in range(c.n_s)]
+        with self.device:
+            model = c.build_model()
+        load_weights(c, model, {n: self._get(c.w_t_index(n)) for n in c.weight_names})
+        plan = c.call_plan(model, records)
+        index = {spec.name: c.product_index(spec.m) for spec in c.products}
+        mode = CommittedProducts(plan, lambda slot: self._get(index[slot]))
+        model.zero_grad(set_to_none=True)
+        with torch.enable_grad(), mode:
+            c.forward_backward(model, records, mode.phase)
+        if mode.calls != plan.n_calls or len(mode.held) != c.M:
+            raise ReplayError(f"the replay made {mode.calls} calls for {len(mode.held)} slots; "
+                              f"the plan has {plan.n_calls} calls for {c.M}")
+        self._held = mode.held
+        self._glue = {}
+        for name in c.glue_gradient_weights:
+            g = model.get_parameter(name).grad
+            if g is None:
+                raise ReplayError(f"the replay's backward left no gradient for {name}")
+            self._glue[name] = g.detach()
+
+    def _get(self, index: int) -> Any:
+        reader = getattr(self.leaves, "leaf", None)
+        obj = reader(index) if reader is not None else self.leaves[index]
+        return obj.to(self.device) if isinstance(obj, torch.Tensor) else obj
+
+    def operands(self, m: int) -> tuple[torch.Tensor, torch.Tensor]:
+        name = self.c.product(m).name
+        a, b, va, vb = self._held[name]
+        if a._version != va or b._version != vb:
+            raise ReplayError(f"an operand of {name} changed after its product read it")
+        return a, b
+
+    def glue_gradients(self) -> dict[str, torch.Tensor]:
+        """Each glue weight's full gradient from the replay's backward."""
+        return dict(self._glue)
 
 
 # The configurations the benchmark and the tests use (BASELINE.json's configs).

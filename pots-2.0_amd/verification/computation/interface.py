@@ -173,6 +173,13 @@ class DeclaredComputation(abc.ABC):
         return {}
 
     @property
+    def glue_gradient_weights(self) -> tuple[str, ...]:
+        """Check 6b's weights: those whose gradient is (or includes) glue the replay
+        recomputes, every weight that is not linear, in leaf order (reference
+        interface.py:288-290)."""
+        return tuple(n for n in self.weight_names if n not in self.linear_weights)
+
+    @property
     def weight_dtype(self) -> torch.dtype:
         return torch.float32
 

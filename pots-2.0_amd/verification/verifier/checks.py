@@ -6,9 +6,8 @@ Reference: verification/verifier/checks.py:204-251 (``check_2_commitment``), :25
 the reference's check ids, rejection kinds and detail strings.
 
 Of the reference's order ``4 → 7 → 2 → 6a → 5 → 6b → 2.root`` this build runs
-:data:`DEFAULT_ORDER` = ``7 → 2 → 6a → 5 → 2.root``. Check 4 (the batch anchor into ``h_D`` at
-the schedule's indices) and 6b (the glue weights' update identity, which needs the model
-replay's glue gradients) are not part of it.
+:data:`DEFAULT_ORDER` = ``7 → 2 → 6a → 5 → 6b → 2.root``. Check 4 (the batch anchor into
+``h_D`` at the schedule's indices) is not part of it.
 
 - **Check 7** (check 0 on the first step) hashes the ``W_t`` leaves on the GPU and compares
   them with the hashes the verifier kept: the agreed ``W_0``'s, or step ``t−1``'s
@@ -25,6 +24,8 @@ replay's glue gradients) are not part of it.
   device verdict kernel judges the same rows; the two must agree on the first failure.
 - **Check 6a** streams every linear weight's ``W_t``, ``W_{t+1}`` and gradient product leaves
   once on the GPU and words the first failing weight's rejection as the reference does.
+- **Check 6b** runs the same pass over the glue weights with the gradients check 5's replay
+  recomputed through the glue.
 - **Check 2's root comparison** runs last and compares the Merkle root over check 2's hashes
   (built on the GPU) with the claimed root.
 
@@ -63,7 +64,8 @@ from verification.verifier.context import (
 from verification.verifier.matmul_check.freivalds import ProductMeasure, finish_rows
 
 __all__ = ["DEFAULT_ORDER", "ROOT_SLOT", "CHECKS", "protocol_id", "check_7_chaining",
-           "check_2_commitment", "check_2_root", "check_6a_linear_update", "check_5_matmuls"]
+           "check_2_commitment", "check_2_root", "check_6a_linear_update", "check_5_matmuls",
+           "check_6b_glue_update"]
 
 ROOT_SLOT = "2.root"
 
@@ -186,6 +188,47 @@ def _entry_values(w: native.UpdateWeight, i: int, eta: float, eps_w: float
     return float(r), float(scale)
 
 
+def _update_identity(check_id: str, names: list[str], weights: list[native.UpdateWeight],
+                     c: DeclaredComputation, ctx: StepContext) -> Rejection | None:
+    """One GPU pass of the update identity over ``weights`` (``ρ_max`` bit for bit the
+    reference's, first non-finite ``R`` or scale, first ``ρ`` over ``τ_W``), then recording and
+    judging in declaration order with the reference's wording (checks.py:380-467): the first
+    weight with a non-finite entry, or (when judging) an entry over its band, rejects, and the
+    weights after it are not recorded."""
+    with ctx.timed(f"{check_id}.measure"):
+        plan = native.get().update_plan(weights, c.eta, ctx.eps_w)
+        try:
+            results = native.UpdatePlan.decode(plan.run())
+        finally:
+            plan.close()
+    for name, w, (rho_max, first_nf, first_over) in zip(names, weights, results):
+        ctx.stats.tensors.append(TensorStat(name, check_id, rho_max))
+        if first_nf is not None:
+            r, scale = _entry_values(w, first_nf, c.eta, ctx.eps_w)
+            return ctx.reject(check_id, f"{name}: entry {first_nf} has a non-finite residual "
+                                        f"or bound (|R| = {r:.3e}, scale {scale:.3e})")
+        if ctx.judge and first_over is not None:
+            r, scale = _entry_values(w, first_over, c.eta, ctx.eps_w)
+            tau_w = w.tau_w
+            return ctx.reject(check_id, f"{name}: entry {first_over} has |R| = {r:.3e}, bound "
+                                        f"{tau_w * scale:.3e} (ρ_max = {rho_max:.3g}, "
+                                        f"τ_W = {tau_w:g})")
+    return None
+
+
+def _update_weight(name: str, w_t: torch.Tensor, w_next: torch.Tensor,
+                   parts: list[torch.Tensor], tau_w: float) -> native.UpdateWeight:
+    dev = torch.device("cuda", torch.cuda.current_device())
+    w_t, w_next = w_t.to(dev), w_next.to(dev)
+    parts = [p.to(dev) for p in parts]
+    for t in (w_next, *parts):
+        if tuple(t.shape) != tuple(w_t.shape):
+            raise RuntimeError(f"{name}: gradient or update of shape {tuple(t.shape)} "
+                               f"!= {tuple(w_t.shape)}")
+    return native.UpdateWeight(w_t.contiguous(), w_next.contiguous(),
+                               [p.contiguous() for p in parts], tau_w)
+
+
 @_checked
 def check_6a_linear_update(store: TranscriptStore, c: DeclaredComputation, ctx: StepContext,
                            bands: Bands) -> Rejection | None:
@@ -195,47 +238,55 @@ def check_6a_linear_update(store: TranscriptStore, c: DeclaredComputation, ctx: 
     ``W_t``, ``W_{t+1}`` and the gradient's product leaves are read from check 2's committed
     leaves; one GPU pass over every linear weight gives each weight's ``ρ_max`` (bit for bit
     the reference's), its first non-finite ``R`` or scale and its first ``ρ`` over ``τ_W``.
-    The weights are then recorded and judged in declaration order: the first one with a
-    non-finite entry, or (when judging) an entry over its band, rejects with the reference's
-    wording, and the weights after it are not recorded.
     """
     names = list(c.linear_weights)
     if not names:
         return None
     leaves = ctx.state.committed()
-    dev = torch.device("cuda", torch.cuda.current_device())
     with _guard(ctx, "6a", _AFTER_COMMIT):
-        weights = []
-        for name in names:
-            w_t = leaves.leaf(c.w_t_index(name)).to(dev)
-            w_next = leaves.leaf(c.w_next_index(name)).to(dev)
-            parts = [leaves.leaf(c.product_index(m)).to(dev) for m in c.linear_weights[name]]
-            for t in (w_next, *parts):
-                if tuple(t.shape) != tuple(w_t.shape):
-                    raise RuntimeError(f"{name}: gradient or update of shape {tuple(t.shape)} "
-                                       f"!= {tuple(w_t.shape)}")
-            weights.append(native.UpdateWeight(w_t.contiguous(), w_next.contiguous(),
-                                               [p.contiguous() for p in parts],
-                                               bands.tau_w_for(name)))
-    with ctx.timed("6a.measure"):
-        plan = native.get().update_plan(weights, c.eta, ctx.eps_w)
-        try:
-            results = native.UpdatePlan.decode(plan.run())
-        finally:
-            plan.close()
-    for name, w, (rho_max, first_nf, first_over) in zip(names, weights, results):
-        ctx.stats.tensors.append(TensorStat(name, "6a", rho_max))
-        if first_nf is not None:
-            r, scale = _entry_values(w, first_nf, c.eta, ctx.eps_w)
-            return ctx.reject("6a", f"{name}: entry {first_nf} has a non-finite residual or "
-                                    f"bound (|R| = {r:.3e}, scale {scale:.3e})")
-        if ctx.judge and first_over is not None:
-            r, scale = _entry_values(w, first_over, c.eta, ctx.eps_w)
-            tau_w = w.tau_w
-            return ctx.reject("6a", f"{name}: entry {first_over} has |R| = {r:.3e}, bound "
-                                    f"{tau_w * scale:.3e} (ρ_max = {rho_max:.3g}, "
-                                    f"τ_W = {tau_w:g})")
-    return None
+        weights = [_update_weight(name, leaves.leaf(c.w_t_index(name)),
+                                  leaves.leaf(c.w_next_index(name)),
+                                  [leaves.leaf(c.product_index(m))
+                                   for m in c.linear_weights[name]], bands.tau_w_for(name))
+                   for name in names]
+    return _update_identity("6a", names, weights, c, ctx)
+
+
+# ---- check 6b: the update identity of the glue weights ----------------------------------
+
+
+@_checked
+def check_6b_glue_update(store: TranscriptStore, c: DeclaredComputation, ctx: StepContext,
+                         bands: Bands) -> Rejection | None:
+    """Check 6 for every glue weight (the norms' γ, the biases, the tied embedding), with the
+    gradient check 5's replay recomputed through the glue (reference checks.py:960-995).
+
+    The gradient is the replay's, in fp32; ``W_t`` and ``W_{t+1}`` are check 2's committed
+    leaves; the identity, its ``ρ_max`` and its wording are check 6a's. A replay of the prover's
+    captured operands has no glue to recompute: the step's statistics already say check 5
+    measured the prover's operands, and 6b is not run.
+    """
+    names = list(c.glue_gradient_weights)
+    if not names:
+        return None
+    replay = ctx.state.replay
+    if replay is None:
+        raise RuntimeError("check 6b needs check 5's replay")
+    if getattr(replay, "prover_supplied", False):
+        return None
+    with _guard(ctx, "6b", _AFTER_COMMIT), ctx.timed("6b.glue"):
+        grads = replay.glue_gradients()
+    missing = [name for name in names if name not in grads]
+    if missing:
+        raise RuntimeError(f"the replay returned no glue gradient for {missing}")
+    leaves = ctx.state.committed()
+    with _guard(ctx, "6b", _AFTER_COMMIT):
+        weights = [_update_weight(name, leaves.leaf(c.w_t_index(name)),
+                                  leaves.leaf(c.w_next_index(name)),
+                                  [grads[name].detach().to(torch.float32)],
+                                  bands.tau_w_for(name))
+                   for name in names]
+    return _update_identity("6b", names, weights, c, ctx)
 
 
 # ---- check 5: matmuls -------------------------------------------------------------------
@@ -397,6 +448,7 @@ CHECKS: dict[str, Callable[..., Rejection | None]] = {
     "2": check_2_commitment,
     "6a": check_6a_linear_update,
     "5": check_5_matmuls,
+    "6b": check_6b_glue_update,
     ROOT_SLOT: check_2_root,
 }
-DEFAULT_ORDER: tuple[str, ...] = ("7", "2", "6a", "5", ROOT_SLOT)
+DEFAULT_ORDER: tuple[str, ...] = ("7", "2", "6a", "5", "6b", ROOT_SLOT)

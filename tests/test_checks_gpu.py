@@ -58,7 +58,7 @@ def test_honest_step_accepts_with_stats(lib):
     stats = v.stats[1].products
     assert [s.m for s in stats] == [s.m for s in c.products]
     assert all(max(s.normalized) <= 8.0 for s in stats)
-    assert set(v.timings[1]) == {"7", "2", "6a", "5", "2.root"}
+    assert set(v.timings[1]) == {"7", "2", "6a", "5", "6b", "2.root"}
     assert v.stats[1].operands_from_prover
 
 

@@ -47,7 +47,7 @@ def _mp(nu=1.0, p_abs1=1.0, res=(0.0, 0.0), p_norm=1.0, unit=1e-3, u=1.0):
 
 
 def test_slot_order_and_ids():
-    assert DEFAULT_ORDER == ("7", "2", "6a", "5", "2.root")
+    assert DEFAULT_ORDER == ("7", "2", "6a", "5", "6b", "2.root")
     assert protocol_id("2.root") == "2" and protocol_id("5") == "5"
 
 

@@ -1,12 +1,15 @@
-"""The prover on the GPU and the MLP step verified with its replay (reference
-tests/verification/test_m1_smoke.py: an honest MLP step accepts, a perturbed product rejects).
+"""The prover on the GPU, and its steps verified from the committed leaves alone (reference
+tests/verification/test_m1_smoke.py: an honest MLP step accepts, a perturbed product rejects;
+the decoder's replay, reference decoder.py:1142-1751).
 
 The products stay in HBM (the capture keeps each op's own output) and the commit hashes every
 leaf there; the root must equal the CPU oracle's over the same leaves. The verifier then
 rebuilds every operand from the committed leaves (``MLPReplay``, no captured operands) and
 must accept the honest step through ``Verifier`` and ``DeviceStepVerifier`` alike, and reject
 a step whose committed product was changed at check 5, and one whose ``W_{t+1}`` was changed
-at check 6a.
+at check 6a. A transformers decoder step is verified the same way through ``DecoderReplay``:
+its operands equal the prover's bit for bit, a product forged together with its claimed
+operands is caught at check 5, and a forged glue-weight update at check 6b.
 """
 
 from __future__ import annotations
@@ -128,7 +131,6 @@ def _decoder_prove(seed=0, qkv_bias=True, n_kv=2, perturb=None):
         ids = torch.randint(0, c.n_v, (c.n,), generator=g, dtype=torch.int32)
         records.append(Record(ids, torch.roll(ids, -1), torch.ones(c.n, dtype=torch.int32)))
     step = prove_step(c, model, w0, records, keep_operands=True, perturb=perturb)
-    c.use_operands(step.replay())
     return c, step, commit(c, step)
 
 
@@ -146,24 +148,33 @@ def _decoder_oracle_root(c, leaves):
 @pytest.mark.parametrize("qkv_bias,n_kv", [(True, 2), (False, 4)])
 def test_real_decoder_step_commits_and_verifies(lib, qkv_bias, n_kv):
     """A transformers Qwen2/Llama training step proved on the GPU: the products stay in HBM,
-    the device commit equals the CPU oracle's root, and the verifier accepts the step with the
-    captured operands through the check-level API and the device step alike."""
-    from verification.transcript.store import InMemoryStore
+    the device commit equals the CPU oracle's root, and the verifier accepts the step from the
+    committed leaves alone (the decoder replay serves check 5's operands and check 6b's glue
+    gradients) through the check-level API and the device step alike; the replay's operands
+    are the prover's, bit for bit."""
     from conftest import started_verifier
+    from verification.computation.instances.decoder import DecoderReplay
+    from verification.transcript.store import InMemoryStore
     from verification.verifier.step import DeviceStepVerifier
     c, step, tree = _decoder_prove(seed=7, qkv_bias=qkv_bias, n_kv=n_kv)
     assert step.capture["device_resident"]
     assert tree.root == _decoder_oracle_root(c, step.leaves())
     v = started_verifier(c, step.leaves(), k=2)
     assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
-    assert len(v.stats[1].products) == c.M
-    out = DeviceStepVerifier(c, step.leaves(), lambda s: step.operands[s.m], k=2).run(tree.root)
+    assert len(v.stats[1].products) == c.M and not v.stats[1].operands_from_prover
+    assert [t.weight for t in v.stats[1].tensors if t.check_id == "6b"] == \
+        list(c.glue_gradient_weights)
+    replay = DecoderReplay(c, step.leaves())
+    for spec in c.products[::7]:
+        assert all(torch.equal(x, y) for x, y in zip(replay.operands(spec.m),
+                                                     step.operands[spec.m])), spec.name
+    out = DeviceStepVerifier(c, step.leaves(), lambda s: replay.operands(s.m), k=2).run(tree.root)
     assert out.check is None and out.root == tree.root, out.detail
 
 
 def test_real_decoder_step_with_a_changed_member_rejects_at_check_5(lib):
-    from verification.transcript.store import InMemoryStore
     from conftest import started_verifier
+    from verification.transcript.store import InMemoryStore
     c0, _, _ = _decoder_prove(seed=8)
     spec = next(s for s in c0.products if s.name == "L2.O[1,3]")
     c, step, tree = _decoder_prove(seed=8, perturb={spec.m: lambda p: p.index_add_(
@@ -172,6 +183,50 @@ def test_real_decoder_step_with_a_changed_member_rejects_at_check_5(lib):
         1, InMemoryStore(step.leaves(), tree))
     assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
     assert rej.detail.startswith(f"P_{spec.m} (L2.O[1,3])")
+
+
+def test_forged_operands_are_caught_by_the_replay(lib):
+    """A prover that commits ``P' = A'·B`` for a forged input ``A'`` has a product consistent
+    with the operands it would claim: trusting those operands accepts the step, the replay of
+    the committed leaves rejects it at that product."""
+    from conftest import started_verifier
+    from verification.commitment.leaves import commit_leaves_device
+    from verification.prover.synthetic import CapturedReplay
+    from verification.transcript.store import InMemoryStore
+    c, step, _ = _decoder_prove(seed=9)
+    spec = next(s for s in c.products if s.name == "L2.Y_gate")
+    a, b = step.operands[spec.m]
+    a_forged = a.clone()
+    a_forged[7] += 0.25
+    leaves = step.leaves()
+    leaves[c.product_index(spec.m)] = torch.mm(a_forged, b)
+    tree = commit_leaves_device(c, leaves)
+    claimed = {m: ((a_forged, b) if m == spec.m else ops) for m, ops in step.operands.items()}
+    c.use_operands(CapturedReplay(claimed))
+    trusted = started_verifier(c, leaves, k=2).verify_step(1, InMemoryStore(leaves, tree))
+    c.use_operands(None)
+    rej = started_verifier(c, leaves, k=2).verify_step(1, InMemoryStore(leaves, tree))
+    assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
+    assert rej.detail.startswith(f"P_{spec.m} (L2.Y_gate)")
+    # with the prover's operands every check passes (6b, which needs the replay's glue, is
+    # not run for them): the forgery is caught only by the replay
+    assert trusted is None
+
+
+def test_forged_glue_update_rejects_at_check_6b(lib):
+    from conftest import started_verifier
+    from verification.commitment.leaves import commit_leaves_device
+    from verification.transcript.store import InMemoryStore
+    c, step, _ = _decoder_prove(seed=10)
+    name = next(n for n in c.glue_gradient_weights if "post_attention_layernorm" in n)
+    leaves = step.leaves()
+    i = c.w_next_index(name)
+    leaves[i] = leaves[i].clone()
+    leaves[i][3] += 1e-3
+    rej = started_verifier(c, leaves, k=2).verify_step(
+        1, InMemoryStore(leaves, commit_leaves_device(c, leaves)))
+    assert rej is not None and (rej.check_id, rej.kind) == ("6b", "failed"), rej
+    assert rej.detail.startswith(f"{name}: entry 3 has |R| = ")
 
 
 def test_c1_real_smollm2_step_proves_commits_and_verifies(lib):
@@ -199,7 +254,6 @@ def test_c1_real_smollm2_step_proves_commits_and_verifies(lib):
     assert len(step.products) == c.M == 7113
     tree = commit(c, step)
     assert tree.root == _decoder_oracle_root(c, step.leaves())
-    c.use_operands(step.replay())
     v = started_verifier(c, step.leaves(), k=1)
     assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
     assert len(v.stats[1].products) == c.M and v.stats[1].max_normalized() <= 8.0

@@ -262,3 +262,47 @@ def test_decoder_prover_refuses_bf16_compute_over_fp32_masters():
     model = fp32.build_model()
     assert not model.training
     assert all(p.dtype == torch.float32 for p in model.parameters())
+
+
+@pytest.mark.parametrize("qkv_bias,n_kv", [(True, 2), (False, 4)])
+def test_decoder_replay_rebuilds_the_operands_from_the_leaves(qkv_bias, n_kv):
+    """The verifier's replay (the committed leaves only, every product substituted by its
+    leaf) gives every product the operands the prover's capture saw, bit for bit, and each
+    glue weight (γ, biases, the tied embedding) the gradient SGD stepped with."""
+    from verification.computation.instances.decoder import DecoderReplay
+    c, w0, step = _decoder_step(qkv_bias, n_kv)
+    leaves = step.leaves()
+    replay = DecoderReplay(c, leaves, device="cpu")
+    for spec in c.products:
+        a, b = replay.operands(spec.m)
+        ca, cb = step.operands[spec.m]
+        assert torch.equal(a, ca) and torch.equal(b, cb), spec.name
+    glue = replay.glue_gradients()
+    assert set(glue) == set(c.glue_gradient_weights) and c.w_out in glue
+    for name, g in glue.items():
+        want = torch.add(leaves[c.w_t_index(name)], g, alpha=-c.eta)
+        assert torch.equal(want, leaves[c.w_next_index(name)]), name
+    # a second replay reuses the plan and gives the same operands
+    again = DecoderReplay(c, leaves, device="cpu")
+    m = c.products[len(c.products) // 2].m
+    assert all(torch.equal(x, y) for x, y in zip(again.operands(m), replay.operands(m)))
+
+
+def test_decoder_replay_follows_a_forged_product():
+    """A forged forward product changes the glue downstream of it: the replay serves the
+    operands the committed leaves imply, so the forged product itself no longer equals its
+    operands' product, and later products' operands move with it."""
+    from verification.computation.instances.decoder import DecoderReplay
+    c, w0, step = _decoder_step(True, 2)
+    leaves = step.leaves()
+    spec = next(s for s in c.products if s.name == "L1.Y_up")
+    i = c.product_index(spec.m)
+    forged = list(leaves)
+    forged[i] = leaves[i].clone()
+    forged[i][3, 5] += 1.0
+    replay = DecoderReplay(c, forged, device="cpu")
+    a, b = replay.operands(spec.m)
+    assert torch.equal(a, step.operands[spec.m][0])  # Y_up's own input is upstream
+    assert not torch.equal(torch.mm(a, b) + 0, forged[i])
+    down = next(s for s in c.products if s.name == "L1.Y_down")
+    assert not torch.equal(replay.operands(down.m)[0], step.operands[down.m][0])
