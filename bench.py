@@ -37,6 +37,14 @@ for _p in (ROOT / "pots-2.0_amd", ROOT / "oracle"):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBPS = 8000.0
+# Whole-GPU 32-bit VALU issue rate: 256 CUs x 4 SIMDs x 16 lanes per clock at the 2.4 GHz peak
+# engine clock, in lane operations per second.
+VALU_PEAK_OPS = 256 * 4 * 16 * 2.4e9
+# VALU instructions per byte of message on the chunk kernels' interior path (two 64-byte blocks
+# per 128-byte pair), from a static count of this build's gfx950 assembly: two compressions
+# and the NaN/Inf test, 1,438 per pair; with the fused P sums, 1,933 per pair of bf16 and 1,704
+# of fp32 products. Edge blocks and the tree levels are left out.
+VALU_OPS_PER_BYTE = {"plain": 1438 / 128, "fused_bf16": 1933 / 128, "fused_fp32": 1704 / 128}
 METRIC = "Freivalds-verified GB/s + BLAKE3 Merkle GB/s (% HBM roofline); step verify ms"
 CONFIGS = {
     "c1": ("SmolLM2-135M step, 4x256 tokens, fp32, k=1", "smollm2_135m", 1),
@@ -134,42 +142,63 @@ def cpu_baseline(step, items, fv_budget_s: float = 3.0, runs: int = 3) -> dict:
                       f"challenges included)"}
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "chunk_kernels_c4_traffic.md"
+TRAFFIC_FILE = ROOT / "profiles" / "c4_kernel_counters.md"
+
+
+def kernel_label(name: str) -> str:
+    """A kernel's name as the bench reports it: the chunk kernels by name, a row pass by the
+    pass its template arguments make it (``row_pass<XT, WEIGHTED, SQ64, NJG>``: B is
+    unweighted, A weighted, P takes its squares in fp64)."""
+    base = name.split("(")[0].replace("void ", "").strip()
+    short = base.split("::")[-1]
+    if short.startswith("row_pass<"):
+        xt, weighted, sq64, _ = (x.strip().rstrip("u") for x in short[9:-1].split(","))
+        dt = "bf16" if xt == "1" else "fp32"
+        if weighted == "true":
+            return f"row_pass<{dt}, weighted> (A pass)"
+        if sq64 == "true":
+            return f"row_pass<{dt}, fp64 squares> (P pass)"
+        return f"row_pass<{dt}> (B pass)"
+    return short
 
 
 def counter_summary(d: Path, copy_mib: int) -> int:
-    """Mean FETCH_SIZE / WRITE_SIZE (KiB) per dispatch of each kernel in a rocprofv3 --pmc
-    CSV run, and the chunk kernel's HBM bytes per launch scaled by the same counter's reading
-    for the calibration copy (two copies of ``copy_mib`` MiB, read and written once each)."""
+    """Mean value per dispatch of each counter for each kernel in a rocprofv3 --pmc CSV run;
+    for FETCH_SIZE and WRITE_SIZE (KiB) also the bytes per launch, scaled by the same
+    counter's reading for the calibration copy (two copies of ``copy_mib`` MiB, each read and
+    written once), as JSON lines for the committed profile."""
     import collections
     import csv
     sums: dict = collections.defaultdict(float)
     disp: dict = collections.defaultdict(set)
     for f in d.rglob("*counter_collection.csv"):
         for r in csv.DictReader(f.open()):
-            key = (r["Kernel_Name"].split("(")[0], r["Counter_Name"])
+            raw = r["Kernel_Name"]
+            key = ("copyBuffer" if "copyBuffer" in raw else kernel_label(raw), r["Counter_Name"])
             sums[key] += float(r["Counter_Value"])
             disp[key].add(r["Dispatch_Id"])
     if not sums:
         print(f"no counter_collection.csv under {d}", file=sys.stderr)
         return 1
-    print("| kernel | counter | dispatches | mean KiB per dispatch | total KiB |")
+    print("| kernel | counter | dispatches | mean per dispatch | total |")
     print("|---|---|---|---|---|")
     for (k, cn), v in sorted(sums.items()):
-        print(f"| `{k}` | {cn} | {len(disp[(k, cn)])} | {v / len(disp[(k, cn)]):.1f} | {v:.1f} |")
+        n = len(disp[(k, cn)])
+        print(f"| `{k}` | {cn} | {n} | {v / n:.2f} | {v:.1f} |")
     if copy_mib:
-        for cn in sorted({cn for _, cn in sums}):
-            copy_kib = sum(v for (k, c2), v in sums.items() if c2 == cn and "copyBuffer" in k)
+        for cn in sorted({cn for _, cn in sums} & {"FETCH_SIZE", "WRITE_SIZE"}):
+            copy_kib = sums.get(("copyBuffer", cn), 0.0)
             if not copy_kib:
                 continue
             factor = 2 * copy_mib * 1024 / copy_kib  # true KiB per reported KiB
             print(f"\n{cn}: calibration copy reports {copy_kib:.0f} KiB for "
                   f"{2 * copy_mib * 1024} KiB moved, factor {factor:.3f}")
             for (k, c2), v in sorted(sums.items()):
-                if c2 == cn and k.split("::")[-1] in ("chunk_kernel", "chunk_kernel_fused"):
+                if c2 == cn and k != "copyBuffer":
                     n = len(disp[(k, c2)])
-                    print(f"  {k}: {v / n * factor * 1024:.0f} bytes "
-                          f"({v / n * factor * 1024 / 1e9:.3f} GB) per launch")
+                    print(json.dumps({"kernel": k, "counter": cn,
+                                      "bytes_per_launch": round(v / n * factor * 1024),
+                                      "factor": round(factor, 3)}))
     return 0
 
 
@@ -211,18 +240,18 @@ def trace_summary(d: Path, steps: int, warmup: int) -> int:
 
 
 def traffic_from_profile(kernel: str) -> int | None:
-    """HBM bytes per launch of ``kernel`` from the committed counter summary (the fenced
-    JSON block of TRAFFIC_FILE: one object per kernel), or None when it holds no figure for
-    that kernel."""
+    """HBM bytes per launch of ``kernel`` (read + written) from the committed counter summary
+    (the fenced JSON block of TRAFFIC_FILE, one object per kernel and counter), or None when it
+    holds no figure for that kernel."""
     try:
         text = TRAFFIC_FILE.read_text()
         block = text.split("```json", 1)[1].split("```", 1)[0]
-        d = json.loads(block)
+        rows = [json.loads(line) for line in block.splitlines() if line.strip()]
     except (OSError, IndexError, ValueError):
         return None
-    for e in d if isinstance(d, list) else [d]:
-        if e.get("kernel") == kernel:
-            return int(e["fetch_bytes_per_launch"]) + int(e["write_bytes_per_launch"])
+    got = {r["counter"]: int(r["bytes_per_launch"]) for r in rows if r.get("kernel") == kernel}
+    if {"FETCH_SIZE", "WRITE_SIZE"} <= set(got):
+        return got["FETCH_SIZE"] + got["WRITE_SIZE"]
     return None
 
 
@@ -463,6 +492,43 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int 
             "avoided_d2h_s": round(product_bytes / d2h_gbps / 1e9, 3)}
 
 
+def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 3) -> dict:
+    """``Verifier.verify_step`` on the resident transcript, as a caller of the reference's
+    driver runs it: checks 7, 2, 6a, 5, 6b and 2.root, host judging included (operands from
+    the synthetic capture, so trusted; 6b needs the replay's glue and is not run). Each step
+    builds its plans afresh."""
+    import torch
+
+    from verification.commitment.leaves import leaf_hashes_of
+    from verification.commitment.merkle import merkle_root
+    from verification.transcript.store import InMemoryStore
+    from verification.verifier.bands import Bands
+    from verification.verifier.driver import Verifier
+    c.use_operands(step.replay())
+    records = [step.leaves[c.record_index(i)] for i in range(c.n_s)]
+    h_d = merkle_root(leaf_hashes_of(c, ((0, r) for r in records)))
+    times, slots = [], []
+    for _ in range(runs):
+        v = Verifier(c, h_D=h_d, n_records=c.n_s, k=k, n_steps=1, bands=Bands.provisional(),
+                     seed=0, w0={n: step.leaves[c.w_t_index(n)] for n in c.weight_names},
+                     schedule=lambda t: list(range(c.n_s)), allow_provisional=True,
+                     trust_prover_operands=True)
+        assert v.start_run(records) is None
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        rej = v.verify_step(1, InMemoryStore(step.leaves, claimed_root=claimed))
+        times.append((time.perf_counter() - t0) * 1e3)
+        slots.append(v.timings[1])
+        assert rej is None, rej
+    best = min(range(runs), key=lambda i: times[i])
+    c.use_operands(None)
+    log(f"[bench] check-level Verifier.verify_step: {times[best]:.1f} ms (best of {runs}), "
+        + ", ".join(f"{s} {t * 1e3:.1f}" for s, t in slots[best].items()))
+    return {"verify_step_ms": round(times[best], 1),
+            "slots_ms": {s: round(t * 1e3, 2) for s, t in slots[best].items()},
+            "runs_ms": [round(t, 1) for t in times]}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -492,6 +558,9 @@ def main() -> int:
                          "verifies it with the replay; 'qwen2' proves a Qwen2-1.5B-shaped "
                          "training step (transformers, random init, fp32, 14 of 28 layers, "
                          "4x2048 tokens), commits it in HBM and verifies it")
+    ap.add_argument("--check-level", action=argparse.BooleanOptionalAction, default=True,
+                    help="time Verifier.verify_step (the reference's check-level entry point) "
+                         "on the same transcript, beside the step")
     ap.add_argument("--counter-summary", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSV output under DIR and exit")
     ap.add_argument("--trace-summary", metavar="DIR",
@@ -535,9 +604,14 @@ def main() -> int:
 
     stream = torch.cuda.current_stream()
     items = product_inputs(step)
+    t0 = time.perf_counter()
     v = DeviceStepVerifier(c, step.leaves, lambda spec: step.operands[spec.m], k=k,
                            a_grid=args.a_grid, b_grid=args.b_grid,
                            hash_after_b=not args.hash_first, plain_early=args.plain_early)
+    torch.cuda.synchronize()
+    plan_build_ms = (time.perf_counter() - t0) * 1e3
+    log(f"[bench] plans built in {plan_build_ms:.1f} ms (leaf plan fused with the Freivalds "
+        f"plan, verdict table)")
     # The claimed root: the honest root of this transcript, as the prover would send it.
     v.hasher.digests(v.digests, v.bad, stream)
     claimed = lib.merkle_tree_device(v.digests, stream)[0].clone()
@@ -645,25 +719,39 @@ def main() -> int:
             f"{u_ms:.3f} ms ({check_6a['gbps']:.0f} GB/s), {n_over} rejected")
         uplan.close()
 
-    # Algorithmic HBM bytes of each single-kernel stage: the operand every element of which
-    # the kernel reads once (A, B or P of every product; every leaf's message bytes plus one
-    # 32-byte chaining value written per 1 KiB chunk).
+    # Algorithmic bytes of each single-kernel stage, per the survey's measurement plan: the
+    # message bytes (1 + header + payload) of the leaves a chunk kernel hashes, or the operand
+    # a row pass reads (A, B, or the P of the products the chunk kernel did not take), each
+    # element once. Writes (chaining values, run records, partial sums) are not counted.
     a_bytes = sum(a.nbytes for a, _, _, _, _ in items)
     b_bytes = sum(b.nbytes for _, b, _, _, _ in items)
     p_bytes = sum(p.nbytes for _, _, p, _, _ in items)
     hp = v.hasher.plan
+    fused_p_bytes = hp.fused_bytes - 12 * v.fused  # payload: 0x00 || 11-byte 2-D header off
     kernels = {
-        "hash.chunks": ("chunk_kernel", hash_bytes - hp.fused_bytes +
-                        32 * (hp.chunks - hp.fused_chunks)),
+        "hash.chunks": ("chunk_kernel", hash_bytes - hp.fused_bytes),
         "freivalds.a_pass": ("row_pass<bf16, weighted> (A pass)", a_bytes),
         "freivalds.b_pass": ("row_pass<bf16> (B pass)", b_bytes),
     }
-    if v.fused:  # message bytes read, chaining values and run records written
-        kernels["hash.chunks_fused"] = ("chunk_kernel_fused", hp.fused_bytes +
-                                        32 * hp.fused_chunks + 32 * hp.fused_records)
-    else:  # fused, the P pass reads only the products the chunk kernel did not take
-        kernels["freivalds.p_pass"] = ("row_pass<bf16, fp64 squares> (P pass)", p_bytes)
+    if v.fused:
+        kernels["hash.chunks_fused"] = ("chunk_kernel_fused", hp.fused_bytes)
+    if p_bytes - fused_p_bytes > 0:
+        kernels["freivalds.p_pass"] = ("row_pass<bf16, fp64 squares> (P pass)",
+                                       p_bytes - fused_p_bytes)
     dom = max(kernels, key=lambda nm: stage_ms[nm])
+    # The chunk kernels are bound by 32-bit VALU issue, not HBM: their fraction of it.
+    fused_key = "fused_bf16" if c.product_dtype == torch.bfloat16 else "fused_fp32"
+    valu = {}
+    for nm, (kname, nbytes), per in (
+            ("hash.chunks", kernels["hash.chunks"], VALU_OPS_PER_BYTE["plain"]),
+            ("hash.chunks_fused", kernels.get("hash.chunks_fused", ("", 0)),
+             VALU_OPS_PER_BYTE[fused_key])):
+        if nbytes and stage_ms[nm] > 0:
+            ops = per * nbytes
+            valu[kname] = {"ops_per_byte": round(per, 2), "ops": int(ops),
+                           "achieved_tops": round(ops / (stage_ms[nm] * 1e-3) / 1e12, 2),
+                           "peak_tops": round(VALU_PEAK_OPS / 1e12, 2),
+                           "frac": round(ops / (stage_ms[nm] * 1e-3) / VALU_PEAK_OPS, 4)}
     # the kernel the step's chunk events bracket
     in_step_kernel = "hash.chunks_fused" if v.fused else "hash.chunks"
     dom_name, dom_bytes = kernels[dom]
@@ -674,7 +762,9 @@ def main() -> int:
     value = total / (ms * 1e-3) / 1e9
     # P of a fused product is read once, by the hashing kernel (its leaf message is the
     # 12-byte 0x00 || header of a 2-D tensor, then P)
-    read_bytes = hash_bytes + a_bytes + b_bytes + p_bytes - (hp.fused_bytes - 12 * v.fused)
+    read_bytes = hash_bytes + a_bytes + b_bytes + p_bytes - fused_p_bytes
+    # the bytes the Freivalds stages read themselves: A, B, and the P the hash did not take
+    fv_read_bytes = a_bytes + b_bytes + p_bytes - fused_p_bytes
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
@@ -701,7 +791,9 @@ def main() -> int:
                   "hash_ms": round(hash_ms, 3),
                   "hash_gbps": round(hash_bytes / (hash_ms * 1e-3) / 1e9, 1),
                   "freivalds_ms": round(fv_ms, 3),
-                  "freivalds_gbps": round(fv_bytes / (fv_ms * 1e-3) / 1e9, 1),
+                  "freivalds_read_bytes": fv_read_bytes,
+                  "freivalds_gbps": round(fv_read_bytes / (fv_ms * 1e-3) / 1e9, 1),
+                  "plan_build_ms": round(plan_build_ms, 1),
                   "stages_ms": {nm: round(t, 4) for nm, t in stage_ms.items()},
                   "rejected": n_rej,
                   "check_6a": check_6a},
@@ -711,8 +803,11 @@ def main() -> int:
                      "kernel": dom_name,
                      "algorithmic_bytes": dom_bytes, "launch_ms": round(stage_ms[dom], 4),
                      "launch_ms_in_step": (round(chunks_in_step_ms, 4)
-                                           if dom == in_step_kernel else None)},
+                                           if dom == in_step_kernel else None),
+                     "valu": valu},
     }
+    if args.check_level:
+        out["parts"]["check_level"] = check_level_leg(c, step, k, claimed_b)
     if args.disk_leg:
         out["parts"]["disk_load"] = disk_leg(Path(args.disk_leg), c, step, k, claimed_b, v)
     if args.prover_leg == "mlp":

@@ -128,11 +128,18 @@ struct StageRegs {
   u32x4 v[KU][NJG];
 };
 
-// The per-lane view of one tile: X row, V slot base, weights and bounds.
+// The per-lane view of one tile: X row, V slot base, weights and bounds. The full stages'
+// loads address memory as a wave-uniform base, advanced in scalar registers from K-step to
+// K-step, plus a per-lane 32-bit offset fixed for the tile, so most of the per-K-step address
+// arithmetic is scalar work.
 struct Lane {
   const char* xrow;   // this lane's X row (clamped to the matrix)
   const char* vlane;  // V slot of this lane for K-group g of group jt·NJG
+  const char* xbase;  // wave-uniform: the wave's first X row, column 0
+  const char* vbase;  // wave-uniform: V of K-group 0 of group jt·NJG, slot 0
   uint64_t vstep;     // bytes of V per K-group
+  uint32_t xoff;      // this lane's X bytes past xbase (its row, its 8 or 4 columns)
+  uint32_t voff;      // this lane's V bytes past vbase (its K-group, its slot)
   uint32_t g, c1;
   uint32_t nvalid;    // groups of this block that exist (the last block of a row may hold fewer)
 };
@@ -144,14 +151,15 @@ __device__ __forceinline__ void load_full(StageRegs<NJG>& r, const Lane& L, uint
 #pragma unroll
   for (uint32_t u = 0; u < KU; u++) {
     const uint32_t cu = cs + u * G::KSTEP;
-    r.x[u] = gload<u32x4>(L.xrow + (uint64_t)(cu + G::PER * L.g) * G::ESZ);
-    const char* vp = L.vlane + (uint64_t)(cu / G::PER) * L.vstep;
+    const char* xb = L.xbase + (uint64_t)cu * G::ESZ;               // uniform
+    const char* vb = L.vbase + (uint64_t)(cu / G::PER) * L.vstep;   // uniform
+    r.x[u] = gload<u32x4>(xb + L.xoff);
     // Every load is unconditional, so the compiler's wait counts stay exact across the
     // pipeline: a group past n_jg (only in a row's last column-group block) rereads the last
     // valid group, and its results are not stored.
 #pragma unroll
     for (uint32_t q = 0; q < NJG; q++)
-      r.v[u][q] = gload<u32x4>(vp + (q < L.nvalid ? q : L.nvalid - 1) * 256);
+      r.v[u][q] = gload<u32x4>(vb + (q < L.nvalid ? q : L.nvalid - 1) * 256 + L.voff);
   }
 }
 
@@ -291,11 +299,17 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   const uint32_t row = r0 + i;
   Lane L;
   // Rows past the matrix read its last row; their results are never written.
-  L.xrow = reinterpret_cast<const char*>(J.x) +
-           (uint64_t)(row < J.rows ? row : J.rows - 1) * J.ld * G::ESZ;
+  const uint32_t rowc = row < J.rows ? row : J.rows - 1;
+  L.xrow = reinterpret_cast<const char*>(J.x) + (uint64_t)rowc * J.ld * G::ESZ;
   L.vstep = (uint64_t)J.n_jg * 256;
   L.vlane = reinterpret_cast<const char*>(J.v) + (uint64_t)g * L.vstep +
             (uint64_t)jt * NJG * 256 + i * 16;
+  // the same addresses as uniform bases and 32-bit lane offsets (plan creation keeps 16 rows
+  // of an aligned job's X below 2^31 bytes; 4 K-groups of V are far below)
+  L.xbase = reinterpret_cast<const char*>(J.x) + (uint64_t)r0 * J.ld * G::ESZ;
+  L.xoff = (uint32_t)((uint64_t)(rowc - r0) * J.ld * G::ESZ) + G::PER * g * G::ESZ;
+  L.vbase = reinterpret_cast<const char*>(J.v) + (uint64_t)jt * NJG * 256;
+  L.voff = (uint32_t)((uint64_t)g * L.vstep) + i * 16;
   L.g = g;
   L.c1 = c1;
   L.nvalid = min(NJG, J.n_jg - jt * NJG);
@@ -923,7 +937,10 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     J.n_jg = groups_for(s.dt, k);
     J.n_jt = (J.n_jg + njg_for(s.dt, k) - 1) / njg_for(s.dt, k);
     const uint32_t esz = s.dt == DT_BF16 ? 2 : 4;
-    J.aligned = (s.x % 16 == 0) && ((s.ld * esz) % 16 == 0);
+    // The full stages address a wave's 16 rows by 32-bit offsets from its first row: a row
+    // stride beyond that (rows of over 128 MiB) takes the guarded loads' 64-bit addresses.
+    J.aligned = (s.x % 16 == 0) && ((s.ld * esz) % 16 == 0) &&
+                (uint64_t)s.ld * esz * 16 < (1ull << 31);
     return J;
   };
   // Partial buffers, per job: dot [chunks][rows_pad][k] f32, abs [chunks][rows_pad] f32,
