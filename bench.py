@@ -492,11 +492,12 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int 
             "avoided_d2h_s": round(product_bytes / d2h_gbps / 1e9, 3)}
 
 
-def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 3) -> dict:
+def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 4) -> dict:
     """``Verifier.verify_step`` on the resident transcript, as a caller of the reference's
     driver runs it: checks 7, 2, 6a, 5, 6b and 2.root, host judging included (operands from
-    the synthetic capture, so trusted; 6b needs the replay's glue and is not run). Each step
-    builds its plans afresh."""
+    the synthetic capture, so trusted; 6b needs the replay's glue and is not run). The first
+    run builds the verifier's plans (a run's first step); the later ones find them in the plan
+    cache, as every later step of a run whose transcript keeps its layout does."""
     import torch
 
     from verification.commitment.leaves import leaf_hashes_of
@@ -508,11 +509,14 @@ def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 3) -> dict:
     records = [step.leaves[c.record_index(i)] for i in range(c.n_s)]
     h_d = merkle_root(leaf_hashes_of(c, ((0, r) for r in records)))
     times, slots = [], []
+    cache = None
     for _ in range(runs):
         v = Verifier(c, h_D=h_d, n_records=c.n_s, k=k, n_steps=1, bands=Bands.provisional(),
                      seed=0, w0={n: step.leaves[c.w_t_index(n)] for n in c.weight_names},
                      schedule=lambda t: list(range(c.n_s)), allow_provisional=True,
                      trust_prover_operands=True)
+        if cache is not None:
+            v.plans = cache
         assert v.start_run(records) is None
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -520,12 +524,18 @@ def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 3) -> dict:
         times.append((time.perf_counter() - t0) * 1e3)
         slots.append(v.timings[1])
         assert rej is None, rej
-    best = min(range(runs), key=lambda i: times[i])
+        cache = v.plans
+    hits, builds = cache.hits, cache.builds
+    cache.close()
+    best = min(range(1, runs), key=lambda i: times[i])
     c.use_operands(None)
-    log(f"[bench] check-level Verifier.verify_step: {times[best]:.1f} ms (best of {runs}), "
-        + ", ".join(f"{s} {t * 1e3:.1f}" for s, t in slots[best].items()))
+    log(f"[bench] check-level Verifier.verify_step: {times[0]:.1f} ms building its plans, "
+        f"{times[best]:.1f} ms with them cached (best of {runs - 1}; {builds} built, "
+        f"{hits} reused); " + ", ".join(f"{s} {t * 1e3:.1f}" for s, t in slots[best].items()))
     return {"verify_step_ms": round(times[best], 1),
+            "verify_step_first_ms": round(times[0], 1),
             "slots_ms": {s: round(t * 1e3, 2) for s, t in slots[best].items()},
+            "first_slots_ms": {s: round(t * 1e3, 2) for s, t in slots[0].items()},
             "runs_ms": [round(t, 1) for t in times]}
 
 

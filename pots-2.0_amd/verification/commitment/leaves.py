@@ -14,6 +14,7 @@ copied to the GPU by the library as part of the call. :func:`hash_step_leaves_de
 
 from __future__ import annotations
 
+import weakref
 from collections.abc import Iterable, Sequence
 from time import perf_counter
 from typing import TYPE_CHECKING, Any
@@ -135,8 +136,11 @@ class _Batch:
         self.host_bytes = 0
 
 
-def _hash_batch(b: _Batch, stats: HashStats | None) -> tuple[list[bytes], int]:
-    """One GPU call: the batch's digests and its first non-finite position (or its size)."""
+def _hash_batch(b: _Batch, stats: HashStats | None, plans: Any = None,
+                site: str = "") -> tuple[list[bytes], int]:
+    """One GPU call: the batch's digests and its first non-finite position (or its size).
+    With ``plans`` (a verifier's plan cache) a batch whose payloads all lie in device memory
+    runs the cached leaf plan of ``site`` when its layout is unchanged."""
     n = len(b.headers)
     if n == 0:
         return [], 0
@@ -150,9 +154,19 @@ def _hash_batch(b: _Batch, stats: HashStats | None) -> tuple[list[bytes], int]:
     hdr_off = np.zeros(len(hdrs), dtype=np.uint64)
     if len(hdrs) > 1:
         hdr_off[1:] = np.cumsum(hdr_len[:-1], dtype=np.uint64)
-    digests, bad = native.get().hash_leaves(
-        b"".join(hdrs), hdr_off, hdr_len, idx, np.array(b.ptr, dtype=np.uint64),
-        np.array(b.nbytes, dtype=np.uint64), np.array(b.kind, dtype=np.uint8))
+    ptr = np.array(b.ptr, dtype=np.uint64)
+    nbytes = np.array(b.nbytes, dtype=np.uint64)
+    kind = np.array(b.kind, dtype=np.uint8)
+    if plans is not None and b.host_bytes == 0 and b.keep and \
+            all(t.is_cuda for t in b.keep):
+        dev = b.keep[0].device
+        plan = plans.leaf_plan(site, b"".join(hdrs), hdr_off, hdr_len, idx, ptr, nbytes, kind,
+                               dev)
+        out, first_bad = plan.run()
+        digests, bad = out.cpu().numpy(), int(first_bad.item())
+    else:
+        digests, bad = native.get().hash_leaves(b"".join(hdrs), hdr_off, hdr_len, idx, ptr,
+                                                nbytes, kind)
     if stats is not None:
         stats.native_s += perf_counter() - t0
         stats.batches += 1
@@ -160,8 +174,43 @@ def _hash_batch(b: _Batch, stats: HashStats | None) -> tuple[list[bytes], int]:
     return [raw[32 * i:32 * i + 32] for i in range(min(bad, n))], bad
 
 
+class _Slot:
+    """What a tensor slot of ``C``'s layout requires, and its interned header."""
+
+    __slots__ = ("tag", "shape", "dtype", "header", "kind")
+
+    def __init__(self, tag: int, shape: tuple[int, ...], dtype: torch.dtype) -> None:
+        self.tag, self.shape, self.dtype = tag, torch.Size(shape), dtype
+        self.kind = native.FINITE_KIND.get(dtype)
+        try:
+            self.header: bytes | None = tensor_leaf_header(
+                tag, torch.empty(shape, dtype=dtype, device="meta"))
+        except Exception:  # an uncoded dtype: the slow path raises its error per leaf
+            self.header = None
+
+
+_SLOT_TABLES: weakref.WeakKeyDictionary[Any, list[_Slot]] = weakref.WeakKeyDictionary()
+
+
+def _slot_table(c: DeclaredComputation) -> list[_Slot]:
+    """The tensor slots of ``C`` (leaf ``n_s + j`` is entry ``j``), built once per
+    computation: the layout of a declared computation does not change."""
+    try:
+        table = _SLOT_TABLES.get(c)
+    except TypeError:  # not weakly referenceable: build it every time
+        table = None
+    if table is None or len(table) != c.n_leaves - c.n_s:
+        table = [_Slot(*_tensor_slot(c, i)[:3]) for i in range(c.n_s, c.n_leaves)]
+        try:
+            _SLOT_TABLES[c] = table
+        except TypeError:
+            pass
+    return table
+
+
 def _until_error(c: DeclaredComputation, items: Iterable[tuple[int, Any]],
-                 stats: HashStats | None) -> tuple[list[bytes], Exception | None]:
+                 stats: HashStats | None, plans: Any = None,
+                 site: str = "") -> tuple[list[bytes], Exception | None]:
     t_start = perf_counter()
     r0 = stats.read_s if stats is not None else 0.0
     n0 = stats.native_s if stats is not None else 0.0
@@ -170,14 +219,20 @@ def _until_error(c: DeclaredComputation, items: Iterable[tuple[int, Any]],
     finite_kind = native.FINITE_KIND
     hdr_cache: dict[tuple[int, torch.dtype, tuple[int, ...]], bytes] = {}
     error: Exception | None = None
+    n_s = c.n_s
+    table = _slot_table(c)
+    n_table = len(table)
+    tensor_type = torch.Tensor
 
     def flush() -> bool:
         nonlocal batch
-        d, bad = _hash_batch(batch, stats)
+        d, bad = _hash_batch(batch, stats, plans, site)
         digests.extend(d)
         ok = bad >= len(batch.headers)
         batch = _Batch()
         return ok
+
+    records_open = False  # the batch holds records (a cached plan takes tensor leaves only)
 
     it = iter(items)
     try:
@@ -192,24 +247,47 @@ def _until_error(c: DeclaredComputation, items: Iterable[tuple[int, Any]],
             if stats is not None:
                 stats.read_s += perf_counter() - t0
                 stats.leaves += 1
+            if plans is not None:
+                if 0 <= i < n_s:
+                    records_open = True
+                elif records_open:
+                    records_open = False
+                    if not flush():
+                        return digests, NonFiniteError(_NONFINITE)
             try:
-                as_tensor = c.record_leaf(obj) if 0 <= i < c.n_s else None
-                if 0 <= i < c.n_s and as_tensor is None:
-                    batch.headers.append(c.encode_record(obj))
-                    batch.ptr.append(0)
-                    batch.nbytes.append(0)
-                    batch.kind.append(0)
+                j = i - n_s
+                slot = table[j] if 0 <= j < n_table else None
+                # The common case, a tensor leaf exactly as its slot declares, on the fast
+                # path; anything else goes through the full validation, which raises the
+                # reference's error for it.
+                if (slot is not None and slot.header is not None and
+                        isinstance(obj, tensor_type) and obj.dtype is slot.dtype and
+                        obj.shape == slot.shape and obj.is_contiguous() and
+                        (obj.is_cuda or obj.device.type == "cpu")):
+                    t, h, kind = obj, slot.header, slot.kind
                 else:
-                    tag, t = as_tensor if as_tensor is not None else _checked_tensor(c, i, obj)
-                    key = (tag, t.dtype, tuple(t.shape))
-                    h = hdr_cache.get(key)
-                    if h is None:
-                        h = hdr_cache[key] = tensor_leaf_header(tag, t)
-                    ptr, nbytes = tensor_payload_span(t)
+                    as_tensor = c.record_leaf(obj) if 0 <= i < n_s else None
+                    if 0 <= i < n_s and as_tensor is None:
+                        batch.headers.append(c.encode_record(obj))
+                        batch.ptr.append(0)
+                        batch.nbytes.append(0)
+                        batch.kind.append(0)
+                        t = None
+                    else:
+                        tag, t = as_tensor if as_tensor is not None \
+                            else _checked_tensor(c, i, obj)
+                        key = (tag, t.dtype, tuple(t.shape))
+                        h = hdr_cache.get(key)
+                        if h is None:
+                            h = hdr_cache[key] = tensor_leaf_header(tag, t)
+                        tensor_payload_span(t)  # the payload's own checks
+                        kind = finite_kind[t.dtype]
+                if t is not None:
+                    nbytes = t.nbytes
                     batch.headers.append(h)
-                    batch.ptr.append(ptr)
+                    batch.ptr.append(t.data_ptr())
                     batch.nbytes.append(nbytes)
-                    batch.kind.append(finite_kind[t.dtype])
+                    batch.kind.append(kind)
                     batch.keep.append(t)
                     if not t.is_cuda:
                         batch.host_bytes += nbytes
@@ -232,20 +310,23 @@ def _until_error(c: DeclaredComputation, items: Iterable[tuple[int, Any]],
 
 
 def leaf_hashes_of(c: DeclaredComputation, items: Iterable[tuple[int, Any]],
-                   stats: HashStats | None = None) -> list[bytes]:
+                   stats: HashStats | None = None, plans: Any = None,
+                   site: str = "") -> list[bytes]:
     """The leaf hash of each ``(index, obj)`` in order; raises the first error a
-    leaf-by-leaf loop raises. The objects must not change until this returns."""
-    digests, err = _until_error(c, items, stats)
+    leaf-by-leaf loop raises. The objects must not change until this returns. ``plans`` (a
+    verifier's plan cache) and ``site`` let device-resident leaves reuse the leaf plan of the
+    same site's last call when their layout repeats."""
+    digests, err = _until_error(c, items, stats, plans, site)
     if err is not None:
         raise err
     return digests
 
 
 def leaf_hashes_until_error(c: DeclaredComputation, items: Iterable[tuple[int, Any]],
-                            stats: HashStats | None = None
-                            ) -> tuple[list[bytes], Exception | None]:
+                            stats: HashStats | None = None, plans: Any = None,
+                            site: str = "") -> tuple[list[bytes], Exception | None]:
     """:func:`leaf_hashes_of` up to the first error: ``(digests before it, error or None)``."""
-    return _until_error(c, items, stats)
+    return _until_error(c, items, stats, plans, site)
 
 
 def leaf_hashes(c: DeclaredComputation, reader: Any) -> list[bytes]:

@@ -24,6 +24,7 @@ import os
 import threading
 import weakref
 from collections.abc import Iterator, Sequence
+from typing import Any
 from contextlib import contextmanager
 from pathlib import Path
 
@@ -313,8 +314,6 @@ class LeafPlan:
         n = len(payloads)
         if not (len(headers) == len(kinds) == n) or n == 0:
             raise ValueError("one header and one kind per payload, at least one leaf")
-        self._lib = lib
-        self._keep = list(payloads)
         uniq: dict[bytes, int] = {}
         idx = np.empty(n, dtype=np.uint32)
         for i, h in enumerate(headers):
@@ -324,14 +323,43 @@ class LeafPlan:
         hdr_off = np.zeros(len(hdrs), dtype=np.uint64)
         if len(hdrs) > 1:
             hdr_off[1:] = np.cumsum(hdr_len[:-1], dtype=np.uint64)
-        hb = np.frombuffer(b"".join(hdrs) or b"\0", dtype=np.uint8)
         ptr = np.empty(n, dtype=np.uint64)
         ln = np.empty(n, dtype=np.uint64)
         for i, t in enumerate(payloads):
             if not (t.is_cuda and t.is_contiguous()):
                 raise ValueError(f"payload {i} must be a contiguous GPU tensor")
             ptr[i], ln[i] = t.data_ptr(), t.nbytes
-        kd = np.asarray(kinds, dtype=np.uint8)
+        self._create(lib, b"".join(hdrs), hdr_off, hdr_len, idx, ptr, ln,
+                     np.asarray(kinds, dtype=np.uint8), fuse, list(payloads),
+                     payloads[0].device)
+
+    @classmethod
+    def from_arrays(cls, lib: Native, hdr_buf: bytes, hdr_off: np.ndarray, hdr_len: np.ndarray,
+                    hdr_idx: np.ndarray, payload_ptr: np.ndarray, payload_len: np.ndarray,
+                    kind: np.ndarray, device: torch.device) -> LeafPlan:
+        """A plan over ``pots_hash_leaves``'s arguments (every payload in device memory, or
+        empty). It keeps no tensor: the caller keeps the payloads alive and in place while
+        its runs are in flight."""
+        self = cls.__new__(cls)
+        self._create(lib, hdr_buf, hdr_off, hdr_len, hdr_idx, payload_ptr, payload_len, kind,
+                     None, [], device)
+        return self
+
+    def _create(self, lib: Native, hdr_buf: bytes, hdr_off: np.ndarray, hdr_len: np.ndarray,
+                idx: np.ndarray, ptr: np.ndarray, ln: np.ndarray, kd: np.ndarray,
+                fuse: FvPlan | None, keep: list[Any], device: torch.device) -> None:
+        n = len(idx)
+        if not (len(ptr) == len(ln) == len(kd) == n) or n == 0:
+            raise ValueError("one header index, payload and kind per leaf, at least one leaf")
+        self._lib = lib
+        self._keep = keep
+        hb = np.frombuffer(hdr_buf or b"\0", dtype=np.uint8)
+        idx = np.ascontiguousarray(idx, dtype=np.uint32)
+        hdr_off = np.ascontiguousarray(hdr_off, dtype=np.uint64)
+        hdr_len = np.ascontiguousarray(hdr_len, dtype=np.uint32)
+        ptr = np.ascontiguousarray(ptr, dtype=np.uint64)
+        ln = np.ascontiguousarray(ln, dtype=np.uint64)
+        kd = np.ascontiguousarray(kd, dtype=np.uint8)
         h = ctypes.c_void_p()
         if fuse is None:
             lib._check(lib._lib.pots_leaf_plan_create(
@@ -360,7 +388,7 @@ class LeafPlan:
         self.n = n
         self.chunks = int(lib._lib.pots_leaf_plan_chunks(h))
         self.bytes = int(lib._lib.pots_leaf_plan_bytes(h))
-        self.device = payloads[0].device
+        self.device = device
 
     def run(self, out: torch.Tensor | None = None, bad: torch.Tensor | None = None,
             stream: torch.cuda.Stream | None = None) -> tuple[torch.Tensor, torch.Tensor]:
@@ -468,45 +496,72 @@ def _row_major(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def fv_table(products: Sequence[FvProduct]
+             ) -> tuple[np.ndarray, list[torch.Tensor], dict[tuple[int, str], torch.Tensor]]:
+    """The product table ``pots_fv_plan_create`` reads (one ``pots_fv_product`` per product),
+    the tensors it points into, which must stay alive while a plan built on it runs, and the
+    ones of those this call made, by ``(product index, field)``: a product's fp32 bias
+    (``"bias"``) and row-major copies of operands in another layout (``"a"``, ``"b"``,
+    ``"p"``)."""
+    table = []
+    keep = []
+    made: dict[tuple[int, str], torch.Tensor] = {}
+    dts = _DT
+    for i, pr in enumerate(products):
+        a, b, p = pr.a, pr.b, pr.p
+        sa, sb, sp = a.stride(), b.stride(), p.stride()
+        ash, bsh, psh = a.shape, b.shape, p.shape
+        # The common case (row-major 2-D GPU operands in fp32 or bf16) is read once;
+        # anything else is made row-major and validated operand by operand.
+        if not (len(sa) == len(sb) == len(sp) == 2 and sa[1] == sb[1] == sp[1] == 1 and
+                sa[0] >= ash[1] and sb[0] >= bsh[1] and sp[0] >= psh[1] and
+                a.is_cuda and b.is_cuda and p.is_cuda and a.dtype in dts and
+                b.dtype in dts and p.dtype in dts):
+            given = (a, b, p)
+            a, b, p = (_row_major(t) for t in given)
+            for name, t, t0 in (("a", a, given[0]), ("b", b, given[1]), ("p", p, given[2])):
+                if t is not t0:
+                    made[(i, name)] = t
+                if not t.is_cuda or t.dim() != 2 or t.stride(1) != 1 or t.dtype not in dts:
+                    raise ValueError(f"product {i}: {name} must be a 2-D GPU tensor in "
+                                     f"fp32 or bf16")
+            sa, sb, sp = a.stride(), b.stride(), p.stride()
+            ash, bsh, psh = a.shape, b.shape, p.shape
+        nn, q = ash
+        q2, w = bsh
+        if q2 != q or psh[0] != nn or psh[1] != w:
+            raise ValueError(f"product {i}: shapes {tuple(ash)}·{tuple(bsh)} vs "
+                             f"{tuple(psh)}")
+        if not 1 <= pr.m < 1 << 32:
+            raise ValueError(f"m must be in [1, 2^32), got {pr.m}")
+        bias = pr.bias
+        if bias is not None:
+            bias = bias.detach().to(device=a.device, dtype=torch.float32).contiguous()
+            if bias.shape != (w,):
+                raise ValueError(f"product {i}: bias of shape {tuple(bias.shape)}, "
+                                 f"expected ({w},)")
+            keep.append(bias)
+            made[(i, "bias")] = bias
+        table.append((a.data_ptr(), b.data_ptr(), p.data_ptr(),
+                      bias.data_ptr() if bias is not None else 0, sa[0], sb[0], sp[0],
+                      nn, q, w, pr.m, dts[a.dtype], dts[b.dtype], dts[p.dtype], 0))
+        keep += [a, b, p]
+    return np.array(table, dtype=_FV_RECORD), keep, made
+
+
 class FvPlan:
     """``pots_fv_plan_*``: operand layout and workspace fixed once; :meth:`rows` enqueues the
     challenges, the three streaming passes and the reduction for every product."""
 
     def __init__(self, lib: Native, products: Sequence[FvProduct], k: int,
-                 guard: bool = True) -> None:
+                 guard: bool = True,
+                 table: tuple[np.ndarray, list[torch.Tensor], Any] | None = None) -> None:
         n = len(products)
         if n == 0:
             raise ValueError("a Freivalds plan needs at least one product")
         if not 1 <= k <= 255:
             raise ValueError(f"k must be in [1, 255], got {k}")
-        table = []
-        keep = []
-        for i, pr in enumerate(products):
-            a, b, p = (_row_major(t) for t in (pr.a, pr.b, pr.p))
-            for name, t in (("a", a), ("b", b), ("p", p)):
-                if not t.is_cuda or t.dim() != 2 or t.stride(1) != 1 or t.dtype not in _DT:
-                    raise ValueError(f"product {i}: {name} must be a 2-D GPU tensor in fp32 or "
-                                     f"bf16")
-            nn, q = a.shape
-            q2, w = b.shape
-            if q2 != q or tuple(p.shape) != (nn, w):
-                raise ValueError(f"product {i}: shapes {tuple(a.shape)}·{tuple(b.shape)} vs "
-                                 f"{tuple(p.shape)}")
-            if not 1 <= pr.m < 1 << 32:
-                raise ValueError(f"m must be in [1, 2^32), got {pr.m}")
-            bias = pr.bias
-            if bias is not None:
-                bias = bias.detach().to(device=a.device, dtype=torch.float32).contiguous()
-                if bias.shape != (w,):
-                    raise ValueError(f"product {i}: bias of shape {tuple(bias.shape)}, "
-                                     f"expected ({w},)")
-                keep.append(bias)
-            table.append((a.data_ptr(), b.data_ptr(), p.data_ptr(),
-                          bias.data_ptr() if bias is not None else 0, a.stride(0), b.stride(0),
-                          p.stride(0), nn, q, w, pr.m, _DT[a.dtype], _DT[b.dtype],
-                          _DT[p.dtype], 0))
-            keep += [a, b, p]
-        arr = np.array(table, dtype=_FV_RECORD)
+        arr, keep, _ = table if table is not None else fv_table(products)
         h = ctypes.c_void_p()
         lib._check(lib._lib.pots_fv_plan_create(n, arr.ctypes.data, k, int(bool(guard)),
                                                 ctypes.byref(h)), "pots_fv_plan_create")

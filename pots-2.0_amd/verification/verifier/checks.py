@@ -38,9 +38,11 @@ the step's statistics with it.
 from __future__ import annotations
 
 import math
+import weakref
 from collections.abc import Callable, Iterator
 from typing import Any
 
+import numpy as np
 import torch
 
 from verification.commitment import native
@@ -61,7 +63,8 @@ from verification.verifier.context import (
     _guard,
     _is_digest,
 )
-from verification.verifier.matmul_check.freivalds import ProductMeasure, finish_rows
+from verification.verifier.matmul_check.freivalds import (ProductMeasure, RowArrays,
+                                                           finish_row_arrays)
 
 __all__ = ["DEFAULT_ORDER", "ROOT_SLOT", "CHECKS", "protocol_id", "check_7_chaining",
            "check_2_commitment", "check_2_root", "check_6a_linear_update", "check_5_matmuls",
@@ -102,7 +105,7 @@ def check_7_chaining(store: TranscriptStore, c: DeclaredComputation, ctx: StepCo
             read_at.add(obj)
             yield i, obj
 
-    hashes, error = leaf_hashes_until_error(c, read())
+    hashes, error = leaf_hashes_until_error(c, read(), plans=ctx.plans, site="7")
     for pos, got in enumerate(hashes):
         i, name = slots[pos], c.weight_names[pos]
         if read_at.changed(pos):
@@ -139,21 +142,20 @@ def check_2_commitment(store: TranscriptStore, c: DeclaredComputation, ctx: Step
 
     with _guard(ctx, "2"):
         with ctx.timed("2.hash"):
-            hashes = leaf_hashes_of(c, read(), ctx.hash_stats())
-        stale = any(leaves.changed(i) for i in range(len(leaves)))
+            hashes = leaf_hashes_of(c, read(), ctx.hash_stats(), ctx.plans, "2")
+        stale = leaves.first_changed()
         claimed = store.root
-    if stale:
-        changed = [i for i in range(len(leaves)) if leaves.changed(i)]
-        return ctx.reject("2", f"leaf {changed[0]} changed in place during check 2", "malformed")
+    if stale is not None:
+        return ctx.reject("2", f"leaf {stale} changed in place during check 2", "malformed")
     for i, h in sorted(ctx.state.early_hashes.items()):
         if hashes[i] != h:
             return ctx.reject("2", f"leaf {i} hashes differently from the bytes an earlier "
                                    f"check read: the store served two versions")
     if not _is_digest(claimed):
         return ctx.reject("2", f"claimed root is not a {DIGEST_SIZE}-byte digest", "malformed")
-    changed = [i for i in range(len(leaves)) if leaves.changed(i)]
-    if changed:
-        return ctx.reject("2", f"leaf {changed[0]} changed in place during check 2", "malformed")
+    stale = leaves.first_changed()  # reading the root may have written a leaf
+    if stale is not None:
+        return ctx.reject("2", f"leaf {stale} changed in place during check 2", "malformed")
     ctx.state.claimed_root, ctx.state.leaf_hashes, ctx.state.leaves = claimed, hashes, leaves
     return None
 
@@ -292,86 +294,153 @@ def check_6b_glue_update(store: TranscriptStore, c: DeclaredComputation, ctx: St
 # ---- check 5: matmuls -------------------------------------------------------------------
 
 
-def _served(c: DeclaredComputation, spec: ProductSpec, ctx: StepContext, leaves: CommittedLeaves,
-            replay: Any) -> native.FvProduct:
-    """Product ``spec.m``'s ``A``, ``B`` (from the replay), committed ``P`` and, for a biased
-    product, its committed ``W_t`` bias in the operand format (as ``[A | 1]·[B ; bᵀ]``), on
-    the current GPU (a store may serve host tensors, as the on-disk one does). A prover-data
-    error while serving is a malformed rejection at check 5; operands of the wrong shape are a
-    verifier error (reference checks.py:805-833)."""
-
-    def on_gpu(x: torch.Tensor) -> torch.Tensor:
-        return x if x.is_cuda else x.to(torch.device("cuda", torch.cuda.current_device()))
-
-    bias = None
-    with _guard(ctx, "5", _AFTER_COMMIT):
-        with ctx.timed("5.glue"):
-            a, b = replay.operands(spec.m)
-        p = leaves.leaf(c.product_index(spec.m))
-        if spec.bias is not None:
-            bias = on_gpu(leaves.leaf(c.w_t_index(spec.bias))).to(c.operand_dtype) \
-                .to(torch.float32)
-    if (tuple(a.shape), tuple(b.shape)) != (spec.a_shape, spec.b_shape):
-        raise RuntimeError(f"{spec.name}: replay operands {tuple(a.shape)}·{tuple(b.shape)} "
-                           f"!= declared {spec.a_shape}·{spec.b_shape}")
-    return native.FvProduct(on_gpu(a), on_gpu(b), on_gpu(p), spec.m, bias)
-
-
 def _serve_until_error(c: DeclaredComputation, ctx: StepContext, leaves: CommittedLeaves,
                        replay: Any) -> tuple[list[native.FvProduct], Exception | None]:
     """Every product served in canonical order, up to the first whose serving raises: the
-    products before it and that error (``None`` when all are served)."""
+    products before it and that error (``None`` when all are served).
+
+    Product ``m`` is its ``A``, ``B`` from the replay, its committed ``P`` and, for a biased
+    product, its committed ``W_t`` bias in the operand format (as ``[A | 1]·[B ; bᵀ]``), on
+    the current GPU (a store may serve host tensors, as the on-disk one does). A prover-data
+    error while serving is check 5's malformed rejection; operands of the wrong shape are a
+    verifier error (reference checks.py:805-833). Either is returned, to be raised after the
+    products before it are judged."""
+    def dev() -> torch.device:
+        return torch.device("cuda", torch.cuda.current_device())
+
+    operands = replay.operands
+    timed = ctx.section is not None
+    p_base = c.n_s + c.n_w - 1
     out: list[native.FvProduct] = []
     for spec in c.products:
         try:
-            out.append(_served(c, spec, ctx, leaves, replay))
+            try:
+                if timed:
+                    with ctx.timed("5.glue"):
+                        a, b = operands(spec.m)
+                else:
+                    a, b = operands(spec.m)
+                p = leaves.leaf(p_base + spec.m)
+                bias = None
+                if spec.bias is not None:
+                    bias = leaves.leaf(c.w_t_index(spec.bias)).to(dev()) \
+                        .to(c.operand_dtype).to(torch.float32)
+            except _AFTER_COMMIT as e:  # prover data: check 5's malformed rejection
+                with _guard(ctx, "5", _AFTER_COMMIT):
+                    raise e
+            if a.shape != spec.a_shape or b.shape != spec.b_shape:
+                raise RuntimeError(f"{spec.name}: replay operands {tuple(a.shape)}·"
+                                   f"{tuple(b.shape)} != declared {spec.a_shape}·{spec.b_shape}")
+            if not a.is_cuda:
+                a = a.to(dev())
+            if not b.is_cuda:
+                b = b.to(dev())
+            if not p.is_cuda:
+                p = p.to(dev())
+            out.append(native.FvProduct(a, b, p, spec.m, bias))
         except Exception as e:  # judged after the products before it
             return out, e
     return out, None
+
+
+_PRODUCT_TABLES: weakref.WeakKeyDictionary[Any, tuple[list[str], np.ndarray, np.ndarray,
+                                                      np.ndarray]] = weakref.WeakKeyDictionary()
+
+
+def _product_table(c: DeclaredComputation) -> tuple[list[str], np.ndarray, np.ndarray,
+                                                    np.ndarray]:
+    """Per product in canonical order: its κ class, ``q``, ``n`` and whether it is biased;
+    built once per computation (its layout does not change)."""
+    try:
+        table = _PRODUCT_TABLES.get(c)
+    except TypeError:
+        table = None
+    if table is None or len(table[0]) != c.M:
+        table = ([product_class(c, s) for s in c.products],
+                 np.array([s.q for s in c.products], dtype=np.int64),
+                 np.array([s.a_shape[0] for s in c.products], dtype=np.int64),
+                 np.array([s.bias is not None for s in c.products], dtype=bool))
+        try:
+            _PRODUCT_TABLES[c] = table
+        except TypeError:
+            pass
+    return table
+
+
+def _first_rejected(f: RowArrays, kappa_max: np.ndarray, ctx: StepContext,
+                    bands: Bands) -> int:
+    """The index of the first product :func:`_judge_product` rejects, or ``M``: the same
+    tests on arrays (finiteness of what is judged; then, when judging, ``ν ≤ κ_max·‖|P|·1‖``
+    and every residual ``≤ τ·unit``, where NaN fails)."""
+    bad = ~(np.isfinite(f.p_norm) & np.isfinite(f.u) & np.isfinite(f.unit)
+            & np.isfinite(f.residuals).all(axis=1))
+    if ctx.kappa_guard:
+        bad |= ~(np.isfinite(f.nu) & np.isfinite(f.p_abs1))
+    if ctx.judge:
+        with np.errstate(invalid="ignore", over="ignore"):
+            if ctx.kappa_guard:
+                bad |= ~(f.nu <= kappa_max * f.p_abs1)
+            bad |= ~(f.residuals <= bands.tau * f.unit[:, None]).all(axis=1)
+    hit = np.flatnonzero(bad)
+    return int(hit[0]) if hit.size else len(bad)
 
 
 def _measure_and_judge(c: DeclaredComputation, prods: list[native.FvProduct], root: bytes,
                        ctx: StepContext, bands: Bands) -> Rejection | None:
     """Measure ``prods`` (the first ``len(prods)`` products in canonical order) in one
     Freivalds plan, read the rows back once, then record and judge them in order; the device
-    verdict kernel judges the same rows and must agree on the first failure."""
-    specs = c.products[:len(prods)]
+    verdict kernel judges the same rows and must agree on the first failure.
+
+    Judging is the reference's per-product closed form and tests (``finish_row``,
+    ``_judge_product``) evaluated on arrays, with the same IEEE operations; the first
+    rejected product is then judged on its own, which words its rejection."""
+    n = len(prods)
+    specs = c.products[:n]
     if not specs:
         return None
+    classes, qs, ns, biased = _product_table(c)
+    qs, ns, biased = qs[:n], ns[:n], biased[:n]
+    kappa_of = {cls: bands.kappa_for(cls) for cls in set(classes[:n])}
+    kappa_max = np.array([kappa_of[cls] for cls in classes[:n]], dtype=np.float64)
     lib = native.get()
     with ctx.timed("5.measure"):
-        plan = lib.fv_plan(prods, ctx.k, ctx.kappa_guard)
+        cache = ctx.plans
+        plan = cache.fv_plan(prods, ctx.k, ctx.kappa_guard) if cache is not None \
+            else lib.fv_plan(prods, ctx.k, ctx.kappa_guard)
         try:
             rows = plan.rows(root)
-            vspecs = native.verdict_specs(
-                [s.q for s in specs], [s.a_shape[0] for s in specs],
-                [s.bias is not None for s in specs],
-                [bands.kappa_for(product_class(c, s)) for s in specs], device=rows.device)
+            vspecs = native.verdict_specs(qs, ns, biased, kappa_max, device=rows.device)
             _, _, first = lib.verdicts(rows, vspecs, k=ctx.k, eps_in=ctx.eps_in,
                                        eps_acc=ctx.eps_acc, tau=bands.tau,
                                        guard=ctx.kappa_guard, judge=ctx.judge)
             host = rows.cpu().numpy()
             device_first = int(first.item())
         finally:
-            plan.close()
+            if cache is not None:
+                cache.release(plan)
+            else:
+                plan.close()
     with ctx.timed("5.judge"):
-        # finish_row on every row at once (the same fp64 operations, bit for bit)
-        mps = finish_rows(host, q=[s.q for s in specs], n=[s.a_shape[0] for s in specs],
-                          eps_in=ctx.eps_in, eps_acc=ctx.eps_acc, guard=ctx.kappa_guard,
-                          biased=[s.bias is not None for s in specs])
-        done = list(zip(specs, mps))
-        for i, (spec, mp) in enumerate(done):
-            rej = _judge_product(c, spec, mp, ctx, bands)
-            if rej is not None:
-                if i != device_first:
-                    raise RuntimeError(f"check 5: the device verdicts reject product index "
-                                       f"{device_first}, the host closed form {i}")
-                ctx.state.run_rest = done[i + 1:]
-                return rej
-    if device_first != len(specs):
-        raise RuntimeError(f"check 5: the device verdicts reject product index {device_first}, "
-                           f"the host closed form accepts every product")
-    return None
+        f = finish_row_arrays(host, q=qs, n=ns, eps_in=ctx.eps_in, eps_acc=ctx.eps_acc,
+                              guard=ctx.kappa_guard, biased=biased)
+        stop = _first_rejected(f, kappa_max, ctx, bands)
+        if stop != device_first:
+            raise RuntimeError(f"check 5: the device verdicts reject product index "
+                               f"{device_first}, the host closed form {stop}")
+        cols = (f.kappa.tolist(), f.normalized.tolist(), f.p_norm.tolist(), f.nu.tolist(),
+                f.p_abs1.tolist(), f.u.tolist())
+        ctx.stats.products.extend(
+            ProductStat(s.m, s.name, cls, kp, tuple(nz), s.q, pn, nu, pa, uu)
+            for s, cls, kp, nz, pn, nu, pa, uu in zip(specs[:stop], classes, *cols))
+        if stop == n:
+            return None
+        rej = _judge_product(c, specs[stop], f.measure(stop), ctx, bands)
+        if rej is None:
+            raise RuntimeError(f"check 5: product index {stop} fails the array tests but "
+                               f"not the per-product judge")
+        ctx.state.run_rest = [(s, f.measure(i)) for i, s in enumerate(specs[stop + 1:],
+                                                                      start=stop + 1)]
+        return rej
 
 
 @_checked

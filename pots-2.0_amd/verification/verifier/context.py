@@ -127,30 +127,46 @@ class CommittedLeaves:
 
     Each tensor's ``_version`` is recorded when the leaf is added and compared on every read,
     so an in-place write through any alias after hashing raises :class:`StoreMutationError`
-    instead of serving changed bytes.
+    instead of serving changed bytes. A tensor leaf keeps its one version as an int, a record
+    the tuple of its tensors' versions.
     """
 
     def __init__(self) -> None:
         self._objs: list[Any] = []
-        self._versions: list[tuple[int, ...]] = []
+        self._versions: list[int | tuple[int, ...]] = []
+
+    @staticmethod
+    def _version(obj: Any) -> int | tuple[int, ...]:
+        if isinstance(obj, torch.Tensor):
+            return obj._version
+        return tuple(t._version for t in _leaf_tensors(obj))
 
     def add(self, obj: Any) -> None:
-        self._versions.append(tuple(t._version for t in _leaf_tensors(obj)))
+        self._versions.append(self._version(obj))
         self._objs.append(obj)
 
     def __len__(self) -> int:
         return len(self._objs)
 
     def changed(self, index: int) -> bool:
-        return tuple(t._version for t in _leaf_tensors(self._objs[index])) != self._versions[index]
+        return self._version(self._objs[index]) != self._versions[index]
+
+    def first_changed(self) -> int | None:
+        """The first leaf written in place since it was added, or ``None``."""
+        version = self._version
+        for i, (obj, v) in enumerate(zip(self._objs, self._versions)):
+            if version(obj) != v:
+                return i
+        return None
 
     def leaf(self, index: int) -> Any:
         # Indices come from C, never from the prover, so a bad one is a verifier bug.
         if not (isinstance(index, int) and 0 <= index < len(self._objs)):
             raise RuntimeError(f"committed leaf index {index!r} outside 0..{len(self._objs) - 1}")
-        if self.changed(index):
+        obj = self._objs[index]
+        if self._version(obj) != self._versions[index]:
             raise StoreMutationError(f"leaf {index} changed in place after check 2 hashed it")
-        return self._objs[index]
+        return obj
 
     def objects(self) -> list[Any]:
         """Every leaf object, in order, without the version test (for one batched read right
@@ -194,6 +210,8 @@ class StepContext:
     judge: bool = True
     kappa_guard: bool = True
     trust_prover_operands: bool = False
+    # the verifier's plan cache (verification.verifier.plans.PlanCache), kept across steps
+    plans: Any = None
     state: StepState = field(default_factory=StepState)
     stats: StepStats = field(default_factory=StepStats)
     section: Section | None = None

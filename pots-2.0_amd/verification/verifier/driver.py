@@ -46,6 +46,7 @@ from verification.verifier.bands import Bands, product_class
 from verification.verifier.checks import CHECKS, DEFAULT_ORDER, ROOT_SLOT
 from verification.verifier.context import (Rejection, Section, StepContext, StepStats,
                                            no_section)
+from verification.verifier.plans import PlanCache
 
 __all__ = ["RUN_START", "RunVerdict", "Verifier"]
 
@@ -139,6 +140,8 @@ class Verifier:
         self.run_timings: dict[str, float] = {}
         self.stats: dict[int, StepStats] = {}
         self.record_pass: dict[int, str] = {}
+        # the leaf and Freivalds plans of the last step, run again while the layout repeats
+        self.plans = PlanCache()
 
     def _adopt(self, bands: Bands) -> None:
         if bands.source == "provisional" and not self.allow_provisional:
@@ -229,7 +232,7 @@ class Verifier:
             h_D=self.h_D, n_records=self.n_records, prev_w_hashes=self._chain,
             chain_check_id="0" if t == 1 else "7", k=self.k, judge=not self.calibrate,
             section=self.section, kappa_guard=self.kappa_guard,
-            trust_prover_operands=self.trust_prover_operands)
+            trust_prover_operands=self.trust_prover_operands, plans=self.plans)
         timings = self.timings[t] = {}
         self.stats[t] = ctx.stats
         with _collector_paused():
@@ -296,8 +299,15 @@ class Verifier:
 
     # ---- run end: checks 8 and 9 --------------------------------------------------------
 
+    def close(self) -> None:
+        """Free the plans kept between steps (their device memory); a later step builds them
+        again."""
+        self.plans.close()
+
     def end_run(self, final: Mapping[str, torch.Tensor] | Sequence[bytes]) -> RunVerdict:
-        """Check 8 against the agreed final weights (tensors or leaf hashes), then check 9."""
+        """Check 8 against the agreed final weights (tensors or leaf hashes), then check 9.
+        The plans kept between steps are freed."""
+        self.plans.close()
         rejected_at_start = self._chain is None and self.rejection is not None
         if self.calibrate and not rejected_at_start:
             raise RuntimeError("calibration is unfrozen: call freeze(bands) before end_run")

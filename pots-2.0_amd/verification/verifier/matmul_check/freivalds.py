@@ -32,7 +32,8 @@ from verification.commitment import native
 from verification.verifier.matmul_check.challenges import SIGMA_R
 from verification.verifier.matmul_check.sizing import product_e_m
 
-__all__ = ["ROW", "MeasureScratch", "ProductMeasure", "band_unit", "finish_row", "finish_rows",
+__all__ = ["ROW", "MeasureScratch", "ProductMeasure", "RowArrays", "band_unit", "finish_row",
+           "finish_rows", "finish_row_arrays",
            "measure_product", "measure_product_row", "measure_products",
            "measure_products_rows", "row_width", "term_scale", "term_scales",
            "measure_batch_rows"]
@@ -168,9 +169,30 @@ def finish_row(row: Sequence[float], *, q: int, n: int, eps_in: float, eps_acc: 
     return mp if guard else replace(mp, kappa=math.nan)
 
 
-def finish_rows(rows: np.ndarray, *, q: Sequence[int], n: Sequence[int], eps_in: float,
-                eps_acc: float, guard: bool = True,
-                biased: Sequence[bool] | None = None) -> list[ProductMeasure]:
+@dataclass(frozen=True)
+class RowArrays:
+    """:func:`finish_row`'s fields for ``M`` rows as fp64 arrays (``residuals`` and
+    ``normalized`` are ``[M, k]``)."""
+
+    nu: np.ndarray
+    p_abs1: np.ndarray
+    kappa: np.ndarray
+    residuals: np.ndarray
+    p_norm: np.ndarray
+    unit: np.ndarray
+    normalized: np.ndarray
+    u: np.ndarray
+
+    def measure(self, i: int) -> ProductMeasure:
+        return ProductMeasure(float(self.nu[i]), float(self.p_abs1[i]), float(self.kappa[i]),
+                              tuple(self.residuals[i].tolist()), float(self.p_norm[i]),
+                              float(self.unit[i]), tuple(self.normalized[i].tolist()),
+                              float(self.u[i]))
+
+
+def finish_row_arrays(rows: np.ndarray, *, q: Sequence[int], n: Sequence[int], eps_in: float,
+                      eps_acc: float, guard: bool = True,
+                      biased: Sequence[bool] | None = None) -> RowArrays:
     """:func:`finish_row` for every row of ``rows`` (fp64 ``[M, 5 + k]``) at once, with the
     same IEEE operations in the same order on arrays, so every field equals
     :func:`finish_row`'s bit for bit; one array pass instead of a Python loop per product."""
@@ -196,8 +218,17 @@ def finish_rows(rows: np.ndarray, *, q: Sequence[int], n: Sequence[int], eps_in:
         unit = np.where(zero, SIGMA_R * np.sqrt(qf) * eps_acc * u, SIGMA_R * e * p_norm)
         normalized = np.where(unit[:, None] > 0, res / unit[:, None],
                               np.where(res == 0, 0.0, np.inf))
-    cols = (nu.tolist(), p_abs1.tolist(), kappa.tolist(), res.tolist(), p_norm.tolist(),
-            unit.tolist(), normalized.tolist(), u.tolist())
+    return RowArrays(nu, p_abs1, kappa, res, p_norm, unit, normalized, u)
+
+
+def finish_rows(rows: np.ndarray, *, q: Sequence[int], n: Sequence[int], eps_in: float,
+                eps_acc: float, guard: bool = True,
+                biased: Sequence[bool] | None = None) -> list[ProductMeasure]:
+    """:func:`finish_row_arrays` as one :class:`ProductMeasure` per row."""
+    f = finish_row_arrays(rows, q=q, n=n, eps_in=eps_in, eps_acc=eps_acc, guard=guard,
+                          biased=biased)
+    cols = (f.nu.tolist(), f.p_abs1.tolist(), f.kappa.tolist(), f.residuals.tolist(),
+            f.p_norm.tolist(), f.unit.tolist(), f.normalized.tolist(), f.u.tolist())
     return [ProductMeasure(a, b, kp, tuple(r), pn, un, tuple(nz), uu)
             for a, b, kp, r, pn, un, nz, uu in zip(*cols)]
 

@@ -223,3 +223,43 @@ def test_serving_error_after_a_forged_product(lib):
             assert rej.detail == (f"malformed prover data: TranscriptFormatError: operands of "
                                   f"product {m_spec.m} unreadable")
             assert [s.m for s in v.stats[1].products] == [s.m for s in c.products[:40]]
+
+
+def test_plans_kept_between_steps_run_again_only_on_the_same_layout(lib):
+    """A verifier keeps its last step's leaf and Freivalds plans. A step with the same layout
+    (here the same tensors) runs them again with the same hashes and statistics; a product
+    changed in place, at the same address, still rejects at check 5; a product moved to
+    another buffer makes check 2's leaf plan and the Freivalds plan be built again."""
+    from conftest import started_verifier
+    from verification.transcript.store import InMemoryStore
+    c, step = _step(21)
+    claimed = _root(c, step.leaves)
+    v1 = started_verifier(c, step.leaves, k=2)
+    assert v1.verify_step(1, InMemoryStore(step.leaves, claimed_root=claimed)) is None
+    cache = v1.plans
+    assert (cache.builds, cache.hits) == (3, 0)  # check 7's and 2's leaf plans, Freivalds
+    v2 = started_verifier(c, step.leaves, k=2)
+    v2.plans = cache
+    assert v2.verify_step(1, InMemoryStore(step.leaves, claimed_root=claimed)) is None
+    assert (cache.builds, cache.hits) == (3, 3)
+    assert [repr(s) for s in v2.stats[1].products] == [repr(s) for s in v1.stats[1].products]
+
+    spec = c.products[7]
+    honest = step.product(spec.m)[0, 1].clone()
+    step.product(spec.m)[0, 1] += 8.0  # forged in place: the layout is unchanged
+    v3 = started_verifier(c, step.leaves, k=2)
+    v3.plans = cache
+    rej = v3.verify_step(1, InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves)))
+    assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
+    assert rej.detail.startswith(f"P_{spec.m} ("), rej.detail
+    assert (cache.builds, cache.hits) == (3, 6)
+
+    step.product(spec.m)[0, 1] = honest
+    i = c.product_index(spec.m)
+    step.leaves[i] = step.leaves[i].clone()  # the same bytes in another buffer
+    v4 = started_verifier(c, step.leaves, k=2)
+    v4.plans = cache
+    assert v4.verify_step(1, InMemoryStore(step.leaves, claimed_root=claimed)) is None
+    assert (cache.builds, cache.hits) == (5, 7)
+    assert [repr(s) for s in v4.stats[1].products] == [repr(s) for s in v1.stats[1].products]
+    v4.close()

@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -283,3 +284,50 @@ def test_verifier_constructor_refuses_what_the_reference_refuses():
     with pytest.raises(RuntimeError, match="start_run"):
         v.verify_step(1, None)
     assert v.band_source == "provisional"
+
+
+@pytest.mark.parametrize("guard", [True, False])
+@pytest.mark.parametrize("judge", [True, False])
+@pytest.mark.parametrize("seed", range(6))
+def test_array_judge_stops_where_the_per_product_judge_does(guard, judge, seed):
+    """Check 5 finds the first rejected product with array tests; on rows with NaN, inf,
+    zero norms, κ at and over its band and residuals at and over τ·unit, it must stop at the
+    product a per-product ``finish_row`` + ``_judge_product`` loop stops at, record the same
+    statistics before it, and word the same rejection."""
+    from verification.verifier.checks import _first_rejected, _judge_product, _product_table
+    from verification.verifier.matmul_check.freivalds import finish_row, finish_row_arrays
+    c = _tiny_decoder()
+    bands = Bands.provisional()
+    classes, qs, ns, biased = _product_table(c)
+    kmax = np.array([bands.kappa_for(cls) for cls in classes])
+    g = np.random.default_rng(seed)
+    M, k = c.M, 2
+    rows = np.abs(g.normal(size=(M, 5 + k)))
+    rows[:, 5:] *= 1e-12
+    specials = [np.nan, np.inf, 0.0, 1e300]
+    for _ in range(3):  # a few rows with special entries at random places
+        i, j = g.integers(M), g.integers(5 + k)
+        rows[i, j] = specials[g.integers(len(specials))]
+    i = g.integers(M)
+    rows[i, 1] = rows[i, 0] / kmax[i] * (1 - 1e-12)  # κ just over its band
+    ctx = _ctx(k=k, judge=judge, kappa_guard=guard)
+    f = finish_row_arrays(rows, q=qs, n=ns, eps_in=ctx.eps_in, eps_acc=ctx.eps_acc,
+                          guard=guard, biased=biased)
+    i = int(g.integers(M))
+    rows[i, 5] = bands.tau * f.unit[i] * (1 + 1e-9)  # a residual just over τ·unit
+    f = finish_row_arrays(rows, q=qs, n=ns, eps_in=ctx.eps_in, eps_acc=ctx.eps_acc,
+                          guard=guard, biased=biased)
+    stop = _first_rejected(f, kmax, ctx, bands)
+    ref_ctx = _ctx(k=k, judge=judge, kappa_guard=guard)
+    want, ref_rej = M, None
+    for m, spec in enumerate(c.products):
+        mp = finish_row(rows[m].tolist(), q=spec.q, n=spec.a_shape[0], eps_in=ctx.eps_in,
+                        eps_acc=ctx.eps_acc, guard=guard, biased=bool(biased[m]))
+        ref_rej = _judge_product(c, spec, mp, ref_ctx, bands)
+        if ref_rej is not None:
+            want = m
+            break
+    assert stop == want
+    if stop < M:
+        assert _judge_product(c, c.products[stop], f.measure(stop), ctx, bands) == ref_rej
+        assert repr(ctx.stats.products[-1]) == repr(ref_ctx.stats.products[-1])  # NaN κ
