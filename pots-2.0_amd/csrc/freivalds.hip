@@ -401,20 +401,39 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   }
 }
 
-// The row pass over n_tiles tiles: block b takes tiles b, b + gridDim.x, ... A grid smaller
-// than the tile count keeps the pass to a bounded share of each CU (a block holds 4 waves and
-// 32 KiB of LDS), so that a kernel on another stream (the leaf hasher) keeps the rest.
+// The row pass over n_tiles tiles. With a block per tile (queue null), block b takes tile b.
+// With a smaller grid, the pass holds a bounded share of each CU (a block holds 4 waves and
+// 32 KiB of LDS) so that a kernel on another stream (the leaf hasher) keeps the rest, and the
+// blocks take tiles from a queue: a counter (zero at launch) that each block's first thread
+// advances by one per tile. A block that lands on a CU shared with more hashing waves then
+// takes fewer tiles, where a fixed split would leave it the last to finish. Every thread of a
+// block reads the same tile index, so all of its waves leave the loop together once the
+// counter passes n_tiles.
 template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
 __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
                                                 const uint32_t* __restrict__ blk_job,
-                                                uint32_t k, uint32_t n_tiles) {
+                                                uint32_t k, uint32_t n_tiles,
+                                                uint32_t* __restrict__ queue) {
   using G = Geo<XT>;
   __shared__ float s_u[WEIGHTED ? G::CHUNK : 4], s_w[WEIGHTED ? G::CHUNK : 4];
-  for (uint32_t b = blockIdx.x; b < n_tiles; b += gridDim.x) {
+  __shared__ uint32_t s_tile;
+  if (queue == nullptr) {
+    if (blockIdx.x < n_tiles) row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, blockIdx.x,
+                                                                 s_u, s_w);
+    return;
+  }
+  for (;;) {
+    if (threadIdx.x == 0) s_tile = atomicAdd(queue, 1u);
+    __syncthreads();
+    const uint32_t b = s_tile;
+    __syncthreads();  // every thread has read s_tile before thread 0 writes the next one
+    if (b >= n_tiles) break;
     row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, b, s_u, s_w);
     if (WEIGHTED) __syncthreads();  // the next tile restages the weights
   }
 }
+
+__global__ void queue_reset(uint32_t* q) { *q = 0u; }
 
 // ---- B-pass reduction: B·R, |B|·1, B²·1 per row of B, packed for the A pass -------------
 
@@ -783,6 +802,7 @@ struct FvPlan {
   char* base = nullptr;
   size_t total = 0;
   uint32_t* d_key = nullptr;
+  uint32_t* d_queue = nullptr;  // a row pass's tile queue counter per stage (grid-limited passes)
   ChallengeItem* d_items_b3 = nullptr;  // items whose R is read by bf16 passes
   ChallengeItem* d_items_f4 = nullptr;
   uint32_t n_items = 0;
@@ -865,6 +885,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     return a;
   };
   const size_t o_key = place(32);
+  const size_t o_queue = place(POTS_FV_STAGES * sizeof(uint32_t));
   const uint64_t b3_per_row = (uint64_t)groups_b3(k) * 16;  // bf16 elements per row of V
   const uint64_t f4_per_row = (uint64_t)groups_f4(k) * 16;  // floats per row of V
   std::vector<ChallengeItem> items(n);
@@ -1089,6 +1110,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   }
   const uint64_t base = reinterpret_cast<uint64_t>(P->base);
   P->d_key = reinterpret_cast<uint32_t*>(P->base + o_key);
+  P->d_queue = reinterpret_cast<uint32_t*>(P->base + o_queue);
   P->d_items_b3 = reinterpret_cast<ChallengeItem*>(P->base + o_items_b3);
   P->d_items_f4 = reinterpret_cast<ChallengeItem*>(P->base + o_items_f4);
   P->d_r = reinterpret_cast<float*>(P->base + o_r);
@@ -1348,34 +1370,42 @@ int fv_fuse_commit(void* fv, const std::vector<uint32_t>& prods,
 
 template <uint32_t XT, bool W, bool S, uint32_t NJG>
 static void launch_pass(const FvPlan* P, const PassLaunch& L, uint32_t max_grid,
-                        hipStream_t s) {
-  const uint32_t grid = max_grid ? std::min(max_grid, L.n_blocks) : L.n_blocks;
+                        uint32_t* queue, hipStream_t s) {
+  const bool queued = max_grid != 0 && max_grid < L.n_blocks;
+  const uint32_t grid = queued ? max_grid : L.n_blocks;
+  if (queued) hipLaunchKernelGGL(queue_reset, dim3(1), dim3(1), 0, s, queue);
   hipLaunchKernelGGL((row_pass<XT, W, S, NJG>), dim3(grid), dim3(256), 0, s,
-                     P->d_jobs + L.job_off, P->d_blk + L.blk_off, P->k, L.n_blocks);
+                     P->d_jobs + L.job_off, P->d_blk + L.blk_off, P->k, L.n_blocks,
+                     queued ? queue : nullptr);
 }
 
 template <uint32_t XT, bool W, bool S>
-static int launch_njg(const FvPlan* P, const PassLaunch& L, uint32_t g, hipStream_t s) {
+static int launch_njg(const FvPlan* P, const PassLaunch& L, uint32_t g, uint32_t* q,
+                      hipStream_t s) {
   switch (L.njg) {
-    case 1: launch_pass<XT, W, S, 1>(P, L, g, s); return POTS_E_OK;
-    case 2: launch_pass<XT, W, S, 2>(P, L, g, s); return POTS_E_OK;
-    case 3: launch_pass<XT, W, S, 3>(P, L, g, s); return POTS_E_OK;
-    case 4: launch_pass<XT, W, S, 4>(P, L, g, s); return POTS_E_OK;
+    case 1: launch_pass<XT, W, S, 1>(P, L, g, q, s); return POTS_E_OK;
+    case 2: launch_pass<XT, W, S, 2>(P, L, g, q, s); return POTS_E_OK;
+    case 3: launch_pass<XT, W, S, 3>(P, L, g, q, s); return POTS_E_OK;
+    case 4: launch_pass<XT, W, S, 4>(P, L, g, q, s); return POTS_E_OK;
     default: return POTS_E_ARG;
   }
 }
 
-static int run_pass(const FvPlan* P, const PassLaunch& L, uint32_t g, hipStream_t s) {
+// A pass launch of stage `stage` (1 B, 3 A, 4 P) with grid limit g; the stage's tile queue
+// counter is the plan's d_queue[stage].
+static int run_pass(const FvPlan* P, const PassLaunch& L, int stage, hipStream_t s) {
   if (L.n_blocks == 0) return POTS_E_OK;
   const uint32_t key = L.xt * 4 + L.weighted * 2 + L.sq64;
+  const uint32_t g = P->max_grid[stage];
+  uint32_t* q = P->d_queue + stage;
   int rc;
   switch (key) {
-    case 0: rc = launch_njg<DT_F32, false, false>(P, L, g, s); break;
-    case 1: rc = launch_njg<DT_F32, false, true>(P, L, g, s); break;
-    case 2: rc = launch_njg<DT_F32, true, false>(P, L, g, s); break;
-    case 4: rc = launch_njg<DT_BF16, false, false>(P, L, g, s); break;
-    case 5: rc = launch_njg<DT_BF16, false, true>(P, L, g, s); break;
-    case 6: rc = launch_njg<DT_BF16, true, false>(P, L, g, s); break;
+    case 0: rc = launch_njg<DT_F32, false, false>(P, L, g, q, s); break;
+    case 1: rc = launch_njg<DT_F32, false, true>(P, L, g, q, s); break;
+    case 2: rc = launch_njg<DT_F32, true, false>(P, L, g, q, s); break;
+    case 4: rc = launch_njg<DT_BF16, false, false>(P, L, g, q, s); break;
+    case 5: rc = launch_njg<DT_BF16, false, true>(P, L, g, q, s); break;
+    case 6: rc = launch_njg<DT_BF16, true, false>(P, L, g, q, s); break;
     default: return POTS_E_ARG;
   }
   if (rc != POTS_E_OK) return rc;
@@ -1404,7 +1434,7 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
       return POTS_E_OK;
     case 1:
       for (const PassLaunch& L : P->pass_b)
-        if ((rc = run_pass(P, L, P->max_grid[1], s)) != POTS_E_OK) return rc;
+        if ((rc = run_pass(P, L, 1, s)) != POTS_E_OK) return rc;
       return POTS_E_OK;
     case 2: {
       const uint64_t blocks = (P->n_red_threads + 255) / 256;
@@ -1418,7 +1448,7 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
     case POTS_FV_STAGE_P_PASS:
       for (const PassLaunch& L : P->pass_ap)
         if ((L.weighted != 0) == (stage == 3) &&
-            (rc = run_pass(P, L, P->max_grid[stage == 3 ? 3 : 4], s)) != POTS_E_OK)
+            (rc = run_pass(P, L, stage == 3 ? 3 : 4, s)) != POTS_E_OK)
           return rc;
       return POTS_E_OK;
     case 4:  // the P pass, then the fused products' records

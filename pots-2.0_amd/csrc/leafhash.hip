@@ -157,9 +157,14 @@ __device__ __forceinline__ void run_add(const uint32_t* w, uint64_t rcol, uint32
 #pragma unroll
   for (int t = 0; t < NE; t++) {
     if (MASKED && !((uint32_t)t >= lo && (uint32_t)t < hi)) continue;
+    uint32_t wt = w[ESZ == 2 ? t >> 1 : t];
+    // A masked pair is taken in two calls over the same words: an empty asm statement per
+    // element keeps each conversion under its own bounds test, where the compiler would
+    // otherwise convert all of the pair's elements once, ahead of both calls, and hold them.
+    if (MASKED) asm volatile("" : "+v"(wt));
     float x;
-    if (ESZ == 2) x = __uint_as_float((t & 1) ? (w[t >> 1] & 0xFFFF0000u) : (w[t >> 1] << 16));
-    else x = __uint_as_float(w[t]);
+    if (ESZ == 2) x = __uint_as_float((t & 1) ? (wt & 0xFFFF0000u) : (wt << 16));
+    else x = __uint_as_float(wt);
     const v4f32 r = R[t];
     a.d0 = fmaf(x, r[0], a.d0);
     a.d1 = fmaf(x, r[1], a.d1);

@@ -136,16 +136,22 @@ class DeviceStepVerifier:
             ready = torch.cuda.Event()
             ready.record(main)
             side.wait_event(ready)
+            # The row pass over the unfused products' P needs only the challenges: it runs on
+            # the side stream after the chunk kernels, off the A pass's critical path.
+            p_done = torch.cuda.Event()
             with torch.cuda.stream(side):
                 c_begin.record(side)
                 hp.run_stage(native.LeafPlan.FUSED_CHUNKS, self.digests, self.bad, side)
                 c_end.record(side)
                 if not self.plain_early:
                     hp.run_stage(native.LeafPlan.PLAIN_CHUNKS, self.digests, self.bad, side)
+                plan.run_stage(native.FvPlan.P_PASS, self.key, self.rows, side)
+                p_done.record(side)
             for st in range(3 if self.hash_after_b else 1, 4):
                 plan.run_stage(st, self.key, self.rows, main)
-            main.wait_event(c_end)  # the P stage adds up the fused kernel's run records
-            plan.run_stage(4, self.key, self.rows, main)
+            main.wait_event(c_end)  # the fused products' sums add up the chunk kernel's records
+            plan.run_stage(native.FvPlan.P_FUSED, self.key, self.rows, main)
+            main.wait_event(p_done)
         with torch.cuda.stream(side):
             hp.run_stage(2, self.digests, self.bad, side)
             nodes = self.lib.merkle_tree_device(self.digests, side)

@@ -283,3 +283,27 @@ def test_verdicts_bit_exact_with_python(lib, guard, biased):
         if want[0] != 0:
             first_want = min(first_want, i)
     assert int(first.item()) == first_want
+
+
+@pytest.mark.parametrize("k", [4, 7])
+def test_grid_limited_passes_take_tiles_from_a_queue(lib, k):
+    """Row passes limited to fewer blocks than they have tiles take their tiles from a queue
+    that each launch resets: two runs in a row give the rows of the plan with a block per tile
+    bit for bit, for bf16 and fp32 operands and a bias."""
+    from verification.commitment import native
+    items = []
+    for i, (shape, dtype, biased) in enumerate([((1024, 2048, 640), torch.bfloat16, True),
+                                                ((777, 4500, 300), torch.bfloat16, False),
+                                                ((300, 1100, 200), torch.float32, False),
+                                                ((2048, 256, 1536), torch.bfloat16, False)]):
+        a, b, p, bias = _operands(*shape, 70 + i, dtype, bias=biased)
+        items.append(native.FvProduct(a.cuda(), b.cuda(), p.cuda(), 200 + i,
+                                      None if bias is None else bias.cuda()))
+    want = lib.fv_plan(items, k).rows(H)
+    plan = lib.fv_plan(items, k)
+    for stage, blocks in ((1, 3), (3, 5), (4, 7)):
+        plan.set_grid(stage, blocks)
+    for _ in range(2):
+        got = plan.rows(H)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int64), want.view(torch.int64))
