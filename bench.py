@@ -227,15 +227,21 @@ def trace_summary(d: Path, steps: int, warmup: int) -> int:
         if k.startswith("pots::") or k.startswith("__amd"):
             print(f"| `{k}` | {len(ds)} | {sum(ds) / len(ds):.3f} | {min(ds):.3f} | "
                   f"{max(ds):.3f} |")
-    name = "pots::chunk_kernel_fused" if "pots::chunk_kernel_fused" in by else \
+    chunk = "pots::chunk_kernel_fused" if "pots::chunk_kernel_fused" in by else \
         "pots::chunk_kernel"
-    ck = by.get(name, [])
-    n_pre = 1 + warmup
-    timed, leg = ck[n_pre:n_pre + steps], ck[n_pre + steps:]
-    if timed and leg:
-        print(f"\n{name[6:]}: {len(timed)} launches in the timed steps, mean "
-              f"{sum(timed) / len(timed):.3f} ms (beside the Freivalds passes); {len(leg)} "
-              f"launches in the serialised stage leg, mean {sum(leg) / len(leg):.3f} ms")
+    # (kernel, launches before the warm-up steps: the claimed root's hashing), then its
+    # launches in the warm-up steps, the timed steps and the serialised stage leg
+    print()
+    for name, n_root, beside in ((chunk, 1, "the Freivalds passes"),
+                                 ("pots::row_pass<1u, true, false, 1u>", 0, "the chunk kernels")):
+        ck = by.get(name, [])
+        n_pre = n_root + warmup
+        n_leg = max(3, min(steps, 5))  # the stage leg's runs, as main() makes them
+        timed, leg = ck[n_pre:n_pre + steps], ck[n_pre + steps:n_pre + steps + n_leg]
+        if timed and leg:
+            print(f"{name[6:]}: {len(timed)} launches in the timed steps, mean "
+                  f"{sum(timed) / len(timed):.3f} ms (beside {beside}); {len(leg)} launches "
+                  f"in the serialised stage leg, mean {sum(leg) / len(leg):.3f} ms")
     return 0
 
 
@@ -650,6 +656,8 @@ def main() -> int:
     measured_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / args.steps
     # the chunk kernel inside the timed steps, on its own (side) stream, beside the Freivalds
     chunks_in_step_ms = sum(e[4].elapsed_time(e[5]) for e in evs) / args.steps
+    # the A pass inside the timed steps, beside the chunk kernels
+    a_in_step_ms = sum(e[6].elapsed_time(e[7]) for e in evs) / args.steps
     root = flags[:8].numpy().tobytes()
     first_bad, first_fail = int(flags[8]), int(flags[9])
     assert root == claimed_b, "recomputed root differs from the claim"
@@ -762,10 +770,23 @@ def main() -> int:
                            "achieved_tops": round(ops / (stage_ms[nm] * 1e-3) / 1e12, 2),
                            "peak_tops": round(VALU_PEAK_OPS / 1e12, 2),
                            "frac": round(ops / (stage_ms[nm] * 1e-3) / VALU_PEAK_OPS, 4)}
-    # the kernel the step's chunk events bracket
-    in_step_kernel = "hash.chunks_fused" if v.fused else "hash.chunks"
+    # the kernels the step's events bracket
+    in_step = {"hash.chunks_fused" if v.fused else "hash.chunks": chunks_in_step_ms,
+               "freivalds.a_pass": a_in_step_ms}
     dom_name, dom_bytes = kernels[dom]
     achieved = dom_bytes / (stage_ms[dom] * 1e-3) / 1e9
+
+    def kernel_roofline(nm: str) -> dict:
+        kname, nbytes = kernels[nm]
+        gbps = nbytes / (stage_ms[nm] * 1e-3) / 1e9
+        out = {"bound": "valu" if nm.startswith("hash.") else "hbm",
+               "achieved": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+               "algorithmic_bytes": nbytes, "launch_ms": round(stage_ms[nm], 4),
+               "launch_ms_in_step": (round(in_step[nm], 4) if nm in in_step else None),
+               "traffic": traffic_from_profile(kname)}
+        if kname in valu:
+            out["valu_frac"] = valu[kname]["frac"]
+        return out
     hash_ms = sum(stage_ms[nm] for _, nm in leaf_stages)
     fv_ms = sum(stage_ms[f"freivalds.{s}"] for s in native.FvPlan.STAGES)
     total = hash_bytes + fv_bytes
@@ -812,9 +833,12 @@ def main() -> int:
                      "traffic": traffic_from_profile(dom_name),
                      "kernel": dom_name,
                      "algorithmic_bytes": dom_bytes, "launch_ms": round(stage_ms[dom], 4),
-                     "launch_ms_in_step": (round(chunks_in_step_ms, 4)
-                                           if dom == in_step_kernel else None),
-                     "valu": valu},
+                     "launch_ms_in_step": (round(in_step[dom], 4) if dom in in_step else None),
+                     "valu": valu,
+                     # every kernel of the step with its own roofline: the chunk kernels are
+                     # bound by 32-bit VALU issue ("valu_frac"), the row passes by HBM
+                     "kernels": {kernels[nm][0]: kernel_roofline(nm) for nm in
+                                 sorted(kernels, key=lambda nm: -stage_ms[nm])}},
     }
     if args.check_level:
         out["parts"]["check_level"] = check_level_leg(c, step, k, claimed_b)

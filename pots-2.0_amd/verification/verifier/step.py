@@ -103,7 +103,8 @@ class DeviceStepVerifier:
         """Enqueue the whole step on the current stream (Freivalds, verdicts) and a side
         stream (hashing, tree); returns GPU tensors ``(nodes, codes, first_fail)``.
         ``events``, if given, receives (start, hashed, measured, judged, chunks_begin,
-        chunks_end) CUDA events; the last two bracket the chunk kernel on the side stream."""
+        chunks_end, a_begin, a_end) CUDA events: chunks_* bracket the chunk kernel on the side
+        stream, a_* the A pass on the current stream."""
         main = torch.cuda.current_stream()
         if isinstance(claimed, torch.Tensor):
             self.key.copy_(claimed)
@@ -115,6 +116,8 @@ class DeviceStepVerifier:
         plan, hp, side = self.plan, self.hasher.plan, self.side
         c_begin = torch.cuda.Event(enable_timing=timing)
         c_end = torch.cuda.Event(enable_timing=timing)
+        a_begin = torch.cuda.Event(enable_timing=timing)
+        a_end = torch.cuda.Event(enable_timing=timing)
         side.wait_event(start)
         if not self.fused:
             with torch.cuda.stream(side):
@@ -123,7 +126,11 @@ class DeviceStepVerifier:
                 hp.run_stage(1, self.digests, self.bad, side)
                 c_end.record(side)
             for st in range(5):
+                if st == 3:
+                    a_begin.record(main)
                 plan.run_stage(st, self.key, self.rows, main)
+                if st == 3:
+                    a_end.record(main)
         else:
             # The fused chunk kernel reads the challenges and, started after the B pass,
             # shares the CUs with a bounded A pass; the other leaves' chunks go first.
@@ -136,22 +143,22 @@ class DeviceStepVerifier:
             ready = torch.cuda.Event()
             ready.record(main)
             side.wait_event(ready)
-            # The row pass over the unfused products' P needs only the challenges: it runs on
-            # the side stream after the chunk kernels, off the A pass's critical path.
-            p_done = torch.cuda.Event()
             with torch.cuda.stream(side):
                 c_begin.record(side)
                 hp.run_stage(native.LeafPlan.FUSED_CHUNKS, self.digests, self.bad, side)
                 c_end.record(side)
                 if not self.plain_early:
                     hp.run_stage(native.LeafPlan.PLAIN_CHUNKS, self.digests, self.bad, side)
-                plan.run_stage(native.FvPlan.P_PASS, self.key, self.rows, side)
-                p_done.record(side)
             for st in range(3 if self.hash_after_b else 1, 4):
+                if st == 3:
+                    a_begin.record(main)
                 plan.run_stage(st, self.key, self.rows, main)
-            main.wait_event(c_end)  # the fused products' sums add up the chunk kernel's records
+            a_end.record(main)
+            # the unfused products' P pass needs only the challenges; the fused products' sums
+            # add up the chunk kernel's run records
+            plan.run_stage(native.FvPlan.P_PASS, self.key, self.rows, main)
+            main.wait_event(c_end)
             plan.run_stage(native.FvPlan.P_FUSED, self.key, self.rows, main)
-            main.wait_event(p_done)
         with torch.cuda.stream(side):
             hp.run_stage(2, self.digests, self.bad, side)
             nodes = self.lib.merkle_tree_device(self.digests, side)
@@ -169,7 +176,7 @@ class DeviceStepVerifier:
         # keep the side stream's tensors alive for the main stream's consumers
         nodes.record_stream(main)
         if events is not None:
-            events.append((start, hashed, measured, judged, c_begin, c_end))
+            events.append((start, hashed, measured, judged, c_begin, c_end, a_begin, a_end))
         return nodes, codes, first
 
     def run(self, claimed: bytes) -> StepVerdict:
