@@ -9,7 +9,9 @@ name is the reference code it follows:
 
 - ``blake3`` / ``hash_leaf`` / ``hash_node`` — BLAKE3 from the spec (``blake3_spec.c``),
   ``verification/commitment/merkle.py:37-44,153-155``.
-- ``hash_leaves`` — ``verification/commitment/native.c:243`` (``native_twin.c``).
+- ``hash_leaves`` — ``verification/commitment/native.c:243`` (``native_twin.c``; with
+  ``simd=True`` ``blake3_simd.c``, the same leaves 16 chunks per AVX-512 instruction, as the
+  reference's BLAKE3 library hashes them on the CPU).
 - ``merkle_tree`` / ``merkle_root`` / ``verify_path`` — ``native.c:315-337``,
   ``merkle.py:181-224,309-328``.
 - ``tensor_leaf_header`` / ``encode_record`` — ``verification/commitment/encoding.py:45-56``,
@@ -87,6 +89,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_blake3.restype = None
         L.oracle_hash_leaves.argtypes = [sz, vp, vp, vp, vp, vp, vp, vp, vp, u32]
         L.oracle_hash_leaves.restype = sz
+        L.oracle_hash_leaves_simd.argtypes = [sz, vp, vp, vp, vp, vp, vp, vp, vp, u32]
+        L.oracle_hash_leaves_simd.restype = sz
+        L.oracle_simd_degree.argtypes = []
+        L.oracle_simd_degree.restype = ctypes.c_int
         L.oracle_all_finite.argtypes = [vp, u64, ctypes.c_uint8]
         L.oracle_all_finite.restype = ctypes.c_int
         L.oracle_merkle_tree.argtypes = [sz, vp, vp]
@@ -195,10 +201,18 @@ def tensor_leaf_hash(tag: int, t: torch.Tensor) -> bytes:
     return hash_leaf(tensor_leaf_header(tag, t), payload_bytes(t))
 
 
+def simd_degree() -> int:
+    """Chunks ``hash_leaves(..., simd=True)`` compresses per instruction: 16 with AVX-512, 1
+    (the spec hasher) without."""
+    return int(lib().oracle_simd_degree())
+
+
 def hash_leaves(items: Sequence[tuple[bytes, torch.Tensor | bytes, int]],
-                threads: int | None = None) -> tuple[list[bytes], int]:
+                threads: int | None = None, simd: bool = False) -> tuple[list[bytes], int]:
     """``oracle_hash_leaves`` over ``(header, payload, kind)`` items (CPU payloads): the
-    digests (those from the first bad leaf on are not meaningful) and the first bad index."""
+    digests (those from the first bad leaf on are not meaningful) and the first bad index.
+    ``simd`` takes the 16-lane chunk compressor of ``blake3_simd.c`` (the bench's CPU
+    baseline, at the reference's CPU speed), checked against the spec hasher by the tests."""
     n = len(items)
     if n == 0:
         return [], 0
@@ -221,11 +235,13 @@ def hash_leaves(items: Sequence[tuple[bytes, torch.Tensor | bytes, int]],
             ptrs[i], lens[i] = b.ctypes.data, b.nbytes
     kind = np.array([k for _, _, k in items], dtype=np.uint8)
     out = np.zeros((n, 32), dtype=np.uint8)
-    bad = lib().oracle_hash_leaves(n, hdr_buf, hdr_off.ctypes.data, hdr_len.ctypes.data,
-                                   hdr_idx.ctypes.data, ptrs.ctypes.data, lens.ctypes.data,
-                                   kind.ctypes.data, out.ctypes.data,
-                                   threads or _threads())
+    fn = lib().oracle_hash_leaves_simd if simd else lib().oracle_hash_leaves
+    bad = fn(n, hdr_buf, hdr_off.ctypes.data, hdr_len.ctypes.data, hdr_idx.ctypes.data,
+             ptrs.ctypes.data, lens.ctypes.data, kind.ctypes.data, out.ctypes.data,
+             threads or _threads())
     del keep
+    if bad == (1 << 64) - 1:
+        raise MemoryError("oracle_hash_leaves_simd: out of memory or a header over 1 KiB")
     return [bytes(r) for r in out], int(bad)
 
 

@@ -105,6 +105,47 @@ def test_hash_leaves_first_bad_and_kinds():
     assert bad == 1
 
 
+def test_simd_leaf_hashing_equals_the_spec_hasher():
+    """The bench's CPU baseline hashes with 16 chunks per AVX-512 instruction
+    (``blake3_simd.c``); every digest must equal the spec hasher's: message lengths around one
+    chunk, 16 chunks (one full batch) and 17 (a batch plus a partial chunk), whole batches with
+    and without a tail, headers of 1 to 4 dimensions (the 0x00 ‖ header prefix shifts every
+    chunk's start), and a leaf of over 2^16 chunks."""
+    g = torch.Generator().manual_seed(8)
+    items = []
+    for hl_dims in (1, 2, 4):
+        shape = (3,) * hl_dims
+        hdr = O.tensor_leaf_header(O.TAG_PRODUCT, torch.zeros(shape))
+        m0 = 1 + len(hdr)
+        for msg in (m0, 1023, 1024, 1025, 2048, 2049, 16 * 1024, 16 * 1024 + 1, 17 * 1024 - 3,
+                    32 * 1024, 33 * 1024 + 7, 100_000):
+            p = torch.randint(0, 256, (msg - m0,), dtype=torch.uint8, generator=g)
+            items.append((hdr, p, 0))
+    items.append((b"", torch.randint(0, 256, ((1 << 26) + 5,), dtype=torch.uint8,
+                                     generator=g), 0))
+    want, bad_want = O.hash_leaves(items)
+    got, bad_got = O.hash_leaves(items, simd=True)
+    assert bad_got == bad_want == len(items)
+    assert got == want
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_simd_leaf_hashing_finds_the_same_first_bad_leaf(dtype):
+    """The SIMD path tests each payload for NaN/Inf before hashing it, 64 bytes per compare:
+    a value in the vector body or in the scalar tail, in any leaf, gives the spec hasher's first
+    bad index and the same digests before it."""
+    kind = O.FINITE_KIND[dtype]
+    for n, pos in ((1000, 3), (1000, 999), (40, 39), (5000, 2048)):
+        ts = [torch.randn(n).to(dtype) for _ in range(6)]
+        ts[4][pos] = float("nan")
+        ts[2][pos] = float("-inf")
+        items = [(O.tensor_leaf_header(3, t), t, kind) for t in ts]
+        want, bad_want = O.hash_leaves(items)
+        got, bad_got = O.hash_leaves(items, simd=True)
+        assert bad_got == bad_want == 2
+        assert got[:2] == want[:2]
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_half_kinds_flag_either_half_of_a_word(dtype):
     kind = O.FINITE_KIND[dtype]
