@@ -263,3 +263,24 @@ def test_plans_kept_between_steps_run_again_only_on_the_same_layout(lib):
     assert (cache.builds, cache.hits) == (5, 7)
     assert [repr(s) for s in v4.stats[1].products] == [repr(s) for s in v1.stats[1].products]
     v4.close()
+
+
+def test_new_records_keep_check_2s_plan(lib):
+    """Records are hashed as their own batch, so a step with other records over the same
+    tensor buffers still reuses check 2's leaf plan; the new root is the oracle's."""
+    from conftest import started_verifier
+    from setup.records import Record
+    from verification.transcript.store import InMemoryStore
+    c, step = _step(22)
+    v1 = started_verifier(c, step.leaves, k=2)
+    assert v1.verify_step(1, InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves))) \
+        is None
+    cache = v1.plans
+    r = step.leaves[0]
+    step.leaves[0] = Record(torch.flip(r.ids, [0]).contiguous(), r.targets, r.mask)
+    claimed = _root(c, step.leaves)
+    v2 = started_verifier(c, step.leaves, k=2)
+    v2.plans = cache
+    assert v2.verify_step(1, InMemoryStore(step.leaves, claimed_root=claimed)) is None
+    assert (cache.builds, cache.hits) == (3, 3)
+    assert v2.stats[1].products  # check 5 ran on the cached Freivalds plan
