@@ -164,7 +164,7 @@ def kernel_label(name: str) -> str:
         if sq64 == "true":
             return f"row_pass<{dt}, fp64 squares> (P pass)"
         return f"row_pass<{dt}> (B pass)"
-    return short
+    return short.split("<")[0]  # chunk_kernel_fused<K>: one name for every K
 
 
 def counter_summary(d: Path, copy_mib: int) -> int:
@@ -232,8 +232,8 @@ def trace_summary(d: Path, steps: int, warmup: int) -> int:
         if k.startswith("pots::") or k.startswith("__amd"):
             print(f"| `{k}` | {len(ds)} | {sum(ds) / len(ds):.3f} | {min(ds):.3f} | "
                   f"{max(ds):.3f} |")
-    chunk = "pots::chunk_kernel_fused" if "pots::chunk_kernel_fused" in by else \
-        "pots::chunk_kernel"
+    chunk = next((k for k in by if k.startswith("pots::chunk_kernel_fused")),
+                 "pots::chunk_kernel")
     # (kernel, launches before the warm-up steps: the claimed root's hashing), then its
     # launches in the warm-up steps, the timed steps and the serialised stage leg
     print()

@@ -47,13 +47,14 @@ constexpr uint32_t kRunBytes = 32;  // float d[4], float s1, exact flag, double 
 
 // What the leaf plan needs of a product it fuses.
 struct FusedProduct {
-  uint64_t r;     // R [w][4] fp32, row-major (the plan's k is 4)
+  uint64_t r;     // R [w][k] fp32, row-major
   uint32_t n, w;  // P's rows and columns
   uint32_t esz;   // 2 (bf16) or 4 (fp32)
   uint32_t prod;  // index of the product in the plan
+  uint32_t k;     // the plan's challenges per product: 1, 2 or 4
 };
 
-// The product of `fv` whose P is this leaf's payload, if it can be fused: k == 4, P
+// The product of `fv` whose P is this leaf's payload, if it can be fused: k of 1, 2 or 4, P
 // contiguous with the leaf's kind, rows of at least 1 KiB, not yet fused. Returns false
 // otherwise.
 bool fv_fuse_candidate(void* fv, uint64_t payload, uint64_t len, uint32_t kind,

@@ -713,12 +713,12 @@ __global__ __launch_bounds__(256) void finish_final(const FinJob* __restrict__ j
 // One fused product (freivalds.h): its P is a leaf whose message is 0x00 || header (head
 // bytes) || P, and the chunk kernel wrote one record per run of a row.
 struct FixJob {
-  uint64_t p, r, seg;        // P, R [w][4], run records [J][n]
+  uint64_t p, r, seg;        // P, R [w][k], run records [J][n]
   uint64_t pdot, pabs, psq;  // the P job's partials: column chunk 0 of [rows_pad]
   uint64_t row_first;        // prefix of rows over the jobs before it
   uint32_t n, w;
   uint32_t head, esz;
-  uint32_t J, pad;
+  uint32_t J, k;             // record slots per row; challenges (1, 2 or 4)
 };
 static_assert(sizeof(FixJob) == 80, "FixJob layout");
 
@@ -749,7 +749,7 @@ __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ job
     for (uint64_t c = fs >> 10; c <= (fe - 1) >> 10; c++, rec += stride) {
       const v4f32 a = gload<v4f32>(rec);
       const u32x4 b = gload<u32x4>(rec + 16);
-      for (int j = 0; j < 4; j++) d[j] += (double)a[j];
+      for (uint32_t j = 0; j < J.k; j++) d[j] += (double)a[j];
       s1 += (double)__uint_as_float(b.x);
       exact |= b.y != 0u;
       s2 += __longlong_as_double((long long)((uint64_t)b.w << 32 | b.z));
@@ -766,7 +766,8 @@ __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ job
     for (uint64_t e = b0 / J.esz; e < b1 / J.esz; e++) {
       const float x = elem(e);
       const uint64_t col = e - (uint64_t)i * J.w;
-      for (int j = 0; j < 4; j++) d[j] += (double)x * (double)gload<float>(R + col * 4 + j);
+      for (uint32_t j = 0; j < J.k; j++)
+        d[j] += (double)x * (double)gload<float>(R + col * J.k + j);
       s1 += fabs((double)x);
       s2 += (double)x * (double)x;
     }
@@ -781,7 +782,7 @@ __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ job
     }
   }
   float* pdot = reinterpret_cast<float*>(J.pdot);
-  for (int j = 0; j < 4; j++) gstore<float>(pdot + (uint64_t)i * 4 + j, (float)d[j]);
+  for (uint32_t j = 0; j < J.k; j++) gstore<float>(pdot + (uint64_t)i * J.k + j, (float)d[j]);
   gstore<float>(reinterpret_cast<float*>(J.pabs) + i, (float)s1);
   gstore<double>(reinterpret_cast<double*>(J.psq) + i, s2);
 }
@@ -1235,7 +1236,7 @@ namespace pots {
 bool fv_fuse_candidate(void* fv, uint64_t payload, uint64_t len, uint32_t kind,
                        FusedProduct* out) {
   FvPlan* P = static_cast<FvPlan*>(fv);
-  if (!P || P->fused || P->k != 4) return false;
+  if (!P || P->fused || !(P->k == 1 || P->k == 2 || P->k == 4)) return false;
   auto it = P->p_index.find(payload);
   if (it == P->p_index.end() || it->second < 0) return false;
   const uint32_t i = (uint32_t)it->second;
@@ -1252,6 +1253,7 @@ bool fv_fuse_candidate(void* fv, uint64_t payload, uint64_t len, uint32_t kind,
   out->w = p.w;
   out->esz = esz;
   out->prod = i;
+  out->k = P->k;
   return true;
 }
 
@@ -1311,6 +1313,7 @@ int fv_fuse_commit(void* fv, const std::vector<uint32_t>& prods,
     x.head = head_len[f];
     x.esz = p.p_dtype == DT_BF16 ? 2 : 4;
     x.J = (uint32_t)(((uint64_t)p.w * x.esz + 1023) / 1024 + 1);
+    x.k = P->k;
     rows += p.n;
     (*seg_out)[f] = x.seg;
   }

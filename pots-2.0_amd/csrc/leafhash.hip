@@ -64,7 +64,7 @@ static_assert(sizeof(LeafDesc) == 48, "LeafDesc layout");
 // pair and no P-pass work; it is left out of the classes (nf = n_chunks - 1) and hashed by a
 // wave of its own after them, so that the header's few bytes do not pad every class.
 struct FuseDesc {
-  uint64_t r;          // R [m][4] fp32, row-major
+  uint64_t r;          // R [m][k] fp32, row-major
   uint64_t seg;        // run records [J][n_rows]
   uint32_t row_bytes;  // m · esz
   uint32_t n_rows;
@@ -142,17 +142,20 @@ struct PRun {
 };
 
 // The elements t in [lo, hi) of a 128-byte pair (words w[0..31] of payload) into the run;
-// element t's column is R row rcol + t (rcol: wave-uniform address of R's row for t = 0).
-// Unmasked, every element of the pair is taken and the bounds are not read.
+// element t's column is R row rcol + t (rcol: wave-uniform address of R's row for t = 0; a
+// row is the plan's K challenges, K of 1, 2 or 4). Unmasked, every element of the pair is
+// taken and the bounds are not read.
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Elements t in [lo, hi) of a pair (its 32 payload words w) into the run. `emax`: the pair's
 // largest biased exponent; outside [kSqLo, kSqHi] the run is marked for the exact squares.
-template <int ESZ, bool MASKED>
+typedef float v2f32 __attribute__((ext_vector_type(2)));
+
+template <int ESZ, bool MASKED, int K>
 __device__ __forceinline__ void run_add(const uint32_t* w, uint64_t rcol, uint32_t lo,
                                         uint32_t hi, uint32_t emax, PRun& a) {
   constexpr int NE = 128 / ESZ;
-  const POTS_CONST v4f32* R = reinterpret_cast<const POTS_CONST v4f32*>(rcol);
+  static_assert(K == 1 || K == 2 || K == 4, "R rows of 1, 2 or 4 challenges");
   float q = 0.f;
 #pragma unroll
   for (int t = 0; t < NE; t++) {
@@ -165,11 +168,19 @@ __device__ __forceinline__ void run_add(const uint32_t* w, uint64_t rcol, uint32
     float x;
     if (ESZ == 2) x = __uint_as_float((t & 1) ? (wt & 0xFFFF0000u) : (wt << 16));
     else x = __uint_as_float(wt);
-    const v4f32 r = R[t];
-    a.d0 = fmaf(x, r[0], a.d0);
-    a.d1 = fmaf(x, r[1], a.d1);
-    a.d2 = fmaf(x, r[2], a.d2);
-    a.d3 = fmaf(x, r[3], a.d3);
+    if constexpr (K == 4) {
+      const v4f32 r = reinterpret_cast<const POTS_CONST v4f32*>(rcol)[t];
+      a.d0 = fmaf(x, r[0], a.d0);
+      a.d1 = fmaf(x, r[1], a.d1);
+      a.d2 = fmaf(x, r[2], a.d2);
+      a.d3 = fmaf(x, r[3], a.d3);
+    } else if constexpr (K == 2) {
+      const v2f32 r = reinterpret_cast<const POTS_CONST v2f32*>(rcol)[t];
+      a.d0 = fmaf(x, r[0], a.d0);
+      a.d1 = fmaf(x, r[1], a.d1);
+    } else {
+      a.d0 = fmaf(x, reinterpret_cast<const POTS_CONST float*>(rcol)[t], a.d0);
+    }
     a.s1 += fabsf(x);
     if (MASKED || ESZ == 4) q = fmaf(x, x, q);
   }
@@ -251,7 +262,7 @@ __device__ __forceinline__ void edge_block(const LeafDesc& d, const uint32_t* __
 //
 // ESZ != 0 (a fused product leaf, SH == 1): each interior pair's elements also go into the
 // lane's P-pass run.
-template <int SH, int ESZ>
+template <int SH, int ESZ, int K = 4>
 __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __restrict__ head,
                                            uint64_t c, bool root, uint32_t cv[8], Fin& fin,
                                            const FuseDesc& f) {
@@ -335,8 +346,8 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
             (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(f.r >> 32)) << 32 |
             (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)f.r);
         if (rb + 128 <= f.row_bytes) {
-          run_add<ESZ, false>(w + SH, rbase + (uint64_t)(rb / ESZ) * 16, 0, 128 / ESZ, emax,
-                              run);
+          run_add<ESZ, false, K>(w + SH, rbase + (uint64_t)(rb / ESZ) * (4 * K), 0, 128 / ESZ,
+                                 emax, run);
           prb = rb + 128;
           if (prb == f.row_bytes) {
             run_flush(f, H, prow, c, run);
@@ -345,10 +356,12 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
           }
         } else {  // the pair ends row prow at element tb and starts row prow + 1
           const uint32_t tb = (f.row_bytes - rb) / ESZ;
-          run_add<ESZ, true>(w + SH, rbase + (uint64_t)(rb / ESZ) * 16, 0, tb, emax, run);
+          run_add<ESZ, true, K>(w + SH, rbase + (uint64_t)(rb / ESZ) * (4 * K), 0, tb, emax,
+                                run);
           run_flush(f, H, prow, c, run);
           prow++;
-          run_add<ESZ, true>(w + SH, rbase - (uint64_t)tb * 16, tb, 128 / ESZ, emax, run);
+          run_add<ESZ, true, K>(w + SH, rbase - (uint64_t)tb * (4 * K), tb, 128 / ESZ, emax,
+                                run);
           prb = rb + 128 - f.row_bytes;
         }
       }
@@ -438,6 +451,7 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel(
 // holding a multiple of 64: a wave's slots are one leaf's and one class's, so the entry, the
 // leaf's descriptors and R's rows are wave-uniform and live in scalar registers. Local slot l
 // is chunk l / Q + T·(l mod Q) for l < T·Q, the short last chunk after that.
+template <int K>
 __global__ __launch_bounds__(kThreads) void chunk_kernel_fused(
     const LeafDesc* __restrict__ leaves, const FuseDesc* __restrict__ fuses, Order od,
     const uint32_t* __restrict__ head, uint32_t* __restrict__ cv_out,
@@ -458,8 +472,8 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel_fused(
     if (l32 < tq) {
       c = (uint64_t)(l32 / f.Q) + (uint64_t)f.T * (l32 % f.Q);
       if (c >= f.nf) continue;
-      if (f.esz == 2) hash_chunk<1, 2>(d, head, c, false, cv, fin, f);
-      else hash_chunk<1, 4>(d, head, c, false, cv, fin, f);
+      if (f.esz == 2) hash_chunk<1, 2, K>(d, head, c, false, cv, fin, f);
+      else hash_chunk<1, 4, K>(d, head, c, false, cv, fin, f);
     } else {  // the short last chunk, if any
       c = (uint64_t)f.nf + (l32 - tq);
       if (c >= d.n_chunks) continue;
@@ -554,6 +568,7 @@ struct LeafPlan {
   size_t n = 0;
   uint64_t n_chunks = 0, bytes = 0;
   uint32_t n_fused = 0;  // product leaves whose P-pass sums the chunk kernel takes
+  uint32_t fuse_k = 4;   // the fused plan's challenges per product (1, 2 or 4)
   uint64_t fused_msg = 0, fused_chunks = 0, fused_records = 0;  // per run of the fused kernel
   FuseDesc* d_fuse = nullptr;
   Order plain{}, fused{};  // the two kernels' chunk orders (device tables)
@@ -699,6 +714,7 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
         (ptr - hl) % 16 == 4 && fv_fuse_candidate(fv, ptr, len, kind[i], &fp) &&
         !fused_prods.count(fp.prod) && fuse_shape(L, fp.w * fp.esz, &T, &Q, &nf, &slots)) {
       fused_prods.insert(fp.prod);
+      P->fuse_k = fp.k;  // one Freivalds plan: every fused product has the plan's k
       FuseDesc f;
       memset(&f, 0, sizeof f);
       f.r = fp.r;
@@ -932,11 +948,27 @@ static int plan_stage(LeafPlan* P, int stage, uint32_t* d_digests, uint32_t* d_f
       return plan_stage(P, POTS_LEAF_STAGE_PLAIN_CHUNKS, d_digests, d_first_bad, stream);
     case POTS_LEAF_STAGE_FUSED_CHUNKS:
       if (P->fused.n_blocks) {
-        hipLaunchKernelGGL(chunk_kernel_fused,
-                           dim3(P->max_grid ? std::min(P->max_grid, P->fused.n_blocks)
-                                            : P->fused.n_blocks),
-                           dim3(kThreads), 0, stream, P->d_leaves, P->d_fuse, P->fused,
-                           P->d_head, P->d_cv[0], d_first_bad);
+        const dim3 grid(P->max_grid ? std::min(P->max_grid, P->fused.n_blocks)
+                                    : P->fused.n_blocks);
+        switch (P->fuse_k) {
+          case 1:
+            hipLaunchKernelGGL(chunk_kernel_fused<1>, grid, dim3(kThreads), 0, stream,
+                               P->d_leaves, P->d_fuse, P->fused, P->d_head, P->d_cv[0],
+                               d_first_bad);
+            break;
+          case 2:
+            hipLaunchKernelGGL(chunk_kernel_fused<2>, grid, dim3(kThreads), 0, stream,
+                               P->d_leaves, P->d_fuse, P->fused, P->d_head, P->d_cv[0],
+                               d_first_bad);
+            break;
+          case 4:
+            hipLaunchKernelGGL(chunk_kernel_fused<4>, grid, dim3(kThreads), 0, stream,
+                               P->d_leaves, P->d_fuse, P->fused, P->d_head, P->d_cv[0],
+                               d_first_bad);
+            break;
+          default:
+            return POTS_E_ARG;
+        }
         POTS_HIP(hipGetLastError());
       }
       return POTS_E_OK;

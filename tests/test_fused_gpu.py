@@ -7,7 +7,7 @@ Freivalds plan fused with the leaf plan and run through ``pots_step_run``. The s
 boundaries inside 128-byte pairs and at chunk boundaries, the leaf's first bytes after the
 header and its last bytes in the regions no chunk's interior pairs take, and include products
 that must not be fused (rows under 1 KiB, a class padding over 1/16, a payload at an offset,
-a P shared by two products, k != 4).
+a P shared by two products, k outside 1, 2 and 4).
 
 Tolerances: digests, first-bad and verdict codes bit for bit; the rows' non-negative columns
 relative 1e-6 against the unfused plan and 1e-5 against the fp64 oracle; residuals against the
@@ -105,6 +105,22 @@ def test_fused_rows_equal_unfused_and_oracle(lib, dt):
     _check_rows(prods, rows_f, rows_u)
 
 
+@pytest.mark.parametrize("k", [1, 2])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_fused_rows_for_one_and_two_challenges(lib, k, dt):
+    """The fused kernel for plans of k = 1 and 2 (R rows of 4 and 8 bytes): rows ending mid-pair
+    and on a chunk boundary, many classes, and a changed entry, against the unfused plan and
+    the fp64 oracle."""
+    esz = 2 if dt == torch.bfloat16 else 4
+    shapes = [(64, 96, 1024 // esz), (128, 64, 2560 // esz), (64, 48, 3072 // esz),
+              (128, 32, 8960 * 2 // esz)]
+    prods = [_product(n, q, w, dt, seed=40 + s) for s, (n, q, w) in enumerate(shapes)]
+    n, q, w = shapes[1]
+    prods[1] = _product(n, q, w, dt, seed=41, tamper=[(77, w - 1, 3.0)])
+    rows_f, rows_u = _run_case(lib, prods, k=k, expect_fused=len(prods))
+    _check_rows(prods, rows_f, rows_u, k=k, tampered=(1,))
+
+
 def test_fused_large_rows_and_many_classes(lib):
     # 17.5 KiB rows (35 classes) and a header-only last chunk
     prods = [_product(128, 64, 8960, torch.bfloat16, seed=7)]
@@ -192,7 +208,7 @@ def test_products_that_are_not_fused(lib):
     for i in range(4):  # unfused products: the same kernels, the same bits
         assert rows[i] == rows_u[i]
     assert rows[4][:5] == pytest.approx(rows_u[4][:5], rel=1e-6)
-    # k != 4: nothing is fused
+    # k of 3 (R rows of 12 bytes): nothing is fused
     fv3 = lib.fv_plan(fvp, 3)
     assert lib.leaf_plan(hdrs, leaves, kinds, fuse=fv3).fused == 0
     # a plan is fused once
