@@ -42,7 +42,8 @@ HBM_PEAK_GBPS = 8000.0
 VALU_PEAK_OPS = 256 * 4 * 16 * 2.4e9
 # VALU instructions per byte of message on the chunk kernels' interior path (two 64-byte blocks
 # per 128-byte pair), from a static count of this build's gfx950 assembly: two compressions
-# and the NaN/Inf test, 1,438 per pair; with the fused P sums, 1,933 per pair of bf16 and 1,704
+# and the NaN/Inf test, 1,438 per pair; with the fused P sums of a k = 4 plan, 1,933 per pair of
+# bf16 and 1,704
 # of fp32 products. Edge blocks and the tree levels are left out.
 VALU_OPS_PER_BYTE = {"plain": 1438 / 128, "fused_bf16": 1933 / 128, "fused_fp32": 1704 / 128}
 METRIC = "Freivalds-verified GB/s + BLAKE3 Merkle GB/s (% HBM roofline); step verify ms"
@@ -765,10 +766,11 @@ def main() -> int:
     # The chunk kernels are bound by 32-bit VALU issue, not HBM: their fraction of it.
     fused_key = "fused_bf16" if c.product_dtype == torch.bfloat16 else "fused_fp32"
     valu = {}
+    # (the fused kernel's count is its k = 4 instantiation's; other k leave it out)
     for nm, (kname, nbytes), per in (
             ("hash.chunks", kernels["hash.chunks"], VALU_OPS_PER_BYTE["plain"]),
-            ("hash.chunks_fused", kernels.get("hash.chunks_fused", ("", 0)),
-             VALU_OPS_PER_BYTE[fused_key])):
+            ("hash.chunks_fused", kernels.get("hash.chunks_fused", ("", 0)) if k == 4
+             else ("", 0), VALU_OPS_PER_BYTE[fused_key])):
         if nbytes and stage_ms[nm] > 0:
             ops = per * nbytes
             valu[kname] = {"ops_per_byte": round(per, 2), "ops": int(ops),
