@@ -130,7 +130,7 @@ int pots_leaf_plan_set_grid(void *plan, uint32_t max_blocks);
 /* As pots_leaf_plan_create, and the leaves that are the P operand of a product of fv_plan (a
  * Freivalds plan, below) also have that product's P-pass sums taken by the chunk kernel while
  * it hashes them, so P is read from HBM once for both checks. A product qualifies when the
- * plan's k is 4, its P is the leaf's whole payload (contiguous, same dtype: bf16 or fp32, at a
+ * plan's k is 1, 2 or 4, its P is the leaf's whole payload (contiguous, same dtype: bf16 or fp32, at a
  * 16-byte aligned address after a 12-byte 0x00 || header, i.e. a 2-D tensor leaf), its rows
  * hold at least 1 KiB, and no other product shares that P. The Freivalds plan's stage 4 then
  * reads what the chunk stage (stage 1 of this plan) wrote for the same claimed root: run

@@ -591,13 +591,61 @@ __global__ __launch_bounds__(256) void bias_terms(const FinJob* __restrict__ job
   }
 }
 
+// block_sum of N values at once: each value's additions are block_sum's, in the same order.
+template <int N>
+__device__ __forceinline__ void block_sums(double (&v)[N], double* sh) {
+#pragma unroll
+  for (int n = 0; n < N; n++)
+    for (int o = 32; o > 0; o >>= 1) v[n] += __shfl_xor(v[n], o);
+  const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+  __syncthreads();
+  if (ln == 0) {
+#pragma unroll
+    for (int n = 0; n < N; n++) sh[n * 4 + wv] = v[n];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int n = 0; n < N; n++) {
+    double t = 0.0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += sh[n * 4 + i];
+    v[n] = t;
+  }
+  __syncthreads();
+}
+
+// Adds a row's partial dot products X·V_j, j = j0 .. j0 + nj − 1, over its column chunks in
+// chunk order; 16-byte loads when every row's k values start 16-byte aligned.
+__device__ __forceinline__ void chunk_dots(const float* __restrict__ dot, uint32_t rows_pad,
+                                           uint32_t chunks, uint32_t r, uint32_t k,
+                                           uint32_t j0, uint32_t nj, bool vec, double (&acc)[8]) {
+  for (uint32_t c = 0; c < chunks; c++) {
+    const float* src = dot + ((uint64_t)c * rows_pad + r) * k + j0;
+    if (vec) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        if ((uint32_t)(4 * h) < nj) {
+          const v4f32 x = gload<v4f32>(src + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[4 * h + e] += (double)x[e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++)
+        if ((uint32_t)jj < nj) acc[jj] += (double)gload<float>(src + jj);
+    }
+  }
+}
+
 // One block per slice. Record layout: [Σν², Σ|P|1², Σ‖P_i‖², Σ(A²(B²1))_i, Σd_1², ..., Σd_k²].
+// One sweep over the slice's rows takes the four sums and the residuals of challenges 1..8;
+// each further 8 challenges take a sweep of their own.
 __global__ __launch_bounds__(256) void finish_slices(const FinJob* __restrict__ jobs,
                                                      const SliceJob* __restrict__ slices,
                                                      uint32_t k, const BiasOut* __restrict__ bout,
                                                      const float* __restrict__ br,
                                                      double* __restrict__ recs) {
-  __shared__ double sh[4];
+  __shared__ double sh[12 * 4];
   const SliceJob S = slices[blockIdx.x];
   const FinJob J = jobs[S.prod];
   const uint32_t tid = threadIdx.x;
@@ -610,77 +658,61 @@ __global__ __launch_bounds__(256) void finish_slices(const FinJob* __restrict__ 
   const float* pdot = reinterpret_cast<const float*>(J.p_dot);
   const float* pabs = reinterpret_cast<const float*>(J.p_abs);
   const double* psq = reinterpret_cast<const double*>(J.p_sq);
+  const bool vec = k % 4 == 0 && (J.a_dot & 15) == 0 && (J.p_dot & 15) == 0;
 
-  // A row's chunk partials are summed in fp64 in chunk order, then rounded to fp32 where the
-  // reference's matvec output is fp32.
-  double s_nu = 0.0, s_p1 = 0.0, s_psq = 0.0, s_t2 = 0.0;
-  for (uint32_t r = S.r0 + tid; r < S.r1; r += blockDim.x) {
-    double nu = 0.0, t2 = 0.0, p1 = 0.0, pq = 0.0;
-    for (uint32_t c = 0; c < J.a_chunks; c++) {
-      nu += (double)gload<float>(aabs + (uint64_t)c * J.a_rows_pad + r);
-      t2 += gload<double>(asq + (uint64_t)c * J.a_rows_pad + r);
-    }
-    for (uint32_t c = 0; c < J.p_chunks; c++) {
-      p1 += (double)gload<float>(pabs + (uint64_t)c * J.p_rows_pad + r);
-      pq += gload<double>(psq + (uint64_t)c * J.p_rows_pad + r);
-    }
-    float nuf = (float)nu;
-    if (biased) nuf = nuf + babs;
-    const float p1f = (float)p1;
-    s_nu += (double)nuf * (double)nuf;
-    s_p1 += (double)p1f * (double)p1f;
-    s_psq += pq;
-    s_t2 += (double)(float)t2;
-  }
-  s_nu = block_sum(s_nu, sh);
-  s_p1 = block_sum(s_p1, sh);
-  s_psq = block_sum(s_psq, sh);
-  s_t2 = block_sum(s_t2, sh);
-  if (tid == 0) {
-    out[0] = s_nu;
-    out[1] = s_p1;
-    out[2] = s_psq;
-    out[3] = s_t2;
-  }
-  // Residuals d_ij = A(Br_j)_i (+ bᵀr_j) − (Pr_j)_i in fp32, 8 columns at a time.
   for (uint32_t j0 = 0; j0 < k; j0 += 8) {
+    const bool first = j0 == 0;
     const uint32_t nj = min(8u, k - j0);
     float bj[8];
 #pragma unroll
     for (int jj = 0; jj < 8; jj++)
       bj[jj] = (biased && (uint32_t)jj < nj) ? br[(uint64_t)S.prod * k + j0 + jj] : 0.f;
-    double sd[8];
+    // acc[0..3]: Σν², Σ|P|1², Σ‖P_i‖², Σ(A²(B²1))_i (first sweep); acc[4 + jj]: Σd².
+    double acc[12];
 #pragma unroll
-    for (int jj = 0; jj < 8; jj++) sd[jj] = 0.0;
+    for (int t = 0; t < 12; t++) acc[t] = 0.0;
     for (uint32_t r = S.r0 + tid; r < S.r1; r += blockDim.x) {
+      // A row's chunk partials are summed in fp64 in chunk order, then rounded to fp32 where
+      // the reference's matvec output is fp32.
       double ab[8], pr[8];
 #pragma unroll
       for (int jj = 0; jj < 8; jj++) ab[jj] = pr[jj] = 0.0;
-      for (uint32_t c = 0; c < J.a_chunks; c++) {
-        const float* src = adot + ((uint64_t)c * J.a_rows_pad + r) * k + j0;
-#pragma unroll
-        for (int jj = 0; jj < 8; jj++)
-          if ((uint32_t)jj < nj) ab[jj] += (double)gload<float>(src + jj);
+      chunk_dots(adot, J.a_rows_pad, J.a_chunks, r, k, j0, nj, vec, ab);
+      chunk_dots(pdot, J.p_rows_pad, J.p_chunks, r, k, j0, nj, vec, pr);
+      if (first) {
+        double nu = 0.0, t2 = 0.0, p1 = 0.0, pq = 0.0;
+        for (uint32_t c = 0; c < J.a_chunks; c++) {
+          nu += (double)gload<float>(aabs + (uint64_t)c * J.a_rows_pad + r);
+          t2 += gload<double>(asq + (uint64_t)c * J.a_rows_pad + r);
+        }
+        for (uint32_t c = 0; c < J.p_chunks; c++) {
+          p1 += (double)gload<float>(pabs + (uint64_t)c * J.p_rows_pad + r);
+          pq += gload<double>(psq + (uint64_t)c * J.p_rows_pad + r);
+        }
+        float nuf = (float)nu;
+        if (biased) nuf = nuf + babs;
+        const float p1f = (float)p1;
+        acc[0] += (double)nuf * (double)nuf;
+        acc[1] += (double)p1f * (double)p1f;
+        acc[2] += pq;
+        acc[3] += (double)(float)t2;
       }
-      for (uint32_t c = 0; c < J.p_chunks; c++) {
-        const float* src = pdot + ((uint64_t)c * J.p_rows_pad + r) * k + j0;
-#pragma unroll
-        for (int jj = 0; jj < 8; jj++)
-          if ((uint32_t)jj < nj) pr[jj] += (double)gload<float>(src + jj);
-      }
+      // Residuals d_ij = A(Br_j)_i (+ bᵀr_j) − (Pr_j)_i in fp32.
 #pragma unroll
       for (int jj = 0; jj < 8; jj++) {
         if ((uint32_t)jj < nj) {
           float abf = (float)ab[jj];
           if (biased) abf = abf + bj[jj];
           const float d = abf - (float)pr[jj];
-          sd[jj] += (double)d * (double)d;
+          acc[4 + jj] += (double)d * (double)d;
         }
       }
     }
-    for (uint32_t jj = 0; jj < nj; jj++) {
-      const double t = block_sum(sd[jj], sh);
-      if (tid == 0) out[4 + j0 + jj] = t;
+    block_sums<12>(acc, sh);
+    if (tid == 0) {
+      if (first)
+        for (int t = 0; t < 4; t++) out[t] = acc[t];
+      for (uint32_t jj = 0; jj < nj; jj++) out[4 + j0 + jj] = acc[4 + jj];
     }
   }
 }
@@ -746,14 +778,26 @@ __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ job
   if (fs < fe) {
     const char* rec = reinterpret_cast<const char*>(J.seg) + (uint64_t)kRunBytes * i;
     const uint64_t stride = (uint64_t)kRunBytes * J.n;
-    for (uint64_t c = fs >> 10; c <= (fe - 1) >> 10; c++, rec += stride) {
-      const v4f32 a = gload<v4f32>(rec);
-      const u32x4 b = gload<u32x4>(rec + 16);
+    auto add = [&](const v4f32& a, const u32x4& b) {
       for (uint32_t j = 0; j < J.k; j++) d[j] += (double)a[j];
       s1 += (double)__uint_as_float(b.x);
       exact |= b.y != 0u;
       s2 += __longlong_as_double((long long)((uint64_t)b.w << 32 | b.z));
+    };
+    // Four records' loads are issued before their sums, which are taken in record order.
+    uint64_t left = ((fe - 1) >> 10) - (fs >> 10) + 1;
+    for (; left >= 4; left -= 4, rec += 4 * stride) {
+      v4f32 a[4];
+      u32x4 b[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        a[u] = gload<v4f32>(rec + u * stride);
+        b[u] = gload<u32x4>(rec + u * stride + 16);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) add(a[u], b[u]);
     }
+    for (; left > 0; left--, rec += stride) add(gload<v4f32>(rec), gload<u32x4>(rec + 16));
   }
   const float* R = reinterpret_cast<const float*>(J.r);
   auto elem = [&](uint64_t e) {

@@ -138,7 +138,11 @@ class DeviceStepVerifier:
                 hp.run_stage(0, self.digests, self.bad, side)
                 if self.plain_early:
                     hp.run_stage(native.LeafPlan.PLAIN_CHUNKS, self.digests, self.bad, side)
-            for st in range(3 if self.hash_after_b else 1):
+            # The unfused products' P pass needs only the challenges: it goes first, so that
+            # the step's end waits only for the fused products' sums.
+            plan.run_stage(0, self.key, self.rows, main)
+            plan.run_stage(native.FvPlan.P_PASS, self.key, self.rows, main)
+            for st in range(1, 3 if self.hash_after_b else 1):
                 plan.run_stage(st, self.key, self.rows, main)
             ready = torch.cuda.Event()
             ready.record(main)
@@ -154,9 +158,7 @@ class DeviceStepVerifier:
                     a_begin.record(main)
                 plan.run_stage(st, self.key, self.rows, main)
             a_end.record(main)
-            # the unfused products' P pass needs only the challenges; the fused products' sums
-            # add up the chunk kernel's run records
-            plan.run_stage(native.FvPlan.P_PASS, self.key, self.rows, main)
+            # the fused products' sums add up the chunk kernel's run records
             main.wait_event(c_end)
             plan.run_stage(native.FvPlan.P_FUSED, self.key, self.rows, main)
         with torch.cuda.stream(side):
