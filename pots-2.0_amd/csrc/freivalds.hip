@@ -260,6 +260,42 @@ __device__ __forceinline__ void compute_stage(const StageRegs<NJG>& r, v4f32 acc
   }
 }
 
+// The A pass's weights u, w of columns c0 .. c1 − 1 into LDS (zero up to chunk_cols): 16-byte
+// loads, every one issued before the first store, so a tile waits for one load's latency
+// here, not one per element. Chunk starts are whole pipeline stages (multiples of 64 columns)
+// and the weights 256-byte aligned, so the vector loads are aligned.
+template <uint32_t CHUNK>
+__device__ __forceinline__ void stage_weights(const PassJob& J, uint32_t c0, uint32_t c1,
+                                              float* s_u, float* s_w) {
+  constexpr uint32_t NV = (CHUNK + 1023) / 1024;  // 4-column groups per thread
+  const float* up = reinterpret_cast<const float*>(J.u) + c0;
+  const float* wp = reinterpret_cast<const float*>(J.w) + c0;
+  const uint32_t n = c1 - c0;
+  v4f32 ua[NV], wa[NV];
+#pragma unroll
+  for (uint32_t v = 0; v < NV; v++) {
+    const uint32_t t = 4 * (threadIdx.x + 256 * v);
+    if (t + 4 <= n) {
+      ua[v] = gload<v4f32>(up + t);
+      wa[v] = gload<v4f32>(wp + t);
+    } else {
+#pragma unroll
+      for (uint32_t e = 0; e < 4; e++) {
+        ua[v][e] = t + e < n ? gload<float>(up + t + e) : 0.f;
+        wa[v][e] = t + e < n ? gload<float>(wp + t + e) : 0.f;
+      }
+    }
+  }
+#pragma unroll
+  for (uint32_t v = 0; v < NV; v++) {
+    const uint32_t t = 4 * (threadIdx.x + 256 * v);
+    if (t < J.chunk_cols) {
+      *reinterpret_cast<v4f32*>(s_u + t) = ua[v];
+      *reinterpret_cast<v4f32*>(s_w + t) = wa[v];
+    }
+  }
+}
+
 // One tile: job blk_job[bidx], 64-row group, column chunk and column-group block decoded
 // from its index within the job (row group fastest). Every wave of the block calls it with the
 // same tile and reaches its barrier.
@@ -282,19 +318,8 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   const uint32_t c0 = chunk * J.chunk_cols;
   const uint32_t c1 = min(c0 + J.chunk_cols, J.cols);
   const bool sums = jt == 0;  // the two sums are taken once, by the first column-group block
-  if (WEIGHTED) {
-    if (sums) {
-      const float* up = reinterpret_cast<const float*>(J.u);
-      const float* wp = reinterpret_cast<const float*>(J.w);
-      for (uint32_t t = threadIdx.x; t < J.chunk_cols; t += 256) {
-        s_u[t] = c0 + t < c1 ? gload<float>(up + c0 + t) : 0.f;
-        s_w[t] = c0 + t < c1 ? gload<float>(wp + c0 + t) : 0.f;
-      }
-    }
-    __syncthreads();
-  }
   const uint32_t r0 = rg * kRowsPerBlock + wave * 16;
-  if (r0 >= J.rows) return;
+  const bool active = r0 < J.rows;  // waves past the matrix only take part in the staging
   const uint32_t g = lane >> 4, i = lane & 15;
   const uint32_t row = r0 + i;
   Lane L;
@@ -313,6 +338,17 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   L.g = g;
   L.c1 = c1;
   L.nvalid = min(NJG, J.n_jg - jt * NJG);
+  const uint32_t nfull = J.aligned ? (c1 - c0) / SSTEP : 0;
+
+  // The first stage's loads go out before the weights are staged, so the two latencies
+  // overlap.
+  StageRegs<NJG> ra;
+  if (active && nfull > 0) load_full<XT, NJG>(ra, L, c0);
+  if (WEIGHTED) {
+    if (sums) stage_weights<G::CHUNK>(J, c0, c1, s_u, s_w);
+    __syncthreads();
+  }
+  if (!active) return;
 
   v4f32 acc[NJG];
 #pragma unroll
@@ -323,11 +359,9 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
 
   // Full stages of an aligned job run as a two-buffer software pipeline; the rest (the
   // chunk's last partial stage, or every stage of an unaligned job) takes the guarded loads.
-  const uint32_t nfull = J.aligned ? (c1 - c0) / SSTEP : 0;
   uint32_t cs = c0;
   if (nfull > 0) {
-    StageRegs<NJG> ra, rb;
-    load_full<XT, NJG>(ra, L, cs);
+    StageRegs<NJG> rb;
     uint32_t s = 1;
     for (; s + 1 < nfull; s += 2) {
       load_full<XT, NJG>(rb, L, cs + SSTEP);
@@ -405,7 +439,7 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
 // With a smaller grid, the pass holds a bounded share of each CU (a block holds 4 waves and
 // 32 KiB of LDS) so that a kernel on another stream (the leaf hasher) keeps the rest, and the
 // blocks take tiles from a queue: a counter (zero at launch) that each block's first thread
-// advances by one per tile. A block that lands on a CU shared with more hashing waves then
+// advances by one per tile, a tile ahead of the one the block works on. A block that lands on a CU shared with more hashing waves then
 // takes fewer tiles, where a fixed split would leave it the last to finish. Every thread of a
 // block reads the same tile index, so all of its waves leave the loop together once the
 // counter passes n_tiles.
@@ -415,21 +449,28 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
                                                 uint32_t k, uint32_t n_tiles,
                                                 uint32_t* __restrict__ queue) {
   using G = Geo<XT>;
-  __shared__ float s_u[WEIGHTED ? G::CHUNK : 4], s_w[WEIGHTED ? G::CHUNK : 4];
+  __shared__ __align__(16) float s_u[WEIGHTED ? G::CHUNK : 4];
+  __shared__ __align__(16) float s_w[WEIGHTED ? G::CHUNK : 4];
   __shared__ uint32_t s_tile;
   if (queue == nullptr) {
     if (blockIdx.x < n_tiles) row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, blockIdx.x,
                                                                  s_u, s_w);
     return;
   }
-  for (;;) {
-    if (threadIdx.x == 0) s_tile = atomicAdd(queue, 1u);
-    __syncthreads();
-    const uint32_t b = s_tile;
-    __syncthreads();  // every thread has read s_tile before thread 0 writes the next one
-    if (b >= n_tiles) break;
+  if (threadIdx.x == 0) s_tile = atomicAdd(queue, 1u);
+  __syncthreads();
+  uint32_t b = s_tile;
+  while (b < n_tiles) {
+    // The next tile's index is taken now; its latency passes under this tile. (An increment
+    // that wraps only at 2^32 − 1 is an add of one; written as atomicInc, the compiler does
+    // not rewrite it into a wave-level add whose result it must wait for at once.)
+    uint32_t next = 0;
+    if (threadIdx.x == 0) next = atomicInc(queue, 0xFFFFFFFFu);
     row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, b, s_u, s_w);
-    if (WEIGHTED) __syncthreads();  // the next tile restages the weights
+    __syncthreads();  // every wave is done with this tile's weights and has read s_tile
+    if (threadIdx.x == 0) s_tile = next;
+    __syncthreads();
+    b = s_tile;
   }
 }
 
