@@ -58,9 +58,11 @@ static_assert(sizeof(LeafDesc) == 48, "LeafDesc layout");
 
 // A leaf whose product's P-pass sums the chunk kernel takes (freivalds.h). Its first nf
 // chunks are hashed in class order: class kappa = c mod T holds the chunks whose payload
-// offset is the same modulo the row length, so the T classes of Q lanes each (Q a multiple of
-// 64, padding lanes idle) give every wave chunks at one common column offset: R is read with
-// scalar loads, one copy for the wave. A last chunk with fewer than 128 bytes has no interior
+// offset is the same modulo the row length. A lane hashes a run of consecutive chunks (of
+// classes t0 .. t0 + RC − 1 of one period when T >= 4; of PG whole periods when T < 4), and
+// the runs of one class range get Q lanes (Q a multiple of 64, padding lanes idle), so every
+// wave is at one common column offset at each step of its runs: R is read with scalar loads,
+// one copy for the wave. A last chunk with fewer than 128 bytes has no interior
 // pair and no P-pass work; it is left out of the classes (nf = n_chunks - 1) and hashed by a
 // wave of its own after them, so that the header's few bytes do not pad every class.
 struct FuseDesc {
@@ -73,7 +75,7 @@ struct FuseDesc {
   uint32_t Q;          // lanes per class
   uint32_t esz;        // 2 (bf16) or 4 (fp32)
   uint32_t nf;         // chunks in class order
-  uint32_t pad;
+  uint32_t run;        // a lane's run: classes (low 16 bits) x periods (high 16 bits)
 };
 static_assert(sizeof(FuseDesc) == 48, "FuseDesc layout");
 
@@ -87,6 +89,13 @@ struct LevelEntry {     // one leaf with >= 2 nodes at the input level of one fo
 static_assert(sizeof(LevelEntry) == 32, "LevelEntry layout");
 
 constexpr int kThreads = 256;
+// Consecutive chunks one lane hashes in a row: each chunk after the first takes its first
+// bytes from the unit its predecessor's last pair loaded, so the 128-byte line before a 1 KiB
+// boundary is read once, not again by the next chunk.
+#ifndef POTS_CHUNK_RUN
+#define POTS_CHUNK_RUN 4
+#endif
+constexpr uint32_t kRun = POTS_CHUNK_RUN;
 // Tree levels one launch of level_kernel reduces.
 constexpr uint32_t kFold = 3;
 
@@ -262,10 +271,14 @@ __device__ __forceinline__ void edge_block(const LeafDesc& d, const uint32_t* __
 //
 // ESZ != 0 (a fused product leaf, SH == 1): each interior pair's elements also go into the
 // lane's P-pass run.
+//
+// `carry`, `have_carry`: with SH != 0, the last unit the previous pair loaded, kept across the
+// chunks of a lane's run (the caller starts a run with have_carry false; chunk c + 1's first
+// window begins with chunk c's last unit).
 template <int SH, int ESZ, int K = 4>
 __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __restrict__ head,
                                            uint64_t c, bool root, uint32_t cv[8], Fin& fin,
-                                           const FuseDesc& f) {
+                                           const FuseDesc& f, u32x4& carry, bool& have_carry) {
   const uint64_t H = d.head_len;
   const uint64_t L = H + d.len;
   const uint64_t cstart = c * 1024u;
@@ -276,8 +289,6 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
   // With SH != 0 a pair's window starts with the last 16 bytes of the previous pair's line;
   // they are carried over in registers rather than loaded again (a second load of a line
   // already streamed past is often an HBM refetch).
-  u32x4 carry = u32x4{0, 0, 0, 0};
-  bool have_carry = false;
   PRun run;
   uint32_t prow = 0, prb = 0;  // row of the next pair and its byte offset in the row
   bool pinit = false;
@@ -415,11 +426,29 @@ __device__ __forceinline__ void store_cv(uint32_t* p, const uint32_t cv[8]) {
   gstore<u32x4>(dst + 1, u32x4{cv[4], cv[5], cv[6], cv[7]});
 }
 
-// Every chunk of the unfused leaves: slot g of the plain order is chunk g − first[e] of leaf
-// leaf[e] (slots past a leaf's chunks are idle). The chaining value goes to cv_out, or the
-// digest itself for a one-chunk leaf. Block b hashes slot blocks b, b + gridDim.x, ... so a
-// grid smaller than the order holds a bounded share of the GPU and leaves the rest to kernels
-// on other streams.
+// Chunks c0 .. c1 − 1 of leaf i, one after another on one lane, each chaining value to cv_out
+// (or the leaf digest itself for a one-chunk leaf).
+template <int SH>
+__device__ __forceinline__ void hash_run(const LeafDesc& d, const uint32_t* __restrict__ head,
+                                         uint32_t i, uint64_t c0, uint64_t c1, Fin& fin,
+                                         uint32_t* __restrict__ cv_out,
+                                         uint32_t* __restrict__ digests) {
+  const FuseDesc none{};
+  const bool root = d.n_chunks == 1;
+  u32x4 carry = u32x4{0, 0, 0, 0};
+  bool have_carry = false;
+#pragma unroll 1
+  for (uint64_t c = c0; c < c1; c++) {
+    uint32_t cv[8];
+    hash_chunk<SH, 0>(d, head, c, root, cv, fin, none, carry, have_carry);
+    store_cv(root ? digests + 8ull * i : cv_out + 8ull * (d.cv_first + c), cv);
+  }
+}
+
+// Every chunk of the unfused leaves: slot g of the plain order is run g − first[e] of leaf
+// leaf[e], its chunks kRun·(g − first[e]) onwards (slots past a leaf's runs are idle). Block b
+// hashes slot blocks b, b + gridDim.x, ... so a grid smaller than the order holds a bounded
+// share of the GPU and leaves the rest to kernels on other streams.
 __global__ __launch_bounds__(kThreads) void chunk_kernel(
     const LeafDesc* __restrict__ leaves, Order od, const uint32_t* __restrict__ head,
     uint32_t* __restrict__ cv_out, uint32_t* __restrict__ digests,
@@ -430,27 +459,26 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel(
     const uint32_t e = order_entry(od, g, blk);
     const uint32_t i = od.leaf[e];
     const LeafDesc d = leaves[i];
-    const uint64_t c = g - od.first[e];
-    if (c >= d.n_chunks) continue;
-    uint32_t cv[8];
+    const uint64_t c0 = (g - od.first[e]) * kRun;
+    if (c0 >= d.n_chunks) continue;
+    const uint64_t c1 = min<uint64_t>(c0 + kRun, d.n_chunks);
     Fin fin(d.kind);
-    const FuseDesc none{};
-    const bool root = d.n_chunks == 1;
     switch ((uint32_t)((d.payload - d.head_len) >> 2) & 3u) {
-      case 0: hash_chunk<0, 0>(d, head, c, root, cv, fin, none); break;
-      case 1: hash_chunk<1, 0>(d, head, c, root, cv, fin, none); break;
-      case 2: hash_chunk<2, 0>(d, head, c, root, cv, fin, none); break;
-      default: hash_chunk<3, 0>(d, head, c, root, cv, fin, none); break;
+      case 0: hash_run<0>(d, head, i, c0, c1, fin, cv_out, digests); break;
+      case 1: hash_run<1>(d, head, i, c0, c1, fin, cv_out, digests); break;
+      case 2: hash_run<2>(d, head, i, c0, c1, fin, cv_out, digests); break;
+      default: hash_run<3>(d, head, i, c0, c1, fin, cv_out, digests); break;
     }
     if (fin.bad()) atomicMin(first_bad, i);
-    store_cv(root ? digests + 8ull * i : cv_out + 8ull * (d.cv_first + c), cv);
   }
 }
 
 // The fused leaves (FuseDesc), each starting at a multiple of 64 slots in the fused order and
-// holding a multiple of 64: a wave's slots are one leaf's and one class's, so the entry, the
-// leaf's descriptors and R's rows are wave-uniform and live in scalar registers. Local slot l
-// is chunk l / Q + T·(l mod Q) for l < T·Q, the short last chunk after that.
+// holding a multiple of 64: a wave's slots are one leaf's and one class range's, so the entry,
+// the leaf's descriptors and, at each step of the runs, R's rows are wave-uniform and live in
+// scalar registers. Local slot l < NR·Q (NR = ceil(T / RC) class ranges) is the run of class
+// range l / Q in period group l mod Q: chunks t0 + T·PG·(l mod Q) onwards (t0 = RC·(l / Q)),
+// RC·PG of them, which are consecutive; the short last chunk follows.
 template <int K>
 __global__ __launch_bounds__(kThreads) void chunk_kernel_fused(
     const LeafDesc* __restrict__ leaves, const FuseDesc* __restrict__ fuses, Order od,
@@ -464,23 +492,33 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel_fused(
     const uint32_t i = od.leaf[e];
     const LeafDesc d = leaves[i];
     const FuseDesc f = fuses[d.fuse];
-    const uint32_t l32 = (uint32_t)(g0 - od.first[e]) + (threadIdx.x & 63u);  // < T·Q + 64
-    const uint32_t tq = f.T * f.Q;
-    uint32_t cv[8];
+    const uint32_t rc = f.run & 0xFFFFu, pg = f.run >> 16;
+    const uint32_t tq = (f.T + rc - 1) / rc * f.Q;
+    const uint32_t l32 = (uint32_t)(g0 - od.first[e]) + (threadIdx.x & 63u);  // < tq + 64
     Fin fin(d.kind);
-    uint64_t c;
+    uint32_t cv[8];
     if (l32 < tq) {
-      c = (uint64_t)(l32 / f.Q) + (uint64_t)f.T * (l32 % f.Q);
-      if (c >= f.nf) continue;
-      if (f.esz == 2) hash_chunk<1, 2, K>(d, head, c, false, cv, fin, f);
-      else hash_chunk<1, 4, K>(d, head, c, false, cv, fin, f);
+      const uint32_t t0 = l32 / f.Q * rc;
+      const uint64_t cs = (uint64_t)t0 + (uint64_t)f.T * pg * (l32 % f.Q);
+      const uint64_t ce = min<uint64_t>(cs + (uint64_t)min(rc, f.T - t0) * pg, f.nf);
+      u32x4 carry = u32x4{0, 0, 0, 0};
+      bool have_carry = false;
+#pragma unroll 1
+      for (uint64_t c = cs; c < ce; c++) {
+        if (f.esz == 2) hash_chunk<1, 2, K>(d, head, c, false, cv, fin, f, carry, have_carry);
+        else hash_chunk<1, 4, K>(d, head, c, false, cv, fin, f, carry, have_carry);
+        store_cv(cv_out + 8ull * (d.cv_first + c), cv);
+      }
+      if (cs >= ce) continue;
     } else {  // the short last chunk, if any
-      c = (uint64_t)f.nf + (l32 - tq);
+      const uint64_t c = (uint64_t)f.nf + (l32 - tq);
       if (c >= d.n_chunks) continue;
-      hash_chunk<1, 0>(d, head, c, false, cv, fin, f);
+      u32x4 carry = u32x4{0, 0, 0, 0};
+      bool have_carry = false;
+      hash_chunk<1, 0>(d, head, c, false, cv, fin, f, carry, have_carry);
+      store_cv(cv_out + 8ull * (d.cv_first + c), cv);
     }
     if (fin.bad()) atomicMin(first_bad, i);
-    store_cv(cv_out + 8ull * (d.cv_first + c), cv);
   }
 }
 
@@ -617,10 +655,12 @@ struct OrderHost {
 };
 
 // A fused leaf's chunk order: T classes (chunk c in class c mod T, T = lcm(row bytes, 1024) /
-// 1024, so a class's chunks start at one offset in the row) of Q lanes each, Q the class size
-// rounded up to 64. Fusing is declined when the padding would exceed 1/16 of the chunks.
+// 1024, so a class's chunks start at one offset in the row). A lane's run is RC = min(T, kRun)
+// consecutive classes of one period, or, when T < kRun, PG = kRun / T whole periods; the runs
+// of one class range get Q lanes, the number of runs rounded up to 64. Fusing is declined when
+// the padding would exceed 1/16 of the chunks even with runs of one chunk.
 static bool fuse_shape(uint64_t msg_bytes, uint32_t row_bytes, uint32_t* T, uint32_t* Q,
-                       uint32_t* nf, uint64_t* slots) {
+                       uint32_t* run, uint32_t* nf, uint64_t* slots) {
   const uint64_t n_chunks = (msg_bytes + 1023) / 1024;
   const uint64_t f = msg_bytes % 1024 != 0 && msg_bytes % 1024 < 128 ? n_chunks - 1 : n_chunks;
   uint64_t a = row_bytes, b = 1024;
@@ -630,14 +670,24 @@ static bool fuse_shape(uint64_t msg_bytes, uint32_t row_bytes, uint32_t* T, uint
     b = t;
   }
   const uint64_t t = (uint64_t)row_bytes / a;  // lcm / 1024
-  const uint64_t q = ((f + t - 1) / t + 63) / 64 * 64;
-  const uint64_t total = t * q + (f < n_chunks ? 64 : 0);
-  if (total >= 0xFFFFFFFFull || (t * q - f) * 16 > f) return false;
-  *T = (uint32_t)t;
-  *Q = (uint32_t)q;
-  *nf = (uint32_t)f;
-  *slots = total;
-  return true;
+  const uint64_t periods = (f + t - 1) / t;
+  // Runs of kRun chunks, or, where rounding their count up to 64 pads too much (a leaf of
+  // few periods with T < kRun), runs of one chunk.
+  const uint64_t shapes[2][2] = {{std::min<uint64_t>(t, kRun), t >= kRun ? 1 : kRun / t},
+                                 {1, 1}};
+  for (const auto& sh : shapes) {
+    const uint64_t rc = sh[0], pg = sh[1];
+    const uint64_t q = ((periods + pg - 1) / pg + 63) / 64 * 64;
+    const uint64_t total = (t + rc - 1) / rc * q + (f < n_chunks ? 64 : 0);
+    if (total >= 0xFFFFFFFFull || (t * pg * q - f) * 16 > f) continue;
+    *T = (uint32_t)t;
+    *Q = (uint32_t)q;
+    *run = (uint32_t)(rc | pg << 16);
+    *nf = (uint32_t)f;
+    *slots = total;
+    return true;
+  }
+  return false;
 }
 
 static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
@@ -708,11 +758,11 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
     d.n_chunks = (uint32_t)nck;
     d.fuse = kNoFuse;
     FusedProduct fp;
-    uint32_t T = 0, Q = 0, nf = 0;
+    uint32_t T = 0, Q = 0, run = 0, nf = 0;
     uint64_t slots = 0;
     if (fv && !stage && (kind[i] == POTS_KIND_BF16 || kind[i] == POTS_KIND_F32) &&
         (ptr - hl) % 16 == 4 && fv_fuse_candidate(fv, ptr, len, kind[i], &fp) &&
-        !fused_prods.count(fp.prod) && fuse_shape(L, fp.w * fp.esz, &T, &Q, &nf, &slots)) {
+        !fused_prods.count(fp.prod) && fuse_shape(L, fp.w * fp.esz, &T, &Q, &run, &nf, &slots)) {
       fused_prods.insert(fp.prod);
       P->fuse_k = fp.k;  // one Freivalds plan: every fused product has the plan's k
       FuseDesc f;
@@ -725,6 +775,7 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
       f.Q = Q;
       f.esz = fp.esz;
       f.nf = nf;
+      f.run = run;
       d.fuse = (uint32_t)fdesc.size();
       fdesc.push_back(f);
       fprod.push_back(fp.prod);
@@ -741,7 +792,7 @@ static int plan_build(size_t n, const uint8_t* hdr_buf, const uint64_t* hdr_off,
         }
       }
     } else {
-      plain.add((uint32_t)i, nck);
+      plain.add((uint32_t)i, (nck + kRun - 1) / kRun);
     }
     nc += nck;
     P->bytes += L;
