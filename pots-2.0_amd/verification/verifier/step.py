@@ -78,9 +78,8 @@ class DeviceStepVerifier:
         # each P is read from HBM once (pots_leaf_plan_create_fused).
         self.hasher = StepHasher(c, leaves, fuse=self.plan if fuse else None)
         self.fused = self.hasher.plan.fused
-        if a_grid is None:  # fused: one A-pass block per CU beside the chunk kernel
-            a_grid = torch.cuda.get_device_properties(leaves[-1].device).multi_processor_count \
-                if self.fused else 0
+        if a_grid is None:
+            a_grid = self._a_grid(prods, leaves[-1].device) if self.fused else 0
         self.plan.set_grid(3, a_grid)
         self.plan.set_grid(1, b_grid)
         self.a_grid = a_grid
@@ -98,6 +97,29 @@ class DeviceStepVerifier:
         self.side = torch.cuda.Stream(device=dev)
         self.hash_bytes = self.hasher.bytes
         self.freivalds_bytes = self.plan.bytes
+
+    # MI355X figures for sharing the GPU between the two halves: the chunk kernels hash about
+    # 2.5 TB/s of message bytes (bound by the VALUs); an A-pass block, one per CU, spends
+    # about 4.5 µs on each tile (64 rows by at most 4096 bf16 or 1024 fp32 columns) and
+    # 0.034 µs per KiB it streams (fitted to C3's and C4's A passes, 11.3 and 16.9 ms).
+    HASH_GBPS, TILE_US, KIB_US = 2500.0, 4.5, 0.034
+
+    def _a_grid(self, prods: Sequence[native.FvProduct], device: torch.device) -> int:
+        """The A pass's grid beside the fused chunk kernel: one 4-wave block per CU, or one
+        and a half where the hashing would otherwise wait for it (hashing estimated under
+        1.3x the A pass's time at one block per CU). Measured: C3, at 1.14x, takes 24.5 ms
+        instead of 25.5 with the larger grid; C4 (1.5x) and C1 (1.7x) are fastest at one
+        block per CU."""
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+        tiles = kib = 0
+        for p in prods:
+            n, q = p.a.shape
+            width = 4096 if p.a.element_size() == 2 else 1024
+            tiles += -(-n // 64) * -(-q // width)
+            kib += p.a.numel() * p.a.element_size() / 1024
+        hash_ms = self.hasher.bytes / self.HASH_GBPS / 1e6
+        a_ms = (tiles * self.TILE_US + kib * self.KIB_US) / cus / 1e3
+        return cus * 3 // 2 if hash_ms < 1.3 * a_ms else cus
 
     def enqueue(self, claimed: bytes | torch.Tensor, events: list | None = None):
         """Enqueue the whole step on the current stream (Freivalds, verdicts) and a side
