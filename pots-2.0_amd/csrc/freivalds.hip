@@ -435,14 +435,31 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   }
 }
 
+// One tile queue per XCD: queue x holds tiles [n·x/8, n·(x+1)/8), a contiguous range, so the
+// tiles that share a column chunk's B·R and weights run on one XCD and find them in its L2
+// (the GPU's 8 XCDs each have their own). A block works from its own XCD's queue, then from
+// the others in turn.
+constexpr uint32_t kQueues = 8;
+
+__device__ __forceinline__ uint32_t queue_lo(uint32_t n, uint32_t x) {
+  return (uint32_t)((uint64_t)n * x / kQueues);
+}
+
+// The XCD this wave runs on (hardware register XCC_ID); only a locality hint.
+__device__ __forceinline__ uint32_t xcd_id() {
+  return (uint32_t)__builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) % kQueues;
+}
+
 // The row pass over n_tiles tiles. With a block per tile (queue null), block b takes tile b.
 // With a smaller grid, the pass holds a bounded share of each CU (a block holds 4 waves and
 // 32 KiB of LDS) so that a kernel on another stream (the leaf hasher) keeps the rest, and the
-// blocks take tiles from a queue: a counter (zero at launch) that each block's first thread
-// advances by one per tile, a tile ahead of the one the block works on. A block that lands on a CU shared with more hashing waves then
+// blocks take tiles from the queues: counters (zero at launch) that each block's first thread
+// advances by one per tile, a tile ahead of the one the block works on, moving to the next
+// queue when one runs out. A block that lands on a CU shared with more hashing waves then
 // takes fewer tiles, where a fixed split would leave it the last to finish. Every thread of a
-// block reads the same tile index, so all of its waves leave the loop together once the
-// counter passes n_tiles.
+// block reads the same tile index, so all of its waves leave the loop together once every
+// queue is empty; each counter value below its range hands out one tile, so every tile is
+// taken exactly once.
 template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
 __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
                                                 const uint32_t* __restrict__ blk_job,
@@ -457,24 +474,52 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
                                                                  s_u, s_w);
     return;
   }
-  if (threadIdx.x == 0) s_tile = atomicAdd(queue, 1u);
+  // Thread 0's state: the queues tried so far, from this XCD's own.
+  const uint32_t home = xcd_id();
+  uint32_t qi = 0;
+  auto take = [&]() -> uint32_t {  // the next tile, or n_tiles once every queue is empty
+    for (; qi < kQueues; qi++) {
+      const uint32_t x = (home + qi) % kQueues;
+      const uint32_t lo = queue_lo(n_tiles, x);
+      const uint32_t t = atomicInc(queue + x, 0xFFFFFFFFu);
+      if (t < queue_lo(n_tiles, x + 1) - lo) return lo + t;
+    }
+    return n_tiles;
+  };
+  if (threadIdx.x == 0) s_tile = take();
   __syncthreads();
   uint32_t b = s_tile;
   while (b < n_tiles) {
-    // The next tile's index is taken now; its latency passes under this tile. (An increment
-    // that wraps only at 2^32 − 1 is an add of one; written as atomicInc, the compiler does
-    // not rewrite it into a wave-level add whose result it must wait for at once.)
+    // The next tile's counter value is taken now; its latency passes under this tile. (An
+    // increment that wraps only at 2^32 − 1 is an add of one; written as atomicInc, the
+    // compiler does not rewrite it into a wave-level add whose result it must wait for.)
     uint32_t next = 0;
-    if (threadIdx.x == 0) next = atomicInc(queue, 0xFFFFFFFFu);
+    if (threadIdx.x == 0 && qi < kQueues)
+      next = atomicInc(queue + (home + qi) % kQueues, 0xFFFFFFFFu);
     row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, b, s_u, s_w);
     __syncthreads();  // every wave is done with this tile's weights and has read s_tile
-    if (threadIdx.x == 0) s_tile = next;
+    if (threadIdx.x == 0) {
+      uint32_t nb = n_tiles;
+      if (qi < kQueues) {
+        const uint32_t x = (home + qi) % kQueues;
+        const uint32_t lo = queue_lo(n_tiles, x);
+        if (next < queue_lo(n_tiles, x + 1) - lo) {
+          nb = lo + next;
+        } else {
+          qi++;
+          nb = take();
+        }
+      }
+      s_tile = nb;
+    }
     __syncthreads();
     b = s_tile;
   }
 }
 
-__global__ void queue_reset(uint32_t* q) { *q = 0u; }
+__global__ void queue_reset(uint32_t* q) {
+  if (threadIdx.x < kQueues) q[threadIdx.x] = 0u;
+}
 
 // ---- B-pass reduction: B·R, |B|·1, B²·1 per row of B, packed for the A pass -------------
 
@@ -888,7 +933,7 @@ struct FvPlan {
   char* base = nullptr;
   size_t total = 0;
   uint32_t* d_key = nullptr;
-  uint32_t* d_queue = nullptr;  // a row pass's tile queue counter per stage (grid-limited passes)
+  uint32_t* d_queue = nullptr;  // a row pass's kQueues tile queue counters per stage (grid-limited)
   ChallengeItem* d_items_b3 = nullptr;  // items whose R is read by bf16 passes
   ChallengeItem* d_items_f4 = nullptr;
   uint32_t n_items = 0;
@@ -971,7 +1016,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     return a;
   };
   const size_t o_key = place(32);
-  const size_t o_queue = place(POTS_FV_STAGES * sizeof(uint32_t));
+  const size_t o_queue = place(POTS_FV_STAGES * kQueues * sizeof(uint32_t));
   const uint64_t b3_per_row = (uint64_t)groups_b3(k) * 16;  // bf16 elements per row of V
   const uint64_t f4_per_row = (uint64_t)groups_f4(k) * 16;  // floats per row of V
   std::vector<ChallengeItem> items(n);
@@ -1461,7 +1506,7 @@ static void launch_pass(const FvPlan* P, const PassLaunch& L, uint32_t max_grid,
                         uint32_t* queue, hipStream_t s) {
   const bool queued = max_grid != 0 && max_grid < L.n_blocks;
   const uint32_t grid = queued ? max_grid : L.n_blocks;
-  if (queued) hipLaunchKernelGGL(queue_reset, dim3(1), dim3(1), 0, s, queue);
+  if (queued) hipLaunchKernelGGL(queue_reset, dim3(1), dim3(kQueues), 0, s, queue);
   hipLaunchKernelGGL((row_pass<XT, W, S, NJG>), dim3(grid), dim3(256), 0, s,
                      P->d_jobs + L.job_off, P->d_blk + L.blk_off, P->k, L.n_blocks,
                      queued ? queue : nullptr);
@@ -1480,12 +1525,12 @@ static int launch_njg(const FvPlan* P, const PassLaunch& L, uint32_t g, uint32_t
 }
 
 // A pass launch of stage `stage` (1 B, 3 A, 4 P) with grid limit g; the stage's tile queue
-// counter is the plan's d_queue[stage].
+// counters are the plan's d_queue[kQueues·stage ..].
 static int run_pass(const FvPlan* P, const PassLaunch& L, int stage, hipStream_t s) {
   if (L.n_blocks == 0) return POTS_E_OK;
   const uint32_t key = L.xt * 4 + L.weighted * 2 + L.sq64;
   const uint32_t g = P->max_grid[stage];
-  uint32_t* q = P->d_queue + stage;
+  uint32_t* q = P->d_queue + (size_t)kQueues * stage;
   int rc;
   switch (key) {
     case 0: rc = launch_njg<DT_F32, false, false>(P, L, g, q, s); break;
