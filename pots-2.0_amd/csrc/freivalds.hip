@@ -450,7 +450,10 @@ __device__ __forceinline__ uint32_t xcd_id() {
   return (uint32_t)__builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) % kQueues;
 }
 
-// The row pass over n_tiles tiles. With a block per tile (queue null), block b takes tile b.
+// The row pass over n_tiles tiles. With a block per tile (queue null), block b takes tile b
+// (mapping blocks XCD by XCD, as the fused chunk kernel does, cut the B pass's reads 1.08x ->
+// 1.02x but made it slower: with no stealing, XCDs given equal tile counts of unequal tiles
+// finish apart).
 // With a smaller grid, the pass holds a bounded share of each CU (a block holds 4 waves and
 // 32 KiB of LDS) so that a kernel on another stream (the leaf hasher) keeps the rest, and the
 // blocks take tiles from the queues: counters (zero at launch) that each block's first thread

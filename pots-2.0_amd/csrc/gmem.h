@@ -23,4 +23,16 @@ __device__ __forceinline__ void gstore(void* p, const T& v) {
   *(POTS_GLOBAL T*)(p) = v;
 }
 
+// The GPU hands a launch's blocks to its 8 XCDs in turn (block b to XCD b mod 8), and each
+// XCD has its own L2. Block b of a launch of n blocks taking unit xcd_block(b, n) gives each
+// XCD a contiguous range of units, so neighbouring units that read the same small data (rows
+// of R, a column chunk's B·R) run beside one L2 instead of each XCD fetching it. A bijection
+// on [0, n).
+constexpr uint32_t kXcds = 8;
+__device__ __forceinline__ uint32_t xcd_block(uint32_t b, uint32_t n) {
+  const uint32_t per = n / kXcds, rem = n % kXcds;
+  const uint32_t x = b % kXcds, i = b / kXcds;
+  return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
 }  // namespace pots

@@ -410,20 +410,6 @@ struct Order {
   uint32_t n_blocks;  // ceil(n_slots / kThreads)
 };
 
-// The GPU hands a launch's blocks to its 8 XCDs in turn (block b to XCD b mod 8), and each
-// XCD has its own L2. With one block per order block, block b of the fused chunk kernel takes
-// order block xcd_block(b, n), which gives each XCD a contiguous range of the fused order:
-// neighbouring slots, which read the same rows of R, are then hashed beside one L2 instead of
-// each XCD fetching those rows again (the kernel's reads went from 1.12x to 1.05x its message
-// bytes). The plain order has no R and keeps the hardware's interleave, which balances its
-// blocks' uneven work better. (A bijection on [0, n).)
-constexpr uint32_t kXcds = 8;
-__device__ __forceinline__ uint32_t xcd_block(uint32_t b, uint32_t n) {
-  const uint32_t per = n / kXcds, rem = n % kXcds;
-  const uint32_t x = b % kXcds, i = b / kXcds;
-  return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
-}
-
 __device__ __forceinline__ uint32_t order_entry(const Order& od, uint64_t g, uint32_t blk) {
   uint32_t lo = od.blk_ent[blk], hi = od.blk_ent[blk + 1];
   while (lo < hi) {  // the last entry whose first slot is <= g
@@ -487,6 +473,11 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel(
   }
 }
 
+// With a block per order block, block b takes order block xcd_block(b, n) (gmem.h): each XCD
+// hashes a contiguous range of the fused order, and neighbouring slots read the same rows of
+// R, which one L2 then holds (the kernel's reads went from 1.12x to 1.05x its message bytes).
+// The plain order has no R and keeps the hardware's interleave.
+//
 // The fused leaves (FuseDesc), each starting at a multiple of 64 slots in the fused order and
 // holding a multiple of 64: a wave's slots are one leaf's and one class range's, so the entry,
 // the leaf's descriptors and, at each step of the runs, R's rows are wave-uniform and live in
