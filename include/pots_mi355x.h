@@ -120,8 +120,9 @@ int pots_leaf_plan_run(void *plan, uint8_t *d_out, uint32_t *d_first_bad, void *
 int pots_leaf_plan_run_stage(void *plan, int stage, uint8_t *d_out, uint32_t *d_first_bad,
                              void *stream);
 
-/* Limit the chunk kernel's grid to max_blocks blocks of 256 lanes (0: no limit, one block per
- * 256 chunks). Each block then hashes several slots of 256 chunks in turn, and the kernel
+/* Limit the chunk kernels' grid to max_blocks blocks of 256 lanes (0: no limit, one block per
+ * 256 slots; a slot is one lane's run of up to four consecutive chunks). Each block then
+ * hashes several blocks' worth of slots in turn, and the kernel
  * holds at most that many blocks' worth of the GPU, leaving the rest to work on other
  * streams (the Freivalds passes, which are bound by HBM, not by the VALUs hashing needs).
  * Results do not depend on it. No counterpart in the reference. */
@@ -215,7 +216,8 @@ int pots_fv_plan_run_stage(void *plan, int stage, const uint8_t *d_key, double *
                            void *stream);
 
 /* Limit the row-pass grid of stage 1 (B pass), 3 (A pass) or 4 (P pass) to max_blocks blocks
- * of 256 lanes (0: no limit, one block per tile). Each block then takes several tiles in turn
+ * of 256 lanes (0: no limit, one block per tile). Each block then takes several tiles in turn,
+ * from a queue per XCD (a contiguous range of the tiles each, then the other XCDs' ranges),
  * and the pass holds at most that many blocks' worth of the GPU, so that a kernel on another
  * stream (the leaf hasher, which needs every SIMD's VALUs) can share the CUs. Results do not
  * depend on it. No counterpart in the reference. */
