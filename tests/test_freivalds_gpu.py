@@ -307,3 +307,24 @@ def test_grid_limited_passes_take_tiles_from_a_queue(lib, k):
         got = plan.rows(H)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int64), want.view(torch.int64))
+
+
+def test_queues_with_fewer_tiles_than_xcds(lib):
+    """The tiles are split into one queue per XCD; with fewer tiles than queues some ranges
+    are empty, and a grid of 2 blocks must still drain every range (from whichever XCD the
+    blocks run on): rows bit for bit those of a block per tile."""
+    from verification.commitment import native
+    items = []
+    for i, (shape, dtype) in enumerate([((100, 96, 80), torch.bfloat16),
+                                        ((64, 200, 48), torch.float32),
+                                        ((130, 64, 40), torch.bfloat16)]):
+        a, b, p, _ = _operands(*shape, 90 + i, dtype)
+        items.append(native.FvProduct(a.cuda(), b.cuda(), p.cuda(), 300 + i))
+    want = lib.fv_plan(items, 4).rows(H)
+    plan = lib.fv_plan(items, 4)
+    for stage in (1, 3, 4):
+        plan.set_grid(stage, 2)
+    for _ in range(2):
+        got = plan.rows(H)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int64), want.view(torch.int64))
