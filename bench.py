@@ -475,6 +475,36 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int 
     torch.cuda.synchronize()
     verify_ms = (time.perf_counter() - t0) * 1e3
     assert verdict.check is None and verdict.root == tree.root, verdict.detail
+    # The reference-shaped path on the same step: Verifier.verify_step in the reference's
+    # order, every operand and check 6b's glue gradients from the decoder replay of the
+    # committed leaves; the first run builds the plans, the second finds them cached.
+    from verification.commitment.leaves import leaf_hashes_of
+    from verification.commitment.merkle import merkle_root
+    from verification.transcript.store import InMemoryStore
+    from verification.verifier.bands import Bands
+    from verification.verifier.driver import Verifier
+    recs = [leaves[c.record_index(i)] for i in range(c.n_s)]
+    h_d = merkle_root(leaf_hashes_of(c, ((0, r) for r in recs)))
+    cl_ms, cl_slots, cache = [], [], None
+    for _ in range(2):
+        cv = Verifier(c, h_D=h_d, n_records=c.n_s, k=k, n_steps=1, bands=Bands.provisional(),
+                      seed=0, w0={n: leaves[c.w_t_index(n)] for n in c.weight_names},
+                      schedule=lambda t: list(range(c.n_s)), allow_provisional=True)
+        if cache is not None:
+            cv.plans = cache
+        assert cv.start_run(recs) is None
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        rej = cv.verify_step(1, InMemoryStore(leaves, tree))
+        cl_ms.append((time.perf_counter() - t0) * 1e3)
+        cl_slots.append({s_: round(t_ * 1e3, 2) for s_, t_ in cv.timings[1].items()})
+        assert rej is None, rej
+        cache = cv.plans
+    cache.close()
+    log(f"[bench] qwen2 check-level Verifier.verify_step (decoder replay, check 6b on "
+        f"{len(c.glue_gradient_weights)} glue weights): {cl_ms[0]:.0f} ms building its plans, "
+        f"{cl_ms[1]:.0f} ms with them cached; " +
+        ", ".join(f"{s_} {t_:.1f}" for s_, t_ in cl_slots[1].items()))
     # the reference's per-product copy to pinned host memory, on every 8th product
     sample = list(step.products[::8])
     host = [torch.empty(p.shape, dtype=p.dtype, pin_memory=True) for p in sample]
@@ -499,6 +529,9 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int 
             "training_step_ms": round(plain_ms, 1), "prove_step_ms": round(prove_ms, 1),
             "commit_ms": round(commit_ms, 1), "verifier_setup_ms": round(setup_ms, 1),
             "verify_ms": round(verify_ms, 2), "verified": True,
+            "check_level": {"verify_step_first_ms": round(cl_ms[0], 1),
+                            "verify_step_ms": round(cl_ms[1], 1), "slots_ms": cl_slots[1],
+                            "glue_weights": len(c.glue_gradient_weights)},
             "avoided_d2h_gbps": round(d2h_gbps, 1),
             "avoided_d2h_s": round(product_bytes / d2h_gbps / 1e9, 3)}
 
@@ -564,7 +597,8 @@ def main() -> int:
     ap.add_argument("--b-grid", type=int, default=0,
                     help="blocks of the B pass (0: one per tile)")
     ap.add_argument("--a-grid", type=int, default=None,
-                    help="blocks of the A pass (default: one per CU when fused, else one per "
+                    help="blocks of the A pass (default when fused: one per CU, or one and "
+                         "a half where the hashing is the smaller half; unfused: one per "
                          "tile); see pots_fv_plan_set_grid")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="copy this many MiB device to device twice before timing, so a "
@@ -605,6 +639,14 @@ def main() -> int:
     from verification.verifier.step import DeviceStepVerifier
 
     lib = native.get()
+    # The prover legs build their own model and step; they run first, on an empty GPU, so
+    # that the resident C4 transcript need not share HBM with them.
+    prover = None
+    if args.prover_leg:
+        prover = prover_leg() if args.prover_leg == "mlp" else capture_leg_qwen2()
+        import gc
+        gc.collect()
+        torch.cuda.empty_cache()
     desc, ctor, k = CONFIGS[args.config]
     c = getattr(decoder, ctor)()
     log(f"[bench] {args.config}: {c.M} products, {c.n_leaves} leaves, k={k}")
@@ -850,13 +892,11 @@ def main() -> int:
         out["parts"]["check_level"] = check_level_leg(c, step, k, claimed_b)
     if args.disk_leg:
         out["parts"]["disk_load"] = disk_leg(Path(args.disk_leg), c, step, k, claimed_b, v)
-    if args.prover_leg == "mlp":
-        out["parts"]["prover"] = prover_leg()
-    elif args.prover_leg == "qwen2":
-        out["parts"]["prover"] = capture_leg_qwen2()
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")
         out["cpu_baseline"] = cpu_baseline(step, items)
+    if prover is not None:
+        out["parts"]["prover"] = prover
     print(json.dumps(out), flush=True)
     return 0
 
