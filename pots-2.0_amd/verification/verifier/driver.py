@@ -12,11 +12,13 @@ without ``allow_provisional``, and κ classes or τ_W tensors that name nothing 
   adopted for every step when the caller passes ``schedule``; the reference's default schedule
   (a BLAKE3 shuffle of ``D`` by ``seed``, ``setup/data.py:325``) and check 4, the only check
   that reads ``π``, are not part of this build.
-- :meth:`Verifier.verify_step` runs :data:`~.checks.DEFAULT_ORDER` (``7 → 2 → 6a → 5 →
-  2.root``; check 7 reports as check 0 on the first step, against ``W_0``), stops at the first
+- :meth:`Verifier.verify_step` runs :data:`~.checks.DEFAULT_ORDER` (``7 → 2 → 6a → 5 → 6b →
+  2.root``; check 7 reports as check 0 on the first step, against ``W_0``; 6b is skipped when
+  check 5 measured the prover's own operands), stops at the first
   rejection, keeps each step's statistics and per-slot wall clock, and on acceptance keeps the
   step's ``W_{t+1}`` leaf hashes for the next step's check 7.
-- :meth:`Verifier.freeze` ends a calibration run by judging the recorded numbers.
+- :meth:`Verifier.freeze` ends a calibration run by judging the recorded numbers of every
+  calibrated step in check order: 6a, then 5, then 6b.
 - :meth:`Verifier.end_run` compares the kept hashes with the agreed final weights (check 8,
   which a run shorter than ``T`` also fails) and returns check 9's :class:`RunVerdict`.
 
@@ -282,10 +284,30 @@ class Verifier:
 
     @staticmethod
     def _rejudge(t: int, stats: StepStats, bands: Bands) -> Rejection | None:
+        """One calibrated step's recorded numbers against ``bands``, in the slots' order:
+        6a's ``ρ_max`` per linear weight, check 5's ``κ`` and normalized residuals per
+        product, then 6b's ``ρ_max`` per glue weight (reference driver.py:321-341)."""
+        rej = Verifier._rejudge_updates(t, stats, bands, "6a")
+        if rej is None:
+            rej = Verifier._rejudge_products(t, stats, bands)
+        if rej is None:
+            rej = Verifier._rejudge_updates(t, stats, bands, "6b")
+        return rej
+
+    @staticmethod
+    def _rejudge_updates(t: int, stats: StepStats, bands: Bands,
+                         check_id: str) -> Rejection | None:
         for s in stats.tensors:
-            if s.check_id == "6a" and not s.rho_max <= bands.tau_w_for(s.weight):
-                return Rejection(t, "6a", f"{s.weight}: ρ_max = {s.rho_max:.3g} > "
-                                          f"τ_W = {bands.tau_w_for(s.weight):g}")
+            if s.check_id != check_id:
+                continue
+            tau_w = bands.tau_w_for(s.weight)
+            if not s.rho_max <= tau_w:
+                return Rejection(t, check_id, f"{s.weight}: ρ_max = {s.rho_max:.3g} > "
+                                              f"τ_W = {tau_w:g}")
+        return None
+
+    @staticmethod
+    def _rejudge_products(t: int, stats: StepStats, bands: Bands) -> Rejection | None:
         for p in stats.products:
             kmax = bands.kappa_for(p.cls)
             if not p.kappa <= kmax:

@@ -331,3 +331,56 @@ def test_array_judge_stops_where_the_per_product_judge_does(guard, judge, seed):
     if stop < M:
         assert _judge_product(c, c.products[stop], f.measure(stop), ctx, bands) == ref_rej
         assert repr(ctx.stats.products[-1]) == repr(ref_ctx.stats.products[-1])  # NaN κ
+
+
+# ---- freeze(): a calibration run's recorded numbers judged in slot order --------------------
+
+def _calibrated(stats):
+    """A calibration-mode Verifier over the MLP with one calibrated step whose recorded
+    numbers are ``stats`` (as verify_step leaves them while judge=False)."""
+    from verification.computation.instances.mlp import MLPComputation
+    from verification.verifier.driver import Verifier
+    c = MLPComputation((4, 8, 4), n_s=2, eta=1e-4)
+    v = Verifier(c, h_D=bytes(32), n_records=2, k=1, n_steps=1, bands=None, seed=0,
+                 w0_hashes=[bytes(32)] * c.n_w, calibrate=True)
+    v.calibrated_steps.append(1)
+    v.stats[1] = stats
+    v.timings[1] = {}
+    return v
+
+
+# the MLP's two weights, standing for a linear weight (6a) and a glue weight (6b)
+W_LIN, W_GLUE = "layers.0.weight", "layers.1.weight"
+
+
+def _stats(rho_6a=1.0, rho_6b=1.0, kappa=1.0, res=0.5):
+    from verification.verifier.context import ProductStat, StepStats, TensorStat
+    s = StepStats()
+    s.tensors.append(TensorStat(W_LIN, "6a", rho_6a))
+    s.products.append(ProductStat(m=1, name="Y_1", cls="forward:Y_1", kappa=kappa,
+                                  normalized=(res,)))
+    s.tensors.append(TensorStat(W_GLUE, "6b", rho_6b))
+    return s
+
+
+def test_freeze_judges_a_glue_update_over_its_band():
+    v = _calibrated(_stats(rho_6b=9.0))
+    rej = v.freeze(Bands(tau=8.0, kappa_max=1e4, tau_w=4.0, source="file"))
+    assert rej == Rejection(1, "6b", f"{W_GLUE}: ρ_max = 9 > τ_W = 4")
+    assert v.rejection == rej
+
+
+def test_freeze_order_is_6a_then_5_then_6b():
+    bands = Bands(tau=8.0, kappa_max=1e4, tau_w=4.0, source="file")
+    every = _stats(rho_6a=5.0, rho_6b=9.0, res=9.5)
+    assert _calibrated(every).freeze(bands).check_id == "6a"
+    no_6a = _stats(rho_6b=9.0, res=9.5)
+    rej = _calibrated(no_6a).freeze(bands)
+    assert rej.check_id == "5" and "challenge j=1" in rej.detail
+    assert _calibrated(_stats()).freeze(bands) is None
+    # a NaN ρ_max is not ≤ τ_W, so it rejects as the live check would
+    assert _calibrated(_stats(rho_6b=math.nan)).freeze(bands).check_id == "6b"
+    # a per-tensor τ_W judges that weight alone
+    wide = Bands(tau=8.0, kappa_max=1e4, tau_w=4.0, tau_w_tensors={W_GLUE: 16.0},
+                 source="file")
+    assert _calibrated(_stats(rho_6b=9.0)).freeze(wide) is None
