@@ -71,6 +71,9 @@ size_t pots_hash_leaves(size_t n, const uint8_t *hdr_buf, const uint64_t *hdr_of
  * device array, one per GPU, held until the process ends: about 2 M chunks of 1 KiB, i.e.
  * some 2 GiB of leaf bytes in device memory (host payloads also take their size in it). A
  * larger request returns SIZE_MAX with the reason in pots_last_error(), before any GPU work.
+ * The array belongs to the library's code object: loading the library reserves its 64 MiB
+ * of device memory on each GPU where the code is loaded, even if this entry point is never
+ * called.
  * Calls in one process are serialised, since they share the array; calls from two processes
  * on one GPU use separate arrays. Synchronous, on the null stream. */
 size_t pots_hash_leaves_noalloc(size_t n, const uint8_t *hdr_buf, const uint64_t *hdr_off,

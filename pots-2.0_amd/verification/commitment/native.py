@@ -771,14 +771,16 @@ _disabled_lock = threading.Lock()
 
 
 def enabled() -> bool:
-    """False inside :func:`disabled`. Kept for the reference's callers; the GPU library is
-    used either way."""
+    """False inside :func:`disabled`. Kept for the reference's callers, which read it. Unlike
+    the reference (native.py:353-368), nothing switches on it: there is no CPU hashing path in
+    the product, so the GPU library serves every call either way."""
     return _disabled == 0
 
 
 @contextmanager
 def disabled() -> Iterator[None]:
-    """Make :func:`enabled` return False inside the block. Nestable."""
+    """Make :func:`enabled` return False inside the block. Nestable. A flag only: calls
+    inside the block still run on the GPU library."""
     global _disabled
     with _disabled_lock:
         _disabled += 1
