@@ -516,7 +516,7 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int 
     d2h_gbps = sum(p.nbytes for p in sample) / (time.perf_counter() - t0) / 1e9
     summary = step.capture
     log(f"[bench] qwen2 prover leg: training step {plain_ms:.0f} ms, proved (capture, "
-        f"labeling, SGD) {prove_ms:.0f} ms; {c.M} products ({summary['n_calls']} calls), "
+        f"labeling, SGD) {prove_ms:.0f} ms; {c.M} products ({summary['calls']} calls), "
         f"{product_bytes / 1e9:.2f} GB in HBM; commit of {leaf_bytes / 1e9:.2f} GB "
         f"{commit_ms:.0f} ms (root {tree.root.hex()[:16]}…); verifier plans {setup_ms:.0f} ms, "
         f"verify {verify_ms:.1f} ms (accepted); the host copy it avoids runs at "
@@ -524,7 +524,7 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int 
     return {"model": f"Qwen2-1.5B-shaped, {layers} of 28 layers (transformers "
                      f"Qwen2ForCausalLM, random init, fp32, eager attention), {batch}x{seq} "
                      "tokens",
-            "k": k, "products": c.M, "calls": summary["n_calls"],
+            "k": k, "products": c.M, "calls": summary["calls"],
             "product_bytes": product_bytes, "leaf_bytes": leaf_bytes,
             "training_step_ms": round(plain_ms, 1), "prove_step_ms": round(prove_ms, 1),
             "commit_ms": round(commit_ms, 1), "verifier_setup_ms": round(setup_ms, 1),

@@ -7,8 +7,7 @@ committed batch and ``W_t``, so that everything between products (norms, softmax
 activations, residual sums, the loss and autograd's glue) is recomputed from committed values
 and every product is the leaf the prover committed. Two passes do it:
 
-1. **The plan.** One training pass under :class:`~verification.computation.recording.
-   MatmulCapture`, labeled by the computation's own ``label_with_operands``, gives for every
+1. **The plan.** One training pass under :class:`~verification.prover.capture.MatmulCapture`, labeled by the computation's own ``label_with_operands``, gives for every
    matmul call of a pass (counted in dispatch order, outer products included) the product
    slots its output fills: one slot, or one per member of a batched call, and whether the slot
    holds the member's output transposed. The call sequence of a pass depends on the model's
@@ -35,7 +34,7 @@ import torch
 from torch.utils._python_dispatch import TorchDispatchMode
 
 from verification.computation.matmul_ops import HANDLED_OPS, param_storage_map
-from verification.computation.recording import MatmulCapture
+from verification.prover.capture import MatmulCapture
 
 __all__ = ["ReplayError", "CallPlan", "plan_calls", "CommittedProducts"]
 

@@ -49,7 +49,7 @@ def _oracle_root(c, leaves):
 
 def test_products_stay_in_hbm_and_commit_matches_the_oracle(lib):
     c, step, tree = _prove(seed=1)
-    assert step.capture["device_resident"] and step.capture["n_products"] == c.M
+    assert step.capture["on_device"] and step.capture["products"] == c.M
     assert all(p.is_cuda for p in step.products)
     assert all(w.is_cuda for w in step.w_next.values())
     assert tree.root == _oracle_root(c, step.leaves())
@@ -157,7 +157,7 @@ def test_real_decoder_step_commits_and_verifies(lib, qkv_bias, n_kv):
     from verification.transcript.store import InMemoryStore
     from verification.verifier.step import DeviceStepVerifier
     c, step, tree = _decoder_prove(seed=7, qkv_bias=qkv_bias, n_kv=n_kv)
-    assert step.capture["device_resident"]
+    assert step.capture["on_device"]
     assert tree.root == _decoder_oracle_root(c, step.leaves())
     v = started_verifier(c, step.leaves(), k=2)
     assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None

@@ -49,8 +49,10 @@ def test_capture_records_products_with_their_operands():
     assert [m[2].shape for m in cap.records[2].members()] == [(4, 6), (4, 6)]
     assert all(r.q == 3 for r in cap.records) and not cap.glue_outer
     s = cap.summary()
-    assert s["n_calls"] == 5 and s["n_products"] == 7 and s["products_by_phase"] == {
+    assert s["calls"] == 5 and s["products"] == 7 and s["products_per_phase"] == {
         "forward": 7}
+    assert s["calls_per_op"]["forward:aten.addmm.default"] == 2 and s["q_range"] == (3, 3)
+    assert s["outer_calls"] == 0 and s["product_bytes"] == 4 * (20 + 20 + 48 + 20 + 48)
 
 
 def test_capture_rules_refuse_what_the_inventory_cannot_hold():
@@ -104,6 +106,76 @@ def test_capture_tracks_producers_parameter_copies_and_mutation():
     assert all(r.a is None and r.b is None for r in cap.records)
 
 
+def test_capture_refusals_outside_a_phase():
+    a, b = torch.randn(4, 3), torch.randn(3, 5)
+    cap = MatmulCapture()
+    with cap:
+        # a refused matmul-like op and another overload of a handled op are refused anywhere
+        with pytest.raises(UnsupportedMatmulError):
+            torch.mv(a, torch.randn(3))
+        with pytest.raises(UnsupportedMatmulError):
+            torch.ops.aten.bmm.out(a[None], b[None], out=torch.empty(1, 4, 5))
+        # a handled op, a copy and an ordinary op outside a phase: the first is refused, the
+        # others run and leave nothing behind
+        with pytest.raises(PhaseError):
+            torch.mm(a, b)
+        a.to(torch.float64)
+        torch.relu(a)
+        with cap.phase("backward"):
+            torch.mm(a, b)
+            w = a.to(torch.float64)                          # a copy of no parameter
+    assert [r.phase for r in cap.records] == ["backward"] and len(cap.copies) == 1
+    assert cap.copies[0].param is None and cap.param_of(w) is None
+
+
+def test_capture_refuses_foreign_ops_only_inside_a_phase():
+    lib = torch.library.Library("potstest", "DEF")
+    lib.define("twice(Tensor x) -> Tensor")
+    lib.impl("twice", lambda x: x * 2, "CompositeExplicitAutograd")
+    x = torch.randn(3)
+    cap = MatmulCapture()
+    with cap:
+        torch.ops.potstest.twice(x)                          # outside a phase: runs
+        with cap.phase("forward"):
+            with pytest.raises(UnsupportedMatmulError, match="outside aten and prims"):
+                torch.ops.potstest.twice(x)
+
+
+def test_capture_watch_names_each_moved_role_and_release_keeps_outputs():
+    a, b = torch.randn(4, 3), torch.randn(3, 5)
+    cap = MatmulCapture()
+    with cap, cap.phase("forward"):
+        p = torch.mm(a, b)
+        torch.mm(p, torch.randn(5, 2))
+    a.mul_(2)
+    p.add_(1)
+    with pytest.raises(MutatedCaptureError) as e:
+        cap.assert_unmodified()
+    msg = str(e.value)
+    assert "#0 aten.mm.default (forward): a, out" in msg and "#1 aten.mm.default (forward): a" \
+        in msg
+    cap.release_operands()
+    with pytest.raises(MutatedCaptureError):                 # outputs are still watched
+        cap.assert_unmodified()
+    assert cap.records[0].out is p and cap.records[0].a is None
+    with pytest.raises(Exception, match="released"):
+        list(cap.records[0].members())
+
+
+def test_capture_parameter_copies_are_released():
+    lin = torch.nn.Linear(3, 4, bias=False)
+    cap = MatmulCapture(param_names=param_storage_map(lin))
+    with cap, cap.phase("forward"):
+        w64 = lin.weight.to(torch.float64)
+        ww = w64.to(torch.float32)                          # a copy of the copy
+    assert cap.param_of(w64) == "weight" and cap.param_of(ww) == "weight"
+    assert cap.param_of(lin.weight) == "weight"
+    assert [c.param for c in cap.copies] == ["weight", "weight"]
+    assert cap.summary()["parameter_copies"] == 2
+    cap.release_operands()
+    assert cap.param_of(w64) is None and cap.param_of(lin.weight) == "weight"
+
+
 def test_mlp_inventory_matches_the_reference_layout():
     c = MLPComputation(WIDTHS, n_s=4, eta=0.05)
     assert c.M == 3 * c.L - 1 == 8
@@ -142,7 +214,7 @@ def test_prove_step_labels_products_and_steps_sgd():
         g = step.products[c.m_of(f"G_{l}") - 1]
         assert torch.allclose(step.w_next[c.weight(l)], w0[c.weight(l)] - c.eta * g,
                               rtol=0, atol=1e-7)
-    assert step.capture["n_products"] == c.M
+    assert step.capture["products"] == c.M
     step.assert_unmodified()
     step.products[0].add_(1.0)
     with pytest.raises(MutatedCaptureError):
@@ -198,7 +270,7 @@ def test_decoder_labeling_fills_every_slot_with_its_own_product(qkv_bias, n_kv):
     (bit for bit where the op itself computed it, 1e-5 for the transposed dK leaves and the
     biased forward linears)."""
     c, w0, step = _decoder_step(qkv_bias, n_kv)
-    assert len(step.products) == c.M and step.capture["n_glue_outer_calls"] == 1
+    assert len(step.products) == c.M and step.capture["outer_calls"] == 1
     for spec in c.products:
         a, b = step.operands[spec.m]
         p = step.products[spec.m - 1]
