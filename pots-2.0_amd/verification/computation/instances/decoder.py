@@ -1,11 +1,10 @@
-"""The Llama/Qwen2 decoder's declared computation: leaf layout, product inventory and the
-prover's labeling.
+"""The Llama/Qwen2 decoder's declared computation: leaf layout, product inventory, the
+prover's labeling and the verifier's replay.
 
 Reference: verification/computation/instances/decoder.py:154-160 (``matmul_count_decoder``),
 :320-400 (weight names and shapes) and :416-471 (``_inventory``). The order of weights and
 products, their shapes and their κ classes follow the reference exactly, since they fix which
-leaf is which and what challenge width each product gets. Autocast, head blocks on the prover
-side and the replay that rebuilds operands from the leaves are outside this build.
+leaf is which and what challenge width each product gets.
 
 Per layer: the q/k/v projections (with biases for Qwen2), ``n_s·n_h`` members each of
 ``S = Q·Kᵀ`` and ``O = A·V``, then o/gate/up/down; the head ``Λ = X·W_outᵀ`` in ``B`` row
@@ -13,11 +12,13 @@ blocks; then backward, layers in reverse: input and weight gradients of down/gat
 members' ``dA, dV`` and ``dQ, dK``, and the input and weight gradients of q/k/v.
 
 The prover side (:meth:`DecoderComputation.build_model`, :meth:`~DecoderComputation.loss`,
-:meth:`~DecoderComputation.label_with_operands`) runs transformers' Llama/Qwen2 causal LM with
-eager attention, one head block, in the computation's dtype, and maps the captured records onto
-the slots above by operand identity (reference decoder.py:774-1100, for the cases this build
-takes: one head block, no autocast). The replay that rebuilds the operands from the leaves is
-not built: the labeler returns the captured operands with the products.
+:meth:`~DecoderComputation.label_with_operands`) runs transformers' Llama/Qwen2 causal LM over
+fp32 master weights, under autocast to bf16 for a bf16 computation (reference
+decoder.py:551-598), with one head block and this build's attention core
+(``instances/attention.py``: eager attention's arithmetic, every batched product's right
+operand contiguous), and maps the captured records onto the slots above by operand identity.
+:class:`DecoderReplay` rebuilds check 5's operands and check 6b's glue gradients from the
+committed leaves (reference decoder.py:1142,1682-1751).
 """
 
 from __future__ import annotations
@@ -229,18 +230,19 @@ class DecoderComputation(DeclaredComputation):
     # ---- prover side ----------------------------------------------------------------------
 
     def build_model(self) -> torch.nn.Module:
-        """transformers' causal LM of this shape (Qwen2 with q/k/v biases, else Llama), eager
-        attention, random init, fp32, in eval mode (no dropout), on the current default device.
+        """transformers' causal LM of this shape (Qwen2 with q/k/v biases, else Llama), random
+        init, in the weights' dtype (the fp32 masters the layout declares), in eval mode (no
+        dropout), on the current default device. A bf16 computation runs it under autocast
+        (:meth:`loss`), as the reference does (decoder.py:551-598).
 
-        The weights are the fp32 masters the layout declares. A bf16 computation would run
-        under autocast over those masters (reference decoder.py:568-598), which the prover side
-        of this build does not do: it refuses such a computation rather than commit bf16
-        weight leaves where fp32 ones are declared."""
-        if self.compute_dtype != self.weight_dtype:
-            raise NotImplementedError(
-                f"the prover side runs the decoder in its weight dtype ({self.weight_dtype}); "
-                f"{self.compute_dtype} compute over fp32 masters (autocast) is not built")
+        Attention runs through this build's own core (``instances/attention.py``) instead of
+        transformers' eager function: the same products and glue, with no batched product
+        ever given a transposed right operand."""
+        if self.head_blocks != 1:
+            raise NotImplementedError("the prover side takes one head block")
         from transformers import LlamaConfig, LlamaForCausalLM, Qwen2Config, Qwen2ForCausalLM
+
+        from verification.computation.instances.attention import register
         cfg_cls, model_cls = (Qwen2Config, Qwen2ForCausalLM) if self.qkv_bias else \
             (LlamaConfig, LlamaForCausalLM)
         cfg = cfg_cls(vocab_size=self.n_v, hidden_size=self.d, intermediate_size=self.d_f,
@@ -250,9 +252,7 @@ class DecoderComputation(DeclaredComputation):
         if not self.qkv_bias:
             cfg.attention_bias = False
             cfg.mlp_bias = False
-        cfg._attn_implementation = "eager"
-        if self.head_blocks != 1:
-            raise NotImplementedError("the prover side takes one head block")
+        cfg._attn_implementation = register()
         cfg.attention_dropout = 0.0
         model = model_cls(cfg).to(self.weight_dtype).eval()
         active = [name for name, mod in model.named_modules()
@@ -261,13 +261,24 @@ class DecoderComputation(DeclaredComputation):
             raise ValueError(f"dropout is active in {active[:3]}: a step must be deterministic")
         return model
 
+    def autocast(self, device: torch.device):
+        """The compute format over the fp32 masters: autocast to it on ``device``'s type, or
+        nothing when the two are the same (reference decoder.py:551-556)."""
+        import contextlib
+        if self.compute_dtype == self.weight_dtype:
+            return contextlib.nullcontext()
+        return torch.autocast(device.type, dtype=self.compute_dtype)
+
     def loss(self, model: torch.nn.Module, records) -> torch.Tensor:
-        """Mean cross-entropy of the targets over the masked tokens."""
+        """Mean cross-entropy of the targets over the masked tokens; the model runs in the
+        compute format, the loss in fp32."""
         dev = next(model.parameters()).device
         ids = torch.stack([r.ids for r in records]).to(device=dev, dtype=torch.long)
         targets = torch.stack([r.targets for r in records]).to(device=dev, dtype=torch.long)
         mask = torch.stack([r.mask for r in records]).to(device=dev, dtype=torch.float32)
-        logits = model(input_ids=ids).logits.float()
+        with self.autocast(dev):
+            logits = model(input_ids=ids).logits
+        logits = logits.float()
         ce = torch.nn.functional.cross_entropy(logits.reshape(-1, self.n_v),
                                                targets.reshape(-1), reduction="none")
         return (ce * mask.reshape(-1)).sum() / mask.sum()
@@ -296,31 +307,35 @@ class DecoderComputation(DeclaredComputation):
                             = None
                             ) -> tuple[list[torch.Tensor], dict[int, tuple[torch.Tensor,
                                                                            torch.Tensor]]]:
-        """``(P_1..P_M, {m: (A_m, B_m)})`` from the capture, mapped by operand identity.
+        """``(P_1..P_M, {m: (A_m, B_m)})`` from the capture, mapped by operand identity
+        (reference decoder.py:774-1100 maps the same slots from eager attention's forms).
 
-        Forward: a linear's ``B`` views its weight; the two batched products after layer
-        ``ℓ``'s v projection are ``S`` then ``O``; the head's ``B`` views ``W_out``. Backward:
-        an input gradient's ``B`` is the weight itself; a weight gradient's output is the
-        weight's ``.grad`` (the tied head's, whose ``.grad`` also holds the embedding's share,
-        is the product whose ``B`` is the head's input); ``dA`` reads ``O``'s ``B``, ``dV``
-        ``O``'s ``A``, ``dQ`` ``S``'s ``B``, and the batched product reading ``S``'s ``A`` is
-        ``K̃``'s gradient ``Q̃ᵀ·δS``, whose transpose is the ``dK`` leaf with operands
-        ``(δSᵀ, Q̃)``.
+        Linear products: a forward's ``B`` views its weight, or autocast's copy of it; an
+        input gradient's ``B`` is that weight (or copy); a weight gradient's output is the
+        weight's ``.grad``, or under autocast the product whose whole output ``.grad`` copies
+        to fp32. The head's ``B`` is ``W_out``; the tied head's weight gradient is the product
+        whose ``B`` is the head's input. Attention (the core in ``instances/attention.py``):
+        the two batched products after layer ``ℓ``'s q/k/v are ``S`` then ``O``; in backward,
+        ``dV`` reads ``O``'s ``A`` (transposed) and ``dA`` is the product whose ``A`` is
+        ``dV``'s ``B`` (``δO``); ``dK`` reads ``S``'s ``A`` as its ``B`` and ``dQ`` is the other
+        product over ``dK``'s ``A`` storage (``δS``).
 
         ``call_slots``, when given, receives for each labeled call (by capture index) the slots
-        its output fills: ``(member index or None, slot name, transposed)``, ``transposed``
-        when the slot holds the member's output transposed (the ``dK`` leaves).
+        its output fills: ``(member index or None, slot name, transposed)``; this core fills
+        no slot transposed.
         """
         if len(capture.glue_outer) > 1:
             raise LabelingError(f"{len(capture.glue_outer)} q=1 products; only the rotary "
                                 f"table's is expected")
+        if any(r.a is None for r in capture.records):
+            raise LabelingError("the capture's operands were released before labeling")
         by_weight = {self.w(l, x): (l, x) for l in range(1, self.L + 1) for x in LINEARS}
         slots: dict[str, tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = {}
         spec_by_name = {s.name: s for s in self.products}
 
-        def fill(name, a, b, p, rec=None, member=None, transposed=False):
-            if call_slots is not None and rec is not None:
-                call_slots.setdefault(rec.index, []).append((member, name, transposed))
+        def fill(name, a, b, p, rec, member=None):
+            if call_slots is not None:
+                call_slots.setdefault(rec.index, []).append((member, name, False))
             if name in slots:
                 raise LabelingError(f"slot {name} filled twice")
             spec = spec_by_name.get(name)
@@ -332,44 +347,43 @@ class DecoderComputation(DeclaredComputation):
                 raise LabelingError(f"{name}: shapes {got} != declared {want}")
             slots[name] = (a, b, p)
 
-        def members(role, l, rec, transpose_out=False):
+        def members(role, l, rec):
             if rec.batch != self.n_s * self.n_h:
                 raise LabelingError(f"L{l}.{role}: a batch of {rec.batch}, expected "
                                     f"{self.n_s * self.n_h}")
-            for i in range(rec.batch):
+            for i, (a, b, p) in enumerate(rec.members()):
                 s_, h = divmod(i, self.n_h)
-                a, b, p = rec.a[i], rec.b[i], rec.out[i]
-                if transpose_out:  # K̃'s gradient Q̃ᵀ·δS: the leaf is (δSᵀ·Q̃)
-                    a, b, p = rec.b[i].transpose(0, 1), rec.a[i].transpose(0, 1), \
-                        rec.out[i].transpose(0, 1).contiguous()
-                fill(f"L{l}.{role}[{s_},{h}]", a, b, p, rec, i, transpose_out)
+                fill(f"L{l}.{role}[{s_},{h}]", a, b, p, rec, i)
+
+        def weight_of(info) -> str | None:
+            return info.param_name or info.param_copy
+
+        def storage(t):
+            return t.untyped_storage().data_ptr()
 
         fwd = [r for r in capture.records if r.phase == "forward"]
         bwd = [r for r in capture.records if r.phase == "backward"]
-        if any(r.a is None for r in capture.records):
-            raise LabelingError("the capture's operands were released before labeling")
-        s_rec: dict[int, object] = {}
-        o_rec: dict[int, object] = {}
+        s_rec: dict[int, Any] = {}
+        o_rec: dict[int, Any] = {}
         head_in = None
         layer = None
-        pending = []
+        seen = 0
         for rec in fwd:
-            name = rec.b_info.param_name
+            name = weight_of(rec.b_info)
             if rec.batch is not None:
                 if layer is None:
                     raise LabelingError(f"batched record #{rec.index} before any layer")
-                pending.append(rec)
-                if len(pending) == 1:
+                seen += 1
+                if seen == 1:
                     s_rec[layer] = rec
-                elif len(pending) == 2:
+                elif seen == 2:
                     o_rec[layer] = rec
                 else:
                     raise LabelingError(f"layer {layer}: more than two forward batched products")
-                continue
-            if name in by_weight:
+            elif name in by_weight:
                 l, x = by_weight[name]
                 if x == "q":
-                    layer, pending = l, []
+                    layer, seen = l, 0
                 fill(f"L{l}.Y_{x}", rec.a, rec.b, rec.out, rec)
             elif name == self.w_out and rec.out.shape[-1] == self.n_v:
                 head_in = rec.a
@@ -382,46 +396,53 @@ class DecoderComputation(DeclaredComputation):
             members("S", l, s_rec[l])
             members("O", l, o_rec[l])
 
-        def storage(t):
-            return t.untyped_storage().data_ptr()
-
-        s_a = {storage(s_rec[l].a): l for l in s_rec}
-        s_b = {storage(s_rec[l].b): l for l in s_rec}
-        o_a = {storage(o_rec[l].a): l for l in o_rec}
-        o_b = {storage(o_rec[l].b): l for l in o_rec}
-        grad_owner = {prm.grad.untyped_storage().data_ptr(): n
-                      for n, prm in model.named_parameters() if prm.grad is not None}
-        for rec in bwd:
-            name = rec.b_info.param_name
-            if rec.batch is not None:
-                a_st, b_st = storage(rec.a), storage(rec.b)
-                if b_st in o_b:
-                    members("dA", o_b[b_st], rec)
-                elif a_st in o_a:
-                    members("dV", o_a[a_st], rec)
-                elif b_st in s_b:
-                    members("dQ", s_b[b_st], rec)
-                elif a_st in s_a:
-                    members("dK", s_a[a_st], rec, transpose_out=True)
-                else:
-                    raise LabelingError(f"backward batched record #{rec.index} matches no slot")
+        # which weight's gradient each record's output became (its own storage, or the
+        # fp32 copy autocast makes of it)
+        grad_of: dict[int, str] = {}
+        for pname, prm in model.named_parameters():
+            if prm.grad is None:
                 continue
+            i = capture.output_copied_by(prm.grad)
+            if i is None:
+                i = capture.produced_by(prm.grad)
+            if i is not None:
+                grad_of[i] = pname
+        o_a = {storage(o_rec[l].a): l for l in o_rec}
+        s_a = {storage(s_rec[l].a): l for l in s_rec}
+        pair_a: dict[int, tuple[str, int]] = {}  # storage of δO or δS -> (role, layer)
+        deferred = []
+        for rec in bwd:
+            if rec.batch is not None:
+                if storage(rec.a) in o_a:
+                    l = o_a[storage(rec.a)]
+                    members("dV", l, rec)
+                    pair_a[storage(rec.b)] = ("dA", l)
+                elif storage(rec.b) in s_a:
+                    l = s_a[storage(rec.b)]
+                    members("dK", l, rec)
+                    pair_a[storage(rec.a)] = ("dQ", l)
+                else:
+                    deferred.append(rec)
+                continue
+            name = weight_of(rec.b_info)
             if name in by_weight:
                 l, x = by_weight[name]
                 fill(f"L{l}.dX_{x}", rec.a, rec.b, rec.out, rec)
             elif name == self.w_out:
                 fill(self.head_name("dF", 0), rec.a, rec.b, rec.out, rec)
+            elif grad_of.get(rec.index) in by_weight:
+                l, x = by_weight[grad_of[rec.index]]
+                fill(f"L{l}.G_{x}", rec.a, rec.b, rec.out, rec)
+            elif head_in is not None and storage(rec.b) == storage(head_in) and \
+                    tuple(rec.out.shape) == (self.n_v, self.d):
+                fill(self.head_name("G", 0), rec.a, rec.b, rec.out, rec)
             else:
-                owner = grad_owner.get(rec.out_info.storage_ptr)
-                if owner in by_weight and capture.is_output_of(
-                        model.get_parameter(owner).grad, rec):
-                    l, x = by_weight[owner]
-                    fill(f"L{l}.G_{x}", rec.a, rec.b, rec.out, rec)
-                elif head_in is not None and storage(rec.b) == storage(head_in) and \
-                        rec.out.shape == (self.n_v, self.d):
-                    fill(self.head_name("G", 0), rec.a, rec.b, rec.out, rec)
-                else:
-                    raise LabelingError(f"backward record #{rec.index} matches no slot")
+                raise LabelingError(f"backward record #{rec.index} matches no slot")
+        for rec in deferred:
+            role = pair_a.get(storage(rec.a))
+            if role is None:
+                raise LabelingError(f"backward batched record #{rec.index} matches no slot")
+            members(role[0], role[1], rec)
         missing = [s.name for s in self.products if s.name not in slots]
         if missing:
             raise LabelingError(f"{len(missing)} slots never filled, e.g. {missing[:3]}")

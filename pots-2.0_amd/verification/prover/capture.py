@@ -29,9 +29,10 @@ learn which call fills which product slot. Usage:
   phase raises :class:`PhaseError`.
 - ``aten._to_copy`` inside a phase is noted as a :class:`CopyRecord`. A copy of a parameter
   (autocast's bf16 weight, say) is kept alive until :meth:`MatmulCapture.release_operands`,
-  and operands that alias it name the parameter in :attr:`OperandInfo.param_copy`; other
-  copies are known only through a weak reference to their storage, so no activation outlives
-  the pass because of the capture.
+  and operands that alias it name the parameter in :attr:`OperandInfo.param_copy`. A copy of
+  a record's whole output (autocast's fp32 ``W.grad`` of a bf16 weight-gradient product) is
+  known through :meth:`MatmulCapture.output_copied_by`. Copies are held only through weak
+  references to their storages, so no activation outlives the pass because of the capture.
 
 **How it is built.** Ops are classified once per overload (:func:`_classify`, cached), and the
 dispatch hook looks the verdict up and calls its handler. What the capture knows about a
@@ -172,8 +173,9 @@ class OperandInfo:
 @dataclass
 class _Origin:
     storage: StorageWeakRef
-    producer: int | None = None
-    copy_of: str | None = None
+    producer: int | None = None       # the record whose output this storage is
+    copy_of: str | None = None        # the parameter this storage is a copy of
+    copy_of_output: int | None = None  # the record whose whole output this storage copies
 
 
 class _Ledger:
@@ -206,6 +208,18 @@ class _Ledger:
     def copies_param(self, out: torch.Tensor, param: str) -> None:
         st = out.untyped_storage()
         self._origins[st.data_ptr()] = _Origin(StorageWeakRef(st), copy_of=param)
+
+    def copies_output(self, out: torch.Tensor, index: int) -> None:
+        st = out.untyped_storage()
+        self._origins[st.data_ptr()] = _Origin(StorageWeakRef(st), copy_of_output=index)
+
+    def produced_by(self, t: torch.Tensor) -> int | None:
+        """The index of the record whose output storage ``t`` views, else None."""
+        return self._ledger.describe(t).producer_index
+
+    def output_copied_by(self, t: torch.Tensor) -> int | None:
+        o = self._origin(t.untyped_storage())
+        return None if o is None else o.copy_of_output
 
     def param_of(self, t: torch.Tensor) -> str | None:
         st = t.untyped_storage()
@@ -297,6 +311,7 @@ class MatmulCapture(TorchDispatchMode):
         self._param_copy_tensors: list[torch.Tensor] = []  # kept alive until release
         self._current: str | None = None
         self._calls = 0
+        self._made: dict[int, MatmulRecord] = {}  # record index -> record, glue included
         self._handlers: dict[_Kind, Callable[..., Any]] = {
             _Kind.PRODUCT: self._on_product,
             _Kind.OTHER_OVERLOAD: self._on_other_overload,
@@ -358,6 +373,11 @@ class MatmulCapture(TorchDispatchMode):
             if note.param is not None:
                 self._ledger.copies_param(out, note.param)
                 self._param_copy_tensors.append(out)
+            elif note.src_info.producer_index is not None:
+                made = self._made[note.src_info.producer_index]
+                if src.numel() == made.out.numel() and \
+                        src.storage_offset() == made.out.storage_offset():
+                    self._ledger.copies_output(out, made.index)
             self.copies.append(note)
         return out
 
@@ -384,6 +404,7 @@ class MatmulCapture(TorchDispatchMode):
                            a_info=d(a), b_info=d(b), out_info=d(out), bias=term,
                            alpha=float(alpha), beta=float(beta))
         rec.out_storage = self._ledger.made_by(out, index)
+        self._made[index] = rec
         for role in ("a", "b", "out", "bias"):
             t = getattr(rec, role)
             if t is not None:
@@ -429,6 +450,15 @@ class MatmulCapture(TorchDispatchMode):
         a weight gradient's product as ``W.grad``); storages compare by identity."""
         return rec.out_storage is not None and \
             rec.out_storage == StorageWeakRef(t.untyped_storage())
+
+    def produced_by(self, t: torch.Tensor) -> int | None:
+        """The index of the record whose output storage ``t`` views, else None."""
+        return self._ledger.describe(t).producer_index
+
+    def output_copied_by(self, t: torch.Tensor) -> int | None:
+        """The index of the record whose whole output ``t``'s storage is a ``_to_copy`` of
+        (as autocast's fp32 ``W.grad`` copies a bf16 weight-gradient product), else None."""
+        return self._ledger.output_copied_by(t)
 
     @property
     def n_products(self) -> int:

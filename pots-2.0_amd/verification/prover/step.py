@@ -128,8 +128,9 @@ def prove_step(c: DeclaredComputation, model: torch.nn.Module, w_t: Mapping[str,
 
         def held(t: torch.Tensor) -> torch.Tensor:
             # An operand that views a parameter (a linear's W.t(), an input gradient's W)
-            # would see the SGD step: it is served from the committed W_t leaf instead.
-            name = cap.param_of(t)
+            # would see the SGD step: it is served from the committed W_t leaf instead. A
+            # copy of a parameter (autocast's bf16 weight) is a tensor of its own.
+            name = cap.param_names.get(t.untyped_storage().data_ptr())
             if name is not None and name in w_t_leaves:
                 return w_t_leaves[name].as_strided(t.shape, t.stride(), t.storage_offset())
             return t.detach()

@@ -114,13 +114,15 @@ def test_stored_mlp_step_verifies_from_disk(lib, tmp_path):
         assert started_verifier(c, step.leaves(), k=2).verify_step(1, store) is None
 
 
-def _decoder_prove(seed=0, qkv_bias=True, n_kv=2, perturb=None):
+def _decoder_prove(seed=0, qkv_bias=True, n_kv=2, perturb=None, dtype=torch.float32,
+                   c=None):
     from setup.records import Record
     from verification.computation.instances.decoder import DecoderComputation
     from verification.computation.interface import snapshot_weights
     from verification.prover.step import commit, prove_step
-    c = DecoderComputation(L=2, d=128, d_f=256, n_h=4, n_kv=n_kv, n_v=320, n_s=2, n=64,
-                           qkv_bias=qkv_bias, compute_dtype=torch.float32)
+    if c is None:
+        c = DecoderComputation(L=2, d=128, d_f=256, n_h=4, n_kv=n_kv, n_v=320, n_s=2, n=64,
+                               qkv_bias=qkv_bias, compute_dtype=dtype)
     torch.manual_seed(seed)
     with torch.device("cuda"):
         model = c.build_model()
@@ -145,18 +147,23 @@ def _decoder_oracle_root(c, leaves):
     return O.merkle_root(hashes)
 
 
-@pytest.mark.parametrize("qkv_bias,n_kv", [(True, 2), (False, 4)])
-def test_real_decoder_step_commits_and_verifies(lib, qkv_bias, n_kv):
-    """A transformers Qwen2/Llama training step proved on the GPU: the products stay in HBM,
-    the device commit equals the CPU oracle's root, and the verifier accepts the step from the
-    committed leaves alone (the decoder replay serves check 5's operands and check 6b's glue
-    gradients) through the check-level API and the device step alike; the replay's operands
-    are the prover's, bit for bit."""
+@pytest.mark.parametrize("qkv_bias,n_kv,dtype", [(True, 2, torch.float32),
+                                                  (False, 4, torch.float32),
+                                                  (True, 2, torch.bfloat16),
+                                                  (False, 4, torch.bfloat16)])
+def test_real_decoder_step_commits_and_verifies(lib, qkv_bias, n_kv, dtype):
+    """A transformers Qwen2/Llama training step proved on the GPU, in fp32 or in bf16 under
+    autocast over fp32 masters: the products stay in HBM, the device commit equals the CPU
+    oracle's root, and the verifier accepts the step from the committed leaves alone (the
+    decoder replay serves check 5's operands and check 6b's glue gradients) through the
+    check-level API and the device step alike; the replay's operands are the prover's, bit for
+    bit."""
     from conftest import started_verifier
     from verification.computation.instances.decoder import DecoderReplay
     from verification.transcript.store import InMemoryStore
     from verification.verifier.step import DeviceStepVerifier
-    c, step, tree = _decoder_prove(seed=7, qkv_bias=qkv_bias, n_kv=n_kv)
+    c, step, tree = _decoder_prove(seed=7, qkv_bias=qkv_bias, n_kv=n_kv, dtype=dtype)
+    assert all(p.dtype == dtype for p in step.products)
     assert step.capture["on_device"]
     assert tree.root == _decoder_oracle_root(c, step.leaves())
     v = started_verifier(c, step.leaves(), k=2)
@@ -257,3 +264,67 @@ def test_c1_real_smollm2_step_proves_commits_and_verifies(lib):
     v = started_verifier(c, step.leaves(), k=1)
     assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
     assert len(v.stats[1].products) == c.M and v.stats[1].max_normalized() <= 8.0
+
+
+def test_bf16_decoder_at_c4_dimensions_proves_and_verifies_from_its_leaves(lib):
+    """Two layers of the Qwen2-1.5B shape (d 1536, 12/2 heads of 128, MLP 8960, vocab 151,936,
+    4 x 2048 tokens) in bf16 under autocast over fp32 masters: the device commit equals the
+    CPU oracle's root over every leaf; the replay of the committed leaves serves every
+    product's operands equal to the prover's bit for bit; the honest step accepts with no
+    prover operands trusted (checks 6a and 6b included); and a product forged together with
+    the forged operand it was made from is caught at check 5 by the replay, though the
+    prover's operands would pass it."""
+    import sys
+    from conftest import started_verifier
+    from test_fullsize_gpu import _oracle_digests
+    from verification.commitment.leaves import commit_leaves_device
+    from verification.computation.instances.decoder import DecoderComputation, DecoderReplay
+    from verification.prover.synthetic import CapturedReplay
+    from verification.transcript.store import InMemoryStore
+
+    def say(msg):
+        print(f"[c4-bf16] {msg}", file=sys.__stderr__, flush=True)
+
+    c = DecoderComputation(L=2, d=1536, d_f=8960, n_h=12, n_kv=2, n_v=151936, n_s=4, n=2048,
+                           d_h=128, tied=True, qkv_bias=True, compute_dtype=torch.bfloat16)
+    c, step, tree = _decoder_prove(seed=11, c=c)
+    say(f"proved and committed: {c.M} products")
+    assert all(p.dtype == torch.bfloat16 and p.is_cuda for p in step.products)
+    assert tree.root == O.merkle_root(_oracle_digests(c, step.leaves()))
+    say("root equals the oracle's")
+    replay = DecoderReplay(c, step.leaves())
+    for spec in c.products:
+        got, want = replay.operands(spec.m), step.operands[spec.m]
+        assert all(x.dtype == torch.bfloat16 for x in got), spec.name
+        assert all(torch.equal(x, y) for x, y in zip(got, want)), spec.name
+    say("replay operands equal the prover's")
+    del replay
+    v = started_verifier(c, step.leaves(), k=4)
+    assert not v.trust_prover_operands
+    assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
+    assert not v.stats[1].operands_from_prover and len(v.stats[1].products) == c.M
+    assert {t.check_id for t in v.stats[1].tensors} == {"6a", "6b"}
+    say("honest step accepted")
+    v.close()
+    spec = next(s for s in c.products if s.name == "L2.Y_gate")
+    a, b = step.operands[spec.m]
+    a_forged = a.clone()
+    # one row of the gate's input shifted by 16: at these widths a bf16 product's band unit
+    # (ε_in = 2⁻⁸ on ‖P‖_F ≈ 7e3) hides a shift of 0.25, so the forgery must be larger
+    a_forged[7] += 16.0
+    leaves = step.leaves()
+    leaves[c.product_index(spec.m)] = torch.mm(a_forged, b.contiguous())
+    forged_tree = commit_leaves_device(c, leaves)
+    c.use_operands(CapturedReplay({**step.operands, spec.m: (a_forged, b)}))
+    v = started_verifier(c, leaves, k=4)
+    assert v.trust_prover_operands
+    assert v.verify_step(1, InMemoryStore(leaves, forged_tree)) is None
+    v.close()
+    c.use_operands(None)
+    v = started_verifier(c, leaves, k=4)
+    assert not v.trust_prover_operands
+    rej = v.verify_step(1, InMemoryStore(leaves, forged_tree))
+    v.close()
+    assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
+    assert rej.detail.startswith(f"P_{spec.m} (L2.Y_gate)")
+    say("forged operand caught at check 5")

@@ -246,12 +246,12 @@ def test_replay_operands_reproduce_every_product():
         assert torch.equal(torch.mm(a, b), step.products[spec.m - 1]), spec.name
 
 
-def _decoder_step(qkv_bias=True, n_kv=2):
+def _decoder_step(qkv_bias=True, n_kv=2, dtype=torch.float32):
     from setup.records import Record
     from verification.computation.instances.decoder import DecoderComputation
     from verification.computation.interface import snapshot_weights
     c = DecoderComputation(L=2, d=64, d_f=128, n_h=4, n_kv=n_kv, n_v=160, n_s=2, n=16,
-                           qkv_bias=qkv_bias, compute_dtype=torch.float32)
+                           qkv_bias=qkv_bias, compute_dtype=dtype)
     torch.manual_seed(0)
     model = c.build_model()
     w0 = snapshot_weights(c, model)
@@ -263,29 +263,67 @@ def _decoder_step(qkv_bias=True, n_kv=2):
     return c, w0, prove_step(c, model, w0, records, keep_operands=True)
 
 
-@pytest.mark.parametrize("qkv_bias,n_kv", [(True, 2), (False, 4)])
-def test_decoder_labeling_fills_every_slot_with_its_own_product(qkv_bias, n_kv):
-    """A transformers Qwen2 (biased q/k/v, grouped KV heads) or Llama step under the capture:
-    every declared slot is filled, and each product equals its captured operands' product
-    (bit for bit where the op itself computed it, 1e-5 for the transposed dK leaves and the
-    biased forward linears)."""
-    c, w0, step = _decoder_step(qkv_bias, n_kv)
+DECODERS = [(True, 2, torch.float32), (False, 4, torch.float32), (True, 2, torch.bfloat16),
+            (False, 4, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("qkv_bias,n_kv,dtype", DECODERS)
+def test_decoder_labeling_fills_every_slot_with_its_own_product(qkv_bias, n_kv, dtype):
+    """A transformers Qwen2 (biased q/k/v, grouped KV heads) or Llama step under the capture,
+    in fp32 or in bf16 under autocast over fp32 masters: every declared slot is filled with a
+    product of the compute dtype, and each product equals its captured operands' product
+    (bit for bit for a plain fp32 product; the biased linears within rounding, bf16 products
+    within one bf16 rounding of the fp32 sum)."""
+    c, w0, step = _decoder_step(qkv_bias, n_kv, dtype)
     assert len(step.products) == c.M and step.capture["outer_calls"] == 1
+    assert all(w.dtype == torch.float32 for w in step.w_next.values())
     for spec in c.products:
         a, b = step.operands[spec.m]
         p = step.products[spec.m - 1]
+        assert p.dtype == dtype and a.dtype == dtype and b.dtype == dtype, spec.name
         assert (tuple(a.shape), tuple(b.shape)) == (spec.a_shape, spec.b_shape), spec.name
-        q = torch.mm(a, b)
+        q = torch.mm(a.float(), b.float())
         if spec.bias is not None:
-            q = q + w0[spec.bias]
-        if ".dK[" in spec.name or spec.bias is not None:
+            q = q + w0[spec.bias].to(dtype).float()
+        if dtype == torch.bfloat16:
+            scale = torch.mm(a.float().abs(), b.float().abs()) + 1e-30
+            assert ((q - p.float()).abs() <= 2.0**-8 * scale + 1e-6).all(), spec.name
+        elif spec.bias is not None:
             assert torch.allclose(q, p, rtol=1e-5, atol=1e-6), spec.name
         else:
             assert torch.equal(q, p), spec.name
     # a linear weight's update is its committed weight gradient's SGD step
     name = c.w(1, "up")
     g = step.products[c.product_index(c.linear_weights[name][0]) - c.n_s - c.n_w]
-    assert torch.allclose(step.w_next[name], w0[name] - c.eta * g, rtol=0, atol=1e-7)
+    assert torch.allclose(step.w_next[name], w0[name] - c.eta * g.float(), rtol=0, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decoder_batched_products_never_take_a_transposed_right_operand(dtype):
+    """Every batched product of a decoder step, forward and backward, receives a contiguous
+    right operand (bf16 batched products with a transposed right operand are kept off this
+    pool's GPUs), and the left operands that are transposed views share storage with another
+    product's left operand (dV with O, dK with dQ)."""
+    from verification.computation.instances.decoder import DecoderComputation
+    from verification.computation.matmul_ops import param_storage_map
+    c = DecoderComputation(L=2, d=64, d_f=128, n_h=4, n_kv=2, n_v=160, n_s=2, n=16,
+                           qkv_bias=True, compute_dtype=dtype)
+    torch.manual_seed(0)
+    model = c.build_model()
+    from setup.records import Record
+    ids = torch.randint(0, c.n_v, (c.n,), dtype=torch.int32)
+    records = [Record(ids, torch.roll(ids, -1), torch.ones(c.n, dtype=torch.int32))] * c.n_s
+    cap = MatmulCapture(param_names=param_storage_map(model))
+    with cap:
+        c.forward_backward(model, records, cap.phase)
+    batched = [r for r in cap.records if r.batch is not None]
+    assert len(batched) == 6 * c.L
+    assert all(r.b.is_contiguous() for r in batched)
+    assert all(r.a.dtype == dtype and r.b.dtype == dtype for r in batched)
+    lefts = {r.a.untyped_storage().data_ptr() for r in batched if r.a.is_contiguous()}
+    views = [r for r in batched if not r.a.is_contiguous()]
+    assert len(views) == 2 * c.L and all(r.a.untyped_storage().data_ptr() in lefts
+                                         for r in views)
 
 
 def test_reference_inventory_literals():
@@ -322,27 +360,34 @@ def test_reference_inventory_literals():
     assert matmul_count_decoder(16, 128, 32) == 393_555
 
 
-def test_decoder_prover_refuses_bf16_compute_over_fp32_masters():
-    """A bf16 decoder would need autocast over fp32 masters on the prover side; rather than
-    commit bf16 weight leaves where fp32 ones are declared, building its model refuses."""
+def test_decoder_bf16_runs_under_autocast_over_fp32_masters():
+    """A bf16 decoder keeps fp32 master weights and computes its logits in bf16 under
+    autocast (reference decoder.py:551-598); the loss itself is fp32."""
     from verification.computation.instances.decoder import DecoderComputation
+    from setup.records import Record
     c = DecoderComputation(L=1, d=16, d_f=32, n_h=2, n_kv=1, n_v=40, n_s=1, n=8,
                            compute_dtype=torch.bfloat16)
-    with pytest.raises(NotImplementedError, match="autocast"):
-        c.build_model()
-    fp32 = DecoderComputation(L=1, d=16, d_f=32, n_h=2, n_kv=1, n_v=40, n_s=1, n=8)
-    model = fp32.build_model()
+    model = c.build_model()
     assert not model.training
     assert all(p.dtype == torch.float32 for p in model.parameters())
+    ids = torch.arange(c.n, dtype=torch.int32)
+    with c.autocast(torch.device("cpu")):
+        logits = model(input_ids=ids[None].long()).logits
+    assert logits.dtype == torch.bfloat16
+    loss = c.loss(model, [Record(ids, ids, torch.ones(c.n, dtype=torch.int32))])
+    assert loss.dtype == torch.float32 and torch.isfinite(loss)
+    fp32 = DecoderComputation(L=1, d=16, d_f=32, n_h=2, n_kv=1, n_v=40, n_s=1, n=8)
+    with fp32.autocast(torch.device("cpu")):
+        assert fp32.build_model()(input_ids=ids[None].long()).logits.dtype == torch.float32
 
 
-@pytest.mark.parametrize("qkv_bias,n_kv", [(True, 2), (False, 4)])
-def test_decoder_replay_rebuilds_the_operands_from_the_leaves(qkv_bias, n_kv):
+@pytest.mark.parametrize("qkv_bias,n_kv,dtype", DECODERS)
+def test_decoder_replay_rebuilds_the_operands_from_the_leaves(qkv_bias, n_kv, dtype):
     """The verifier's replay (the committed leaves only, every product substituted by its
     leaf) gives every product the operands the prover's capture saw, bit for bit, and each
     glue weight (γ, biases, the tied embedding) the gradient SGD stepped with."""
     from verification.computation.instances.decoder import DecoderReplay
-    c, w0, step = _decoder_step(qkv_bias, n_kv)
+    c, w0, step = _decoder_step(qkv_bias, n_kv, dtype)
     leaves = step.leaves()
     replay = DecoderReplay(c, leaves, device="cpu")
     for spec in c.products:
