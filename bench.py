@@ -409,16 +409,16 @@ def prover_leg(widths=(4096, 8192, 8192, 4096), n_s: int = 2048, k: int = 2) -> 
             "verified": True}
 
 
-def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int = 4) -> dict:
+def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 28, k: int = 4) -> dict:
     """A real training step of a Qwen2-1.5B-shaped model, proved, committed and verified on
-    the GPU: transformers' Qwen2ForCausalLM at C4's shapes (``layers`` of the 28 decoder
-    layers, random init, eager attention) runs under the device-resident capture; the products
-    are labeled into the declared computation's canonical slots, SGD steps the weights, every
-    leaf is hashed in HBM, and the device step verifier checks the step with the captured
-    operands. The model runs in fp32: the eager attention's batched products and their
-    backward take transposed right operands, which bf16 batched products must not get on
-    these GPUs. The reference copies each product to pinned host memory as it is made
-    (``_offload``) and hashes on the host; that copy is timed on a sample."""
+    the GPU: transformers' Qwen2ForCausalLM at C4's shapes (all 28 decoder layers, random
+    init, bf16 under autocast over fp32 masters, the build's attention core) runs under the
+    device-resident capture; the products are labeled into the declared computation's
+    canonical slots, SGD steps the weights, every leaf is hashed in HBM, and the device step
+    verifier checks the step with the captured operands; then ``Verifier.verify_step`` checks
+    it again from the committed leaves alone (the decoder replay). The reference copies each
+    product to pinned host memory as it is made (``_offload``) and hashes on the host; that
+    copy is timed on a sample."""
     import torch
 
     from setup.records import Record
@@ -429,7 +429,7 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int 
 
     c = DecoderComputation(L=layers, d=1536, d_f=8960, n_h=12, n_kv=2, n_v=151936, n_s=batch,
                            n=seq, d_h=128, tied=True, qkv_bias=True,
-                           compute_dtype=torch.float32)
+                           compute_dtype=torch.bfloat16)
     torch.manual_seed(0)
     with torch.device("cuda"):
         model = c.build_model()
@@ -522,8 +522,8 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 14, k: int 
         f"verify {verify_ms:.1f} ms (accepted); the host copy it avoids runs at "
         f"{d2h_gbps:.1f} GB/s ({product_bytes / d2h_gbps / 1e9:.2f} s for the products)")
     return {"model": f"Qwen2-1.5B-shaped, {layers} of 28 layers (transformers "
-                     f"Qwen2ForCausalLM, random init, fp32, eager attention), {batch}x{seq} "
-                     "tokens",
+                     f"Qwen2ForCausalLM, random init, bf16 autocast over fp32 masters), "
+                     f"{batch}x{seq} tokens",
             "k": k, "products": c.M, "calls": summary["calls"],
             "product_bytes": product_bytes, "leaf_bytes": leaf_bytes,
             "training_step_ms": round(plain_ms, 1), "prove_step_ms": round(prove_ms, 1),
@@ -611,8 +611,9 @@ def main() -> int:
                     help="also run the device-resident prover and report parts.prover: 'mlp' "
                          "proves an MLP step (capture, labeling, SGD), commits it in HBM and "
                          "verifies it with the replay; 'qwen2' proves a Qwen2-1.5B-shaped "
-                         "training step (transformers, random init, fp32, 14 of 28 layers, "
-                         "4x2048 tokens), commits it in HBM and verifies it")
+                         "training step (transformers, random init, bf16 autocast over fp32 "
+                         "masters, 28 layers, 4x2048 tokens), commits it in HBM and verifies "
+                         "it, with the prover's operands and then from the leaves alone")
     ap.add_argument("--check-level", action=argparse.BooleanOptionalAction, default=True,
                     help="time Verifier.verify_step (the reference's check-level entry point) "
                          "on the same transcript, beside the step")

@@ -179,16 +179,24 @@ int pots_merkle_tree_async(size_t n, const uint8_t *d_leaves, uint8_t *d_nodes, 
 #define POTS_DT_F32 0
 #define POTS_DT_BF16 1
 
-/* One checked product P = A·B (+ 1·biasᵀ). All pointers are device memory; A, B and P are
+/* One checked product P = A·B (+ 1·biasᵀ). All pointers are device memory; B and P are
  * row-major with the given row strides (elements). `bias` is fp32 [w] already rounded to the
  * operand format as the reference serves it (checks.py:439), or NULL. `m` is the product's
- * 1-based index, the challenge label. */
+ * 1-based index, the challenge label.
+ *
+ * A is row-major with row stride lda when a_trans is 0. When a_trans is 1, A is the transpose
+ * of a row-major X [q, n] at `a` with row stride lda, and another product of the same plan
+ * must have that X as its row-major A (its twin: same pointer and lda, shape [q, n]); the
+ * plan then reads X once for both (the twin pass). A transposed A is taken only in bf16, with
+ * k <= 4, q a multiple of 16, n a multiple of 128, `a` and lda·2 multiples of 16 bytes;
+ * anything else is POTS_E_ARG. No counterpart in the reference, which multiplies whatever
+ * layout torch hands it. */
 typedef struct {
   const void *a, *b, *p;
   const float *bias;
   uint64_t lda, ldb, ldp;
   uint32_t n, q, w, m;
-  uint32_t a_dtype, b_dtype, p_dtype, pad;
+  uint32_t a_dtype, b_dtype, p_dtype, a_trans;
 } pots_fv_product;
 
 /* A Freivalds plan over n products with k challenge vectors each: operand layout, column
@@ -232,6 +240,11 @@ int pots_fv_plan_copy_challenges(const void *plan, float *d_out, void *stream);
 
 /* Bytes of A, B and P the plan reads (each once). */
 uint64_t pots_fv_plan_bytes(const void *plan);
+
+/* The pairs of twin products the plan reads through the twin pass (a_trans products and their
+ * row-major twins): each pair's shared operand is read once. No counterpart in the
+ * reference. */
+uint32_t pots_fv_plan_twins(const void *plan);
 
 void pots_fv_plan_destroy(void *plan);
 

@@ -56,6 +56,7 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef float v4f32 __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 enum : uint32_t { DT_F32 = 0, DT_BF16 = 1 };
 
@@ -265,11 +266,11 @@ __device__ __forceinline__ void compute_stage(const StageRegs<NJG>& r, v4f32 acc
 // here, not one per element. Chunk starts are whole pipeline stages (multiples of 64 columns)
 // and the weights 256-byte aligned, so the vector loads are aligned.
 template <uint32_t CHUNK>
-__device__ __forceinline__ void stage_weights(const PassJob& J, uint32_t c0, uint32_t c1,
-                                              float* s_u, float* s_w) {
+__device__ __forceinline__ void stage_weights(uint64_t u, uint64_t w, uint32_t c0, uint32_t c1,
+                                              uint32_t chunk_cols, float* s_u, float* s_w) {
   constexpr uint32_t NV = (CHUNK + 1023) / 1024;  // 4-column groups per thread
-  const float* up = reinterpret_cast<const float*>(J.u) + c0;
-  const float* wp = reinterpret_cast<const float*>(J.w) + c0;
+  const float* up = reinterpret_cast<const float*>(u) + c0;
+  const float* wp = reinterpret_cast<const float*>(w) + c0;
   const uint32_t n = c1 - c0;
   v4f32 ua[NV], wa[NV];
 #pragma unroll
@@ -289,7 +290,7 @@ __device__ __forceinline__ void stage_weights(const PassJob& J, uint32_t c0, uin
 #pragma unroll
   for (uint32_t v = 0; v < NV; v++) {
     const uint32_t t = 4 * (threadIdx.x + 256 * v);
-    if (t < J.chunk_cols) {
+    if (t < chunk_cols) {
       *reinterpret_cast<v4f32*>(s_u + t) = ua[v];
       *reinterpret_cast<v4f32*>(s_w + t) = wa[v];
     }
@@ -345,7 +346,7 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   StageRegs<NJG> ra;
   if (active && nfull > 0) load_full<XT, NJG>(ra, L, c0);
   if (WEIGHTED) {
-    if (sums) stage_weights<G::CHUNK>(J, c0, c1, s_u, s_w);
+    if (sums) stage_weights<G::CHUNK>(J.u, J.w, c0, c1, J.chunk_cols, s_u, s_w);
     __syncthreads();
   }
   if (!active) return;
@@ -450,31 +451,21 @@ __device__ __forceinline__ uint32_t xcd_id() {
   return (uint32_t)__builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) % kQueues;
 }
 
-// The row pass over n_tiles tiles. With a block per tile (queue null), block b takes tile b
-// (mapping blocks XCD by XCD, as the fused chunk kernel does, cut the B pass's reads 1.08x ->
-// 1.02x but made it slower: with no stealing, XCDs given equal tile counts of unequal tiles
-// finish apart).
-// With a smaller grid, the pass holds a bounded share of each CU (a block holds 4 waves and
-// 32 KiB of LDS) so that a kernel on another stream (the leaf hasher) keeps the rest, and the
+// The tiles of a launch, from the tile queues when the grid is limited, else one block per
+// tile. With a smaller grid, the pass holds a bounded share of each CU (a block holds 4 waves
+// and its LDS) so that a kernel on another stream (the leaf hasher) keeps the rest, and the
 // blocks take tiles from the queues: counters (zero at launch) that each block's first thread
 // advances by one per tile, a tile ahead of the one the block works on, moving to the next
 // queue when one runs out. A block that lands on a CU shared with more hashing waves then
 // takes fewer tiles, where a fixed split would leave it the last to finish. Every thread of a
 // block reads the same tile index, so all of its waves leave the loop together once every
 // queue is empty; each counter value below its range hands out one tile, so every tile is
-// taken exactly once.
-template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
-__global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
-                                                const uint32_t* __restrict__ blk_job,
-                                                uint32_t k, uint32_t n_tiles,
-                                                uint32_t* __restrict__ queue) {
-  using G = Geo<XT>;
-  __shared__ __align__(16) float s_u[WEIGHTED ? G::CHUNK : 4];
-  __shared__ __align__(16) float s_w[WEIGHTED ? G::CHUNK : 4];
-  __shared__ uint32_t s_tile;
+// taken exactly once. `body(t)` is called by every thread of the block with the same t.
+template <typename F>
+__device__ __forceinline__ void tile_loop(uint32_t n_tiles, uint32_t* __restrict__ queue,
+                                          uint32_t* s_tile, F&& body) {
   if (queue == nullptr) {
-    if (blockIdx.x < n_tiles) row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, blockIdx.x,
-                                                                 s_u, s_w);
+    if (blockIdx.x < n_tiles) body(blockIdx.x);
     return;
   }
   // Thread 0's state: the queues tried so far, from this XCD's own.
@@ -489,9 +480,9 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
     }
     return n_tiles;
   };
-  if (threadIdx.x == 0) s_tile = take();
+  if (threadIdx.x == 0) *s_tile = take();
   __syncthreads();
-  uint32_t b = s_tile;
+  uint32_t b = *s_tile;
   while (b < n_tiles) {
     // The next tile's counter value is taken now; its latency passes under this tile. (An
     // increment that wraps only at 2^32 − 1 is an add of one; written as atomicInc, the
@@ -499,8 +490,8 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
     uint32_t next = 0;
     if (threadIdx.x == 0 && qi < kQueues)
       next = atomicInc(queue + (home + qi) % kQueues, 0xFFFFFFFFu);
-    row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, b, s_u, s_w);
-    __syncthreads();  // every wave is done with this tile's weights and has read s_tile
+    body(b);
+    __syncthreads();  // every wave is done with this tile's LDS and has read s_tile
     if (threadIdx.x == 0) {
       uint32_t nb = n_tiles;
       if (qi < kQueues) {
@@ -513,15 +504,283 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
           nb = take();
         }
       }
-      s_tile = nb;
+      *s_tile = nb;
     }
     __syncthreads();
-    b = s_tile;
+    b = *s_tile;
   }
+}
+
+// The row pass over n_tiles tiles. With a block per tile (queue null), block b takes tile b
+// (mapping blocks XCD by XCD, as the fused chunk kernel does, cut the B pass's reads 1.08x ->
+// 1.02x but made it slower: with no stealing, XCDs given equal tile counts of unequal tiles
+// finish apart). With a smaller grid the blocks take tiles from the queues (tile_loop).
+template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
+__global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
+                                                const uint32_t* __restrict__ blk_job,
+                                                uint32_t k, uint32_t n_tiles,
+                                                uint32_t* __restrict__ queue) {
+  using G = Geo<XT>;
+  __shared__ __align__(16) float s_u[WEIGHTED ? G::CHUNK : 4];
+  __shared__ __align__(16) float s_w[WEIGHTED ? G::CHUNK : 4];
+  __shared__ uint32_t s_tile;
+  tile_loop(n_tiles, queue, &s_tile, [&](uint32_t b) {
+    row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, b, s_u, s_w);
+  });
 }
 
 __global__ void queue_reset(uint32_t* q) {
   if (threadIdx.x < kQueues) q[threadIdx.x] = 0u;
+}
+
+// ---- twin pass: one read of an operand shared as A and Aᵀ ------------------------------
+//
+// Two products of a training step often share their A operand as X and Xᵀ: the attention
+// probabilities are O's A and, transposed, dV's; δS is dQ's A and dK's; a linear layer's
+// output gradient is its input gradient's A and its weight gradient's; the logits' gradient is
+// dF's A and G_head's. The twin pass reads X once for both products: X·V₁ row by row (the A
+// pass of m₁, A₁ = X) and Xᵀ·V₂ column by column (the A pass of m₂, A₂ = Xᵀ), with the sums
+// of both: Σ|x|u₁ and Σx²w₁ per row of X; Σ|x|u₂ per column, and Σx²w₂ over X.
+//
+// A tile is kTwinRows rows by kTwinCols columns of X (bf16, rows a multiple of 16 and columns
+// of 128). Wave w takes the tile's 128-column strips w, w + 4, … and walks each strip down the
+// tile's rows, 16 rows (one stage of four 32-column K-steps) at a time:
+//   - m₁: X·V₁ on the matrix cores as in the row pass (V₁ of the strip loaded once), Σ|x|u₁
+//     and Σx²w₁ on the VALU; a stage's row values are added into the wave's own LDS
+//     accumulator, and the four waves' accumulators are summed in wave order when the tile
+//     ends, so no address has two writers and the result does not depend on timing.
+//   - m₂: each K-step's 16 × 32 block is written to the wave's LDS slab and read back four
+//     rows of one column per lane, the A operand of Xᵀ·V₂ (a 16 × 16 × 16 MFMA whose K is the
+//     16 rows). |Xᵀ|·u₂ runs on the matrix cores too, into the same accumulators: u₂'s three
+//     exact bf16 terms sit in slots 12..14 of m₂'s packed operand (k ≤ 4 leaves them free),
+//     each MFMA seeing only its own slots. The strip's column results accumulate down all
+//     the tile's rows in registers and are written when the strip ends, one partial per
+//     column and tile row.
+//   - Σx²w₂: each lane's row sum of squares (products of bf16 values are exact in fp32) times
+//     w₂ of that row, summed per lane in fp64; the tile's total is m₂'s only nonzero Σx²w
+//     partial of the tile (the finish adds partials in fp64, so where the total sits does
+//     not matter).
+constexpr uint32_t kTwinRows = 512;
+constexpr uint32_t kTwinCols = 1024;
+constexpr uint32_t kTwinStrip = 128;  // columns per strip: one stage of four K-steps
+constexpr uint32_t kSlabRow = 36;     // bf16 per slab row: 32 columns and 4 of padding, so
+                                      // the four row groups a read touches sit 8 banks apart
+
+struct TwinJob {
+  uint64_t x, ld;             // X[0][0] (bf16), row stride in elements
+  uint64_t v1, u1, w1;        // m₁: packed B₁·R₁ over X's columns, |B₁|·1, B₁²·1 (fp32)
+  uint64_t v2, w2;            // m₂: packed B₂·R₂ with |B₂|·1's terms, over X's rows; B₂²·1
+  uint64_t dot1, abs1, sq1;   // m₁ partials: [n_ct][rows_pad1] (dot: × k)
+  uint64_t dot2, abs2, sq2;   // m₂ partials: [n_rt][rows_pad2], rows of m₂ = columns of X
+  uint64_t tile_first;        // prefix of tiles over the twins before this one
+  uint32_t rows, cols;
+  uint32_t rows_pad1, rows_pad2;
+  uint32_t n_rt, n_ct;        // tile rows and tile columns
+  uint32_t pad0, pad1;
+};
+static_assert(sizeof(TwinJob) == 144, "TwinJob layout");
+
+struct TwinStage {
+  u32x4 x[KU];  // 16 rows × 128 columns: lane (g, i) row i, columns 32u + 8g .. + 7
+  v2u32 v2;     // m₂'s packed operand: rows 4g .. 4g + 3 of the group, slot i
+  float w2;     // B₂²·1 of row i
+};
+
+__device__ __forceinline__ void twin_load(TwinStage& st, const TwinJob& J, uint32_t rr,
+                                          uint32_t cs, uint32_t g, uint32_t i) {
+  const char* xrow = reinterpret_cast<const char*>(J.x) + ((uint64_t)(rr + i) * J.ld + cs + 8 * g) * 2;
+#pragma unroll
+  for (uint32_t u = 0; u < KU; u++) st.x[u] = gload<u32x4>(xrow + 64 * u);
+  // K-group (rr + 4g) / 8 of 8 rows, slot i, the half of it holding rows 4g .. 4g + 3
+  const uint64_t e = ((uint64_t)((rr + 4 * g) >> 3) * 16 + i) * 8 + 4 * (g & 1);
+  st.v2 = gload<v2u32>(reinterpret_cast<const uint16_t*>(J.v2) + e);
+  st.w2 = gload<float>(reinterpret_cast<const float*>(J.w2) + rr + i);
+}
+
+__device__ __forceinline__ void twin_stage(const TwinStage& st, const u32x4 (&v1)[KU],
+                                           v4f32 (&acc2)[2 * KU], double& u2sum,
+                                           float* acc_w, uint16_t* slab, const float* s_u,
+                                           const float* s_w, uint32_t row0, uint32_t off,
+                                           uint32_t k, uint32_t lane, uint32_t g, uint32_t i) {
+  // m₁: X·V₁ for the stage's 16 rows, and the two sums of row i over the lane's columns
+  v4f32 acc1 = {0.f, 0.f, 0.f, 0.f};
+  float s1 = 0.f, s2 = 0.f, q2 = 0.f;
+#pragma unroll
+  for (uint32_t u = 0; u < KU; u++) {
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+          __builtin_bit_cast(v4i16, v2u32{st.x[u][2 * h], st.x[u][2 * h + 1]}),
+          __builtin_bit_cast(v4i16, v2u32{v1[u][2 * h], v1[u][2 * h + 1]}), acc1, 0, 0, 0);
+    const uint32_t o = off + 32 * u;
+    const v4f32 ua = *reinterpret_cast<const v4f32*>(s_u + o);
+    const v4f32 ub = *reinterpret_cast<const v4f32*>(s_u + o + 4);
+    const v4f32 wa = *reinterpret_cast<const v4f32*>(s_w + o);
+    const v4f32 wb = *reinterpret_cast<const v4f32*>(s_w + o + 4);
+    const float uc[8] = {ua[0], ua[1], ua[2], ua[3], ub[0], ub[1], ub[2], ub[3]};
+    const float wc[8] = {wa[0], wa[1], wa[2], wa[3], wb[0], wb[1], wb[2], wb[3]};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float xl = bf_lo(st.x[u][e]), xh = bf_hi(st.x[u][e]);
+      s1 = fmaf(fabsf(xl), uc[2 * e], s1);
+      s1 = fmaf(fabsf(xh), uc[2 * e + 1], s1);
+      s2 = fmaf(xl * xl, wc[2 * e], s2);
+      s2 = fmaf(xh * xh, wc[2 * e + 1], s2);
+      // (a bit_cast straight from the vector element compiled to the first element every
+      // time; through a scalar it does not)
+      const uint32_t wv = st.x[u][e];
+      const bf16x2 b = __builtin_bit_cast(bf16x2, wv);
+      q2 = __builtin_amdgcn_fdot2_f32_bf16(b, b, q2, false);
+    }
+  }
+  u2sum = fma((double)q2, (double)st.w2, u2sum);
+
+  // m₂: Xᵀ·V₂ and |Xᵀ|·u₂ through the slab, one K-step at a time
+  const v2u32 zero = {0u, 0u};
+  const v4i16 bv = __builtin_bit_cast(v4i16, i < 12 ? st.v2 : zero);
+  const v4i16 bu = __builtin_bit_cast(v4i16, i >= 12 ? st.v2 : zero);
+#pragma unroll
+  for (uint32_t u = 0; u < KU; u++) {
+    uint16_t* wr = slab + i * kSlabRow + 8 * g;  // row i, columns 8g .. 8g + 7
+    *reinterpret_cast<v2u32*>(wr) = v2u32{st.x[u][0], st.x[u][1]};
+    *reinterpret_cast<v2u32*>(wr + 4) = v2u32{st.x[u][2], st.x[u][3]};
+#pragma unroll
+    for (uint32_t cb = 0; cb < 2; cb++) {
+      const uint16_t* rd = slab + (4 * g) * kSlabRow + 16 * cb + i;  // rows 4g .., column
+      const uint32_t lo = (uint32_t)rd[0] | (uint32_t)rd[kSlabRow] << 16;
+      const uint32_t hi = (uint32_t)rd[2 * kSlabRow] | (uint32_t)rd[3 * kSlabRow] << 16;
+      v4f32& a = acc2[2 * u + cb];
+      a = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4i16, v2u32{lo, hi}),
+                                                    bv, a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+          __builtin_bit_cast(v4i16, v2u32{lo & 0x7FFF7FFFu, hi & 0x7FFF7FFFu}), bu, a, 0, 0,
+          0);
+    }
+  }
+
+  // m₁: the stage's row values into the wave's accumulator. Lane (g, i) holds rows 4g + e and
+  // slot i; challenge j's three terms are slots 3j .. 3j + 2.
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float v0 = acc1[e];
+    const float va = __shfl(v0, (int)lane + 1);
+    const float vb = __shfl(v0, (int)lane + 2);
+    if (i % 3 == 0 && i / 3 < k) acc_w[(row0 + 4 * g + e) * 6 + i / 3] += (v0 + va) + vb;
+  }
+  s1 += __shfl_xor(s1, 16);
+  s1 += __shfl_xor(s1, 32);
+  s2 += __shfl_xor(s2, 16);
+  s2 += __shfl_xor(s2, 32);
+  if (g == 0) {
+    acc_w[(row0 + i) * 6 + 4] += s1;
+    acc_w[(row0 + i) * 6 + 5] += s2;
+  }
+}
+
+__device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
+                                          const uint32_t* __restrict__ tile_job, uint32_t k,
+                                          uint32_t tidx, float* s_u, float* s_w, float* s_acc,
+                                          uint16_t* s_slab, double* s_red) {
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63, g = lane >> 4, i = lane & 15;
+  const TwinJob J = jobs[tile_job[tidx]];
+  const uint32_t local = tidx - (uint32_t)J.tile_first;
+  const uint32_t rt = local % J.n_rt, ct = local / J.n_rt;
+  const uint32_t r0 = rt * kTwinRows, r1 = min(r0 + kTwinRows, J.rows);
+  const uint32_t c0 = ct * kTwinCols, c1 = min(c0 + kTwinCols, J.cols);
+  const uint32_t nrg = (r1 - r0) / 16, nstrip = (c1 - c0) / kTwinStrip;
+  float* acc_w = s_acc + wave * kTwinRows * 6;
+  uint16_t* slab = s_slab + wave * 16 * kSlabRow;
+  stage_weights<kTwinCols>(J.u1, J.w1, c0, c1, kTwinCols, s_u, s_w);
+  for (uint32_t t = lane; t < kTwinRows * 6; t += 64) acc_w[t] = 0.f;
+  __syncthreads();
+
+  double u2sum = 0.0;
+  for (uint32_t s = wave; s < nstrip; s += 4) {
+    const uint32_t cs = c0 + s * kTwinStrip;
+    // V₁ of the strip's four K-steps: the same for every row group
+    u32x4 v1[KU];
+#pragma unroll
+    for (uint32_t u = 0; u < KU; u++)
+      v1[u] = gload<u32x4>(reinterpret_cast<const char*>(J.v1) +
+                           ((uint64_t)((cs + 32 * u) / 8 + g) * 16 + i) * 16);
+    v4f32 acc2[2 * KU];
+#pragma unroll
+    for (uint32_t q = 0; q < 2 * KU; q++) acc2[q] = v4f32{0.f, 0.f, 0.f, 0.f};
+    const uint32_t off = cs - c0 + 8 * g;
+    // Two stages in flight: the next row group's loads go out before this one is computed
+    // (past the last group they reread it, so every load is unconditional).
+    TwinStage sa, sb;
+    twin_load(sa, J, r0, cs, g, i);
+    for (uint32_t rg = 0; rg < nrg; rg += 2) {
+      twin_load(sb, J, r0 + 16 * min(rg + 1, nrg - 1), cs, g, i);
+      twin_stage(sa, v1, acc2, u2sum, acc_w, slab, s_u, s_w, 16 * rg, off, k, lane, g, i);
+      twin_load(sa, J, r0 + 16 * min(rg + 2, nrg - 1), cs, g, i);
+      if (rg + 1 < nrg)
+        twin_stage(sb, v1, acc2, u2sum, acc_w, slab, s_u, s_w, 16 * (rg + 1), off, k, lane,
+                   g, i);
+    }
+    // m₂'s partials of the strip's 128 columns: lane (g, i) of block q holds columns
+    // 16q + 4g + e and slot i.
+    float* dot2 = reinterpret_cast<float*>(J.dot2);
+    float* abs2 = reinterpret_cast<float*>(J.abs2);
+    const uint64_t cbase = (uint64_t)rt * J.rows_pad2;
+#pragma unroll
+    for (uint32_t q = 0; q < 2 * KU; q++) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float v0 = acc2[q][e];
+        const float va = __shfl(v0, (int)lane + 1);
+        const float vb = __shfl(v0, (int)lane + 2);
+        const float t = (v0 + va) + vb;
+        const uint32_t col = cs + 16 * q + 4 * g + e;
+        if (i % 3 == 0 && i / 3 < k) gstore<float>(dot2 + (cbase + col) * k + i / 3, t);
+        if (i == 12) gstore<float>(abs2 + cbase + col, t);
+      }
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) u2sum += __shfl_xor(u2sum, o);
+  if (lane == 0) s_red[wave] = u2sum;
+  __syncthreads();
+  // m₁'s partials of the tile's rows: the four waves' accumulators in wave order
+  float* dot1 = reinterpret_cast<float*>(J.dot1);
+  float* abs1 = reinterpret_cast<float*>(J.abs1);
+  double* sq1 = reinterpret_cast<double*>(J.sq1);
+  const uint64_t rbase = (uint64_t)ct * J.rows_pad1;
+  for (uint32_t row = threadIdx.x; row < r1 - r0; row += blockDim.x) {
+    float d[6];
+#pragma unroll
+    for (int t = 0; t < 6; t++) d[t] = s_acc[row * 6 + t];
+#pragma unroll
+    for (uint32_t w = 1; w < 4; w++)
+#pragma unroll
+      for (int t = 0; t < 6; t++) d[t] += s_acc[(w * kTwinRows + row) * 6 + t];
+    for (uint32_t j = 0; j < k; j++) gstore<float>(dot1 + (rbase + r0 + row) * k + j, d[j]);
+    gstore<float>(abs1 + rbase + r0 + row, d[4]);
+    gstore<double>(sq1 + rbase + r0 + row, (double)d[5]);
+  }
+  // m₂'s Σx²w₂ partials of the tile's columns: the tile's total at its first column
+  const double tot = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
+  double* sq2 = reinterpret_cast<double*>(J.sq2);
+  for (uint32_t c = c0 + threadIdx.x; c < c1; c += blockDim.x)
+    gstore<double>(sq2 + (uint64_t)rt * J.rows_pad2 + c, c == c0 ? tot : 0.0);
+}
+
+// The tiles of every twin, from the tile queues when the grid is limited (as the row pass
+// takes them), else one block per tile.
+__global__ __launch_bounds__(256) void twin_pass(const TwinJob* __restrict__ jobs,
+                                                 const uint32_t* __restrict__ tile_job,
+                                                 uint32_t k, uint32_t n_tiles,
+                                                 uint32_t* __restrict__ queue) {
+  __shared__ __align__(16) float s_u[kTwinCols];
+  __shared__ __align__(16) float s_w[kTwinCols];
+  __shared__ __align__(16) float s_acc[4 * kTwinRows * 6];
+  __shared__ __align__(16) uint16_t s_slab[4 * 16 * kSlabRow];
+  __shared__ double s_red[4];
+  __shared__ uint32_t s_tile;
+  tile_loop(n_tiles, queue, &s_tile, [&](uint32_t t) {
+    twin_tile(jobs, tile_job, k, t, s_u, s_w, s_acc, s_slab, s_red);
+  });
 }
 
 // ---- B-pass reduction: B·R, |B|·1, B²·1 per row of B, packed for the A pass -------------
@@ -533,8 +792,10 @@ struct RedJob {
   uint64_t group_first;      // prefix of (8-row groups x k) over the jobs before it
   uint32_t rows, rows_pad;   // q and its padding
   uint32_t n_chunks, a_dt;   // the A pass's dtype decides the packing
+  uint32_t u_slots, pad;     // 1: also pack b1's three bf16 terms into slots 12..14 (the
+                             // second product of a twin, whose |A|·b1 runs on the matrix cores)
 };
-static_assert(sizeof(RedJob) == 72, "RedJob layout");
+static_assert(sizeof(RedJob) == 80, "RedJob layout");
 
 __global__ __launch_bounds__(256) void reduce_b(const RedJob* __restrict__ jobs, uint32_t n_jobs,
                                                 uint64_t n_threads, uint32_t k) {
@@ -586,6 +847,7 @@ __global__ __launch_bounds__(256) void reduce_b(const RedJob* __restrict__ jobs,
     const double* psq = reinterpret_cast<const double*>(J.psq);
     float* u = reinterpret_cast<float*>(J.u);
     float* w = reinterpret_cast<float*>(J.w);
+    float ua[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // rows past the matrix: zero
 #pragma unroll
     for (int e = 0; e < 8; e++) {
       const uint32_t row = 8 * grp + e;
@@ -597,6 +859,19 @@ __global__ __launch_bounds__(256) void reduce_b(const RedJob* __restrict__ jobs,
       }
       gstore<float>(u + row, (float)a);
       gstore<float>(w + row, (float)q);
+      ua[e] = (float)a;
+    }
+    if (J.u_slots) {
+      uint16_t pl[3][8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) split_bf16x3(ua[e], pl[0][e], pl[1][e], pl[2][e]);
+      uint16_t* dst = reinterpret_cast<uint16_t*>(J.vout) + ((uint64_t)grp * 16 + 12) * 8;
+#pragma unroll
+      for (int p = 0; p < 3; p++)
+        gstore<u32x4>(dst + 8 * p, u32x4{pl[p][0] | (uint32_t)pl[p][1] << 16,
+                                         pl[p][2] | (uint32_t)pl[p][3] << 16,
+                                         pl[p][4] | (uint32_t)pl[p][5] << 16,
+                                         pl[p][6] | (uint32_t)pl[p][7] << 16});
     }
   }
 }
@@ -958,6 +1233,9 @@ struct FvPlan {
   float* d_br = nullptr;      // bᵀR_j per product, [n][k]
   double* d_recs = nullptr;   // slice records, [n_slices][4 + k]
   std::vector<PassLaunch> pass_b, pass_ap;  // B pass; then A and P passes
+  TwinJob* d_twins = nullptr;     // the twin pass: one job per pair of twins
+  uint32_t* d_twin_tile = nullptr;  // tile -> twin job
+  uint32_t n_twins = 0, n_twin_tiles = 0;
   bool need_b3 = false, need_f4 = false;
   uint64_t bytes = 0;  // algorithmic bytes: A, B, P read once
   uint64_t r_floats = 0;
@@ -1030,7 +1308,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
       delete P;
       return POTS_E_ARG;
     }
-    if (p.a_dtype > 1 || p.b_dtype > 1 || p.p_dtype > 1) {
+    if (p.a_dtype > 1 || p.b_dtype > 1 || p.p_dtype > 1 || p.a_trans > 1) {
       delete P;
       return POTS_E_ARG;
     }
@@ -1068,6 +1346,44 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   const size_t o_r = place(r_floats * 4);
   const size_t o_rb3 = place(P->need_b3 ? b3_elems * 2 : 16);
   const size_t o_rf4 = place(P->need_f4 ? f4_floats * 4 : 16);
+
+  // Twins: a product whose A is given transposed takes the row-major product over the same X
+  // as its twin; the pair's A passes become one twin job (twin_pass).
+  std::vector<int64_t> twin_of(n, -1);  // the other product of a pair
+  std::vector<std::pair<uint32_t, uint32_t>> twins;  // (m₁: A = X, m₂: A = Xᵀ)
+  {
+    std::unordered_map<uint64_t, std::vector<uint32_t>> by_x;  // X address -> row-major A's
+    for (size_t i = 0; i < n; i++)
+      if (!prods[i].a_trans && prods[i].a_dtype == DT_BF16)
+        by_x[reinterpret_cast<uint64_t>(prods[i].a)].push_back((uint32_t)i);
+    for (size_t i = 0; i < n; i++) {
+      const pots_fv_product& t = prods[i];
+      if (!t.a_trans) continue;
+      // X is [q, n] for the transposed product: rows of X = its q, columns = its n
+      const uint32_t rows = t.q, cols = t.n;
+      const uint64_t x = reinterpret_cast<uint64_t>(t.a);
+      bool ok = k <= 4 && t.a_dtype == DT_BF16 && rows % 16 == 0 && cols % kTwinStrip == 0 &&
+                x % 16 == 0 && (t.lda * 2) % 16 == 0 && t.lda >= cols;
+      int64_t mate = -1;
+      if (ok) {
+        auto it = by_x.find(x);
+        if (it != by_x.end())
+          for (uint32_t j : it->second)
+            if (twin_of[j] < 0 && prods[j].lda == t.lda && prods[j].n == rows &&
+                prods[j].q == cols) {
+              mate = j;
+              break;
+            }
+      }
+      if (mate < 0) {
+        delete P;
+        return POTS_E_ARG;
+      }
+      twin_of[i] = mate;
+      twin_of[mate] = (int64_t)i;
+      twins.emplace_back((uint32_t)mate, (uint32_t)i);
+    }
+  }
 
   // Jobs: B pass (one per product), then A pass and P pass.
   std::vector<PassJob> jobs;
@@ -1135,6 +1451,10 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     const pots_fv_product& p = prods[i];
     PassJob J = make_job({p.n, p.q, p.a_dtype, reinterpret_cast<uint64_t>(p.a), p.lda});
     jobs.push_back(J);
+    if (twin_of[i] >= 0) {  // its A pass is the twin job's: no row-pass partials
+      J.n_chunks = 0;
+      J.rows_pad = 0;
+    }
     reserve_part(J);
   }
   for (size_t i = 0; i < n; i++) {
@@ -1142,6 +1462,40 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     PassJob J = make_job({p.n, p.w, p.p_dtype, reinterpret_cast<uint64_t>(p.p), p.ldp});
     jobs.push_back(J);
     reserve_part(J);
+  }
+  // Twin partials: m₁'s per tile column [n_ct][rows_pad1], m₂'s per tile row [n_rt][rows_pad2]
+  std::vector<TwinJob> tw(twins.size());
+  uint64_t twin_tiles = 0;
+  for (size_t t = 0; t < twins.size(); t++) {
+    const pots_fv_product& p1 = prods[twins[t].first];
+    TwinJob& T = tw[t];
+    memset(&T, 0, sizeof T);
+    T.x = reinterpret_cast<uint64_t>(p1.a);
+    T.ld = p1.lda;
+    T.rows = p1.n;
+    T.cols = p1.q;
+    T.rows_pad1 = (T.rows + kRowsPerBlock - 1) / kRowsPerBlock * kRowsPerBlock;
+    T.rows_pad2 = (T.cols + kRowsPerBlock - 1) / kRowsPerBlock * kRowsPerBlock;
+    T.n_rt = (T.rows + kTwinRows - 1) / kTwinRows;
+    T.n_ct = (T.cols + kTwinCols - 1) / kTwinCols;
+    T.tile_first = twin_tiles;
+    twin_tiles += (uint64_t)T.n_rt * T.n_ct;
+    auto put = [&](uint64_t chunks, uint64_t rows_pad, uint64_t& dot, uint64_t& ab,
+                   uint64_t& sq) {
+      const uint64_t cr = chunks * rows_pad;
+      dot = part_bytes;
+      part_bytes = align_up(part_bytes + cr * k * 4, 256);
+      ab = part_bytes;
+      part_bytes = align_up(part_bytes + cr * 4, 256);
+      sq = part_bytes;
+      part_bytes = align_up(part_bytes + cr * 8, 256);
+    };
+    put(T.n_ct, T.rows_pad1, T.dot1, T.abs1, T.sq1);  // offsets for now
+    put(T.n_rt, T.rows_pad2, T.dot2, T.abs2, T.sq2);
+  }
+  if (twin_tiles >= 0x7FFFFFFFull) {
+    delete P;
+    return POTS_E_ARG;
   }
   const size_t o_parts = place(part_bytes);
   const size_t o_br = place(br_bytes);
@@ -1169,6 +1523,8 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     adt[i] = prods[i].a_dtype;
     pdt[i] = prods[i].p_dtype;
   }
+  for (size_t i = 0; i < n; i++)
+    if (twin_of[i] >= 0) adt[i] = 2;  // in no row-pass launch: the twin pass takes its A
   std::vector<Pending> lb = group(0, n, 0, 0, bdt.data());
   std::vector<Pending> la = group(n, n, 1, 0, adt.data());
   std::vector<Pending> lp = group(2 * n, n, 0, 1, pdt.data());
@@ -1208,6 +1564,8 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   }
   const size_t o_jobs = place(ordered.size() * sizeof(PassJob));
   const size_t o_blk = place(blk_table.size() * 4);
+  const size_t o_twins = place(tw.size() * sizeof(TwinJob));
+  const size_t o_twin_tile = place(twin_tiles * 4);
   const size_t o_red = place(n * sizeof(RedJob));
   const size_t o_fin = place(n * sizeof(FinJob));
   // Finish: row slices of every product, the biased products, their bias terms, and one
@@ -1261,6 +1619,10 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   P->d_bout = reinterpret_cast<BiasOut*>(P->base + o_bout);
   P->d_br = reinterpret_cast<float*>(P->base + o_bias_r);
   P->d_recs = reinterpret_cast<double*>(P->base + o_recs);
+  P->d_twins = reinterpret_cast<TwinJob*>(P->base + o_twins);
+  P->d_twin_tile = reinterpret_cast<uint32_t*>(P->base + o_twin_tile);
+  P->n_twins = (uint32_t)tw.size();
+  P->n_twin_tiles = (uint32_t)twin_tiles;
 
   // Fill the job pointers now that addresses are known.
   for (size_t oi = 0; oi < ordered.size(); oi++) {
@@ -1302,6 +1664,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     R.rows_pad = J.rows_pad;
     R.n_chunks = J.n_chunks;
     R.a_dt = prods[i].a_dtype;
+    R.u_slots = prods[i].a_trans;  // a twin's second product: |Xᵀ|·b1 on the matrix cores
     gthreads += (uint64_t)(pad32(prods[i].q) / 8) * k;
   }
   P->n_red = (uint32_t)n;
@@ -1328,6 +1691,27 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     F.slice_first = slice_first[i];
     F.n_slices = (uint32_t)((prods[i].n + kSliceRows - 1) / kSliceRows);
   }
+  std::vector<uint32_t> twin_tile(twin_tiles);
+  for (size_t t = 0; t < tw.size(); t++) {
+    TwinJob& T = tw[t];
+    const uint32_t i1 = twins[t].first, i2 = twins[t].second;
+    const uint64_t parts = base + o_parts;
+    T.dot1 += parts, T.abs1 += parts, T.sq1 += parts;
+    T.dot2 += parts, T.abs2 += parts, T.sq2 += parts;
+    T.v1 = base + o_br + off_br[i1];
+    T.u1 = base + o_br + off_b1[i1];
+    T.w1 = base + o_br + off_b2[i1];
+    T.v2 = base + o_br + off_br[i2];
+    T.w2 = base + o_br + off_b2[i2];
+    FinJob& F1 = fin[i1];
+    F1.a_dot = T.dot1, F1.a_abs = T.abs1, F1.a_sq = T.sq1;
+    F1.a_rows_pad = T.rows_pad1, F1.a_chunks = T.n_ct;
+    FinJob& F2 = fin[i2];
+    F2.a_dot = T.dot2, F2.a_abs = T.abs2, F2.a_sq = T.sq2;
+    F2.a_rows_pad = T.rows_pad2, F2.a_chunks = T.n_rt;
+    std::fill(twin_tile.begin() + T.tile_first,
+              twin_tile.begin() + T.tile_first + (uint64_t)T.n_rt * T.n_ct, (uint32_t)t);
+  }
   // Upload the tables.
   auto up = [&](size_t off, const void* src, size_t bytes) -> int {
     if (!bytes) return POTS_E_OK;
@@ -1342,7 +1726,9 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
       (rc = up(o_red, red.data(), n * sizeof(RedJob))) ||
       (rc = up(o_fin, fin.data(), n * sizeof(FinJob))) ||
       (rc = up(o_slices, slices.data(), slices.size() * sizeof(SliceJob))) ||
-      (rc = up(o_biased, biased.data(), biased.size() * 4))) {
+      (rc = up(o_biased, biased.data(), biased.size() * 4)) ||
+      (rc = up(o_twins, tw.data(), tw.size() * sizeof(TwinJob))) ||
+      (rc = up(o_twin_tile, twin_tile.data(), twin_tile.size() * 4))) {
     (void)hipFree(P->base);
     delete P;
     return rc;
@@ -1586,6 +1972,16 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
         if ((L.weighted != 0) == (stage == 3) &&
             (rc = run_pass(P, L, stage == 3 ? 3 : 4, s)) != POTS_E_OK)
           return rc;
+      if (stage == 3 && P->n_twin_tiles) {  // the twins' A passes, after the others
+        const uint32_t g = P->max_grid[3];
+        const bool queued = g != 0 && g < P->n_twin_tiles;
+        uint32_t* q = P->d_queue + (size_t)kQueues * 3;
+        if (queued) hipLaunchKernelGGL(queue_reset, dim3(1), dim3(kQueues), 0, s, q);
+        hipLaunchKernelGGL(twin_pass, dim3(queued ? g : P->n_twin_tiles), dim3(256), 0, s,
+                           P->d_twins, P->d_twin_tile, P->k, P->n_twin_tiles,
+                           queued ? q : nullptr);
+        POTS_HIP(hipGetLastError());
+      }
       return POTS_E_OK;
     case 4:  // the P pass, then the fused products' records
       if ((rc = run_stage(P, POTS_FV_STAGE_P_PASS, d_key, d_rows, s)) != POTS_E_OK) return rc;
@@ -1651,6 +2047,10 @@ extern "C" int pots_fv_plan_copy_challenges(const void* plan, float* d_out, void
 
 extern "C" uint64_t pots_fv_plan_bytes(const void* plan) {
   return plan ? static_cast<const FvPlan*>(plan)->bytes : 0;
+}
+
+extern "C" uint32_t pots_fv_plan_twins(const void* plan) {
+  return plan ? static_cast<const FvPlan*>(plan)->n_twins : 0;
 }
 
 extern "C" void pots_fv_plan_destroy(void* plan) {

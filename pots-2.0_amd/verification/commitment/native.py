@@ -126,6 +126,7 @@ class Native:
             "pots_fv_plan_copy_challenges": ([_vp, _vp, _vp], _int),
             "pots_fv_plan_set_grid": ([_vp, _int, _u32], _int),
             "pots_fv_plan_bytes": ([_vp], _u64),
+            "pots_fv_plan_twins": ([_vp], _u32),
             "pots_fv_plan_destroy": ([_vp], None),
             "pots_verdicts_async": ([_sz, _vp, _u32, _vp, ctypes.c_double, ctypes.c_double,
                                      ctypes.c_double, ctypes.c_double, ctypes.c_double, _u32,
@@ -447,14 +448,14 @@ class _FvProductC(ctypes.Structure):
     _fields_ = [("a", _vp), ("b", _vp), ("p", _vp), ("bias", _vp), ("lda", _u64),
                 ("ldb", _u64), ("ldp", _u64), ("n", _u32), ("q", _u32), ("w", _u32),
                 ("m", _u32), ("a_dtype", _u32), ("b_dtype", _u32), ("p_dtype", _u32),
-                ("pad", _u32)]
+                ("a_trans", _u32)]
 
 
 # _FvProductC as a numpy record, so a plan's table is filled column by column
 _FV_RECORD = np.dtype([("a", "<u8"), ("b", "<u8"), ("p", "<u8"), ("bias", "<u8"),
                        ("lda", "<u8"), ("ldb", "<u8"), ("ldp", "<u8"), ("n", "<u4"),
                        ("q", "<u4"), ("w", "<u4"), ("m", "<u4"), ("a_dtype", "<u4"),
-                       ("b_dtype", "<u4"), ("p_dtype", "<u4"), ("pad", "<u4")])
+                       ("b_dtype", "<u4"), ("p_dtype", "<u4"), ("a_trans", "<u4")])
 assert _FV_RECORD.itemsize == ctypes.sizeof(_FvProductC)
 
 
@@ -496,19 +497,63 @@ def _row_major(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
-def fv_table(products: Sequence[FvProduct]
+def _twin_mates(products: Sequence[FvProduct], k: int | None) -> dict[int, int]:
+    """``{i: j}`` for each product ``i`` whose ``A`` is a transposed view of product ``j``'s
+    row-major ``A`` (the same storage, shape swapped), where the plan's twin pass can read
+    that operand once for both: bf16, ``k ≤ 4``, ``X = A_iᵀ`` with rows a multiple of 16 and
+    columns of 128, 16-byte aligned rows. Each ``j`` is taken once."""
+    if k is None or not 1 <= k <= 4:
+        return {}
+    rowmajor: dict[tuple[int, int, int, int], list[int]] = {}
+    for j, pr in enumerate(products):
+        a = pr.a
+        if a.dim() == 2 and a.dtype == torch.bfloat16 and a.is_cuda and a.stride(1) == 1 \
+                and a.stride(0) >= a.shape[1]:
+            rowmajor.setdefault((a.data_ptr(), a.shape[0], a.shape[1], a.stride(0)),
+                                []).append(j)
+    mates: dict[int, int] = {}
+    taken: set[int] = set()
+    for i, pr in enumerate(products):
+        a = pr.a
+        if not (a.dim() == 2 and a.dtype == torch.bfloat16 and a.is_cuda and
+                a.stride(0) == 1 and a.shape[0] > 1 and a.stride(1) >= a.shape[0]):
+            continue
+        n, q = a.shape            # A = Xᵀ: X is [q, n] with row stride ld
+        ld = a.stride(1)
+        if q % 16 or n % 128 or a.data_ptr() % 16 or (2 * ld) % 16:
+            continue
+        for j in rowmajor.get((a.data_ptr(), q, n, ld), ()):
+            if j not in taken and j != i:
+                mates[i] = j
+                taken.add(j)
+                break
+    return mates
+
+
+def fv_table(products: Sequence[FvProduct], k: int | None = None
              ) -> tuple[np.ndarray, list[torch.Tensor], dict[tuple[int, str], torch.Tensor]]:
     """The product table ``pots_fv_plan_create`` reads (one ``pots_fv_product`` per product),
     the tensors it points into, which must stay alive while a plan built on it runs, and the
     ones of those this call made, by ``(product index, field)``: a product's fp32 bias
     (``"bias"``) and row-major copies of operands in another layout (``"a"``, ``"b"``,
-    ``"p"``)."""
+    ``"p"``).
+
+    With ``k`` given, an ``A`` that is the transpose of another product's row-major ``A`` is
+    passed as it lies (``a_trans``), for the plan's twin pass, where :func:`_twin_mates`
+    allows it; any other transposed operand is copied to row-major."""
     table = []
     keep = []
     made: dict[tuple[int, str], torch.Tensor] = {}
     dts = _DT
+    mates = _twin_mates(products, k)
     for i, pr in enumerate(products):
         a, b, p = pr.a, pr.b, pr.p
+        a_trans = 0
+        if i in mates:  # A = Xᵀ of its twin's X, read by the twin pass where it lies
+            a_trans = 1
+            x = a.t()
+            keep.append(a)
+            a = x
         sa, sb, sp = a.stride(), b.stride(), p.stride()
         ash, bsh, psh = a.shape, b.shape, p.shape
         # The common case (row-major 2-D GPU operands in fp32 or bf16) is read once;
@@ -528,9 +573,11 @@ def fv_table(products: Sequence[FvProduct]
             sa, sb, sp = a.stride(), b.stride(), p.stride()
             ash, bsh, psh = a.shape, b.shape, p.shape
         nn, q = ash
+        if a_trans:
+            nn, q = q, nn  # the product's A is [n, q] = Xᵀ
         q2, w = bsh
         if q2 != q or psh[0] != nn or psh[1] != w:
-            raise ValueError(f"product {i}: shapes {tuple(ash)}·{tuple(bsh)} vs "
+            raise ValueError(f"product {i}: shapes {(nn, q)}·{tuple(bsh)} vs "
                              f"{tuple(psh)}")
         if not 1 <= pr.m < 1 << 32:
             raise ValueError(f"m must be in [1, 2^32), got {pr.m}")
@@ -544,7 +591,7 @@ def fv_table(products: Sequence[FvProduct]
             made[(i, "bias")] = bias
         table.append((a.data_ptr(), b.data_ptr(), p.data_ptr(),
                       bias.data_ptr() if bias is not None else 0, sa[0], sb[0], sp[0],
-                      nn, q, w, pr.m, dts[a.dtype], dts[b.dtype], dts[p.dtype], 0))
+                      nn, q, w, pr.m, dts[a.dtype], dts[b.dtype], dts[p.dtype], a_trans))
         keep += [a, b, p]
     return np.array(table, dtype=_FV_RECORD), keep, made
 
@@ -561,7 +608,7 @@ class FvPlan:
             raise ValueError("a Freivalds plan needs at least one product")
         if not 1 <= k <= 255:
             raise ValueError(f"k must be in [1, 255], got {k}")
-        arr, keep, _ = table if table is not None else fv_table(products)
+        arr, keep, _ = table if table is not None else fv_table(products, k)
         h = ctypes.c_void_p()
         lib._check(lib._lib.pots_fv_plan_create(n, arr.ctypes.data, k, int(bool(guard)),
                                                 ctypes.byref(h)), "pots_fv_plan_create")
@@ -572,6 +619,8 @@ class FvPlan:
         self.widths = [pr.p.shape[1] for pr in products]
         self.device = products[0].a.device
         self.bytes = int(lib._lib.pots_fv_plan_bytes(h))
+        # pairs of products whose shared operand (A and Aᵀ) the twin pass reads once
+        self.twins = int(lib._lib.pots_fv_plan_twins(h))
         self._key = torch.empty(32, dtype=torch.uint8, device=self.device)
 
     def rows(self, h: bytes | torch.Tensor, out: torch.Tensor | None = None,

@@ -83,7 +83,7 @@ class PlanCache:
         (with the addresses of the tensors the table makes, a bias or a row-major copy, left
         out), those tensors' values refreshed; else a new one. The plan holds this step's
         operands until :meth:`release`."""
-        arr, keep, made = native.fv_table(products)
+        arr, keep, made = native.fv_table(products, k)
         keyed = arr.copy()
         for i, f in made:
             keyed[f][i] = 1
