@@ -721,8 +721,13 @@ def main() -> int:
     fv_stages = native.FvPlan.STAGES
     leaf_stages = [(0, "hash.stage"), (native.LeafPlan.FUSED_CHUNKS, "hash.chunks_fused"),
                    (native.LeafPlan.PLAIN_CHUNKS, "hash.chunks"), (2, "hash.levels")]
+    # the Freivalds stages after the challenges; the A pass as its two kernels
+    fv_parts = [(1, "freivalds.b_pass"), (2, "freivalds.reduce"),
+                (native.FvPlan.A_ROWS, "freivalds.a_pass"),
+                (native.FvPlan.TWINS, "freivalds.twin_pass"), (4, "freivalds.p_pass"),
+                (5, "freivalds.rows")]
     names = ([f"freivalds.{fv_stages[0]}"] + [nm for _, nm in leaf_stages] +
-             ["tree"] + [f"freivalds.{s}" for s in fv_stages[1:]] + ["verdicts"])
+             ["tree"] + [nm for _, nm in fv_parts] + ["verdicts"])
 
     def staged(ev):
         i = 0
@@ -738,7 +743,7 @@ def main() -> int:
         lib.merkle_tree_device(v.digests, stream)
         i += 1
         ev[i].record(stream)
-        for st in range(1, len(fv_stages)):
+        for st, _ in fv_parts:
             v.plan.run_stage(st, v.key, v.rows, stream)
             i += 1
             ev[i].record(stream)
@@ -792,13 +797,22 @@ def main() -> int:
     a_bytes = sum(a.nbytes for a, _, _, _, _ in items)
     b_bytes = sum(b.nbytes for _, b, _, _, _ in items)
     p_bytes = sum(p.nbytes for _, _, p, _, _ in items)
+    # Twins: products whose A is another product's A transposed (the same tensor); the twin
+    # pass reads that operand once for both, the row pass the A's of the other products.
+    mates = native._twin_mates([native.FvProduct(a, b, p, m) for a, b, p, _, m in items], k)
+    twin_x_bytes = sum(items[j][0].nbytes for j in mates.values())
+    twinned = set(mates) | set(mates.values())
+    a_row_bytes = sum(items[i][0].nbytes for i in range(len(items)) if i not in twinned)
+    assert v.plan.twins == len(mates), (v.plan.twins, len(mates))
     hp = v.hasher.plan
     fused_p_bytes = hp.fused_bytes - 12 * v.fused  # payload: 0x00 || 11-byte 2-D header off
     kernels = {
         "hash.chunks": ("chunk_kernel", hash_bytes - hp.fused_bytes),
-        "freivalds.a_pass": ("row_pass<bf16, weighted> (A pass)", a_bytes),
+        "freivalds.a_pass": ("row_pass<bf16, weighted> (A pass)", a_row_bytes),
         "freivalds.b_pass": ("row_pass<bf16> (B pass)", b_bytes),
     }
+    if twin_x_bytes:
+        kernels["freivalds.twin_pass"] = ("twin_pass (A pass of twins)", twin_x_bytes)
     if v.fused:
         kernels["hash.chunks_fused"] = ("chunk_kernel_fused", hp.fused_bytes)
     if p_bytes - fused_p_bytes > 0:
@@ -820,8 +834,9 @@ def main() -> int:
                            "peak_tops": round(VALU_PEAK_OPS / 1e12, 2),
                            "frac": round(ops / (stage_ms[nm] * 1e-3) / VALU_PEAK_OPS, 4)}
     # the kernels the step's events bracket
-    in_step = {"hash.chunks_fused" if v.fused else "hash.chunks": chunks_in_step_ms,
-               "freivalds.a_pass": a_in_step_ms}
+    in_step = {"hash.chunks_fused" if v.fused else "hash.chunks": chunks_in_step_ms}
+    if not mates:  # else the step's A-pass events bracket the row pass and the twin pass
+        in_step["freivalds.a_pass"] = a_in_step_ms
     dom_name, dom_bytes = kernels[dom]
     achieved = dom_bytes / (stage_ms[dom] * 1e-3) / 1e9
 
@@ -837,14 +852,15 @@ def main() -> int:
             out["valu_frac"] = valu[kname]["frac"]
         return out
     hash_ms = sum(stage_ms[nm] for _, nm in leaf_stages)
-    fv_ms = sum(stage_ms[f"freivalds.{s}"] for s in native.FvPlan.STAGES)
+    fv_ms = stage_ms[f"freivalds.{fv_stages[0]}"] + sum(stage_ms[nm] for _, nm in fv_parts)
     total = hash_bytes + fv_bytes
     value = total / (ms * 1e-3) / 1e9
     # P of a fused product is read once, by the hashing kernel (its leaf message is the
     # 12-byte 0x00 || header of a 2-D tensor, then P)
-    read_bytes = hash_bytes + a_bytes + b_bytes + p_bytes - fused_p_bytes
+    # and a twin's shared A once, by the twin pass
+    read_bytes = hash_bytes + a_row_bytes + twin_x_bytes + b_bytes + p_bytes - fused_p_bytes
     # the bytes the Freivalds stages read themselves: A, B, and the P the hash did not take
-    fv_read_bytes = a_bytes + b_bytes + p_bytes - fused_p_bytes
+    fv_read_bytes = a_row_bytes + twin_x_bytes + b_bytes + p_bytes - fused_p_bytes
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
@@ -859,6 +875,7 @@ def main() -> int:
                    "p_pass_fused_products": v.fused,
                    "p_pass_fused_leaf_bytes": v.hasher.plan.fused_bytes,
                    "p_pass_fused_records": v.hasher.plan.fused_records,
+                   "twins": len(mates), "twin_shared_bytes": twin_x_bytes,
                    "a_pass_blocks": v.a_grid},
         "parts": {"step_verify_ms": round(ms, 3),
                   "step_frac_hbm": round(value / HBM_PEAK_GBPS, 4),
@@ -867,6 +884,8 @@ def main() -> int:
                   "step_read_gbps": round(read_bytes / (ms * 1e-3) / 1e9, 1),
                   "overlap": {"hashed_at_ms": round(hashed_ms, 3),
                               "rows_at_ms": round(measured_ms, 3),
+                              "a_pass_in_step_ms": round(a_in_step_ms, 3),
+                              "chunks_in_step_ms": round(chunks_in_step_ms, 3),
                               "serial_ms": round(serial_ms, 3)},
                   "hash_ms": round(hash_ms, 3),
                   "hash_gbps": round(hash_bytes / (hash_ms * 1e-3) / 1e9, 1),

@@ -223,6 +223,11 @@ int pots_fv_plan_run(void *plan, const uint8_t *d_key, double *d_rows, void *str
  * products' sums from the records the leaf plan's chunk stage wrote (nothing when unfused). */
 #define POTS_FV_STAGE_P_PASS 6
 #define POTS_FV_STAGE_P_FUSED 7
+/* Stage 3 is two parts as well, which a caller may enqueue apart (each once, both after
+ * stage 2 and before stage 5): the row pass over the A operands of products that have no
+ * twin, and the twin pass over the twins' shared operands (nothing when the plan has none). */
+#define POTS_FV_STAGE_A_ROWS 8
+#define POTS_FV_STAGE_TWINS 9
 int pots_fv_plan_run_stage(void *plan, int stage, const uint8_t *d_key, double *d_rows,
                            void *stream);
 

@@ -540,11 +540,19 @@ __global__ void queue_reset(uint32_t* q) {
 // output gradient is its input gradient's A and its weight gradient's; the logits' gradient is
 // dF's A and G_head's. The twin pass reads X once for both products: X·V₁ row by row (the A
 // pass of m₁, A₁ = X) and Xᵀ·V₂ column by column (the A pass of m₂, A₂ = Xᵀ), with the sums
-// of both: Σ|x|u₁ and Σx²w₁ per row of X; Σ|x|u₂ per column, and Σx²w₂ over X.
+// of both, in one pass over X's tiles:
+//   - the dot products X·V₁ and Xᵀ·V₂ on the matrix cores as in the row pass (V as three exact
+//     bf16 terms);
+//   - ν₂ = |Xᵀ|·u₂ on the matrix cores too, into m₂'s accumulators: u₂'s three exact bf16
+//     terms sit in slots 12..14 of m₂'s packed operand (k ≤ 4 leaves them free);
+//   - ν₁ = |X|·u₁ and Σx²w₁ per row on the VALU, from u₁ and w₁ staged in LDS;
+//   - U₂ = Σ_r w₂(r)·Σ_c x_rc² from each lane's row sums of squares (v_dot2 on bf16 pairs,
+//     exact in fp32). Only U's total enters the row, so each tile writes its total as one
+//     partial and zeros for the rest.
 //
 // A tile is kTwinRows rows by kTwinCols columns of X (bf16, rows a multiple of 16 and columns
-// of 128). Wave w takes the tile's 128-column strips w, w + 4, … and walks each strip down the
-// tile's rows, 16 rows (one stage of four 32-column K-steps) at a time:
+// of 128). Wave w takes the tile's strips (KU K-steps of 32 columns) w, w + 4, … and walks
+// each strip down the tile's rows, 16 rows (one stage) at a time:
 //   - m₁: X·V₁ on the matrix cores as in the row pass (V₁ of the strip loaded once), Σ|x|u₁
 //     and Σx²w₁ on the VALU; a stage's row values are added into the wave's own LDS
 //     accumulator, and the four waves' accumulators are summed in wave order when the tile
@@ -562,7 +570,9 @@ __global__ void queue_reset(uint32_t* q) {
 //     not matter).
 constexpr uint32_t kTwinRows = 512;
 constexpr uint32_t kTwinCols = 1024;
-constexpr uint32_t kTwinStrip = 128;  // columns per strip: one stage of four K-steps
+constexpr uint32_t kTwinStrip = 32 * KU;  // columns per stage: KU K-steps of 32
+constexpr uint32_t kTwinColStep = 128;    // a twin's X has columns in multiples of this
+static_assert(kTwinColStep % kTwinStrip == 0 && kTwinCols % kTwinColStep == 0, "twin tiles");
 constexpr uint32_t kSlabRow = 36;     // bf16 per slab row: 32 columns and 4 of padding, so
                                       // the four row groups a read touches sit 8 banks apart
 
@@ -581,14 +591,15 @@ struct TwinJob {
 static_assert(sizeof(TwinJob) == 144, "TwinJob layout");
 
 struct TwinStage {
-  u32x4 x[KU];  // 16 rows × 128 columns: lane (g, i) row i, columns 32u + 8g .. + 7
+  u32x4 x[KU];   // 16 rows × one strip: lane (g, i) row i, columns 32u + 8g .. + 7
   v2u32 v2;     // m₂'s packed operand: rows 4g .. 4g + 3 of the group, slot i
   float w2;     // B₂²·1 of row i
 };
 
 __device__ __forceinline__ void twin_load(TwinStage& st, const TwinJob& J, uint32_t rr,
                                           uint32_t cs, uint32_t g, uint32_t i) {
-  const char* xrow = reinterpret_cast<const char*>(J.x) + ((uint64_t)(rr + i) * J.ld + cs + 8 * g) * 2;
+  const char* xrow =
+      reinterpret_cast<const char*>(J.x) + ((uint64_t)(rr + i) * J.ld + cs + 8 * g) * 2;
 #pragma unroll
   for (uint32_t u = 0; u < KU; u++) st.x[u] = gload<u32x4>(xrow + 64 * u);
   // K-group (rr + 4g) / 8 of 8 rows, slot i, the half of it holding rows 4g .. 4g + 3
@@ -698,7 +709,7 @@ __device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
   double u2sum = 0.0;
   for (uint32_t s = wave; s < nstrip; s += 4) {
     const uint32_t cs = c0 + s * kTwinStrip;
-    // V₁ of the strip's four K-steps: the same for every row group
+    // V₁ of the strip's K-steps: the same for every row group
     u32x4 v1[KU];
 #pragma unroll
     for (uint32_t u = 0; u < KU; u++)
@@ -720,7 +731,7 @@ __device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
         twin_stage(sb, v1, acc2, u2sum, acc_w, slab, s_u, s_w, 16 * (rg + 1), off, k, lane,
                    g, i);
     }
-    // m₂'s partials of the strip's 128 columns: lane (g, i) of block q holds columns
+    // m₂'s partials of the strip's columns: lane (g, i) of block q holds columns
     // 16q + 4g + e and slot i.
     float* dot2 = reinterpret_cast<float*>(J.dot2);
     float* abs2 = reinterpret_cast<float*>(J.abs2);
@@ -792,8 +803,8 @@ struct RedJob {
   uint64_t group_first;      // prefix of (8-row groups x k) over the jobs before it
   uint32_t rows, rows_pad;   // q and its padding
   uint32_t n_chunks, a_dt;   // the A pass's dtype decides the packing
-  uint32_t u_slots, pad;     // 1: also pack b1's three bf16 terms into slots 12..14 (the
-                             // second product of a twin, whose |A|·b1 runs on the matrix cores)
+  uint32_t u_slots, pad;     // 1: also pack b1's three bf16 terms into slots 12..14 (a
+                             // twin product, whose |A|·b1 runs on the matrix cores)
 };
 static_assert(sizeof(RedJob) == 80, "RedJob layout");
 
@@ -1362,7 +1373,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
       // X is [q, n] for the transposed product: rows of X = its q, columns = its n
       const uint32_t rows = t.q, cols = t.n;
       const uint64_t x = reinterpret_cast<uint64_t>(t.a);
-      bool ok = k <= 4 && t.a_dtype == DT_BF16 && rows % 16 == 0 && cols % kTwinStrip == 0 &&
+      bool ok = k <= 4 && t.a_dtype == DT_BF16 && rows % 16 == 0 && cols % kTwinColStep == 0 &&
                 x % 16 == 0 && (t.lda * 2) % 16 == 0 && t.lda >= cols;
       int64_t mate = -1;
       if (ok) {
@@ -1570,12 +1581,24 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   const size_t o_fin = place(n * sizeof(FinJob));
   // Finish: row slices of every product, the biased products, their bias terms, and one
   // record of 4 + k sums per slice.
+  // A thread of a slice adds each of its rows' partials over the chunks in order, so a
+  // product with many chunks (a wide A, or a twin's many tiles) gets smaller slices.
+  std::vector<uint32_t> a_chunks(n);
+  for (size_t i = 0; i < n; i++) a_chunks[i] = jobs[n + i].n_chunks;
+  for (size_t t = 0; t < twins.size(); t++) {
+    a_chunks[twins[t].first] = tw[t].n_ct;
+    a_chunks[twins[t].second] = tw[t].n_rt;
+  }
   std::vector<SliceJob> slices;
-  std::vector<uint32_t> slice_first(n), biased;
+  std::vector<uint32_t> slice_first(n), slice_rows(n), biased;
   for (size_t i = 0; i < n; i++) {
+    const uint32_t chunks = std::max(a_chunks[i], jobs[2 * n + i].n_chunks);
+    uint32_t sr = kSliceRows;
+    while (sr > 64 && (uint64_t)sr * chunks > 8ull * kSliceRows) sr /= 2;
+    slice_rows[i] = sr;
     slice_first[i] = (uint32_t)slices.size();
-    for (uint32_t r0 = 0; r0 < prods[i].n; r0 += kSliceRows)
-      slices.push_back(SliceJob{(uint32_t)i, r0, std::min(prods[i].n, r0 + kSliceRows), 0});
+    for (uint32_t r0 = 0; r0 < prods[i].n; r0 += sr)
+      slices.push_back(SliceJob{(uint32_t)i, r0, std::min(prods[i].n, r0 + sr), 0});
     if (prods[i].bias) biased.push_back((uint32_t)i);
   }
   const size_t o_slices = place(slices.size() * sizeof(SliceJob));
@@ -1664,7 +1687,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     R.rows_pad = J.rows_pad;
     R.n_chunks = J.n_chunks;
     R.a_dt = prods[i].a_dtype;
-    R.u_slots = prods[i].a_trans;  // a twin's second product: |Xᵀ|·b1 on the matrix cores
+    R.u_slots = twin_of[i] >= 0;  // a twin's |A|·b1 runs on the matrix cores
     gthreads += (uint64_t)(pad32(prods[i].q) / 8) * k;
   }
   P->n_red = (uint32_t)n;
@@ -1689,7 +1712,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     F.p_rows_pad = Pp.rows_pad;
     F.p_chunks = Pp.n_chunks;
     F.slice_first = slice_first[i];
-    F.n_slices = (uint32_t)((prods[i].n + kSliceRows - 1) / kSliceRows);
+    F.n_slices = (uint32_t)((prods[i].n + slice_rows[i] - 1) / slice_rows[i]);
   }
   std::vector<uint32_t> twin_tile(twin_tiles);
   for (size_t t = 0; t < tw.size(); t++) {
@@ -1966,13 +1989,18 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
       POTS_HIP(hipGetLastError());
       return POTS_E_OK;
     }
-    case 3:
+    case 3:  // the A pass: the row pass over the A's that are no twin's, then the twins'
+      if ((rc = run_stage(P, POTS_FV_STAGE_A_ROWS, d_key, d_rows, s)) != POTS_E_OK) return rc;
+      return run_stage(P, POTS_FV_STAGE_TWINS, d_key, d_rows, s);
+    case POTS_FV_STAGE_A_ROWS:
     case POTS_FV_STAGE_P_PASS:
       for (const PassLaunch& L : P->pass_ap)
-        if ((L.weighted != 0) == (stage == 3) &&
-            (rc = run_pass(P, L, stage == 3 ? 3 : 4, s)) != POTS_E_OK)
+        if ((L.weighted != 0) == (stage == POTS_FV_STAGE_A_ROWS) &&
+            (rc = run_pass(P, L, stage == POTS_FV_STAGE_A_ROWS ? 3 : 4, s)) != POTS_E_OK)
           return rc;
-      if (stage == 3 && P->n_twin_tiles) {  // the twins' A passes, after the others
+      return POTS_E_OK;
+    case POTS_FV_STAGE_TWINS:
+      if (P->n_twin_tiles) {
         const uint32_t g = P->max_grid[3];
         const bool queued = g != 0 && g < P->n_twin_tiles;
         uint32_t* q = P->d_queue + (size_t)kQueues * 3;
@@ -2026,7 +2054,7 @@ extern "C" int pots_fv_plan_run(void* plan, const uint8_t* d_key, double* d_rows
 
 extern "C" int pots_fv_plan_run_stage(void* plan, int stage, const uint8_t* d_key,
                                       double* d_rows, void* stream) {
-  if (!plan || !d_key || !d_rows || stage < 0 || stage > POTS_FV_STAGE_P_FUSED) return POTS_E_ARG;
+  if (!plan || !d_key || !d_rows || stage < 0 || stage > POTS_FV_STAGE_TWINS) return POTS_E_ARG;
   return run_stage(static_cast<FvPlan*>(plan), stage, d_key, d_rows,
                    static_cast<hipStream_t>(stream));
 }

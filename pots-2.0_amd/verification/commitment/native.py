@@ -644,6 +644,9 @@ class FvPlan:
     # Stage 4's two parts on their own: the row pass over the unfused products' P, and the
     # fused products' sums from the leaf plan's run records.
     P_PASS, P_FUSED = 6, 7
+    # Stage 3's two parts on their own: the row pass over the A's of products with no twin,
+    # and the twin pass over the twins' shared operands.
+    A_ROWS, TWINS = 8, 9
 
     def run_stage(self, stage: int, key: torch.Tensor, out: torch.Tensor,
                   stream: torch.cuda.Stream | None = None) -> None:

@@ -224,6 +224,27 @@ class DecoderComputation(DeclaredComputation):
     def products(self) -> tuple[ProductSpec, ...]:
         return self._inventory[0]
 
+    @cached_property
+    def operand_twins(self) -> dict[int, int]:
+        """``{m₂: m₁}`` for the products whose ``A`` is, in a training step, the transpose of
+        an earlier product's ``A`` (the same tensor): ``dV`` reads ``O``'s attention
+        probabilities, ``dK`` reads ``dQ``'s ``δS``, a linear's ``G`` reads its ``dX``'s output
+        gradient, and the head's weight gradient reads ``dF``'s logits gradient. The verifier
+        finds such pairs from the operands themselves; this map lets a synthetic transcript
+        lay its operands out the same way."""
+        by_name = {spec.name: spec.m for spec in self.products}
+        out: dict[int, int] = {}
+        members = [(s, h) for s in range(self.n_s) for h in range(self.n_h)]
+        for l in range(1, self.L + 1):
+            for s_, h in members:
+                out[by_name[f"L{l}.dV[{s_},{h}]"]] = by_name[f"L{l}.O[{s_},{h}]"]
+                out[by_name[f"L{l}.dK[{s_},{h}]"]] = by_name[f"L{l}.dQ[{s_},{h}]"]
+            for x in LINEARS:
+                out[by_name[f"L{l}.G_{x}"]] = by_name[f"L{l}.dX_{x}"]
+        for b in range(self.head_blocks):
+            out[by_name[self.head_name("G", b)]] = by_name[self.head_name("dF", b)]
+        return out
+
     def product_class(self, spec: ProductSpec) -> str:
         return self._inventory[1][spec.m - 1]
 

@@ -9,7 +9,9 @@ computed by torch on the GPU with fp32 accumulation and rounded to the compute d
 bf16-autocast step stores it. Attention members of one layer and role are generated and
 multiplied as one stacked batch. A linear weight's ``W_{t+1}`` is ``W_t − η·G`` with ``G`` the
 chain of its committed weight-gradient products (so check 6a holds), a glue weight's moves
-by a random step.
+by a random step. Where the computation names operand twins (``operand_twins``: products
+whose A is, in a real step, the transpose of an earlier product's A), the later product's A
+is that tensor transposed, and its P is the fp32 sum rounded to the compute dtype.
 
 The verifier's work per product (hash the leaf, measure ``A(B·r) − P·r``) depends only on
 shapes and dtypes, so the timings equal a real step's; the values are not a trained model's.
@@ -95,13 +97,34 @@ def synthetic_step(c: DeclaredComputation, *, seed: int = 0, device: str = "cuda
         w_t[name] = w
         leaves.append(w)
     ops: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+    # A product whose A is, in a real step, the transpose of an earlier product's A (dV of O's
+    # attention probabilities, dK of dQ's δS, G of dX's output gradient) gets that very tensor,
+    # transposed, as its A: the verifier's reads depend on which operands alias.
+    twins = getattr(c, "operand_twins", None) or {}
+    firsts: dict[int, torch.Tensor] = {}
+    need = set(twins.values())
     for run in _runs(c):
         s0 = run[0]
         (n, q), (_, w) = s0.a_shape, s0.b_shape
         k = len(run)
+        if s0.m in twins:
+            b = torch.randn(k, q, w, generator=g, device=dev, dtype=torch.float32)
+            b = b.mul_(q ** -0.5).to(dt)
+            for i, spec in enumerate(run):
+                a = firsts.pop(twins[spec.m]).t()
+                # fp32 sums rounded to the compute dtype, as the bf16 products are
+                p = torch.matmul(a.float(), b[i].float())
+                leaves.append(p.to(dt).contiguous())
+                if operands:
+                    ops[spec.m] = (a, b[i])
+            del b
+            continue
         a = torch.randn(k, n, q, generator=g, device=dev, dtype=torch.float32).to(dt)
         b = torch.randn(k, q, w, generator=g, device=dev, dtype=torch.float32)
         b = b.mul_(q ** -0.5).to(dt)
+        for i, spec in enumerate(run):
+            if spec.m in need:
+                firsts[spec.m] = a[i]
         if k == 1:
             acc = torch.matmul(a[0].float(), b[0].float()) if dt == torch.float32 else \
                 torch.matmul(a[0], b[0]).float()

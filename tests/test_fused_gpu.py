@@ -299,13 +299,13 @@ def test_stages_apart_and_grid_limits_equal_one_call(lib):
     fv2.run_stage(0, key, rows2)
     for st in (0, LP.PLAIN_CHUNKS, LP.FUSED_CHUNKS, 2):
         leaf2.run_stage(st, dig2, bad2)
-    for st in (1, 2, FP.P_PASS, 3, FP.P_FUSED, 5):
+    for st in (1, 2, FP.P_PASS, FP.A_ROWS, FP.TWINS, FP.P_FUSED, 5):
         fv2.run_stage(st, key, rows2)
     torch.cuda.synchronize()
     assert torch.equal(dig1, dig2) and int(bad2.item()) == 3
     assert torch.equal(rows1.view(torch.int64), rows2.view(torch.int64))
     with pytest.raises(ValueError):
-        fv2.run_stage(FP.P_FUSED + 1, key, rows2)
+        fv2.run_stage(FP.TWINS + 1, key, rows2)
     with pytest.raises(ValueError):
         fv2.set_grid(2, 4)  # only the row passes take a grid limit
     with pytest.raises(ValueError):

@@ -124,7 +124,7 @@ def test_stage_entry_points_equal_one_call_runs(lib):
     assert torch.equal(d1, d2)
     assert int(bad.item()) == c.n_leaves
     assert torch.equal(r1.view(torch.int64), r2.view(torch.int64))
-    with pytest.raises(ValueError):  # past stage 4's two parts (6, 7)
-        v.plan.run_stage(native.FvPlan.P_FUSED + 1, key, r2)
+    with pytest.raises(ValueError):  # past stage 3's two parts (8, 9)
+        v.plan.run_stage(native.FvPlan.TWINS + 1, key, r2)
     with pytest.raises(ValueError):
         v.hasher.plan.run_stage(-1, d2, bad)

@@ -99,13 +99,24 @@ def test_device_step_verifier_on_a_loaded_step(lib, tmp_path):
     from verification.verifier.step import DeviceStepVerifier
     c, step, tree, disk = _stored(tmp_path, 23)
     res = load_step(disk, c.n_leaves, operand_ms=[s.m for s in c.products])
-    want = DeviceStepVerifier(c, step.leaves, lambda s: step.operands[s.m], k=2).run(tree.root)
-    got = DeviceStepVerifier(c, res.leaves, lambda s: res.operands[s.m], k=2).run(disk.root)
+    dw = DeviceStepVerifier(c, step.leaves, lambda s: step.operands[s.m], k=2)
+    dg = DeviceStepVerifier(c, res.leaves, lambda s: res.operands[s.m], k=2)
+    want, got = dw.run(tree.root), dg.run(disk.root)
     assert got.check is None and want.check is None, got.detail
     assert got.root == want.root == tree.root
     assert (got.first_bad, got.first_fail) == (c.n_leaves, c.M)
-    assert torch.equal(got.rows.cpu(), want.rows.cpu())
     assert torch.equal(got.codes.cpu(), want.codes.cpu())
+    # In memory, a twin's A is a transposed view of its mate's (one read of X measures both);
+    # the loaded operands are files of their own, so the loaded plan measures every twin apart.
+    # Those rows agree to fp32 rounding (the sums run in another order), the rest bit for bit.
+    assert dw.plan.twins > 0 and dg.plan.twins == 0
+    index = {s.m: i for i, s in enumerate(c.products)}
+    twin = sorted(index[m] for pair in c.operand_twins.items() for m in pair)
+    rest = [i for i in range(c.M) if i not in set(twin)]
+    gr, wr = got.rows.cpu(), want.rows.cpu()
+    assert torch.equal(gr[rest], wr[rest])
+    assert torch.allclose(gr[twin, :5], wr[twin, :5], rtol=1e-5, atol=0)
+    assert torch.allclose(gr[twin, 5:], wr[twin, 5:], rtol=1e-3, atol=1e-12)
 
 
 def test_corrupt_leaf_file_rejects_as_malformed(lib, tmp_path):
