@@ -569,14 +569,19 @@ def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 4) -> dict:
         slots.append(v.timings[1])
         assert rej is None, rej
         cache = v.plans
-    hits, builds = cache.hits, cache.builds
+    ov = cache.overlap
+    hits, builds = (ov.hits, ov.builds) if ov is not None else (cache.hits, cache.builds)
+    overlapped = len(v.overlapped) == 1
+    grid_ms = ov.entry.grid_times if ov is not None and ov.entry is not None else {}
     cache.close()
     best = min(range(1, runs), key=lambda i: times[i])
     c.use_operands(None)
-    log(f"[bench] check-level Verifier.verify_step: {times[0]:.1f} ms building its plans, "
-        f"{times[best]:.1f} ms with them cached (best of {runs - 1}; {builds} built, "
-        f"{hits} reused); " + ", ".join(f"{s} {t * 1e3:.1f}" for s, t in slots[best].items()))
-    return {"verify_step_ms": round(times[best], 1),
+    log(f"[bench] check-level Verifier.verify_step ({'overlapped' if overlapped else 'serial'}"
+        f" path): {times[0]:.1f} ms building its plans, {times[best]:.1f} ms with them cached "
+        f"(best of {runs - 1}; {builds} built, {hits} reused); "
+        + ", ".join(f"{s} {t * 1e3:.1f}" for s, t in slots[best].items()))
+    return {"verify_step_ms": round(times[best], 1), "overlapped": overlapped,
+            "a_pass_grid_ms": {str(g): round(t, 2) for g, t in grid_ms.items()},
             "verify_step_first_ms": round(times[0], 1),
             "slots_ms": {s: round(t * 1e3, 2) for s, t in slots[best].items()},
             "first_slots_ms": {s: round(t * 1e3, 2) for s, t in slots[0].items()},
@@ -597,9 +602,9 @@ def main() -> int:
     ap.add_argument("--b-grid", type=int, default=0,
                     help="blocks of the B pass (0: one per tile)")
     ap.add_argument("--a-grid", type=int, default=None,
-                    help="blocks of the A pass (default when fused: one per CU, or one and "
-                         "a half where the hashing is the smaller half; unfused: one per "
-                         "tile); see pots_fv_plan_set_grid")
+                    help="blocks of the A pass (default when fused: the fastest of 1, 1.5 "
+                         "and 2 blocks per CU and one per tile, timed on the step when the "
+                         "plan is built; unfused: one per tile); see pots_fv_plan_set_grid")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="copy this many MiB device to device twice before timing, so a "
                          "counter run sees a plain copy kernel of known size")
@@ -876,7 +881,8 @@ def main() -> int:
                    "p_pass_fused_leaf_bytes": v.hasher.plan.fused_bytes,
                    "p_pass_fused_records": v.hasher.plan.fused_records,
                    "twins": len(mates), "twin_shared_bytes": twin_x_bytes,
-                   "a_pass_blocks": v.a_grid},
+                   "a_pass_blocks": v.a_grid,
+                   "a_pass_grid_ms": {str(g): round(t, 2) for g, t in v.grid_times.items()}},
         "parts": {"step_verify_ms": round(ms, 3),
                   "step_frac_hbm": round(value / HBM_PEAK_GBPS, 4),
                   # bytes the step reads once each: every leaf, and the A and B operands

@@ -337,13 +337,14 @@ class LeafPlan:
     @classmethod
     def from_arrays(cls, lib: Native, hdr_buf: bytes, hdr_off: np.ndarray, hdr_len: np.ndarray,
                     hdr_idx: np.ndarray, payload_ptr: np.ndarray, payload_len: np.ndarray,
-                    kind: np.ndarray, device: torch.device) -> LeafPlan:
+                    kind: np.ndarray, device: torch.device,
+                    fuse: FvPlan | None = None) -> LeafPlan:
         """A plan over ``pots_hash_leaves``'s arguments (every payload in device memory, or
-        empty). It keeps no tensor: the caller keeps the payloads alive and in place while
-        its runs are in flight."""
+        empty), fused with ``fuse`` if given. It keeps no tensor: the caller keeps the
+        payloads alive and in place while its runs are in flight."""
         self = cls.__new__(cls)
         self._create(lib, hdr_buf, hdr_off, hdr_len, hdr_idx, payload_ptr, payload_len, kind,
-                     None, [], device)
+                     fuse, [], device)
         return self
 
     def _create(self, lib: Native, hdr_buf: bytes, hdr_off: np.ndarray, hdr_len: np.ndarray,
@@ -609,6 +610,24 @@ class FvPlan:
         if not 1 <= k <= 255:
             raise ValueError(f"k must be in [1, 255], got {k}")
         arr, keep, _ = table if table is not None else fv_table(products, k)
+        self._create(lib, arr, keep, k, guard, products[0].a.device)
+
+    @classmethod
+    def from_table(cls, lib: Native, table: np.ndarray, keep: list[torch.Tensor], k: int,
+                   guard: bool, device: torch.device) -> FvPlan:
+        """A plan over a product table already made (``fv_table``'s records); ``keep`` holds
+        the tensors it points into while the plan's runs are in flight."""
+        if len(table) == 0:
+            raise ValueError("a Freivalds plan needs at least one product")
+        if not 1 <= k <= 255:
+            raise ValueError(f"k must be in [1, 255], got {k}")
+        self = cls.__new__(cls)
+        self._create(lib, np.ascontiguousarray(table, dtype=_FV_RECORD), keep, k, guard, device)
+        return self
+
+    def _create(self, lib: Native, arr: np.ndarray, keep: list[torch.Tensor], k: int,
+                guard: bool, device: torch.device) -> None:
+        n = len(arr)
         h = ctypes.c_void_p()
         lib._check(lib._lib.pots_fv_plan_create(n, arr.ctypes.data, k, int(bool(guard)),
                                                 ctypes.byref(h)), "pots_fv_plan_create")
@@ -616,8 +635,8 @@ class FvPlan:
         _LIVE_PLANS.add(self)
         self._fused_leaf = None  # weak reference to the leaf plan fused with this one
         self.n, self.k = n, k
-        self.widths = [pr.p.shape[1] for pr in products]
-        self.device = products[0].a.device
+        self.widths = [int(w) for w in arr["w"]]
+        self.device = device
         self.bytes = int(lib._lib.pots_fv_plan_bytes(h))
         # pairs of products whose shared operand (A and Aᵀ) the twin pass reads once
         self.twins = int(lib._lib.pots_fv_plan_twins(h))

@@ -510,6 +510,7 @@ class DecoderReplay(Replay):
             raise ReplayError(f"the replay made {mode.calls} calls for {len(mode.held)} slots; "
                               f"the plan has {plan.n_calls} calls for {c.M}")
         self._held = mode.held
+        self._batched = mode.batched
         self._glue = {}
         for name in c.glue_gradient_weights:
             g = model.get_parameter(name).grad
@@ -528,6 +529,22 @@ class DecoderReplay(Replay):
         if a._version != va or b._version != vb:
             raise ReplayError(f"an operand of {name} changed after its product read it")
         return a, b
+
+    def operand_group(self, ms: Sequence[int],
+                      dtype: torch.dtype | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """The members of one batched product (every member of one attention call, in batch
+        order) served as the call's whole operands, after one version check of each (reference
+        decoder.py:1695-1751 serves the same group, copied); any other ``ms`` takes the
+        default."""
+        c = self.c
+        names = tuple(c.product(m).name for m in ms)
+        got = self._batched.get(names[0]) if names and dtype is None else None
+        if got is None or got[0] != names:
+            return super().operand_group(ms, dtype)
+        _, a, b, va, vb, flipped = got
+        if a._version != va or b._version != vb:
+            raise ReplayError(f"an operand of {names[0]} changed after its product read it")
+        return (b.transpose(1, 2), a.transpose(1, 2)) if flipped else (a, b)
 
     def glue_gradients(self) -> dict[str, torch.Tensor]:
         """Each glue weight's full gradient from the replay's backward."""

@@ -85,7 +85,11 @@ class Replay(abc.ABC):
 
     def operand_group(self, ms: Sequence[int],
                       dtype: torch.dtype | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-        """The operands of products ``ms`` (one shape) stacked ``[len(ms), ·, ·]``."""
+        """The operands of products ``ms`` (one shape pair) stacked ``[len(ms), ·, ·]``, equal
+        to ``torch.stack`` of ``operands(m)`` over ``ms`` (reference interface.py:143-162).
+        Without ``dtype`` an instance may return views of tensors it holds (a batched
+        product's whole operands) instead of copies; the caller must not write to them. This
+        default stacks member by member. An error is the first one ``operands`` raises."""
         pairs = [self.operands(m) for m in ms]
         a = torch.stack([p[0] for p in pairs])
         b = torch.stack([p[1] for p in pairs])
@@ -255,6 +259,29 @@ class DeclaredComputation(abc.ABC):
         import re
         role = spec.weight if spec.weight is not None else spec.name
         return f"{spec.kind.value}:{re.sub(r'[0-9]+', '*', role)}"
+
+    @cached_property
+    def operand_groups(self) -> tuple[tuple[int, ...], ...]:
+        """Product indices (0-based, canonical order) grouped as a step holds their operands:
+        the members of one batched attention product (one layer, one role such as ``L2.dA``,
+        one operand shape pair) form a group, in canonical order, even where two roles of a
+        backward block interleave (``dA[0,0], dV[0,0], dA[0,1], …``); every other product
+        is a group of its own. Groups are listed in order of their first product. A replay
+        serves a group with one :meth:`Replay.operand_group` call."""
+        out: list[list[int]] = []
+        at: dict[tuple[Any, ...], int] = {}
+        for i, s in enumerate(self.products):
+            if s.member is None:
+                out.append([i])
+                continue
+            key = (s.name.split("[", 1)[0], s.kind, s.a_shape, s.b_shape)
+            g = at.get(key)
+            if g is None:
+                at[key] = len(out)
+                out.append([i])
+            else:
+                out[g].append(i)
+        return tuple(tuple(g) for g in out)
 
     @property
     def M(self) -> int:

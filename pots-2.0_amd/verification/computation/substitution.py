@@ -81,6 +81,10 @@ class CommittedProducts(TorchDispatchMode):
         super().__init__()
         self.plan, self.leaf = plan, leaf
         self.held: dict[str, tuple[torch.Tensor, torch.Tensor, int, int]] = {}
+        # each batched call's whole operands, by its first member's slot: (its members' slots
+        # in batch order, A, B, their versions, whether the slots hold the members transposed)
+        self.batched: dict[str, tuple[tuple[str, ...], torch.Tensor, torch.Tensor, int, int,
+                                      bool]] = {}
         self.calls = 0
         self._phase: str | None = None
 
@@ -127,6 +131,12 @@ class CommittedProducts(TorchDispatchMode):
                     self._keep(slot, a[i], b[i])
             if any(p is None for p in members):
                 raise ReplayError(f"call {index}: the plan leaves members unfilled")
+            order = sorted(fills, key=lambda f: f[0])
+            flips = {f[2] for f in order}
+            if len(flips) == 1:
+                wa, wb = a.detach(), b.detach()
+                self.batched[order[0][1]] = (tuple(f[1] for f in order), wa, wb, wa._version,
+                                             wb._version, flips.pop())
             out = torch.stack(members)
         else:
             if len(fills) != 1 or fills[0][0] is not None:

@@ -421,26 +421,41 @@ def _measure_and_judge(c: DeclaredComputation, prods: list[native.FvProduct], ro
             else:
                 plan.close()
     with ctx.timed("5.judge"):
-        f = finish_row_arrays(host, q=qs, n=ns, eps_in=ctx.eps_in, eps_acc=ctx.eps_acc,
-                              guard=ctx.kappa_guard, biased=biased)
-        stop = _first_rejected(f, kappa_max, ctx, bands)
-        if stop != device_first:
-            raise RuntimeError(f"check 5: the device verdicts reject product index "
-                               f"{device_first}, the host closed form {stop}")
-        cols = (f.kappa.tolist(), f.normalized.tolist(), f.p_norm.tolist(), f.nu.tolist(),
-                f.p_abs1.tolist(), f.u.tolist())
-        ctx.stats.products.extend(
-            ProductStat(s.m, s.name, cls, kp, tuple(nz), s.q, pn, nu, pa, uu)
-            for s, cls, kp, nz, pn, nu, pa, uu in zip(specs[:stop], classes, *cols))
-        if stop == n:
-            return None
-        rej = _judge_product(c, specs[stop], f.measure(stop), ctx, bands)
-        if rej is None:
-            raise RuntimeError(f"check 5: product index {stop} fails the array tests but "
-                               f"not the per-product judge")
-        ctx.state.run_rest = [(s, f.measure(i)) for i, s in enumerate(specs[stop + 1:],
-                                                                      start=stop + 1)]
-        return rej
+        return judge_rows(c, host, device_first, kappa_max, ctx, bands)
+
+
+def judge_rows(c: DeclaredComputation, host: np.ndarray, device_first: int,
+               kappa_max: np.ndarray, ctx: StepContext, bands: Bands) -> Rejection | None:
+    """Record and judge the measured rows of the first ``len(host)`` products in canonical
+    order (``kappa_max`` per product); the device verdicts' first rejected index must agree.
+    At a rejection, the products after the failing one go to ``StepState.run_rest``."""
+    n = len(host)
+    specs = c.products[:n]
+    classes, qs, ns, biased = _product_table(c)
+    qs, ns, biased = qs[:n], ns[:n], biased[:n]
+    f = finish_row_arrays(host, q=qs, n=ns, eps_in=ctx.eps_in, eps_acc=ctx.eps_acc,
+                          guard=ctx.kappa_guard, biased=biased)
+    stop = _first_rejected(f, kappa_max, ctx, bands)
+    if stop != device_first:
+        raise RuntimeError(f"check 5: the device verdicts reject product index "
+                           f"{device_first}, the host closed form {stop}")
+    def made(f=f, stop=stop) -> Iterator[ProductStat]:
+        cols = (f.kappa[:stop].tolist(), f.normalized[:stop].tolist(),
+                f.p_norm[:stop].tolist(), f.nu[:stop].tolist(), f.p_abs1[:stop].tolist(),
+                f.u[:stop].tolist())
+        return (ProductStat(s.m, s.name, cls, kp, tuple(nz), s.q, pn, nu, pa, uu)
+                for s, cls, kp, nz, pn, nu, pa, uu in zip(specs[:stop], classes, *cols))
+
+    ctx.stats.add_products(made)  # made into records when first read
+    if stop == n:
+        return None
+    rej = _judge_product(c, specs[stop], f.measure(stop), ctx, bands)
+    if rej is None:
+        raise RuntimeError(f"check 5: product index {stop} fails the array tests but "
+                           f"not the per-product judge")
+    ctx.state.run_rest = [(s, f.measure(i)) for i, s in enumerate(specs[stop + 1:],
+                                                                  start=stop + 1)]
+    return rej
 
 
 @_checked

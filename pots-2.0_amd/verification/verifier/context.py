@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import functools
 import math
-from collections.abc import Callable, Iterator
+from collections.abc import Callable, Iterable, Iterator
 from contextlib import AbstractContextManager, contextmanager, nullcontext
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Any, Literal
@@ -94,12 +94,43 @@ class TensorStat:
     rho_max: float
 
 
-@dataclass
 class StepStats:
-    products: list[ProductStat] = field(default_factory=list)
-    tensors: list[TensorStat] = field(default_factory=list)
-    # check 5 measured the prover's captured operands, not a replay of the committed leaves
-    operands_from_prover: bool = False
+    """One step's statistics: check 5's per product and check 6's per weight, in the order
+    the checks judged them. Check 5 may give its products as columns
+    (:meth:`add_products`), made into :class:`ProductStat` records when first read."""
+
+    def __init__(self, products: list[ProductStat] | None = None,
+                 tensors: list[TensorStat] | None = None,
+                 operands_from_prover: bool = False) -> None:
+        self._products: list[ProductStat] = list(products or [])
+        self._pending: list[Callable[[], Iterable[ProductStat]]] = []
+        self.tensors: list[TensorStat] = list(tensors or [])
+        # check 5 measured the prover's captured operands, not a replay of the committed
+        # leaves
+        self.operands_from_prover = operands_from_prover
+
+    @property
+    def products(self) -> list[ProductStat]:
+        if self._pending:
+            pending, self._pending = self._pending, []
+            for make in pending:
+                self._products.extend(make())
+        return self._products
+
+    def add_products(self, make: Callable[[], Iterable[ProductStat]]) -> None:
+        """Products to append after those recorded so far, made by ``make()`` on first
+        read."""
+        self._pending.append(make)
+
+    def __repr__(self) -> str:
+        return (f"StepStats(products={self.products!r}, tensors={self.tensors!r}, "
+                f"operands_from_prover={self.operands_from_prover!r})")
+
+    def __eq__(self, other: object) -> bool:
+        if not isinstance(other, StepStats):
+            return NotImplemented
+        return (self.products, self.tensors, self.operands_from_prover) == \
+            (other.products, other.tensors, other.operands_from_prover)
 
     def max_normalized(self) -> float:
         return max((max(p.normalized) for p in self.products), default=0.0)
@@ -145,6 +176,15 @@ class CommittedLeaves:
         self._versions.append(self._version(obj))
         self._objs.append(obj)
 
+    @classmethod
+    def of(cls, objs: list[Any]) -> CommittedLeaves:
+        """The leaves ``objs``, in order, as if added one by one."""
+        out = cls()
+        version, tensor = cls._version, torch.Tensor
+        out._versions = [o._version if type(o) is tensor else version(o) for o in objs]
+        out._objs = list(objs)
+        return out
+
     def __len__(self) -> int:
         return len(self._objs)
 
@@ -153,11 +193,11 @@ class CommittedLeaves:
 
     def first_changed(self) -> int | None:
         """The first leaf written in place since it was added, or ``None``."""
-        version = self._version
-        for i, (obj, v) in enumerate(zip(self._objs, self._versions)):
-            if version(obj) != v:
-                return i
-        return None
+        version, tensor = self._version, torch.Tensor
+        now = [o._version if type(o) is tensor else version(o) for o in self._objs]
+        if now == self._versions:
+            return None
+        return next(i for i, (a, b) in enumerate(zip(now, self._versions)) if a != b)
 
     def leaf(self, index: int) -> Any:
         # Indices come from C, never from the prover, so a bad one is a verifier bug.

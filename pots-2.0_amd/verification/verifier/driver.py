@@ -16,7 +16,10 @@ without ``allow_provisional``, and κ classes or τ_W tensors that name nothing 
   2.root``; check 7 reports as check 0 on the first step, against ``W_0``; 6b is skipped when
   check 5 measured the prover's own operands), stops at the first
   rejection, keeps each step's statistics and per-slot wall clock, and on acceptance keeps the
-  step's ``W_{t+1}`` leaf hashes for the next step's check 7.
+  step's ``W_{t+1}`` leaf hashes for the next step's check 7. With ``overlap`` (the default)
+  a step is first tried on the overlapped path (:mod:`.overlap`: one read, the GPU work of
+  checks 2 and 5 in flight together, judged in the same order), which only accepts; anything
+  else runs the slots one at a time, which find and word the rejection.
 - :meth:`Verifier.freeze` ends a calibration run by judging the recorded numbers of every
   calibrated step in check order: 6a, then 5, then 6b.
 - :meth:`Verifier.end_run` compares the kept hashes with the agreed final weights (check 8,
@@ -46,6 +49,7 @@ from verification.computation.interface import DeclaredComputation
 from verification.transcript.store import TranscriptStore
 from verification.verifier.bands import Bands, product_class
 from verification.verifier.checks import CHECKS, DEFAULT_ORDER, ROOT_SLOT
+from verification.verifier.overlap import NOT_DECIDED, OverlapCache, decide
 from verification.verifier.context import (Rejection, Section, StepContext, StepStats,
                                            no_section)
 from verification.verifier.plans import PlanCache
@@ -108,7 +112,7 @@ class Verifier:
                  schedule: Callable[[int], Sequence[int]] | None = None,
                  calibrate: bool = False, allow_provisional: bool = False,
                  section: Section | None = None, kappa_guard: bool = True,
-                 trust_prover_operands: bool = False) -> None:
+                 trust_prover_operands: bool = False, overlap: bool = True) -> None:
         if (w0 is None) == (w0_hashes is None):
             raise ValueError("give exactly one of w0 and w0_hashes")
         if not (isinstance(h_D, bytes) and len(h_D) == DIGEST_SIZE):
@@ -129,6 +133,10 @@ class Verifier:
         self.allow_provisional, self.calibrate = allow_provisional, calibrate
         self.kappa_guard, self.section = kappa_guard, section
         self.trust_prover_operands = trust_prover_operands
+        self.overlap = overlap
+        # steps accepted on the overlapped path, and steps it left to the slots
+        self.overlapped: list[int] = []
+        self.serial: list[int] = []
         self.bands: Bands | None = None
         if bands is not None:
             self._adopt(bands)
@@ -229,24 +237,42 @@ class Verifier:
         if t > self.n_steps:
             raise RuntimeError(f"step {t} is past the declared T = {self.n_steps}")
         bands = self.bands if self.bands is not None else Bands.provisional()
-        ctx = StepContext.for_computation(
-            self.c, step=t, indices=tuple(self._schedule(t)) if self._schedule else (),
-            h_D=self.h_D, n_records=self.n_records, prev_w_hashes=self._chain,
-            chain_check_id="0" if t == 1 else "7", k=self.k, judge=not self.calibrate,
-            section=self.section, kappa_guard=self.kappa_guard,
-            trust_prover_operands=self.trust_prover_operands, plans=self.plans)
+        indices = tuple(self._schedule(t)) if self._schedule else ()
+
+        def context() -> StepContext:
+            return StepContext.for_computation(
+                self.c, step=t, indices=indices, h_D=self.h_D, n_records=self.n_records,
+                prev_w_hashes=self._chain, chain_check_id="0" if t == 1 else "7", k=self.k,
+                judge=not self.calibrate, section=self.section, kappa_guard=self.kappa_guard,
+                trust_prover_operands=self.trust_prover_operands, plans=self.plans)
+
         timings = self.timings[t] = {}
-        self.stats[t] = ctx.stats
         with _collector_paused():
-            for slot in DEFAULT_ORDER:
-                with self._timed(slot):
-                    t0 = time.perf_counter()
-                    rej = CHECKS[slot](store, self.c, ctx, bands)
-                    timings[slot] = time.perf_counter() - t0
-                if rej is not None:
-                    self.rejection = rej
-                    self.record_pass[t] = RECORD_NOT_RUN
-                    return rej
+            decided = NOT_DECIDED
+            if self.overlap:
+                ctx = context()
+                self.stats[t] = ctx.stats
+                if self.plans.overlap is None:
+                    self.plans.overlap = OverlapCache()
+                with self._timed("overlap"):
+                    decided = decide(self.c, store, ctx, bands, self.plans.overlap, timings)
+            if decided is NOT_DECIDED:
+                timings.clear()
+                ctx = context()
+                self.stats[t] = ctx.stats
+                for slot in DEFAULT_ORDER:
+                    with self._timed(slot):
+                        t0 = time.perf_counter()
+                        rej = CHECKS[slot](store, self.c, ctx, bands)
+                        timings[slot] = time.perf_counter() - t0
+                    if rej is not None:
+                        self.rejection = rej
+                        self.record_pass[t] = RECORD_NOT_RUN
+                        self.serial.append(t)
+                        return rej
+                self.serial.append(t)
+            else:
+                self.overlapped.append(t)
         hashes = ctx.state.leaf_hashes
         assert hashes is not None
         lo = self.c.w_next_index(self.c.weight_names[0])

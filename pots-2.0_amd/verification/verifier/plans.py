@@ -25,6 +25,7 @@ from __future__ import annotations
 
 from collections.abc import Sequence
 from dataclasses import dataclass, field
+from typing import Any
 
 import numpy as np
 import torch
@@ -50,6 +51,8 @@ class PlanCache:
         self._fv: _FvEntry | None = None
         self.hits = 0
         self.builds = 0
+        # the overlapped path's plans (verification.verifier.overlap.OverlapCache)
+        self.overlap: Any = None
 
     def leaf_plan(self, site: str, hdr_buf: bytes, hdr_off: np.ndarray, hdr_len: np.ndarray,
                   hdr_idx: np.ndarray, payload_ptr: np.ndarray, payload_len: np.ndarray,
@@ -110,6 +113,8 @@ class PlanCache:
         plan._keep = []
 
     def close(self) -> None:
+        if self.overlap is not None:
+            self.overlap.close()
         for _, plan in self._leaf.values():
             plan.close()
         self._leaf.clear()

@@ -22,7 +22,7 @@ non-finite leaf and the first rejected product.
 
 from __future__ import annotations
 
-from collections.abc import Sequence
+from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 from typing import Any
 
@@ -50,6 +50,98 @@ class StepVerdict:
     detail: str | None
 
 
+# The A stage's grid beside the fused chunk kernel, as multiples of the CU count (0: one block
+# per tile, no limit). Results do not depend on it (pots_fv_plan_set_grid); the time does.
+A_GRID_CANDIDATES = (1.0, 1.5, 2.0, 0.0)
+
+
+def calibrate_a_grid(plan: native.FvPlan, run: Callable[[], tuple[Any, Any]],
+                     device: torch.device, reps: int = 2) -> tuple[int, dict[int, float]]:
+    """The A stage's grid for this plan: each candidate of :data:`A_GRID_CANDIDATES` timed on
+    the step itself (``run`` enqueues one whole step and returns its start and end CUDA
+    events, recorded with timing), after one untimed run, best of ``reps``; the fastest is set
+    on the plan and returned with the table of times (ms). The rule replaces a model of the
+    two halves' rates: which grid lets the hashing and the A stage finish together depends on
+    the shapes, the fused share of the hashing and the host's gaps, and the step measures it
+    directly, once per plan."""
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    times: dict[int, float] = {}
+    for f in A_GRID_CANDIDATES:
+        g = int(round(f * cus))
+        if g in times:
+            continue
+        plan.set_grid(3, g)
+        events = [run() for _ in range(reps + 1)]
+        torch.cuda.synchronize(device)
+        times[g] = min(s.elapsed_time(e) for s, e in events[1:])
+    best = min(times, key=lambda g: (times[g], g))
+    plan.set_grid(3, best)
+    return best, times
+
+
+def enqueue_measure_and_hash(plan: native.FvPlan, hp: native.LeafPlan, fused: int,
+                             key: torch.Tensor, digests: torch.Tensor, bad: torch.Tensor,
+                             rows: torch.Tensor, side: torch.cuda.Stream,
+                             start: torch.cuda.Event, *, timing: bool = False,
+                             hash_after_b: bool = True, plain_early: bool = False
+                             ) -> tuple[torch.cuda.Event, ...]:
+    """Check 5's Freivalds stages on the current stream and check 2's chunk stages on
+    ``side`` (after ``start``), as one step runs them: with a fused leaf plan, the challenges
+    and the unfused P pass first, then the B pass and reduce, then the fused chunk kernel
+    beside the A stage, and the fused products' sums once the chunk kernel is done; the rows
+    last. The leaf plan's levels and the tree are the caller's (on ``side``, after this).
+    Returns the events (chunks begin, chunks end, A begin, A end)."""
+    main = torch.cuda.current_stream()
+    c_begin = torch.cuda.Event(enable_timing=timing)
+    c_end = torch.cuda.Event(enable_timing=timing)
+    a_begin = torch.cuda.Event(enable_timing=timing)
+    a_end = torch.cuda.Event(enable_timing=timing)
+    side.wait_event(start)
+    if not fused:
+        with torch.cuda.stream(side):
+            hp.run_stage(0, digests, bad, side)
+            c_begin.record(side)
+            hp.run_stage(1, digests, bad, side)
+            c_end.record(side)
+        for st in range(5):
+            if st == 3:
+                a_begin.record(main)
+            plan.run_stage(st, key, rows, main)
+            if st == 3:
+                a_end.record(main)
+    else:
+        # The fused chunk kernel reads the challenges and, started after the B pass, shares
+        # the CUs with a bounded A pass; the other leaves' chunks go first.
+        with torch.cuda.stream(side):
+            hp.run_stage(0, digests, bad, side)
+            if plain_early:
+                hp.run_stage(native.LeafPlan.PLAIN_CHUNKS, digests, bad, side)
+        # The unfused products' P pass needs only the challenges: it goes first, so that the
+        # step's end waits only for the fused products' sums.
+        plan.run_stage(0, key, rows, main)
+        plan.run_stage(native.FvPlan.P_PASS, key, rows, main)
+        for st in range(1, 3 if hash_after_b else 1):
+            plan.run_stage(st, key, rows, main)
+        ready = torch.cuda.Event()
+        ready.record(main)
+        side.wait_event(ready)
+        with torch.cuda.stream(side):
+            c_begin.record(side)
+            hp.run_stage(native.LeafPlan.FUSED_CHUNKS, digests, bad, side)
+            c_end.record(side)
+            if not plain_early:
+                hp.run_stage(native.LeafPlan.PLAIN_CHUNKS, digests, bad, side)
+        for st in range(3 if hash_after_b else 1, 4):
+            if st == 3:
+                a_begin.record(main)
+            plan.run_stage(st, key, rows, main)
+        a_end.record(main)
+        # the fused products' sums add up the chunk kernel's run records
+        main.wait_event(c_end)
+        plan.run_stage(native.FvPlan.P_FUSED, key, rows, main)
+    return c_begin, c_end, a_begin, a_end
+
+
 class DeviceStepVerifier:
     """Plans for one step's transcript, built once: the leaf-hashing plan, the Freivalds plan
     over every product (operands served by ``operands(spec)``), and the verdict table. Call
@@ -72,17 +164,15 @@ class DeviceStepVerifier:
             prods.append(native.FvProduct(a, b, p, spec.m, bias))
         self.plan = lib.fv_plan(prods, k, guard)
         # A bounded A pass (``a_grid`` blocks, 0: one per tile) leaves room on every CU for the
-        # hashing kernels beside it.
+        # hashing kernels beside it; by default the grid is timed on the step once
+        # (calibrate_a_grid).
         self.hash_after_b, self.plain_early = hash_after_b, plain_early
         # Fused: the chunk kernel takes the P-pass sums of the product leaves it hashes, so
         # each P is read from HBM once (pots_leaf_plan_create_fused).
         self.hasher = StepHasher(c, leaves, fuse=self.plan if fuse else None)
         self.fused = self.hasher.plan.fused
-        if a_grid is None:
-            a_grid = self._a_grid(prods, leaves[-1].device) if self.fused else 0
-        self.plan.set_grid(3, a_grid)
         self.plan.set_grid(1, b_grid)
-        self.a_grid = a_grid
+        self.grid_times: dict[int, float] = {}
         self.specs = native.verdict_specs(
             [s.q for s in c.products], [s.a_shape[0] for s in c.products],
             [s.bias is not None for s in c.products],
@@ -97,29 +187,19 @@ class DeviceStepVerifier:
         self.side = torch.cuda.Stream(device=dev)
         self.hash_bytes = self.hasher.bytes
         self.freivalds_bytes = self.plan.bytes
+        if a_grid is None and self.fused:
+            zero = torch.zeros(32, dtype=torch.uint8, device=dev)
 
-    # MI355X figures for sharing the GPU between the two halves: the chunk kernels hash about
-    # 2.5 TB/s of message bytes (bound by the VALUs); an A-pass block, one per CU, spends
-    # about 4.5 µs on each tile (64 rows by at most 4096 bf16 or 1024 fp32 columns) and
-    # 0.034 µs per KiB it streams (fitted to C3's and C4's A passes, 11.3 and 16.9 ms).
-    HASH_GBPS, TILE_US, KIB_US = 2500.0, 4.5, 0.034
+            def run() -> tuple[Any, Any]:
+                ev: list = []
+                self.enqueue(zero, ev)
+                return ev[0][0], ev[0][3]
 
-    def _a_grid(self, prods: Sequence[native.FvProduct], device: torch.device) -> int:
-        """The A pass's grid beside the fused chunk kernel: one 4-wave block per CU, or one
-        and a half where the hashing would otherwise wait for it (hashing estimated under
-        1.3x the A pass's time at one block per CU). Measured: C3, at 1.14x, takes 24.5 ms
-        instead of 25.5 with the larger grid; C4 (1.5x) and C1 (1.7x) are fastest at one
-        block per CU."""
-        cus = torch.cuda.get_device_properties(device).multi_processor_count
-        tiles = kib = 0
-        for p in prods:
-            n, q = p.a.shape
-            width = 4096 if p.a.element_size() == 2 else 1024
-            tiles += -(-n // 64) * -(-q // width)
-            kib += p.a.numel() * p.a.element_size() / 1024
-        hash_ms = self.hasher.bytes / self.HASH_GBPS / 1e6
-        a_ms = (tiles * self.TILE_US + kib * self.KIB_US) / cus / 1e3
-        return cus * 3 // 2 if hash_ms < 1.3 * a_ms else cus
+            a_grid, self.grid_times = calibrate_a_grid(self.plan, run, dev)
+        else:
+            a_grid = a_grid or 0
+            self.plan.set_grid(3, a_grid)
+        self.a_grid = a_grid
 
     def enqueue(self, claimed: bytes | torch.Tensor, events: list | None = None):
         """Enqueue the whole step on the current stream (Freivalds, verdicts) and a side
@@ -132,57 +212,15 @@ class DeviceStepVerifier:
             self.key.copy_(claimed)
         else:
             self.key.copy_(torch.frombuffer(bytearray(claimed), dtype=torch.uint8))
-        start = torch.cuda.Event(enable_timing=events is not None)
-        start.record(main)
         timing = events is not None
+        start = torch.cuda.Event(enable_timing=timing)
+        start.record(main)
+        ev = enqueue_measure_and_hash(self.plan, self.hasher.plan, self.fused, self.key,
+                                      self.digests, self.bad, self.rows, self.side, start,
+                                      timing=timing, hash_after_b=self.hash_after_b,
+                                      plain_early=self.plain_early)
+        c_begin, c_end, a_begin, a_end = ev
         plan, hp, side = self.plan, self.hasher.plan, self.side
-        c_begin = torch.cuda.Event(enable_timing=timing)
-        c_end = torch.cuda.Event(enable_timing=timing)
-        a_begin = torch.cuda.Event(enable_timing=timing)
-        a_end = torch.cuda.Event(enable_timing=timing)
-        side.wait_event(start)
-        if not self.fused:
-            with torch.cuda.stream(side):
-                hp.run_stage(0, self.digests, self.bad, side)
-                c_begin.record(side)
-                hp.run_stage(1, self.digests, self.bad, side)
-                c_end.record(side)
-            for st in range(5):
-                if st == 3:
-                    a_begin.record(main)
-                plan.run_stage(st, self.key, self.rows, main)
-                if st == 3:
-                    a_end.record(main)
-        else:
-            # The fused chunk kernel reads the challenges and, started after the B pass,
-            # shares the CUs with a bounded A pass; the other leaves' chunks go first.
-            with torch.cuda.stream(side):
-                hp.run_stage(0, self.digests, self.bad, side)
-                if self.plain_early:
-                    hp.run_stage(native.LeafPlan.PLAIN_CHUNKS, self.digests, self.bad, side)
-            # The unfused products' P pass needs only the challenges: it goes first, so that
-            # the step's end waits only for the fused products' sums.
-            plan.run_stage(0, self.key, self.rows, main)
-            plan.run_stage(native.FvPlan.P_PASS, self.key, self.rows, main)
-            for st in range(1, 3 if self.hash_after_b else 1):
-                plan.run_stage(st, self.key, self.rows, main)
-            ready = torch.cuda.Event()
-            ready.record(main)
-            side.wait_event(ready)
-            with torch.cuda.stream(side):
-                c_begin.record(side)
-                hp.run_stage(native.LeafPlan.FUSED_CHUNKS, self.digests, self.bad, side)
-                c_end.record(side)
-                if not self.plain_early:
-                    hp.run_stage(native.LeafPlan.PLAIN_CHUNKS, self.digests, self.bad, side)
-            for st in range(3 if self.hash_after_b else 1, 4):
-                if st == 3:
-                    a_begin.record(main)
-                plan.run_stage(st, self.key, self.rows, main)
-            a_end.record(main)
-            # the fused products' sums add up the chunk kernel's run records
-            main.wait_event(c_end)
-            plan.run_stage(native.FvPlan.P_FUSED, self.key, self.rows, main)
         with torch.cuda.stream(side):
             hp.run_stage(2, self.digests, self.bad, side)
             nodes = self.lib.merkle_tree_device(self.digests, side)

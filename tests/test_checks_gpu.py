@@ -42,34 +42,40 @@ def _root(c, leaves):
     return O.merkle_root(want)
 
 
-def _verify(c, leaves, claimed, k=2, w0_leaves=None):
+def _verify(c, leaves, claimed, k=2, w0_leaves=None, **kw):
     from conftest import started_verifier
     from verification.transcript.store import InMemoryStore
-    v = started_verifier(c, w0_leaves if w0_leaves is not None else leaves, k=k)
+    v = started_verifier(c, w0_leaves if w0_leaves is not None else leaves, k=k, **kw)
     rej = v.verify_step(1, InMemoryStore(leaves, claimed_root=claimed))
     return v, rej
 
 
-def test_honest_step_accepts_with_stats(lib):
+@pytest.mark.parametrize("overlap", [True, False])
+def test_honest_step_accepts_with_stats(lib, overlap):
     c, step = _step(11)
     claimed = _root(c, step.leaves)
-    v, rej = _verify(c, step.leaves, claimed)
+    v, rej = _verify(c, step.leaves, claimed, overlap=overlap)
     assert rej is None
     stats = v.stats[1].products
     assert [s.m for s in stats] == [s.m for s in c.products]
     assert all(max(s.normalized) <= 8.0 for s in stats)
-    assert set(v.timings[1]) == {"7", "2", "6a", "5", "6b", "2.root"}
+    if overlap:  # accepted on the overlapped path, timed by phase
+        assert v.overlapped == [1]
+        assert set(v.timings[1]) == {"read", "serve", "plans", "gpu", "judge"}
+    else:
+        assert v.serial == [1]
+        assert set(v.timings[1]) == {"7", "2", "6a", "5", "6b", "2.root"}
     assert v.stats[1].operands_from_prover
 
 
 def test_forged_product_rejects_at_check_5(lib):
     c, step = _step(12)
     spec = c.products[len(c.products) // 3]
-    step.product(spec.m)[1, 2] += 8.0
+    step.product(spec.m)[1, 2] += 64.0
     v, rej = _verify(c, step.leaves, _root(c, step.leaves))
     assert rej is not None and (rej.step, rej.check_id, rej.kind) == (1, "5", "failed")
-    assert re.fullmatch(rf"P_{spec.m} \({re.escape(spec.name)}\), challenge j=1: normalized "
-                        rf"residual \S+ > τ = 8", rej.detail), rej.detail
+    assert re.fullmatch(rf"P_{spec.m} \({re.escape(spec.name)}\), challenge j=[12]: "
+                        rf"normalized residual \S+ > τ = 8", rej.detail), rej.detail
     assert v.stats[1].products[-1].m == spec.m  # judged up to the failing product
 
 
@@ -226,7 +232,9 @@ def test_serving_error_after_a_forged_product(lib):
 
 
 def test_plans_kept_between_steps_run_again_only_on_the_same_layout(lib):
-    """A verifier keeps its last step's leaf and Freivalds plans. A step with the same layout
+    """The slots run one at a time (``overlap=False``; the overlapped path's own plans are
+    tested in test_overlap_gpu.py) keep the last step's leaf and Freivalds plans. A step with
+    the same layout
     (here the same tensors) runs them again with the same hashes and statistics; a product
     changed in place, at the same address, still rejects at check 5; a product moved to
     another buffer makes check 2's leaf plan and the Freivalds plan be built again."""
@@ -234,11 +242,11 @@ def test_plans_kept_between_steps_run_again_only_on_the_same_layout(lib):
     from verification.transcript.store import InMemoryStore
     c, step = _step(21)
     claimed = _root(c, step.leaves)
-    v1 = started_verifier(c, step.leaves, k=2)
+    v1 = started_verifier(c, step.leaves, k=2, overlap=False)
     assert v1.verify_step(1, InMemoryStore(step.leaves, claimed_root=claimed)) is None
     cache = v1.plans
     assert (cache.builds, cache.hits) == (3, 0)  # check 7's and 2's leaf plans, Freivalds
-    v2 = started_verifier(c, step.leaves, k=2)
+    v2 = started_verifier(c, step.leaves, k=2, overlap=False)
     v2.plans = cache
     assert v2.verify_step(1, InMemoryStore(step.leaves, claimed_root=claimed)) is None
     assert (cache.builds, cache.hits) == (3, 3)
@@ -247,7 +255,7 @@ def test_plans_kept_between_steps_run_again_only_on_the_same_layout(lib):
     spec = c.products[7]
     honest = step.product(spec.m)[0, 1].clone()
     step.product(spec.m)[0, 1] += 8.0  # forged in place: the layout is unchanged
-    v3 = started_verifier(c, step.leaves, k=2)
+    v3 = started_verifier(c, step.leaves, k=2, overlap=False)
     v3.plans = cache
     rej = v3.verify_step(1, InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves)))
     assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
@@ -257,7 +265,7 @@ def test_plans_kept_between_steps_run_again_only_on_the_same_layout(lib):
     step.product(spec.m)[0, 1] = honest
     i = c.product_index(spec.m)
     step.leaves[i] = step.leaves[i].clone()  # the same bytes in another buffer
-    v4 = started_verifier(c, step.leaves, k=2)
+    v4 = started_verifier(c, step.leaves, k=2, overlap=False)
     v4.plans = cache
     assert v4.verify_step(1, InMemoryStore(step.leaves, claimed_root=claimed)) is None
     assert (cache.builds, cache.hits) == (5, 7)
@@ -267,19 +275,20 @@ def test_plans_kept_between_steps_run_again_only_on_the_same_layout(lib):
 
 def test_new_records_keep_check_2s_plan(lib):
     """Records are hashed as their own batch, so a step with other records over the same
-    tensor buffers still reuses check 2's leaf plan; the new root is the oracle's."""
+    tensor buffers still reuses check 2's leaf plan (the slots one at a time); the new root is
+    the oracle's."""
     from conftest import started_verifier
     from setup.records import Record
     from verification.transcript.store import InMemoryStore
     c, step = _step(22)
-    v1 = started_verifier(c, step.leaves, k=2)
+    v1 = started_verifier(c, step.leaves, k=2, overlap=False)
     assert v1.verify_step(1, InMemoryStore(step.leaves, claimed_root=_root(c, step.leaves))) \
         is None
     cache = v1.plans
     r = step.leaves[0]
     step.leaves[0] = Record(torch.flip(r.ids, [0]).contiguous(), r.targets, r.mask)
     claimed = _root(c, step.leaves)
-    v2 = started_verifier(c, step.leaves, k=2)
+    v2 = started_verifier(c, step.leaves, k=2, overlap=False)
     v2.plans = cache
     assert v2.verify_step(1, InMemoryStore(step.leaves, claimed_root=claimed)) is None
     assert (cache.builds, cache.hits) == (3, 3)

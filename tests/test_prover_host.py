@@ -405,6 +405,46 @@ def test_decoder_replay_rebuilds_the_operands_from_the_leaves(qkv_bias, n_kv, dt
     assert all(torch.equal(x, y) for x, y in zip(again.operands(m), replay.operands(m)))
 
 
+@pytest.mark.parametrize("qkv_bias,n_kv,dtype", DECODERS)
+def test_decoder_replay_serves_each_attention_call_as_one_group(qkv_bias, n_kv, dtype):
+    """``operand_group`` over a batched call's members returns the call's whole operands (a
+    view, no copy) equal to the members' operands stacked; a group it does not hold (a
+    reordered or partial one) is stacked member by member."""
+    from verification.computation.instances.decoder import DecoderReplay
+    c, w0, step = _decoder_step(qkv_bias, n_kv, dtype)
+    replay = DecoderReplay(c, step.leaves(), device="cpu")
+    groups = [g for g in c.operand_groups if len(g) > 1]
+    assert len(groups) == 6 * c.L  # S, O, dA, dV, dQ, dK per layer
+    for g in groups:
+        ms = [c.products[i].m for i in g]
+        a, b = replay.operand_group(ms)
+        pairs = [replay.operands(m) for m in ms]
+        assert torch.equal(a, torch.stack([x for x, _ in pairs]))
+        assert torch.equal(b, torch.stack([y for _, y in pairs]))
+        assert a[0].data_ptr() == pairs[0][0].data_ptr()  # served where the call left it
+    ms = [c.products[i].m for i in groups[0]]
+    a, _ = replay.operand_group(ms[::-1])
+    assert torch.equal(a, torch.stack([replay.operands(m)[0] for m in ms[::-1]]))
+    assert a.data_ptr() != replay.operands(ms[-1])[0].data_ptr()
+
+
+def test_operand_groups_follow_the_batched_products():
+    """Every product in exactly one group, groups in order of their first product; members of
+    one layer's role together even where two roles interleave."""
+    from verification.computation.instances.decoder import DecoderComputation
+    c = DecoderComputation(L=2, d=64, d_f=128, n_h=4, n_kv=2, n_v=160, n_s=2, n=32)
+    groups = c.operand_groups
+    assert sorted(i for g in groups for i in g) == list(range(c.M))
+    assert [g[0] for g in groups] == sorted(g[0] for g in groups)
+    for g in groups:
+        names = {c.products[i].name.split("[")[0] for i in g}
+        assert len(names) == 1 and list(g) == sorted(g)
+        if len(g) > 1:
+            assert len(g) == c.n_s * c.n_h
+    da = next(g for g in groups if c.products[g[0]].name.startswith("L2.dA"))
+    assert da[1] - da[0] == 2  # dA and dV interleave in canonical order
+
+
 def test_decoder_replay_follows_a_forged_product():
     """A forged forward product changes the glue downstream of it: the replay serves the
     operands the committed leaves imply, so the forged product itself no longer equals its

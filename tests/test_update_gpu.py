@@ -184,7 +184,8 @@ def test_check_6a_honest_step_records_every_weight(lib):
     assert all(t.check_id == "6a" and t.rho_max <= TAU_W for t in tensors)
     for t in tensors[::5]:
         assert _bits(t.rho_max) == _bits(_oracle_weight(c, step.leaves, t.weight)["rho_max"])
-    assert list(v.timings[1]) == ["7", "2", "6a", "5", "6b", "2.root"]
+    assert list(v.timings[1]) == (["read", "serve", "plans", "gpu", "judge"] if v.overlapped
+                                  else ["7", "2", "6a", "5", "6b", "2.root"])
 
 
 def test_check_6a_forged_update_rejects_with_the_reference_wording(lib):
