@@ -50,7 +50,12 @@ CONFIGS = {
     "c1": ("SmolLM2-135M step, 4x256 tokens, fp32, k=1", "smollm2_135m", 1),
     "c3": ("Qwen2-0.5B-shaped step, 8x1024 tokens, bf16, k=2", "qwen2_0_5b_shape", 2),
     "c4": ("Qwen2-1.5B-shaped step, 4x2048 tokens, bf16, k=4", "qwen2_1_5b_shape", 4),
+    "c5": ("Qwen2-1.5B-shaped step, 4x2048 tokens, bf16, adversarial: a seeded 1% of the "
+           "products perturbed (one entry each, relative size log-uniform in [1e-6, 1]), "
+           "re-rooted, k=16", "qwen2_1_5b_shape", 16),
 }
+# the perturbation of config 5: which products and entries (prover.synthetic.perturb_products)
+C5_FRACTION, C5_SEED = 0.01, 5
 
 
 def log(msg: str) -> None:
@@ -588,89 +593,17 @@ def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 4) -> dict:
             "runs_ms": [round(t, 1) for t in times]}
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--hash-first", action="store_true",
-                    help="start the fused chunk kernel after the challenges, not the B pass")
-    ap.add_argument("--plain-early", action="store_true",
-                    help="hash the unfused leaves while the B pass runs")
-    ap.add_argument("--b-grid", type=int, default=0,
-                    help="blocks of the B pass (0: one per tile)")
-    ap.add_argument("--a-grid", type=int, default=None,
-                    help="blocks of the A pass (default when fused: the fastest of 1, 1.5 "
-                         "and 2 blocks per CU and one per tile, timed on the step when the "
-                         "plan is built; unfused: one per tile); see pots_fv_plan_set_grid")
-    ap.add_argument("--calibration-copy-mib", type=int, default=0,
-                    help="copy this many MiB device to device twice before timing, so a "
-                         "counter run sees a plain copy kernel of known size")
-    ap.add_argument("--disk-leg", metavar="DIR",
-                    help="also write the transcript under DIR in the on-disk store's format "
-                         "(with the captured operands), load it back into HBM with the native "
-                         "loader, verify the loaded copy, report parts.disk_load, and delete it")
-    ap.add_argument("--prover-leg", nargs="?", const="mlp", choices=("mlp", "qwen2"),
-                    help="also run the device-resident prover and report parts.prover: 'mlp' "
-                         "proves an MLP step (capture, labeling, SGD), commits it in HBM and "
-                         "verifies it with the replay; 'qwen2' proves a Qwen2-1.5B-shaped "
-                         "training step (transformers, random init, bf16 autocast over fp32 "
-                         "masters, 28 layers, 4x2048 tokens), commits it in HBM and verifies "
-                         "it, with the prover's operands and then from the leaves alone")
-    ap.add_argument("--check-level", action=argparse.BooleanOptionalAction, default=True,
-                    help="time Verifier.verify_step (the reference's check-level entry point) "
-                         "on the same transcript, beside the step")
-    ap.add_argument("--counter-summary", metavar="DIR",
-                    help="summarise rocprofv3 --pmc CSV output under DIR and exit")
-    ap.add_argument("--trace-summary", metavar="DIR",
-                    help="summarise rocprofv3 --kernel-trace CSV output under DIR of a run "
-                         "with the same --steps/--warmup, and exit")
-    args = ap.parse_args()
-    if args.counter_summary:
-        return counter_summary(Path(args.counter_summary), args.calibration_copy_mib)
-    if args.trace_summary:
-        return trace_summary(Path(args.trace_summary), args.steps, args.warmup)
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); sharding "
-              "across GPUs is designed but not built or measured.", file=sys.stderr)
-        return 2
-
+def measure_step(c, step, k: int, args, desc: str):
+    """The headline measurement of one configuration on its resident transcript: the plans,
+    the claimed root (the root of the transcript as it is), the timed overlapped steps, the
+    serialised stage leg, check 6a, and every kernel's roofline; returns the JSON line's dict
+    (without the legs), the step verifier, the claimed root and the product inputs."""
     import torch
 
     from verification.commitment import native
-    from verification.computation.instances import decoder
-    from verification.prover.synthetic import synthetic_step
     from verification.verifier.step import DeviceStepVerifier
 
     lib = native.get()
-    # The prover legs build their own model and step; they run first, on an empty GPU, so
-    # that the resident C4 transcript need not share HBM with them.
-    prover = None
-    if args.prover_leg:
-        prover = prover_leg() if args.prover_leg == "mlp" else capture_leg_qwen2()
-        import gc
-        gc.collect()
-        torch.cuda.empty_cache()
-    desc, ctor, k = CONFIGS[args.config]
-    c = getattr(decoder, ctor)()
-    log(f"[bench] {args.config}: {c.M} products, {c.n_leaves} leaves, k={k}")
-    t0 = time.perf_counter()
-    step = synthetic_step(c, seed=0, operands=True)
-    step.k = k
-    torch.cuda.synchronize()
-    log(f"[bench] transcript built in {time.perf_counter() - t0:.1f} s, "
-        f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB resident")
-
-    if args.calibration_copy_mib:
-        src = torch.ones(args.calibration_copy_mib << 20, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(2):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-
     stream = torch.cuda.current_stream()
     items = product_inputs(step)
     t0 = time.perf_counter()
@@ -679,8 +612,9 @@ def main() -> int:
                            hash_after_b=not args.hash_first, plain_early=args.plain_early)
     torch.cuda.synchronize()
     plan_build_ms = (time.perf_counter() - t0) * 1e3
-    log(f"[bench] plans built in {plan_build_ms:.1f} ms (leaf plan fused with the Freivalds "
-        f"plan, verdict table)")
+    log(f"[bench] plans built in {plan_build_ms:.1f} ms (leaf plan "
+        f"{'fused with' if v.fused else 'beside'} the Freivalds plan, verdict table; A-stage "
+        f"grid {v.a_grid})")
     # The claimed root: the honest root of this transcript, as the prover would send it.
     v.hasher.digests(v.digests, v.bad, stream)
     claimed = lib.merkle_tree_device(v.digests, stream)[0].clone()
@@ -914,6 +848,97 @@ def main() -> int:
                      "kernels": {kernels[nm][0]: kernel_roofline(nm) for nm in
                                  sorted(kernels, key=lambda nm: -stage_ms[nm])}},
     }
+    return out, v, claimed_b, items
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--hash-first", action="store_true",
+                    help="start the fused chunk kernel after the challenges, not the B pass")
+    ap.add_argument("--plain-early", action="store_true",
+                    help="hash the unfused leaves while the B pass runs")
+    ap.add_argument("--b-grid", type=int, default=0,
+                    help="blocks of the B pass (0: one per tile)")
+    ap.add_argument("--a-grid", type=int, default=None,
+                    help="blocks of the A pass (default when fused: the fastest of 1, 1.5 "
+                         "and 2 blocks per CU and one per tile, timed on the step when the "
+                         "plan is built; unfused: one per tile); see pots_fv_plan_set_grid")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="copy this many MiB device to device twice before timing, so a "
+                         "counter run sees a plain copy kernel of known size")
+    ap.add_argument("--disk-leg", metavar="DIR",
+                    help="also write the transcript under DIR in the on-disk store's format "
+                         "(with the captured operands), load it back into HBM with the native "
+                         "loader, verify the loaded copy, report parts.disk_load, and delete it")
+    ap.add_argument("--prover-leg", nargs="?", const="mlp", choices=("mlp", "qwen2"),
+                    help="also run the device-resident prover and report parts.prover: 'mlp' "
+                         "proves an MLP step (capture, labeling, SGD), commits it in HBM and "
+                         "verifies it with the replay; 'qwen2' proves a Qwen2-1.5B-shaped "
+                         "training step (transformers, random init, bf16 autocast over fp32 "
+                         "masters, 28 layers, 4x2048 tokens), commits it in HBM and verifies "
+                         "it, with the prover's operands and then from the leaves alone")
+    ap.add_argument("--c5-leg", action=argparse.BooleanOptionalAction, default=True,
+                    help="after the C4 headline and its legs, perturb the resident transcript "
+                         "as config 5 does and time it at k=16 (parts.c5)")
+    ap.add_argument("--check-level", action=argparse.BooleanOptionalAction, default=True,
+                    help="time Verifier.verify_step (the reference's check-level entry point) "
+                         "on the same transcript, beside the step")
+    ap.add_argument("--counter-summary", metavar="DIR",
+                    help="summarise rocprofv3 --pmc CSV output under DIR and exit")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="summarise rocprofv3 --kernel-trace CSV output under DIR of a run "
+                         "with the same --steps/--warmup, and exit")
+    args = ap.parse_args()
+    if args.counter_summary:
+        return counter_summary(Path(args.counter_summary), args.calibration_copy_mib)
+    if args.trace_summary:
+        return trace_summary(Path(args.trace_summary), args.steps, args.warmup)
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); sharding "
+              "across GPUs is designed but not built or measured.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from verification.commitment import native
+    from verification.computation.instances import decoder
+    from verification.prover.synthetic import perturb_products, synthetic_step
+
+    native.get()
+    # The prover legs build their own model and step; they run first, on an empty GPU, so
+    # that the resident C4 transcript need not share HBM with them.
+    prover = None
+    if args.prover_leg:
+        prover = prover_leg() if args.prover_leg == "mlp" else capture_leg_qwen2()
+        import gc
+        gc.collect()
+        torch.cuda.empty_cache()
+    desc, ctor, k = CONFIGS[args.config]
+    c = getattr(decoder, ctor)()
+    log(f"[bench] {args.config}: {c.M} products, {c.n_leaves} leaves, k={k}")
+    t0 = time.perf_counter()
+    step = synthetic_step(c, seed=0, operands=True)
+    step.k = k
+    if args.config == "c5":
+        perturb_products(step, C5_FRACTION, seed=C5_SEED)
+    torch.cuda.synchronize()
+    log(f"[bench] transcript built in {time.perf_counter() - t0:.1f} s, "
+        f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB resident")
+
+    if args.calibration_copy_mib:
+        src = torch.ones(args.calibration_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    out, v, claimed_b, items = measure_step(c, step, k, args, desc)
     if args.check_level:
         out["parts"]["check_level"] = check_level_leg(c, step, k, claimed_b)
     if args.disk_leg:
@@ -923,8 +948,41 @@ def main() -> int:
         out["cpu_baseline"] = cpu_baseline(step, items)
     if prover is not None:
         out["parts"]["prover"] = prover
+    if args.c5_leg and args.config == "c4":
+        v.close()
+        del v
+        out["parts"]["c5"] = c5_leg(c, step, args)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def c5_leg(c, step, args) -> dict:
+    """Config 5 on the resident C4 transcript, beside the headline: a seeded 1% of the
+    products perturbed in place (one entry each, relative size log-uniform in [1e-6, 1]), the
+    transcript re-rooted as the forging prover would commit it, and the step timed at k = 16
+    with every kernel's roofline. Runs last: it changes the transcript."""
+    import torch
+
+    from verification.prover.synthetic import perturb_products
+    forged = perturb_products(step, C5_FRACTION, seed=C5_SEED)
+    log(f"[bench] c5 leg: {len(forged)} products perturbed, k=16")
+    sub = argparse.Namespace(**{**vars(args), "steps": max(3, min(args.steps, 5)),
+                                "warmup": 1, "a_grid": None})
+    out, v, _, _ = measure_step(c, step, 16, sub, CONFIGS["c5"][0])
+    v.close()
+    torch.cuda.synchronize()
+    parts = out["parts"]
+    return {"k": 16, "perturbed": len(forged), "rejected": parts["rejected"],
+            "ms_per_step": out["ms_per_step"], "value": out["value"], "unit": "GB/s",
+            "step_frac_hbm": parts["step_frac_hbm"],
+            "hash_bytes": out["config"]["hash_bytes"],
+            "freivalds_bytes": out["config"]["freivalds_bytes"],
+            "twins": out["config"]["twins"], "a_pass_blocks": out["config"]["a_pass_blocks"],
+            "p_pass_fused_products": out["config"]["p_pass_fused_products"],
+            "overlap": parts["overlap"], "stages_ms": parts["stages_ms"],
+            "dominant": {key: out["roofline"][key] for key in
+                         ("kernel", "bound", "achieved", "frac", "launch_ms")},
+            "kernels": out["roofline"]["kernels"]}
 
 
 if __name__ == "__main__":

@@ -201,6 +201,12 @@ class DeviceStepVerifier:
             self.plan.set_grid(3, a_grid)
         self.a_grid = a_grid
 
+    def close(self) -> None:
+        """Free the plans' device memory (the leaf plan first: the Freivalds plan it may be
+        fused with must outlive it)."""
+        self.hasher.plan.close()
+        self.plan.close()
+
     def enqueue(self, claimed: bytes | torch.Tensor, events: list | None = None):
         """Enqueue the whole step on the current stream (Freivalds, verdicts) and a side
         stream (hashing, tree); returns GPU tensors ``(nodes, codes, first_fail)``.
