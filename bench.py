@@ -169,6 +169,8 @@ def kernel_label(name: str) -> str:
         if sq64 == "true":
             return f"row_pass<{dt}, fp64 squares> (P pass)"
         return f"row_pass<{dt}> (B pass)"
+    if short == "twin_pass":
+        return "twin_pass (A pass of twins)"
     return short.split("<")[0]  # chunk_kernel_fused<K>: one name for every K
 
 
