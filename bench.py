@@ -482,6 +482,14 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 28, k: int 
     torch.cuda.synchronize()
     verify_ms = (time.perf_counter() - t0) * 1e3
     assert verdict.check is None and verdict.root == tree.root, verdict.detail
+    # What the check-level leg does not read goes before it: the device verifier's plans,
+    # the prover's kept operands and model (the replay builds its own).
+    v.close()
+    del v, verdict, model
+    step.operands.clear()
+    import gc
+    gc.collect()
+    torch.cuda.empty_cache()
     # The reference-shaped path on the same step: Verifier.verify_step in the reference's
     # order, every operand and check 6b's glue gradients from the decoder replay of the
     # committed leaves; the first run builds the plans, the second finds them cached.
@@ -507,10 +515,13 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 28, k: int 
         cl_slots.append({s_: round(t_ * 1e3, 2) for s_, t_ in cv.timings[1].items()})
         assert rej is None, rej
         cache = cv.plans
+    overlapped = cv.overlapped == [1]
+    declined = cache.overlap.declined if cache.overlap is not None else None
     cache.close()
     log(f"[bench] qwen2 check-level Verifier.verify_step (decoder replay, check 6b on "
-        f"{len(c.glue_gradient_weights)} glue weights): {cl_ms[0]:.0f} ms building its plans, "
-        f"{cl_ms[1]:.0f} ms with them cached; " +
+        f"{len(c.glue_gradient_weights)} glue weights; "
+        f"{'overlapped' if overlapped else f'serial: {declined}'}): {cl_ms[0]:.0f} ms "
+        f"building its plans, {cl_ms[1]:.0f} ms with them cached; " +
         ", ".join(f"{s_} {t_:.1f}" for s_, t_ in cl_slots[1].items()))
     # the reference's per-product copy to pinned host memory, on every 8th product
     sample = list(step.products[::8])
@@ -538,6 +549,7 @@ def capture_leg_qwen2(batch: int = 4, seq: int = 2048, layers: int = 28, k: int 
             "verify_ms": round(verify_ms, 2), "verified": True,
             "check_level": {"verify_step_first_ms": round(cl_ms[0], 1),
                             "verify_step_ms": round(cl_ms[1], 1), "slots_ms": cl_slots[1],
+                            "overlapped": overlapped, "declined": declined,
                             "glue_weights": len(c.glue_gradient_weights)},
             "avoided_d2h_gbps": round(d2h_gbps, 1),
             "avoided_d2h_s": round(product_bytes / d2h_gbps / 1e9, 3)}
@@ -579,6 +591,7 @@ def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 4) -> dict:
     ov = cache.overlap
     hits, builds = (ov.hits, ov.builds) if ov is not None else (cache.hits, cache.builds)
     overlapped = len(v.overlapped) == 1
+    declined = ov.declined if ov is not None else None
     grid_ms = ov.entry.grid_times if ov is not None and ov.entry is not None else {}
     cache.close()
     best = min(range(1, runs), key=lambda i: times[i])
@@ -588,6 +601,7 @@ def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 4) -> dict:
         f"(best of {runs - 1}; {builds} built, {hits} reused); "
         + ", ".join(f"{s} {t * 1e3:.1f}" for s, t in slots[best].items()))
     return {"verify_step_ms": round(times[best], 1), "overlapped": overlapped,
+            "declined": declined,
             "a_pass_grid_ms": {str(g): round(t, 2) for g, t in grid_ms.items()},
             "verify_step_first_ms": round(times[0], 1),
             "slots_ms": {s: round(t * 1e3, 2) for s, t in slots[best].items()},

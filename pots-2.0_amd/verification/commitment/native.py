@@ -23,7 +23,7 @@ import ctypes
 import os
 import threading
 import weakref
-from collections.abc import Iterator, Sequence
+from collections.abc import Callable, Iterator, Sequence
 from typing import Any
 from contextlib import contextmanager
 from pathlib import Path
@@ -59,6 +59,18 @@ FINITE_KIND: dict[torch.dtype, int] = {
 }
 
 E_OK, E_NOMEM, E_HIP, E_ARG, E_IO = 0, -1, -3, -4, -5
+
+
+def _create(lib: Native, make: Callable[[], int], what: str) -> None:
+    """A plan's create call. The plans take their device memory with hipMalloc, beside
+    torch's caching allocator, which keeps the blocks a program has freed: when the device
+    is out of memory, those go back to the driver (``torch.cuda.empty_cache``) and the call
+    runs once more."""
+    rc = make()
+    if rc == E_NOMEM:
+        torch.cuda.empty_cache()
+        rc = make()
+    lib._check(rc, what)
 _SIZE_MAX = (1 << (8 * ctypes.sizeof(ctypes.c_size_t))) - 1
 
 
@@ -364,13 +376,13 @@ class LeafPlan:
         kd = np.ascontiguousarray(kd, dtype=np.uint8)
         h = ctypes.c_void_p()
         if fuse is None:
-            lib._check(lib._lib.pots_leaf_plan_create(
+            _create(lib, lambda: lib._lib.pots_leaf_plan_create(
                 n, _addr(hb), _addr(hdr_off), _addr(hdr_len), _addr(idx), _addr(ptr), _addr(ln),
                 _addr(kd), ctypes.byref(h)), "pots_leaf_plan_create")
         else:
             if fuse._fused_leaf is not None:
                 raise ValueError("this Freivalds plan is already fused with a leaf plan")
-            lib._check(lib._lib.pots_leaf_plan_create_fused(
+            _create(lib, lambda: lib._lib.pots_leaf_plan_create_fused(
                 n, _addr(hb), _addr(hdr_off), _addr(hdr_len), _addr(idx), _addr(ptr), _addr(ln),
                 _addr(kd), fuse._h, ctypes.byref(h)), "pots_leaf_plan_create_fused")
             fuse._fused_leaf = weakref.ref(self)
@@ -629,8 +641,9 @@ class FvPlan:
                 guard: bool, device: torch.device) -> None:
         n = len(arr)
         h = ctypes.c_void_p()
-        lib._check(lib._lib.pots_fv_plan_create(n, arr.ctypes.data, k, int(bool(guard)),
-                                                ctypes.byref(h)), "pots_fv_plan_create")
+        _create(lib, lambda: lib._lib.pots_fv_plan_create(n, arr.ctypes.data, k,
+                                                          int(bool(guard)), ctypes.byref(h)),
+                "pots_fv_plan_create")
         self._lib, self._h, self._keep = lib, h, keep
         _LIVE_PLANS.add(self)
         self._fused_leaf = None  # weak reference to the leaf plan fused with this one
@@ -772,10 +785,9 @@ class UpdatePlan:
             c.tau_w = float(w.tau_w)
             keep += list(ts)
         h = ctypes.c_void_p()
-        lib._check(lib._lib.pots_update_plan_create(n, ctypes.addressof(arr),
-                                                    float(np.float32(eta)),
-                                                    float(np.float32(eps_w)), ctypes.byref(h)),
-                   "pots_update_plan_create")
+        _create(lib, lambda: lib._lib.pots_update_plan_create(
+            n, ctypes.addressof(arr), float(np.float32(eta)), float(np.float32(eps_w)),
+            ctypes.byref(h)), "pots_update_plan_create")
         self._lib, self._h, self._keep = lib, h, keep
         _LIVE_PLANS.add(self)
         self.n = n

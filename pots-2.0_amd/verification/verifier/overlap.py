@@ -86,6 +86,7 @@ class OverlapCache:
         self.entry: _Entry | None = None
         self.hits = 0
         self.builds = 0
+        self.declined: str | None = None  # why the last step was left to the slots
 
     def close(self) -> None:
         if self.entry is not None:
@@ -299,8 +300,15 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
            cache: OverlapCache, timings: dict[str, float]) -> Any:
     """Accept step ``ctx.step`` (``None``, with ``ctx`` filled as the slots fill it) or
     return :data:`NOT_DECIDED`; never a rejection (see the module)."""
+    cache.declined = None
+
+    def no(reason: str, wait: torch.cuda.Stream | None = None,
+           alone: native.FvPlan | None = None) -> Any:
+        cache.declined = reason
+        return _undecided(wait, alone)
+
     if c.M == 0:
-        return NOT_DECIDED
+        return no("no products")
     t0 = perf_counter()
     # ---- one read of every leaf, in order (checks 7 and 2 judge the same objects): each
     # tensor leaf on one GPU as its slot declares, the records' bytes
@@ -317,19 +325,19 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
                 [o.shape for o in tensors] == lay.slot_shapes and
                 all([o.is_cuda for o in tensors]) and
                 all([o.is_contiguous() for o in tensors])):
-            return NOT_DECIDED
+            return no("a tensor leaf is not on the GPU as its slot declares")
         devices = {o.get_device() for o in tensors}
         if len(devices) != 1 or any(c.record_leaf(objs[i]) is not None for i in range(n_s)):
-            return NOT_DECIDED
+            return no("leaves on several devices, or records that are tensor leaves")
         dev_index = devices.pop()
         leaf_ptr = np.zeros(c.n_leaves, dtype=np.uint64)
         leaf_ptr[n_s:] = np.fromiter((o.data_ptr() for o in tensors), dtype=np.uint64,
                                      count=len(tensors))
         records = [c.encode_record(objs[i]) for i in range(n_s)]
-    except Exception:
-        return NOT_DECIDED
+    except Exception as e:
+        return no(f"reading the leaves: {type(e).__name__}: {e}")
     if not _is_digest(claimed) or not lay.headers_ok:
-        return NOT_DECIDED
+        return no("the claimed root is not a digest, or a slot's dtype has no encoding")
     dev = torch.device("cuda", dev_index)
     ctx.state.leaves, ctx.state.claimed_root = leaves, claimed
     rec_len = np.array([len(r) for r in records], dtype=np.uint64)
@@ -349,8 +357,8 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
     if early:
         try:
             update = _update_plan(c, e, objs, leaf_key, ctx, bands)
-        except (ValueError, RuntimeError):
-            return NOT_DECIDED
+        except (ValueError, RuntimeError) as err:
+            return no(f"check 6a's plan: {err}")
         buf = e.buffers
         key = buf["key"]
         _stage_records(e, records)
@@ -362,10 +370,11 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
             upd = update.run(buf["update"], main)
 
     # ---- check 5's operands, a group at a time
+    wait = main if early else None
     try:
         replay = c.replay(leaves)
-    except Exception:
-        return _undecided(main if early else None)
+    except Exception as err:
+        return no(f"the replay: {type(err).__name__}: {err}", wait)
     ctx.state.replay = replay
     if getattr(replay, "prover_supplied", False):
         if not ctx.trust_prover_operands:
@@ -380,16 +389,16 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
             if len(grp) == 1:
                 a, b = replay.operands(s0.m)
                 if a.shape != s0.a_shape or b.shape != s0.b_shape:
-                    return _undecided(main if early else None)
+                    return no(f"{s0.name}: served operands of other shapes", wait)
             else:
                 a, b = replay.operand_group([specs[i].m for i in grp])
                 g = len(grp)
                 if a.shape != (g, *s0.a_shape) or b.shape != (g, *s0.b_shape):
-                    return _undecided(main if early else None)
+                    return no(f"{s0.name}: a served group of other shapes", wait)
             served.add(gi, grp, a, b)
         served.finish()
-    except Exception:
-        return _undecided(main if early else None)
+    except Exception as err:
+        return no(f"serving the products: {type(err).__name__}: {err}", wait)
     bias = None
     if lay.bias_names:
         bias = torch.cat([objs[c.w_t_index(nm)].reshape(-1) for nm in lay.bias_names]) \
@@ -410,8 +419,10 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
         cache.hits += 1
         _enqueue_measuring(e, key)
     elif early:
-        # The operands moved, the leaves did not: the hashing already in flight stands, this
-        # step is measured on a plan of its own, and the next step builds a new pair.
+        # The operands moved, the leaves did not (a replay rebuilt for the step allocates its
+        # operands anew): the kept leaf plan hashes as planned (its fused kernel still reads
+        # the kept plan's challenges, and its sums go unused), and this step is measured on a
+        # Freivalds plan of its own, freed once its rows are read.
         table = served.rows.copy()
         keep = list(served.keep)
         if bias is not None:
@@ -419,21 +430,22 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
             keep.append(bias)
         try:
             alone = native.FvPlan.from_table(lib, table, keep, ctx.k, ctx.kappa_guard, dev)
-        except (ValueError, RuntimeError):
-            return _undecided(main)
+        except (ValueError, RuntimeError) as err:
+            return no(f"the Freivalds plan: {err}", main)
+        _enqueue_chunks(e)
         alone.rows(key, buf["rows"], main)
     else:
         cache.close()
         try:
             e = _build(c, served, bias, records, objs, leaf_key, fv_key, ctx, dev)
-        except (ValueError, RuntimeError):  # a layout the plans refuse: the slots decide
-            return NOT_DECIDED
+        except (ValueError, RuntimeError) as err:  # a layout the plans refuse
+            return no(f"the plans: {err}")
         cache.entry = e
         cache.builds += 1
         try:
             update = _update_plan(c, e, objs, leaf_key, ctx, bands)
-        except (ValueError, RuntimeError):
-            return NOT_DECIDED
+        except (ValueError, RuntimeError) as err:
+            return no(f"check 6a's plan: {err}")
         buf = e.buffers
         key = buf["key"]
         _stage_records(e, records)
@@ -483,7 +495,6 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
     main.synchronize()
     if alone is not None:
         alone.close()
-        cache.close()
     t4 = perf_counter()
     timings["gpu"] = t4 - t3
 
@@ -496,10 +507,10 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
     if len(ctx.prev_w_hashes) != c.n_w:
         raise RuntimeError(f"{len(ctx.prev_w_hashes)} chained hashes for {c.n_w} weights")
     if dig[lay.w_t_slots].tobytes() != b"".join(ctx.prev_w_hashes):
-        return NOT_DECIDED
+        return no(f"check {ctx.chain_check_id} would not pass")
     # 2: every leaf finite, none written in place since it was read
     if first_bad < c.n_leaves or leaves.first_changed() is not None:
-        return NOT_DECIDED
+        return no("check 2 would not pass")
     raw = dig.tobytes()
     ctx.state.leaf_hashes = [raw[i:i + 32] for i in range(0, 32 * c.n_leaves, 32)]
     # 6a
@@ -507,18 +518,18 @@ def decide(c: Any, store: TranscriptStore, ctx: StepContext, bands: Bands,
         res = native.UpdatePlan.decode(host["update"])
         for nm, (rho_max, first_nf, first_over) in zip(c.linear_weights, res):
             if first_nf is not None or (ctx.judge and first_over is not None):
-                return NOT_DECIDED
+                return no("check 6a would not pass")
             ctx.stats.tensors.append(TensorStat(nm, "6a", rho_max))
     # 5
     if judge_rows(c, host["rows"].numpy(), device_first, kappa_max, ctx, bands) is not None:
-        return NOT_DECIDED
+        return no("check 5 would not pass")
     # 6b (over the replay's glue; nothing to do for the prover's operands)
     if CHECKS["6b"](store, c, ctx, bands) is not None:
-        return NOT_DECIDED
+        return no("check 6b would not pass")
     # 2.root
     ctx.state.recomputed_root = root
     if root != claimed:
-        return NOT_DECIDED
+        return no("the root comparison would not pass")
     timings["judge"] = perf_counter() - t4
     return None
 
@@ -599,18 +610,15 @@ def _enqueue_hashing(e: _Entry, key: torch.Tensor, start: torch.cuda.Event) -> N
     e.fv.run_stage(native.FvPlan.P_PASS, key, rows, main)
 
 
-def _enqueue_measuring(e: _Entry, key: torch.Tensor) -> None:
-    """The B pass and its reduction on the current stream; then the fused chunk kernel and
-    the other leaves' chunks on the side stream beside the A stage, and the fused products'
-    sums once the fused chunk kernel is done."""
+def _enqueue_chunks(e: _Entry) -> torch.cuda.Event | None:
+    """A fused leaf plan's chunk kernels on the side stream, after what the current stream
+    has enqueued so far: the fused one, then the other leaves'. Returns the fused kernel's
+    end (``None`` for an unfused plan, whose chunks :func:`_enqueue_hashing` enqueued)."""
+    if not e.leaf.fused:
+        return None
     main = torch.cuda.current_stream()
     buf = e.buffers
-    side, digests, bad, rows = buf["side"], buf["digests"], buf["bad"], buf["rows"]
-    e.fv.run_stage(1, key, rows, main)
-    e.fv.run_stage(2, key, rows, main)
-    if not e.leaf.fused:
-        e.fv.run_stage(3, key, rows, main)
-        return
+    side, digests, bad = buf["side"], buf["digests"], buf["bad"]
     ready = torch.cuda.Event()
     ready.record(main)
     side.wait_event(ready)
@@ -619,9 +627,22 @@ def _enqueue_measuring(e: _Entry, key: torch.Tensor) -> None:
         e.leaf.run_stage(native.LeafPlan.FUSED_CHUNKS, digests, bad, side)
         c_end.record(side)
         e.leaf.run_stage(native.LeafPlan.PLAIN_CHUNKS, digests, bad, side)
+    return c_end
+
+
+def _enqueue_measuring(e: _Entry, key: torch.Tensor) -> None:
+    """The B pass and its reduction on the current stream; then the fused chunk kernel and
+    the other leaves' chunks on the side stream beside the A stage, and the fused products'
+    sums once the fused chunk kernel is done."""
+    main = torch.cuda.current_stream()
+    rows = e.buffers["rows"]
+    e.fv.run_stage(1, key, rows, main)
+    e.fv.run_stage(2, key, rows, main)
+    c_end = _enqueue_chunks(e)
     e.fv.run_stage(3, key, rows, main)
-    main.wait_event(c_end)
-    e.fv.run_stage(native.FvPlan.P_FUSED, key, rows, main)
+    if c_end is not None:
+        main.wait_event(c_end)
+        e.fv.run_stage(native.FvPlan.P_FUSED, key, rows, main)
 
 
 def _timed_run(e: _Entry, key: torch.Tensor, update: native.UpdatePlan | None

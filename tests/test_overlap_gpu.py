@@ -198,3 +198,30 @@ def test_plans_run_again_only_on_the_same_layout(lib):
     v5, rej = run(step.leaves, _root(c, step.leaves), v1.plans)
     assert rej is None and v5.overlapped == [1] and (ov.builds, ov.hits) == (2, 3)
     v5.close()
+
+
+def test_moved_operands_over_the_same_leaves(lib):
+    """A replay rebuilt for the next step serves its operands from new buffers while the
+    leaves stay where they were: the kept leaf plan still hashes every leaf, the step is
+    measured on a Freivalds plan of its own and accepted on the overlapped path with the same
+    kept hashes; the kept plans stay for the next step."""
+    from verification.prover.synthetic import CapturedReplay
+    c, step = _step(8)
+    claimed = _root(c, step.leaves)
+    v1, rej = _run(c, step.leaves, claimed, overlap=True, replay=step.replay())
+    assert rej is None and v1.overlapped == [1]
+    moved = {m: (a.clone(), b.clone()) for m, (a, b) in step.operands.items()}
+    v2, rej = _run(c, step.leaves, claimed, overlap=True, replay=CapturedReplay(moved),
+                   plans=v1.plans)
+    assert rej is None and v2.overlapped == [1], v2.plans.overlap.declined
+    assert v2._chain == v1._chain
+    assert v2.plans.overlap.builds == 1 and v2.plans.overlap.hits == 0
+    slow, rej = _run(c, step.leaves, claimed, overlap=False, replay=CapturedReplay(moved))
+    assert rej is None
+    _close(v2, slow)
+    v3, rej = _run(c, step.leaves, claimed, overlap=True, replay=step.replay(),
+                   plans=v1.plans)
+    assert rej is None and v3.overlapped == [1]
+    assert (v3.plans.overlap.builds, v3.plans.overlap.hits) == (1, 1)
+    for v in (v1, v2, v3, slow):
+        v.close()
