@@ -5,7 +5,10 @@
 The library lands next to this file, so it travels with the source tree to the GPU host.
 Every HIP source is compiled with packed FP32 instructions switched off
 (``-Xclang -target-feature -Xclang -packed-fp32-ops``) and without fast-math, so the fp64
-verdict arithmetic keeps IEEE semantics.
+verdict arithmetic keeps IEEE semantics. Matrix-core instructions take their accumulators in
+ordinary VGPRs (``-amdgpu-mfma-vgpr-form``): the row and twin passes then keep them there
+instead of copying them between VGPRs and AGPRs around every MFMA (the twin pass's loop went
+from 142 to 111 VALU instructions per 16-row stage, and every row pass lost its copies).
 """
 
 from __future__ import annotations
@@ -32,7 +35,8 @@ def hipcc() -> str:
 def flags() -> list[str]:
     return ["-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}",
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            "-ffp-contract=off", "-fno-fast-math", "-Wall", "-Wno-unused-function",
+            "-ffp-contract=off", "-fno-fast-math", "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+            "-Wall", "-Wno-unused-function",
             f"-I{HERE.parent / 'include'}"]
 
 

@@ -57,6 +57,7 @@ typedef float v4f32 __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 enum : uint32_t { DT_F32 = 0, DT_BF16 = 1 };
 
@@ -294,6 +295,31 @@ __device__ __forceinline__ void stage_weights(uint64_t u, uint64_t w, uint32_t c
       *reinterpret_cast<v4f32*>(s_u + t) = ua[v];
       *reinterpret_cast<v4f32*>(s_w + t) = wa[v];
     }
+  }
+}
+
+// The twin pass's one weight w of columns c0 .. c1 − 1 into LDS, as stage_weights stages two
+// (c1 − c0 ≤ CHUNK; the twin pass reads no column past c1).
+template <uint32_t CHUNK>
+__device__ __forceinline__ void stage_weight(uint64_t w, uint32_t c0, uint32_t c1, float* s_w) {
+  constexpr uint32_t NV = (CHUNK + 1023) / 1024;  // 4-column groups per thread
+  const float* wp = reinterpret_cast<const float*>(w) + c0;
+  const uint32_t n = c1 - c0;
+  v4f32 wa[NV];
+#pragma unroll
+  for (uint32_t v = 0; v < NV; v++) {
+    const uint32_t t = 4 * (threadIdx.x + 256 * v);
+    if (t + 4 <= n) {
+      wa[v] = gload<v4f32>(wp + t);
+    } else {
+#pragma unroll
+      for (uint32_t e = 0; e < 4; e++) wa[v][e] = t + e < n ? gload<float>(wp + t + e) : 0.f;
+    }
+  }
+#pragma unroll
+  for (uint32_t v = 0; v < NV; v++) {
+    const uint32_t t = 4 * (threadIdx.x + 256 * v);
+    if (t < CHUNK) *reinterpret_cast<v4f32*>(s_w + t) = wa[v];
   }
 }
 
@@ -573,6 +599,7 @@ constexpr uint32_t kTwinCols = 1024;
 constexpr uint32_t kTwinStrip = 32 * KU;  // columns per stage: KU K-steps of 32
 constexpr uint32_t kTwinColStep = 128;    // a twin's X has columns in multiples of this
 static_assert(kTwinColStep % kTwinStrip == 0 && kTwinCols % kTwinColStep == 0, "twin tiles");
+constexpr uint32_t kTwinSlots = 5;  // a row's m₁ values in a wave's LDS: X·V₁'s (k ≤ 4), ν₁
 constexpr uint32_t kSlabRow = 36;     // bf16 per slab row: 32 columns and 4 of padding, so
                                       // the four row groups a read touches sit 8 banks apart
 
@@ -608,35 +635,29 @@ __device__ __forceinline__ void twin_load(TwinStage& st, const TwinJob& J, uint3
   st.w2 = gload<float>(reinterpret_cast<const float*>(J.w2) + rr + i);
 }
 
-__device__ __forceinline__ void twin_stage(const TwinStage& st, const u32x4 (&v1)[KU],
-                                           v4f32 (&acc2)[2 * KU], double& u2sum,
-                                           float* acc_w, uint16_t* slab, const float* s_u,
-                                           const float* s_w, uint32_t row0, uint32_t off,
-                                           uint32_t k, uint32_t lane, uint32_t g, uint32_t i) {
-  // m₁: X·V₁ for the stage's 16 rows, and the two sums of row i over the lane's columns
+__device__ __forceinline__ void twin_stage(const TwinStage& st, const u32x4 (&bv1)[KU],
+                                           const u32x4 (&bu1)[KU], v4f32 (&acc2)[2 * KU],
+                                           float (&colsq)[2 * KU], double& u2sum, float* acc_w,
+                                           uint16_t* slab, uint32_t row0, uint32_t k,
+                                           uint32_t lane, uint32_t g, uint32_t i) {
+  // m₁: X·V₁ and |X|·u₁ for the stage's 16 rows on the matrix cores (bv1: V₁'s slots 0..11,
+  // bu1: u₁'s terms in slots 12..14), and row i's sum of squares for U₂
   v4f32 acc1 = {0.f, 0.f, 0.f, 0.f};
-  float s1 = 0.f, s2 = 0.f, q2 = 0.f;
+  float q2 = 0.f;
 #pragma unroll
   for (uint32_t u = 0; u < KU; u++) {
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+    for (int h = 0; h < 2; h++) {
+      const v2u32 xa = {st.x[u][2 * h], st.x[u][2 * h + 1]};
       acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-          __builtin_bit_cast(v4i16, v2u32{st.x[u][2 * h], st.x[u][2 * h + 1]}),
-          __builtin_bit_cast(v4i16, v2u32{v1[u][2 * h], v1[u][2 * h + 1]}), acc1, 0, 0, 0);
-    const uint32_t o = off + 32 * u;
-    const v4f32 ua = *reinterpret_cast<const v4f32*>(s_u + o);
-    const v4f32 ub = *reinterpret_cast<const v4f32*>(s_u + o + 4);
-    const v4f32 wa = *reinterpret_cast<const v4f32*>(s_w + o);
-    const v4f32 wb = *reinterpret_cast<const v4f32*>(s_w + o + 4);
-    const float uc[8] = {ua[0], ua[1], ua[2], ua[3], ub[0], ub[1], ub[2], ub[3]};
-    const float wc[8] = {wa[0], wa[1], wa[2], wa[3], wb[0], wb[1], wb[2], wb[3]};
+          __builtin_bit_cast(v4i16, xa),
+          __builtin_bit_cast(v4i16, v2u32{bv1[u][2 * h], bv1[u][2 * h + 1]}), acc1, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+          __builtin_bit_cast(v4i16, v2u32{xa.x & 0x7FFF7FFFu, xa.y & 0x7FFF7FFFu}),
+          __builtin_bit_cast(v4i16, v2u32{bu1[u][2 * h], bu1[u][2 * h + 1]}), acc1, 0, 0, 0);
+    }
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      const float xl = bf_lo(st.x[u][e]), xh = bf_hi(st.x[u][e]);
-      s1 = fmaf(fabsf(xl), uc[2 * e], s1);
-      s1 = fmaf(fabsf(xh), uc[2 * e + 1], s1);
-      s2 = fmaf(xl * xl, wc[2 * e], s2);
-      s2 = fmaf(xh * xh, wc[2 * e + 1], s2);
       // (a bit_cast straight from the vector element compiled to the first element every
       // time; through a scalar it does not)
       const uint32_t wv = st.x[u][e];
@@ -646,7 +667,8 @@ __device__ __forceinline__ void twin_stage(const TwinStage& st, const u32x4 (&v1
   }
   u2sum = fma((double)q2, (double)st.w2, u2sum);
 
-  // m₂: Xᵀ·V₂ and |Xᵀ|·u₂ through the slab, one K-step at a time
+  // m₂: Xᵀ·V₂ and |Xᵀ|·u₂ through the slab, one K-step at a time; the same reads give each
+  // lane's column sums of squares for U₁ (two rows of one column per word)
   const v2u32 zero = {0u, 0u};
   const v4i16 bv = __builtin_bit_cast(v4i16, i < 12 ? st.v2 : zero);
   const v4i16 bu = __builtin_bit_cast(v4i16, i >= 12 ? st.v2 : zero);
@@ -658,39 +680,44 @@ __device__ __forceinline__ void twin_stage(const TwinStage& st, const u32x4 (&v1
 #pragma unroll
     for (uint32_t cb = 0; cb < 2; cb++) {
       const uint16_t* rd = slab + (4 * g) * kSlabRow + 16 * cb + i;  // rows 4g .., column
-      const uint32_t lo = (uint32_t)rd[0] | (uint32_t)rd[kSlabRow] << 16;
-      const uint32_t hi = (uint32_t)rd[2 * kSlabRow] | (uint32_t)rd[3 * kSlabRow] << 16;
+      // each 16-bit read into its half of the word (a d16 and a d16_hi read, no shifts)
+      u16x2 l2, h2;
+      l2.x = rd[0];
+      l2.y = rd[kSlabRow];
+      h2.x = rd[2 * kSlabRow];
+      h2.y = rd[3 * kSlabRow];
+      const uint32_t lo = __builtin_bit_cast(uint32_t, l2);
+      const uint32_t hi = __builtin_bit_cast(uint32_t, h2);
       v4f32& a = acc2[2 * u + cb];
       a = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4i16, v2u32{lo, hi}),
                                                     bv, a, 0, 0, 0);
       a = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
           __builtin_bit_cast(v4i16, v2u32{lo & 0x7FFF7FFFu, hi & 0x7FFF7FFFu}), bu, a, 0, 0,
           0);
+      float& cq = colsq[2 * u + cb];
+      cq = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, lo),
+                                           __builtin_bit_cast(bf16x2, lo), cq, false);
+      cq = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, hi),
+                                           __builtin_bit_cast(bf16x2, hi), cq, false);
     }
   }
 
   // m₁: the stage's row values into the wave's accumulator. Lane (g, i) holds rows 4g + e and
-  // slot i; challenge j's three terms are slots 3j .. 3j + 2.
+  // slot i; challenge j's three terms are slots 3j .. 3j + 2, u₁'s are slots 12 .. 14.
 #pragma unroll
   for (int e = 0; e < 4; e++) {
     const float v0 = acc1[e];
     const float va = __shfl(v0, (int)lane + 1);
     const float vb = __shfl(v0, (int)lane + 2);
-    if (i % 3 == 0 && i / 3 < k) acc_w[(row0 + 4 * g + e) * 6 + i / 3] += (v0 + va) + vb;
-  }
-  s1 += __shfl_xor(s1, 16);
-  s1 += __shfl_xor(s1, 32);
-  s2 += __shfl_xor(s2, 16);
-  s2 += __shfl_xor(s2, 32);
-  if (g == 0) {
-    acc_w[(row0 + i) * 6 + 4] += s1;
-    acc_w[(row0 + i) * 6 + 5] += s2;
+    const uint32_t slot = i == 12 ? 4u : i / 3;
+    if (i % 3 == 0 && (i / 3 < k || i == 12))
+      acc_w[(row0 + 4 * g + e) * kTwinSlots + slot] += (v0 + va) + vb;
   }
 }
 
 __device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
                                           const uint32_t* __restrict__ tile_job, uint32_t k,
-                                          uint32_t tidx, float* s_u, float* s_w, float* s_acc,
+                                          uint32_t tidx, float* s_w, float* s_acc,
                                           uint16_t* s_slab, double* s_red) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63, g = lane >> 4, i = lane & 15;
@@ -700,37 +727,53 @@ __device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
   const uint32_t r0 = rt * kTwinRows, r1 = min(r0 + kTwinRows, J.rows);
   const uint32_t c0 = ct * kTwinCols, c1 = min(c0 + kTwinCols, J.cols);
   const uint32_t nrg = (r1 - r0) / 16, nstrip = (c1 - c0) / kTwinStrip;
-  float* acc_w = s_acc + wave * kTwinRows * 6;
+  float* acc_w = s_acc + wave * kTwinRows * kTwinSlots;
   uint16_t* slab = s_slab + wave * 16 * kSlabRow;
-  stage_weights<kTwinCols>(J.u1, J.w1, c0, c1, kTwinCols, s_u, s_w);
-  for (uint32_t t = lane; t < kTwinRows * 6; t += 64) acc_w[t] = 0.f;
+  stage_weight<kTwinCols>(J.w1, c0, c1, s_w);
+  for (uint32_t t = lane; t < kTwinRows * kTwinSlots; t += 64) acc_w[t] = 0.f;
   __syncthreads();
 
-  double u2sum = 0.0;
+  double u1sum = 0.0, u2sum = 0.0;
   for (uint32_t s = wave; s < nstrip; s += 4) {
     const uint32_t cs = c0 + s * kTwinStrip;
-    // V₁ of the strip's K-steps: the same for every row group
-    u32x4 v1[KU];
+    // V₁ of the strip's K-steps, the same for every row group: its challenge terms (slots
+    // 0..11) for X·V₁ and its u₁ terms (slots 12..14) for |X|·u₁
+    u32x4 bv1[KU], bu1[KU];
 #pragma unroll
-    for (uint32_t u = 0; u < KU; u++)
-      v1[u] = gload<u32x4>(reinterpret_cast<const char*>(J.v1) +
-                           ((uint64_t)((cs + 32 * u) / 8 + g) * 16 + i) * 16);
+    for (uint32_t u = 0; u < KU; u++) {
+      const u32x4 v = gload<u32x4>(reinterpret_cast<const char*>(J.v1) +
+                                   ((uint64_t)((cs + 32 * u) / 8 + g) * 16 + i) * 16);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      bv1[u] = i < 12 ? v : z;
+      bu1[u] = i < 12 ? z : v;
+    }
     v4f32 acc2[2 * KU];
+    float colsq[2 * KU];
 #pragma unroll
-    for (uint32_t q = 0; q < 2 * KU; q++) acc2[q] = v4f32{0.f, 0.f, 0.f, 0.f};
-    const uint32_t off = cs - c0 + 8 * g;
+    for (uint32_t q = 0; q < 2 * KU; q++) {
+      acc2[q] = v4f32{0.f, 0.f, 0.f, 0.f};
+      colsq[q] = 0.f;
+    }
     // Two stages in flight: the next row group's loads go out before this one is computed
     // (past the last group they reread it, so every load is unconditional).
     TwinStage sa, sb;
     twin_load(sa, J, r0, cs, g, i);
     for (uint32_t rg = 0; rg < nrg; rg += 2) {
       twin_load(sb, J, r0 + 16 * min(rg + 1, nrg - 1), cs, g, i);
-      twin_stage(sa, v1, acc2, u2sum, acc_w, slab, s_u, s_w, 16 * rg, off, k, lane, g, i);
+      twin_stage(sa, bv1, bu1, acc2, colsq, u2sum, acc_w, slab, 16 * rg, k, lane, g, i);
       twin_load(sa, J, r0 + 16 * min(rg + 2, nrg - 1), cs, g, i);
       if (rg + 1 < nrg)
-        twin_stage(sb, v1, acc2, u2sum, acc_w, slab, s_u, s_w, 16 * (rg + 1), off, k, lane,
-                   g, i);
+        twin_stage(sb, bv1, bu1, acc2, colsq, u2sum, acc_w, slab, 16 * (rg + 1), k, lane, g,
+                   i);
     }
+    // U₁ of the strip: lane (g, i)'s squares of column 32u + 16cb + i (rows 4g .. 4g + 3 of
+    // every row group) times w₁ of that column
+#pragma unroll
+    for (uint32_t u = 0; u < KU; u++)
+#pragma unroll
+      for (uint32_t cb = 0; cb < 2; cb++)
+        u1sum = fma((double)colsq[2 * u + cb], (double)s_w[cs - c0 + 32 * u + 16 * cb + i],
+                    u1sum);
     // m₂'s partials of the strip's columns: lane (g, i) of block q holds columns
     // 16q + 4g + e and slot i.
     float* dot2 = reinterpret_cast<float*>(J.dot2);
@@ -750,25 +793,34 @@ __device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
       }
     }
   }
-  for (int o = 32; o > 0; o >>= 1) u2sum += __shfl_xor(u2sum, o);
-  if (lane == 0) s_red[wave] = u2sum;
+  for (int o = 32; o > 0; o >>= 1) {
+    u1sum += __shfl_xor(u1sum, o);
+    u2sum += __shfl_xor(u2sum, o);
+  }
+  if (lane == 0) {
+    s_red[wave] = u2sum;
+    s_red[4 + wave] = u1sum;
+  }
   __syncthreads();
-  // m₁'s partials of the tile's rows: the four waves' accumulators in wave order
+  // m₁'s partials of the tile's rows: the four waves' accumulators in wave order, and the
+  // tile's Σx²w₁ total at its first row
   float* dot1 = reinterpret_cast<float*>(J.dot1);
   float* abs1 = reinterpret_cast<float*>(J.abs1);
   double* sq1 = reinterpret_cast<double*>(J.sq1);
   const uint64_t rbase = (uint64_t)ct * J.rows_pad1;
+  const double tot1 = ((s_red[4] + s_red[5]) + s_red[6]) + s_red[7];
   for (uint32_t row = threadIdx.x; row < r1 - r0; row += blockDim.x) {
-    float d[6];
+    float d[kTwinSlots];
 #pragma unroll
-    for (int t = 0; t < 6; t++) d[t] = s_acc[row * 6 + t];
+    for (uint32_t t = 0; t < kTwinSlots; t++) d[t] = s_acc[row * kTwinSlots + t];
 #pragma unroll
     for (uint32_t w = 1; w < 4; w++)
 #pragma unroll
-      for (int t = 0; t < 6; t++) d[t] += s_acc[(w * kTwinRows + row) * 6 + t];
+      for (uint32_t t = 0; t < kTwinSlots; t++)
+        d[t] += s_acc[(w * kTwinRows + row) * kTwinSlots + t];
     for (uint32_t j = 0; j < k; j++) gstore<float>(dot1 + (rbase + r0 + row) * k + j, d[j]);
     gstore<float>(abs1 + rbase + r0 + row, d[4]);
-    gstore<double>(sq1 + rbase + r0 + row, (double)d[5]);
+    gstore<double>(sq1 + rbase + r0 + row, row == 0 ? tot1 : 0.0);
   }
   // m₂'s Σx²w₂ partials of the tile's columns: the tile's total at its first column
   const double tot = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
@@ -783,14 +835,13 @@ __global__ __launch_bounds__(256) void twin_pass(const TwinJob* __restrict__ job
                                                  const uint32_t* __restrict__ tile_job,
                                                  uint32_t k, uint32_t n_tiles,
                                                  uint32_t* __restrict__ queue) {
-  __shared__ __align__(16) float s_u[kTwinCols];
   __shared__ __align__(16) float s_w[kTwinCols];
-  __shared__ __align__(16) float s_acc[4 * kTwinRows * 6];
+  __shared__ __align__(16) float s_acc[4 * kTwinRows * kTwinSlots];
   __shared__ __align__(16) uint16_t s_slab[4 * 16 * kSlabRow];
-  __shared__ double s_red[4];
+  __shared__ double s_red[8];
   __shared__ uint32_t s_tile;
   tile_loop(n_tiles, queue, &s_tile, [&](uint32_t t) {
-    twin_tile(jobs, tile_job, k, t, s_u, s_w, s_acc, s_slab, s_red);
+    twin_tile(jobs, tile_job, k, t, s_w, s_acc, s_slab, s_red);
   });
 }
 
