@@ -1244,10 +1244,14 @@ __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ job
   };
   if (i == 0 && hc > H) rest(0, hc - H);
   if (i + 1 == J.n && lf < L) rest(lf - H, L - H);
-  if (exact) {  // a run met exponents out of fp32 squares' range: the row's squares in fp64
+  if (exact) {  // a run met exponents out of fp32 squares' range: the row's sums in fp64
+    // (|x| too: the chunk kernel takes a bf16 pair's |x| with v_dot2, whose subnormal inputs
+    // are those of a pair marked here)
+    s1 = 0.0;
     s2 = 0.0;
     for (uint64_t e = (uint64_t)i * J.w; e < (uint64_t)(i + 1) * J.w; e++) {
       const double x = elem(e);
+      s1 += fabs(x);
       s2 += x * x;
     }
   }

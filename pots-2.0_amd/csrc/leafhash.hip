@@ -160,9 +160,14 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 // largest biased exponent; outside [kSqLo, kSqHi] the run is marked for the exact squares.
 typedef float v2f32 __attribute__((ext_vector_type(2)));
 
+//
+// `s1p`, `q2p`: an unmasked bf16 pair's Σ|x| and Σx², taken with the NaN/Inf test (unused
+// otherwise). `zero`: every element of the pair is zero, whose squares are exact whatever the
+// exponent test says.
 template <int ESZ, bool MASKED, int K>
-__device__ __forceinline__ void run_add(const uint32_t* w, uint64_t rcol, uint32_t lo,
-                                        uint32_t hi, uint32_t emax, PRun& a) {
+__device__ __forceinline__ void run_add(const uint32_t* w, float s1p, float q2p, uint64_t rcol,
+                                        uint32_t lo, uint32_t hi, uint32_t emax, bool zero,
+                                        PRun& a) {
   constexpr int NE = 128 / ESZ;
   static_assert(K == 1 || K == 2 || K == 4, "R rows of 1, 2 or 4 challenges");
   float q = 0.f;
@@ -190,18 +195,17 @@ __device__ __forceinline__ void run_add(const uint32_t* w, uint64_t rcol, uint32
     } else {
       a.d0 = fmaf(x, reinterpret_cast<const POTS_CONST float*>(rcol)[t], a.d0);
     }
-    a.s1 += fabsf(x);
-    if (MASKED || ESZ == 4) q = fmaf(x, x, q);
-  }
-  if (!MASKED && ESZ == 2) {  // lo² + hi² per word; products of bf16 values are exact in fp32
-#pragma unroll
-    for (int u = 0; u < 32; u++) {
-      const bf16x2 v = __builtin_bit_cast(bf16x2, w[u]);
-      q = __builtin_amdgcn_fdot2_f32_bf16(v, v, q, false);
+    if (MASKED || ESZ == 4) {
+      a.s1 += fabsf(x);
+      q = fmaf(x, x, q);
     }
   }
+  if (!MASKED && ESZ == 2) {
+    a.s1 += s1p;
+    q = q2p;
+  }
   a.s2 += (double)q;
-  a.exact |= emax < kSqLo || emax > kSqHi;
+  a.exact |= (emax < kSqLo && !zero) || emax > kSqHi;
   a.live = true;
 }
 
@@ -325,15 +329,34 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
         m0[j] = w[j + SH];
         m1[j] = w[16 + j + SH];
       }
-      // The NaN/Inf test's per-pair maximum (a tree, then one merge into the running one).
+      // The NaN/Inf test's per-pair maximum (a tree, then one merge into the running one). A
+      // fused bf16 leaf's words are masked to |x| (sign bits cleared) instead of to their
+      // exponents: a half reaches 0x7F80 for the same values, and the pair's Σ|x| takes the
+      // masked words two elements per v_dot2 against (1, 1), beside Σx² from each word
+      // against itself (products of bf16 values are exact in fp32).
+      const uint32_t pmask = ESZ == 2 ? 0x7FFF7FFFu : fin.mask;
       u16x2 pm[8];
+      float s1p = 0.f, q2p = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; j++) {
+        uint32_t aw[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t wu = w[4 * j + e + SH];
+          aw[e] = wu & pmask;
+          if constexpr (ESZ == 2) {
+            s1p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, aw[e]),
+                                                  __builtin_bit_cast(bf16x2, 0x3F803F80u), s1p,
+                                                  false);
+            q2p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wu),
+                                                  __builtin_bit_cast(bf16x2, wu), q2p, false);
+          }
+        }
         pm[j] = __builtin_elementwise_max(
-            __builtin_elementwise_max(__builtin_bit_cast(u16x2, w[4 * j + SH] & fin.mask),
-                                      __builtin_bit_cast(u16x2, w[4 * j + 1 + SH] & fin.mask)),
-            __builtin_elementwise_max(__builtin_bit_cast(u16x2, w[4 * j + 2 + SH] & fin.mask),
-                                      __builtin_bit_cast(u16x2, w[4 * j + 3 + SH] & fin.mask)));
+            __builtin_elementwise_max(__builtin_bit_cast(u16x2, aw[0]),
+                                      __builtin_bit_cast(u16x2, aw[1])),
+            __builtin_elementwise_max(__builtin_bit_cast(u16x2, aw[2]),
+                                      __builtin_bit_cast(u16x2, aw[3])));
       }
 #pragma unroll
       for (int j = 0; j < 4; j++) pm[j] = __builtin_elementwise_max(pm[j], pm[j + 4]);
@@ -342,8 +365,11 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
       fin.acc = __builtin_elementwise_max(fin.acc, pm[0]);
       if constexpr (ESZ != 0) {
         // the pair's largest biased exponent: bf16 halves hold it at bit 7, fp32 at bit 23
-        const uint32_t emax = ESZ == 2 ? (uint32_t)max(pm[0].x, pm[0].y) >> 7
-                                       : (uint32_t)pm[0].y >> 7;
+        const uint32_t pmax = ESZ == 2 ? (uint32_t)max(pm[0].x, pm[0].y) : (uint32_t)pm[0].y;
+        const uint32_t emax = pmax >> 7;
+        // an all-zero pair, whose squares are exact (bf16; fp32's test keeps only exponents,
+        // which do not tell zeros from subnormals)
+        const bool zero = ESZ == 2 && pmax == 0;
         if (!pinit) {  // the chunk's first interior pair
           const uint64_t po = o - H;
           prow = (uint32_t)(po / f.row_bytes);
@@ -357,8 +383,8 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
             (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(f.r >> 32)) << 32 |
             (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)f.r);
         if (rb + 128 <= f.row_bytes) {
-          run_add<ESZ, false, K>(w + SH, rbase + (uint64_t)(rb / ESZ) * (4 * K), 0, 128 / ESZ,
-                                 emax, run);
+          run_add<ESZ, false, K>(w + SH, s1p, q2p, rbase + (uint64_t)(rb / ESZ) * (4 * K), 0,
+                                 128 / ESZ, emax, zero, run);
           prb = rb + 128;
           if (prb == f.row_bytes) {
             run_flush(f, H, prow, c, run);
@@ -367,12 +393,12 @@ __device__ __forceinline__ void hash_chunk(const LeafDesc& d, const uint32_t* __
           }
         } else {  // the pair ends row prow at element tb and starts row prow + 1
           const uint32_t tb = (f.row_bytes - rb) / ESZ;
-          run_add<ESZ, true, K>(w + SH, rbase + (uint64_t)(rb / ESZ) * (4 * K), 0, tb, emax,
-                                run);
+          run_add<ESZ, true, K>(w + SH, 0.f, 0.f, rbase + (uint64_t)(rb / ESZ) * (4 * K), 0,
+                                tb, emax, zero, run);
           run_flush(f, H, prow, c, run);
           prow++;
-          run_add<ESZ, true, K>(w + SH, rbase - (uint64_t)tb * (4 * K), tb, 128 / ESZ, emax,
-                                run);
+          run_add<ESZ, true, K>(w + SH, 0.f, 0.f, rbase - (uint64_t)tb * (4 * K), tb,
+                                128 / ESZ, emax, zero, run);
           prb = rb + 128 - f.row_bytes;
         }
       }

@@ -37,12 +37,17 @@ def _product(n, q, w, dt, seed, tamper=()):
     return a, b, p
 
 
-def _run_case(lib, prods_cpu, k=4, expect_fused=None, extra_leaves=()):
+def _run_case(lib, prods_cpu, k=4, expect_fused=None, extra_leaves=(), placed=None):
     """prods_cpu: [(a, b, p)] on the CPU. Returns (rows_fused, rows_unfused, digests) after
-    checking digests and fusion counts."""
+    checking digests and fusion counts. ``placed(i, p)``: product i's P on the GPU and its
+    leaf, a view of the same memory (by default a fresh copy, the leaf P itself)."""
     from verification.commitment import native
-    dev = [(a.cuda(), b.cuda(), p.cuda()) for a, b, p in prods_cpu]
-    leaves = [p for _, _, p in dev] + [t.cuda() for t in extra_leaves]
+    dev, leaves = [], []
+    for i, (a, b, p) in enumerate(prods_cpu):
+        pd, leaf = (p.cuda(), None) if placed is None else placed(i, p)
+        dev.append((a.cuda(), b.cuda(), pd))
+        leaves.append(pd if leaf is None else leaf)
+    leaves += [t.cuda() for t in extra_leaves]
     hdrs = [O.tensor_leaf_header(O.TAG_PRODUCT, t) for t in leaves]
     kinds = [native.FINITE_KIND[t.dtype] for t in leaves]
     fvp = [native.FvProduct(a, b, p, i + 1) for i, (a, b, p) in enumerate(dev)]
@@ -119,6 +124,38 @@ def test_fused_rows_for_one_and_two_challenges(lib, k, dt):
     prods[1] = _product(n, q, w, dt, seed=41, tamper=[(77, w - 1, 3.0)])
     rows_f, rows_u = _run_case(lib, prods, k=k, expect_fused=len(prods))
     _check_rows(prods, rows_f, rows_u, k=k, tampered=(1,))
+
+
+def test_fused_leaves_of_every_header_length(lib):
+    """A product leaf's header is 4(1 + ndim) bytes, so its 128-byte pairs start at columns
+    ≡ −2(1 + ndim) (mod 8). The fused kernel reads a leaf whose payload sits 4 bytes past
+    (a 16-byte boundary + its header length), so each P is placed at the byte offset that
+    makes its leaf, a view with 1, 2, 3 or 4 dims, one the kernel fuses: the pairs' elements
+    then start at every even column offset modulo 8. Rows of 516 columns (8,192 of them: 129
+    chunk classes, 64 periods, no class padding) put the pairs at offsets that change from
+    row to row. Rows end mid-pair, and one entry is changed."""
+    shapes = [(128, 40, 1280), (128, 40, 1280), (128, 40, 1280), (128, 40, 1280),
+              (8192, 40, 516)]
+    prods = [_product(n, q, w, torch.bfloat16, seed=60 + s) for s, (n, q, w) in enumerate(shapes)]
+    n, q, w = shapes[2]
+    prods[2] = _product(n, q, w, torch.bfloat16, seed=62, tamper=[(33, 700, 3.0)])
+    dims = [1, 2, 3, 4, 2]
+    bufs = []
+
+    def placed(i, p):
+        nd = dims[i]
+        off = ((4 * (1 + nd) + 4) % 16) // 2  # elements: payload ≡ header + 4 (mod 16)
+        buf = torch.zeros(p.numel() + 8, dtype=p.dtype, device="cuda")
+        assert buf.data_ptr() % 16 == 0
+        bufs.append(buf)
+        pd = buf[off:off + p.numel()].view(p.shape)
+        pd.copy_(p)
+        leaf = pd.reshape((1,) * (nd - 2) + tuple(p.shape)) if nd >= 2 else pd.view(-1)
+        assert leaf.dim() == nd and leaf.data_ptr() == pd.data_ptr()
+        return pd, leaf
+
+    rows_f, rows_u = _run_case(lib, prods, expect_fused=len(prods), placed=placed)
+    _check_rows(prods, rows_f, rows_u, tampered=(2,))
 
 
 def test_fused_large_rows_and_many_classes(lib):
