@@ -42,9 +42,9 @@ HBM_PEAK_GBPS = 8000.0
 VALU_PEAK_OPS = 256 * 4 * 16 * 2.4e9
 # VALU instructions per byte of message on the chunk kernels' interior path (two 64-byte blocks
 # per 128-byte pair), from a static count of this build's gfx950 assembly: two compressions
-# and the NaN/Inf test, 1,438 per pair; with the fused P sums of a k = 4 plan, 1,933 per pair
+# and the NaN/Inf test, 1,438 per pair; with the fused P sums of a k = 4 plan, 1,903 per pair
 # of bf16 and 1,704 of fp32 products. Edge blocks and the tree levels are left out.
-VALU_OPS_PER_BYTE = {"plain": 1438 / 128, "fused_bf16": 1933 / 128, "fused_fp32": 1704 / 128}
+VALU_OPS_PER_BYTE = {"plain": 1438 / 128, "fused_bf16": 1903 / 128, "fused_fp32": 1704 / 128}
 METRIC = "Freivalds-verified GB/s + BLAKE3 Merkle GB/s (% HBM roofline); step verify ms"
 CONFIGS = {
     "c1": ("SmolLM2-135M step, 4x256 tokens, fp32, k=1", "smollm2_135m", 1),
