@@ -157,12 +157,13 @@ TRAFFIC_FILE = ROOT / "profiles" / "c4_kernel_counters.md"
 
 def kernel_label(name: str) -> str:
     """A kernel's name as the bench reports it: the chunk kernels by name, a row pass by the
-    pass its template arguments make it (``row_pass<XT, WEIGHTED, SQ64, NJG>``: B is
-    unweighted, A weighted, P takes its squares in fp64)."""
+    pass its template arguments make it (``row_pass<XT, WEIGHTED, SQ64, NJG, VS>``: B is
+    unweighted, A weighted, P takes its squares in fp64; VS, whether the block shares V, is
+    the launch's and not the pass's)."""
     base = name.split("(")[0].replace("void ", "").strip()
     short = base.split("::")[-1]
     if short.startswith("row_pass<"):
-        xt, weighted, sq64, _ = (x.strip().rstrip("u") for x in short[9:-1].split(","))
+        xt, weighted, sq64 = (x.strip().rstrip("u") for x in short[9:-1].split(",")[:3])
         dt = "bf16" if xt == "1" else "fp32"
         if weighted == "true":
             return f"row_pass<{dt}, weighted> (A pass)"
@@ -245,7 +246,8 @@ def trace_summary(d: Path, steps: int, warmup: int) -> int:
     # launches in the warm-up steps, the timed steps and the serialised stage leg
     print()
     for name, n_root, beside in ((chunk, 1, "the Freivalds passes"),
-                                 ("pots::row_pass<1u, true, false, 1u>", 0, "the chunk kernels")):
+                                 ("pots::row_pass<1u, true, false, 1u, false>", 0,
+                                  "the chunk kernels")):
         ck = by.get(name, [])
         n_pre = n_root + warmup
         n_leg = max(3, min(steps, 5))  # the stage leg's runs, as main() makes them

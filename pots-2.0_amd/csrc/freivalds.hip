@@ -124,52 +124,74 @@ struct SqAcc<false> {
 
 // ---- the row pass ---------------------------------------------------------------------------
 
-template <uint32_t NJG>
+// A stage of a wave's X: KU K-steps, lane (g, i) holding row i's 8 (bf16) or 4 (fp32) columns
+// of K-group g of each; and, unless the block shares V (VS), the lane's own V: slot i of
+// K-group g of each K-step, for each of the NJG groups.
+template <uint32_t NJG, bool VS>
 struct StageRegs {
   u32x4 x[KU];
-  u32x4 v[KU][NJG];
+  u32x4 v[VS ? 1 : KU][VS ? 1 : NJG];
 };
 
-// The per-lane view of one tile: X row, V slot base, weights and bounds. The full stages'
-// loads address memory as a wave-uniform base, advanced in scalar registers from K-step to
-// K-step, plus a per-lane 32-bit offset fixed for the tile, so most of the per-K-step address
-// arithmetic is scalar work.
+// Sharing V (VS): the block's four waves multiply the same columns by the same V, so each
+// stage's V (NJG groups of 16 slots for each of the stage's 4·KU K-groups) is loaded once per
+// block, every thread taking kPer of its 16-byte units, and written to one of two LDS stage
+// buffers, from which each wave reads its lanes' slots. Loaded by every wave, V was four times
+// the block's X traffic through L2 at k = 16, and the row passes ran at 37% of HBM. It costs
+// a barrier per stage, which holds the four waves together: a pass with a full grid (a block
+// per tile, many blocks on each CU) shares V; a pass limited to a block or two per CU, beside
+// the hashing kernels, loads it per lane (measured at C4: the B pass 3.56 → 3.25 ms sharing;
+// the A row pass at one block per CU 2.4-2.8 → 4.15 ms sharing, so it does not).
+template <uint32_t NJG>
+struct VStage {
+  static constexpr uint32_t kUnits = 64 * KU * NJG;  // 16-byte units of one stage's V
+  static constexpr uint32_t kPer = (kUnits + 255) / 256;
+  u32x4 v[kPer];
+};
+
+// The per-lane view of one tile: X row, weights and bounds. The full stages' X loads address
+// memory as a wave-uniform base, advanced in scalar registers from K-step to K-step, plus a
+// per-lane 32-bit offset fixed for the tile, so most of the per-K-step address arithmetic is
+// scalar work.
 struct Lane {
   const char* xrow;   // this lane's X row (clamped to the matrix)
   const char* vlane;  // V slot of this lane for K-group g of group jt·NJG
   const char* xbase;  // wave-uniform: the wave's first X row, column 0
-  const char* vbase;  // wave-uniform: V of K-group 0 of group jt·NJG, slot 0
+  const char* vjt;    // wave-uniform: V of K-group 0, group jt·NJG, slot 0
   uint64_t vstep;     // bytes of V per K-group
   uint32_t xoff;      // this lane's X bytes past xbase (its row, its 8 or 4 columns)
-  uint32_t voff;      // this lane's V bytes past vbase (its K-group, its slot)
+  uint32_t voff;      // this lane's V bytes past vjt (its K-group, its slot)
   uint32_t g, c1;
   uint32_t nvalid;    // groups of this block that exist (the last block of a row may hold fewer)
 };
 
 // A whole stage of an aligned job, every column inside the chunk: plain 16-byte loads.
-template <uint32_t XT, uint32_t NJG>
-__device__ __forceinline__ void load_full(StageRegs<NJG>& r, const Lane& L, uint32_t cs) {
+template <uint32_t XT, uint32_t NJG, bool VS>
+__device__ __forceinline__ void load_full(StageRegs<NJG, VS>& r, const Lane& L, uint32_t cs) {
   using G = Geo<XT>;
 #pragma unroll
   for (uint32_t u = 0; u < KU; u++) {
     const uint32_t cu = cs + u * G::KSTEP;
-    const char* xb = L.xbase + (uint64_t)cu * G::ESZ;               // uniform
-    const char* vb = L.vbase + (uint64_t)(cu / G::PER) * L.vstep;   // uniform
+    const char* xb = L.xbase + (uint64_t)cu * G::ESZ;  // uniform
     r.x[u] = gload<u32x4>(xb + L.xoff);
-    // Every load is unconditional, so the compiler's wait counts stay exact across the
-    // pipeline: a group past n_jg (only in a row's last column-group block) rereads the last
-    // valid group, and its results are not stored.
+    if constexpr (!VS) {
+      const char* vb = L.vjt + (uint64_t)(cu / G::PER) * L.vstep;  // uniform
+      // Every load is unconditional, so the compiler's wait counts stay exact across the
+      // pipeline: a group past n_jg (only in a row's last column-group block) rereads the
+      // last valid group, and its results are not stored.
 #pragma unroll
-    for (uint32_t q = 0; q < NJG; q++)
-      r.v[u][q] = gload<u32x4>(vb + (q < L.nvalid ? q : L.nvalid - 1) * 256 + L.voff);
+      for (uint32_t q = 0; q < NJG; q++)
+        r.v[u][q] = gload<u32x4>(vb + (q < L.nvalid ? q : L.nvalid - 1) * 256 + L.voff);
+    }
   }
 }
 
 // A stage that may run past the chunk's end, or of an unaligned job: element loads with a
-// column guard; columns past c1 read as zero, and so does V of K-steps past c1 (V rows past
-// the matrix are zero in memory).
-template <uint32_t XT, uint32_t NJG>
-__device__ __forceinline__ void load_guarded(StageRegs<NJG>& r, const Lane& L, uint32_t cs) {
+// column guard; columns past c1 read as zero, and so does the lane's own V of K-steps past c1
+// (V rows past the matrix are zero in memory).
+template <uint32_t XT, uint32_t NJG, bool VS>
+__device__ __forceinline__ void load_guarded(StageRegs<NJG, VS>& r, const Lane& L,
+                                             uint32_t cs) {
   using G = Geo<XT>;
 #pragma unroll
   for (uint32_t u = 0; u < KU; u++) {
@@ -188,27 +210,67 @@ __device__ __forceinline__ void load_guarded(StageRegs<NJG>& r, const Lane& L, u
       for (uint32_t t = 0; t < 4; t++) e[t] = cl + t < L.c1 ? gload<uint32_t>(p + cl + t) : 0u;
       r.x[u] = u32x4{e[0], e[1], e[2], e[3]};
     }
-    const char* vp = L.vlane + (uint64_t)(cu / G::PER) * L.vstep;
+    if constexpr (!VS) {
+      const char* vp = L.vlane + (uint64_t)(cu / G::PER) * L.vstep;
 #pragma unroll
-    for (uint32_t q = 0; q < NJG; q++)
-      r.v[u][q] = (q < L.nvalid && cu < L.c1) ? gload<u32x4>(vp + q * 256) : u32x4{0, 0, 0, 0};
+      for (uint32_t q = 0; q < NJG; q++)
+        r.v[u][q] = (q < L.nvalid && cu < L.c1) ? gload<u32x4>(vp + q * 256) : u32x4{0, 0, 0, 0};
+    }
   }
 }
 
-template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
-__device__ __forceinline__ void compute_stage(const StageRegs<NJG>& r, v4f32 acc[NJG],
-                                              float& s1, SqAcc<SQ64>& s2, bool sums,
-                                              const float* wu, const float* ww, uint32_t off) {
+// This thread's units of the stage at column cs: unit n is slot n mod 16 of group
+// (n / 16) mod NJG of the stage's K-group n / (16·NJG). A group past n_jg (only in a row's last
+// column-group block) rereads the last valid group; its results are not stored. A K-step that
+// starts past c1 (only in a partial stage) reads as zero, and V rows past the matrix are zero
+// in memory.
+template <uint32_t XT, uint32_t NJG>
+__device__ __forceinline__ void vstage_load(VStage<NJG>& vs, const Lane& L, uint32_t cs) {
+  using G = Geo<XT>;
+  constexpr uint32_t GPS = G::KSTEP / G::PER;  // K-groups per K-step (4)
+  const char* v0 = L.vjt + (uint64_t)(cs / G::PER) * L.vstep;
+#pragma unroll
+  for (uint32_t e = 0; e < VStage<NJG>::kPer; e++) {
+    const uint32_t n = threadIdx.x + 256 * e;
+    const uint32_t kg = n / (16 * NJG), q = (n / 16) % NJG, slot = n % 16;
+    const uint32_t qv = q < L.nvalid ? q : L.nvalid - 1;
+    const bool in = n < VStage<NJG>::kUnits && cs + (kg / GPS) * G::KSTEP < L.c1;
+    vs.v[e] = in ? gload<u32x4>(v0 + (uint64_t)kg * L.vstep + qv * 256 + slot * 16)
+                 : u32x4{0, 0, 0, 0};
+  }
+}
+
+template <uint32_t NJG>
+__device__ __forceinline__ void vstage_store(const VStage<NJG>& vs, u32x4* sv) {
+#pragma unroll
+  for (uint32_t e = 0; e < VStage<NJG>::kPer; e++) {
+    const uint32_t n = threadIdx.x + 256 * e;
+    if (n < VStage<NJG>::kUnits) sv[n] = vs.v[e];
+  }
+}
+
+// One stage: X from the wave's registers; V from the lanes' registers, or (VS) from the
+// block's LDS stage buffer `sv`, where lane (g, i) finds K-group g of K-step u, group q, slot i
+// at unit (4u + g)·16·NJG + 16q + i.
+template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG, bool VS>
+__device__ __forceinline__ void compute_stage(const StageRegs<NJG, VS>& r, const u32x4* sv,
+                                              v4f32 acc[NJG], float& s1, SqAcc<SQ64>& s2,
+                                              bool sums, const float* wu, const float* ww,
+                                              uint32_t off, uint32_t g, uint32_t i) {
   using G = Geo<XT>;
 #pragma unroll
   for (uint32_t u = 0; u < KU; u++) {
+    u32x4 v[NJG];
+#pragma unroll
+    for (uint32_t q = 0; q < NJG; q++)
+      v[q] = VS ? sv[((4 * u + g) * NJG + q) * 16 + i] : r.v[VS ? 0 : u][VS ? 0 : q];
     if (XT == DT_BF16) {
 #pragma unroll
       for (int h = 0; h < 2; h++) {
         const v4i16 a = __builtin_bit_cast(v4i16, v2u32{r.x[u][2 * h], r.x[u][2 * h + 1]});
 #pragma unroll
         for (uint32_t q = 0; q < NJG; q++) {
-          const v4i16 b = __builtin_bit_cast(v4i16, v2u32{r.v[u][q][2 * h], r.v[u][q][2 * h + 1]});
+          const v4i16 b = __builtin_bit_cast(v4i16, v2u32{v[q][2 * h], v[q][2 * h + 1]});
           acc[q] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc[q], 0, 0, 0);
         }
       }
@@ -218,7 +280,7 @@ __device__ __forceinline__ void compute_stage(const StageRegs<NJG>& r, v4f32 acc
 #pragma unroll
         for (uint32_t q = 0; q < NJG; q++)
           acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(r.x[u][e]),
-                                                        __uint_as_float(r.v[u][q][e]), acc[q],
+                                                        __uint_as_float(v[q][e]), acc[q],
                                                         0, 0, 0);
       }
     }
@@ -326,10 +388,10 @@ __device__ __forceinline__ void stage_weight(uint64_t w, uint32_t c0, uint32_t c
 // One tile: job blk_job[bidx], 64-row group, column chunk and column-group block decoded
 // from its index within the job (row group fastest). Every wave of the block calls it with the
 // same tile and reaches its barrier.
-template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
+template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG, bool VS>
 __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
                                          const uint32_t* __restrict__ blk_job, uint32_t k,
-                                         uint32_t bidx, float* s_u, float* s_w) {
+                                         uint32_t bidx, float* s_u, float* s_w, u32x4* s_v) {
   using G = Geo<XT>;
   constexpr uint32_t SSTEP = G::KSTEP * KU;
   // The wave index is uniform; readfirstlane lets the compiler keep everything derived from
@@ -354,28 +416,37 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   const uint32_t rowc = row < J.rows ? row : J.rows - 1;
   L.xrow = reinterpret_cast<const char*>(J.x) + (uint64_t)rowc * J.ld * G::ESZ;
   L.vstep = (uint64_t)J.n_jg * 256;
-  L.vlane = reinterpret_cast<const char*>(J.v) + (uint64_t)g * L.vstep +
-            (uint64_t)jt * NJG * 256 + i * 16;
+  L.vjt = reinterpret_cast<const char*>(J.v) + (uint64_t)jt * NJG * 256;
+  L.voff = (uint32_t)((uint64_t)g * L.vstep) + i * 16;
+  L.vlane = L.vjt + L.voff;
   // the same addresses as uniform bases and 32-bit lane offsets (plan creation keeps 16 rows
   // of an aligned job's X below 2^31 bytes; 4 K-groups of V are far below)
   L.xbase = reinterpret_cast<const char*>(J.x) + (uint64_t)r0 * J.ld * G::ESZ;
   L.xoff = (uint32_t)((uint64_t)(rowc - r0) * J.ld * G::ESZ) + G::PER * g * G::ESZ;
-  L.vbase = reinterpret_cast<const char*>(J.v) + (uint64_t)jt * NJG * 256;
-  L.voff = (uint32_t)((uint64_t)g * L.vstep) + i * 16;
   L.g = g;
   L.c1 = c1;
   L.nvalid = min(NJG, J.n_jg - jt * NJG);
+  // The chunk's stages: the first nfull of an aligned job are whole (plain 16-byte loads);
+  // the rest (a chunk's last partial stage, every stage of an unaligned job) take the
+  // guarded loads.
   const uint32_t nfull = J.aligned ? (c1 - c0) / SSTEP : 0;
+  const uint32_t nst = (c1 - c0 + SSTEP - 1) / SSTEP;
+  u32x4* const sv0 = s_v;
+  u32x4* const sv1 = s_v + VStage<NJG>::kUnits;
 
-  // The first stage's loads go out before the weights are staged, so the two latencies
-  // overlap.
-  StageRegs<NJG> ra;
-  if (active && nfull > 0) load_full<XT, NJG>(ra, L, c0);
-  if (WEIGHTED) {
-    if (sums) stage_weights<G::CHUNK>(J.u, J.w, c0, c1, J.chunk_cols, s_u, s_w);
-    __syncthreads();
+  // The first stage's X and V loads go out before the weights are staged, so the latencies
+  // overlap. Waves past the matrix take part in the staging and the barriers only.
+  StageRegs<NJG, VS> ra, rb;
+  VStage<NJG> vs;
+  if constexpr (VS) vstage_load<XT, NJG>(vs, L, c0);
+  if (active) {
+    if (nfull > 0) load_full<XT, NJG, VS>(ra, L, c0);
+    else load_guarded<XT, NJG, VS>(ra, L, c0);
   }
-  if (!active) return;
+  if (WEIGHTED && sums) stage_weights<G::CHUNK>(J.u, J.w, c0, c1, J.chunk_cols, s_u, s_w);
+  if constexpr (VS) vstage_store<NJG>(vs, sv0);
+  if (WEIGHTED || VS) __syncthreads();
+  if (!VS && !active) return;
 
   v4f32 acc[NJG];
 #pragma unroll
@@ -384,36 +455,33 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   SqAcc<SQ64> s2;
   const uint32_t woff = G::PER * g - c0;  // LDS weight index = column - c0
 
-  // Full stages of an aligned job run as a two-buffer software pipeline; the rest (the
-  // chunk's last partial stage, or every stage of an unaligned job) takes the guarded loads.
-  uint32_t cs = c0;
-  if (nfull > 0) {
-    StageRegs<NJG> rb;
-    uint32_t s = 1;
-    for (; s + 1 < nfull; s += 2) {
-      load_full<XT, NJG>(rb, L, cs + SSTEP);
-      compute_stage<XT, WEIGHTED, SQ64, NJG>(ra, acc, s1, s2, sums, s_u, s_w, cs + woff);
-      load_full<XT, NJG>(ra, L, cs + 2 * SSTEP);
-      compute_stage<XT, WEIGHTED, SQ64, NJG>(rb, acc, s1, s2, sums, s_u, s_w,
-                                             cs + SSTEP + woff);
-      cs += 2 * SSTEP;
+  // Stage s is multiplied while stage s + 1's loads are in flight (a two-buffer software
+  // pipeline). Sharing V, stage s reads LDS buffer s mod 2, stage s + 1's V goes to the other
+  // buffer once stage s is computed, and one barrier per stage keeps each buffer's writers and
+  // readers apart.
+  auto step = [&](const StageRegs<NJG, VS>& cur, StageRegs<NJG, VS>& nxt, uint32_t s) {
+    const uint32_t cs = c0 + s * SSTEP;
+    const bool more = s + 1 < nst;
+    if (more) {
+      if constexpr (VS) vstage_load<XT, NJG>(vs, L, cs + SSTEP);
+      if (active) {
+        if (s + 1 < nfull) load_full<XT, NJG, VS>(nxt, L, cs + SSTEP);
+        else load_guarded<XT, NJG, VS>(nxt, L, cs + SSTEP);
+      }
     }
-    if (s < nfull) {
-      load_full<XT, NJG>(rb, L, cs + SSTEP);
-      compute_stage<XT, WEIGHTED, SQ64, NJG>(ra, acc, s1, s2, sums, s_u, s_w, cs + woff);
-      compute_stage<XT, WEIGHTED, SQ64, NJG>(rb, acc, s1, s2, sums, s_u, s_w,
-                                             cs + SSTEP + woff);
-      cs += 2 * SSTEP;
-    } else {
-      compute_stage<XT, WEIGHTED, SQ64, NJG>(ra, acc, s1, s2, sums, s_u, s_w, cs + woff);
-      cs += SSTEP;
+    if (active)
+      compute_stage<XT, WEIGHTED, SQ64, NJG, VS>(cur, (s & 1) ? sv1 : sv0, acc, s1, s2, sums,
+                                                 s_u, s_w, cs + woff, g, i);
+    if constexpr (VS) {
+      if (more) vstage_store<NJG>(vs, (s & 1) ? sv0 : sv1);
+      __syncthreads();
     }
+  };
+  for (uint32_t s = 0; s < nst; s += 2) {
+    step(ra, rb, s);
+    if (s + 1 < nst) step(rb, ra, s + 1);
   }
-  for (; cs < c1; cs += SSTEP) {
-    StageRegs<NJG> r;
-    load_guarded<XT, NJG>(r, L, cs);
-    compute_stage<XT, WEIGHTED, SQ64, NJG>(r, acc, s1, s2, sums, s_u, s_w, cs + woff);
-  }
+  if (!active) return;
 
   // X·V: lane (g, i) holds rows 4g + e of the wave's 16 and slot i of each group.
   float* pdot = reinterpret_cast<float*>(J.pdot);
@@ -541,7 +609,7 @@ __device__ __forceinline__ void tile_loop(uint32_t n_tiles, uint32_t* __restrict
 // (mapping blocks XCD by XCD, as the fused chunk kernel does, cut the B pass's reads 1.08x ->
 // 1.02x but made it slower: with no stealing, XCDs given equal tile counts of unequal tiles
 // finish apart). With a smaller grid the blocks take tiles from the queues (tile_loop).
-template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG>
+template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG, bool VS>
 __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs,
                                                 const uint32_t* __restrict__ blk_job,
                                                 uint32_t k, uint32_t n_tiles,
@@ -549,9 +617,10 @@ __global__ __launch_bounds__(256) void row_pass(const PassJob* __restrict__ jobs
   using G = Geo<XT>;
   __shared__ __align__(16) float s_u[WEIGHTED ? G::CHUNK : 4];
   __shared__ __align__(16) float s_w[WEIGHTED ? G::CHUNK : 4];
+  __shared__ __align__(16) u32x4 s_v[VS ? 2 * VStage<NJG>::kUnits : 1];  // two stages of V
   __shared__ uint32_t s_tile;
   tile_loop(n_tiles, queue, &s_tile, [&](uint32_t b) {
-    row_tile<XT, WEIGHTED, SQ64, NJG>(jobs, blk_job, k, b, s_u, s_w);
+    row_tile<XT, WEIGHTED, SQ64, NJG, VS>(jobs, blk_job, k, b, s_u, s_w, s_v);
   });
 }
 
@@ -1981,10 +2050,15 @@ static void launch_pass(const FvPlan* P, const PassLaunch& L, uint32_t max_grid,
                         uint32_t* queue, hipStream_t s) {
   const bool queued = max_grid != 0 && max_grid < L.n_blocks;
   const uint32_t grid = queued ? max_grid : L.n_blocks;
-  if (queued) hipLaunchKernelGGL(queue_reset, dim3(1), dim3(kQueues), 0, s, queue);
-  hipLaunchKernelGGL((row_pass<XT, W, S, NJG>), dim3(grid), dim3(256), 0, s,
-                     P->d_jobs + L.job_off, P->d_blk + L.blk_off, P->k, L.n_blocks,
-                     queued ? queue : nullptr);
+  if (queued) {  // a block or two per CU beside other work: each lane loads its own V
+    hipLaunchKernelGGL(queue_reset, dim3(1), dim3(kQueues), 0, s, queue);
+    hipLaunchKernelGGL((row_pass<XT, W, S, NJG, false>), dim3(grid), dim3(256), 0, s,
+                       P->d_jobs + L.job_off, P->d_blk + L.blk_off, P->k, L.n_blocks, queue);
+  } else {  // a block per tile: the block shares each stage's V through LDS
+    hipLaunchKernelGGL((row_pass<XT, W, S, NJG, true>), dim3(grid), dim3(256), 0, s,
+                       P->d_jobs + L.job_off, P->d_blk + L.blk_off, P->k, L.n_blocks,
+                       nullptr);
+  }
 }
 
 template <uint32_t XT, bool W, bool S>
