@@ -163,6 +163,7 @@ struct Lane {
   uint32_t voff;      // this lane's V bytes past vjt (its K-group, its slot)
   uint32_t g, c1;
   uint32_t nvalid;    // groups of this block that exist (the last block of a row may hold fewer)
+  bool aligned;       // the job's rows and base are 16-byte aligned
 };
 
 // A whole stage of an aligned job, every column inside the chunk: plain 16-byte loads.
@@ -186,9 +187,11 @@ __device__ __forceinline__ void load_full(StageRegs<NJG, VS>& r, const Lane& L, 
   }
 }
 
-// A stage that may run past the chunk's end, or of an unaligned job: element loads with a
-// column guard; columns past c1 read as zero, and so does the lane's own V of K-steps past c1
-// (V rows past the matrix are zero in memory).
+// A stage that may run past the chunk's end, or of an unaligned job: columns past c1 read as
+// zero, and so does the lane's own V of K-steps past c1 (V rows past the matrix are zero in
+// memory). An aligned job's K-steps wholly inside the chunk take one 16-byte load per lane (a
+// narrow X, such as an attention head's 64 columns, is one such partial stage per row); a
+// K-step across c1, or any of an unaligned job, takes element loads with a column guard.
 template <uint32_t XT, uint32_t NJG, bool VS>
 __device__ __forceinline__ void load_guarded(StageRegs<NJG, VS>& r, const Lane& L,
                                              uint32_t cs) {
@@ -197,7 +200,11 @@ __device__ __forceinline__ void load_guarded(StageRegs<NJG, VS>& r, const Lane& 
   for (uint32_t u = 0; u < KU; u++) {
     const uint32_t cu = cs + u * G::KSTEP;
     const uint32_t cl = cu + G::PER * L.g;
-    if (XT == DT_BF16) {
+    if (L.aligned && cu + G::KSTEP <= L.c1) {  // uniform
+      r.x[u] = gload<u32x4>(L.xrow + (uint64_t)cl * G::ESZ);
+    } else if (cu >= L.c1) {  // uniform
+      r.x[u] = u32x4{0, 0, 0, 0};
+    } else if (XT == DT_BF16) {
       const uint16_t* p = reinterpret_cast<const uint16_t*>(L.xrow);
       uint32_t e[8];
 #pragma unroll
@@ -426,6 +433,7 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   L.g = g;
   L.c1 = c1;
   L.nvalid = min(NJG, J.n_jg - jt * NJG);
+  L.aligned = J.aligned != 0;
   // The chunk's stages: the first nfull of an aligned job are whole (plain 16-byte loads);
   // the rest (a chunk's last partial stage, every stage of an unaligned job) take the
   // guarded loads.
