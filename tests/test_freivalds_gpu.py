@@ -285,11 +285,13 @@ def test_verdicts_bit_exact_with_python(lib, guard, biased):
     assert int(first.item()) == first_want
 
 
-@pytest.mark.parametrize("k", [4, 7])
+@pytest.mark.parametrize("k", [4, 7, 16])
 def test_grid_limited_passes_take_tiles_from_a_queue(lib, k):
     """Row passes limited to fewer blocks than they have tiles take their tiles from a queue
-    that each launch resets: two runs in a row give the rows of the plan with a block per tile
-    bit for bit, for bf16 and fp32 operands and a bias."""
+    that each launch resets, each lane loading its own V, where a block per tile shares each
+    stage's V through LDS: two runs in a row give the rows of the plan with a block per tile
+    bit for bit, for bf16 and fp32 operands and a bias, with one, two and four 16-column
+    groups of V (k = 4, 7, 16)."""
     from verification.commitment import native
     items = []
     for i, (shape, dtype, biased) in enumerate([((1024, 2048, 640), torch.bfloat16, True),
