@@ -152,7 +152,10 @@ def cpu_baseline(step, items, fv_budget_s: float = 3.0, runs: int = 3) -> dict:
                       f"challenges included)"}
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "c4_kernel_counters.md"
+# The committed counter summaries whose fenced JSON blocks hold each kernel's HBM bytes per
+# launch, by configuration (a configuration with none reports traffic as null).
+TRAFFIC_FILES = {"c4": ROOT / "profiles" / "c4_kernel_counters.md",
+                 "c5": ROOT / "profiles" / "c5_kernel_counters.md"}
 
 
 def kernel_label(name: str) -> str:
@@ -259,12 +262,14 @@ def trace_summary(d: Path, steps: int, warmup: int) -> int:
     return 0
 
 
-def traffic_from_profile(kernel: str) -> int | None:
-    """HBM bytes per launch of ``kernel`` (read + written) from the committed counter summary
-    (the fenced JSON block of TRAFFIC_FILE, one object per kernel and counter), or None when it
-    holds no figure for that kernel."""
+def traffic_from_profile(kernel: str, config: str) -> int | None:
+    """HBM bytes per launch of ``kernel`` (read + written) in configuration ``config`` from its
+    committed counter summary (the fenced JSON block of TRAFFIC_FILES[config], one object per
+    kernel and counter), or None when there is none or it holds no figure for that kernel."""
+    if config not in TRAFFIC_FILES:
+        return None
     try:
-        text = TRAFFIC_FILE.read_text()
+        text = TRAFFIC_FILES[config].read_text()
         block = text.split("```json", 1)[1].split("```", 1)[0]
         rows = [json.loads(line) for line in block.splitlines() if line.strip()]
     except (OSError, IndexError, ValueError):
@@ -611,7 +616,7 @@ def check_level_leg(c, step, k: int, claimed: bytes, runs: int = 4) -> dict:
             "runs_ms": [round(t, 1) for t in times]}
 
 
-def measure_step(c, step, k: int, args, desc: str):
+def measure_step(c, step, k: int, args, desc: str, config: str):
     """The headline measurement of one configuration on its resident transcript: the plans,
     the claimed root (the root of the transcript as it is), the timed overlapped steps, the
     serialised stage leg, check 6a, and every kernel's roofline; returns the JSON line's dict
@@ -804,7 +809,7 @@ def measure_step(c, step, k: int, args, desc: str):
                "achieved": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
                "algorithmic_bytes": nbytes, "launch_ms": round(stage_ms[nm], 4),
                "launch_ms_in_step": (round(in_step[nm], 4) if nm in in_step else None),
-               "traffic": traffic_from_profile(kname)}
+               "traffic": traffic_from_profile(kname, config)}
         if kname in valu:
             out["valu_frac"] = valu[kname]["frac"]
         return out
@@ -856,7 +861,7 @@ def measure_step(c, step, k: int, args, desc: str):
                   "check_6a": check_6a},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_from_profile(dom_name),
+                     "traffic": traffic_from_profile(dom_name, config),
                      "kernel": dom_name,
                      "algorithmic_bytes": dom_bytes, "launch_ms": round(stage_ms[dom], 4),
                      "launch_ms_in_step": (round(in_step[dom], 4) if dom in in_step else None),
@@ -956,7 +961,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    out, v, claimed_b, items = measure_step(c, step, k, args, desc)
+    out, v, claimed_b, items = measure_step(c, step, k, args, desc, args.config)
     if args.check_level:
         out["parts"]["check_level"] = check_level_leg(c, step, k, claimed_b)
     if args.disk_leg:
@@ -986,7 +991,7 @@ def c5_leg(c, step, args) -> dict:
     log(f"[bench] c5 leg: {len(forged)} products perturbed, k=16")
     sub = argparse.Namespace(**{**vars(args), "steps": max(3, min(args.steps, 5)),
                                 "warmup": 1, "a_grid": None})
-    out, v, _, _ = measure_step(c, step, 16, sub, CONFIGS["c5"][0])
+    out, v, _, _ = measure_step(c, step, 16, sub, CONFIGS["c5"][0], "c5")
     v.close()
     torch.cuda.synchronize()
     parts = out["parts"]
