@@ -14,7 +14,8 @@ members' ``dA, dV`` and ``dQ, dK``, and the input and weight gradients of q/k/v.
 The prover side (:meth:`DecoderComputation.build_model`, :meth:`~DecoderComputation.loss`,
 :meth:`~DecoderComputation.label_with_operands`) runs transformers' Llama/Qwen2 causal LM over
 fp32 master weights, under autocast to bf16 for a bf16 computation (reference
-decoder.py:551-598), with one head block and this build's attention core
+decoder.py:551-598), the output layer in ``B`` row blocks when ``head_blocks`` asks for them
+(:meth:`~DecoderComputation.forward_backward`), with this build's attention core
 (``instances/attention.py``: eager attention's arithmetic, every batched product's right
 operand contiguous), and maps the captured records onto the slots above by operand identity.
 :class:`DecoderReplay` rebuilds check 5's operands and check 6b's glue gradients from the
@@ -259,8 +260,6 @@ class DecoderComputation(DeclaredComputation):
         Attention runs through this build's own core (``instances/attention.py``) instead of
         transformers' eager function: the same products and glue, with no batched product
         ever given a transposed right operand."""
-        if self.head_blocks != 1:
-            raise NotImplementedError("the prover side takes one head block")
         from transformers import LlamaConfig, LlamaForCausalLM, Qwen2Config, Qwen2ForCausalLM
 
         from verification.computation.instances.attention import register
@@ -290,19 +289,79 @@ class DecoderComputation(DeclaredComputation):
             return contextlib.nullcontext()
         return torch.autocast(device.type, dtype=self.compute_dtype)
 
+    def _autocast_off(self, device: torch.device):
+        """Autocast switched off inside an autocast region (a head block's backward)."""
+        import contextlib
+        if self.compute_dtype == self.weight_dtype:
+            return contextlib.nullcontext()
+        return torch.autocast(device.type, enabled=False)
+
+    @staticmethod
+    def _batch(records, dev: torch.device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        ids = torch.stack([r.ids for r in records]).to(device=dev, dtype=torch.long)
+        targets = torch.stack([r.targets for r in records]).to(device=dev, dtype=torch.long)
+        mask = torch.stack([r.mask for r in records]).to(device=dev, dtype=torch.float32)
+        return ids, targets, mask
+
+    def _block_loss(self, logits: torch.Tensor, targets: torch.Tensor, mask: torch.Tensor,
+                    total: torch.Tensor) -> torch.Tensor:
+        """The masked cross-entropy of some rows over the whole batch's mask count, in fp32:
+        the shares of a partition of the batch sum to the loss (reference decoder.py:638-649)."""
+        ce = torch.nn.functional.cross_entropy(logits.float().reshape(-1, self.n_v),
+                                               targets.reshape(-1), reduction="none")
+        return (ce * mask.reshape(-1)).sum() / total
+
     def loss(self, model: torch.nn.Module, records) -> torch.Tensor:
         """Mean cross-entropy of the targets over the masked tokens; the model runs in the
         compute format, the loss in fp32."""
         dev = next(model.parameters()).device
-        ids = torch.stack([r.ids for r in records]).to(device=dev, dtype=torch.long)
-        targets = torch.stack([r.targets for r in records]).to(device=dev, dtype=torch.long)
-        mask = torch.stack([r.mask for r in records]).to(device=dev, dtype=torch.float32)
+        ids, targets, mask = self._batch(records, dev)
         with self.autocast(dev):
             logits = model(input_ids=ids).logits
-        logits = logits.float()
-        ce = torch.nn.functional.cross_entropy(logits.reshape(-1, self.n_v),
-                                               targets.reshape(-1), reduction="none")
-        return (ce * mask.reshape(-1)).sum() / mask.sum()
+        return self._block_loss(logits, targets, mask, mask.sum())
+
+    def forward_backward(self, model: torch.nn.Module, records, stage) -> torch.Tensor:
+        """One training pass. With one head block, the loss over the whole batch and its
+        backward. With ``B = head_blocks`` blocks (reference decoder.py:740-770): the features
+        ``F`` (embedding through the final norm) once; then per block ``b`` (sequences
+        ``b·n_s/B`` onwards), its rows of ``F`` copied off ``F``'s graph, ``Λ_b`` and the
+        block's share of the loss, and right away that share's gradients: ``dF_b`` and the
+        head weight's ``G_b`` (then the block's logits are dropped, so no ``N × n_v`` array
+        is held); the head weight's gradient is the blocks' ``G_b`` widened to the weight
+        dtype and added in block order, plus (tied) the embedding's own; ``F``'s backward
+        takes the blocks' ``dF_b`` stacked. The head weight is cast to the compute format once
+        for all blocks; the backward runs with autocast off."""
+        if self.head_blocks == 1:
+            return super().forward_backward(model, records, stage)
+        dev = next(model.parameters()).device
+        ids, targets, mask = self._batch(records, dev)
+        total = mask.sum()
+        head = model.get_output_embeddings()
+        w = head.weight
+        per = self.n_s // self.head_blocks
+        loss: torch.Tensor | None = None
+        g: torch.Tensor | None = None
+        dfs: list[torch.Tensor] = []
+        with self.autocast(dev):
+            with stage("forward"):
+                f = model.model(input_ids=ids).last_hidden_state
+            for b in range(self.head_blocks):
+                rows = slice(b * per, (b + 1) * per)
+                with stage("forward"):
+                    fb = f.detach()[rows].clone().requires_grad_()
+                    part = self._block_loss(head(fb), targets[rows], mask[rows], total)
+                with stage("backward"), self._autocast_off(dev):
+                    df, gb = torch.autograd.grad(part, [fb, w])
+                dfs.append(df)
+                g = gb.to(self.weight_dtype) if g is None else g + gb.to(self.weight_dtype)
+                part = part.detach()
+                loss = part if loss is None else loss + part
+                del fb, df, gb, part
+            with stage("backward"), self._autocast_off(dev):
+                f.backward(torch.cat(dfs))
+            del f, dfs
+        w.grad = g if w.grad is None else g + w.grad
+        return loss
 
     def label(self, capture, model: torch.nn.Module) -> list[torch.Tensor]:
         return self.label_with_operands(capture, model)[0]
@@ -386,7 +445,7 @@ class DecoderComputation(DeclaredComputation):
         bwd = [r for r in capture.records if r.phase == "backward"]
         s_rec: dict[int, Any] = {}
         o_rec: dict[int, Any] = {}
-        head_in = None
+        head_in: dict[int, int] = {}  # storage of each head block's A -> its block
         layer = None
         seen = 0
         for rec in fwd:
@@ -407,8 +466,12 @@ class DecoderComputation(DeclaredComputation):
                     layer, seen = l, 0
                 fill(f"L{l}.Y_{x}", rec.a, rec.b, rec.out, rec)
             elif name == self.w_out and rec.out.shape[-1] == self.n_v:
-                head_in = rec.a
-                fill(self.head_name("Lambda", 0), rec.a, rec.b, rec.out, rec)
+                b = len(head_in)
+                if b >= self.head_blocks or storage(rec.a) in head_in:
+                    raise LabelingError(f"head record #{rec.index}: more than "
+                                        f"{self.head_blocks} head blocks, or one A twice")
+                head_in[storage(rec.a)] = b
+                fill(self.head_name("Lambda", b), rec.a, rec.b, rec.out, rec)
             else:
                 raise LabelingError(f"forward record #{rec.index} matches no slot")
         for l in range(1, self.L + 1):
@@ -432,6 +495,7 @@ class DecoderComputation(DeclaredComputation):
         s_a = {storage(s_rec[l].a): l for l in s_rec}
         pair_a: dict[int, tuple[str, int]] = {}  # storage of δO or δS -> (role, layer)
         deferred = []
+        n_df = 0
         for rec in bwd:
             if rec.batch is not None:
                 if storage(rec.a) in o_a:
@@ -450,13 +514,16 @@ class DecoderComputation(DeclaredComputation):
                 l, x = by_weight[name]
                 fill(f"L{l}.dX_{x}", rec.a, rec.b, rec.out, rec)
             elif name == self.w_out:
-                fill(self.head_name("dF", 0), rec.a, rec.b, rec.out, rec)
+                if n_df >= self.head_blocks:
+                    raise LabelingError(f"backward record #{rec.index}: more than "
+                                        f"{self.head_blocks} head input gradients")
+                fill(self.head_name("dF", n_df), rec.a, rec.b, rec.out, rec)
+                n_df += 1
             elif grad_of.get(rec.index) in by_weight:
                 l, x = by_weight[grad_of[rec.index]]
                 fill(f"L{l}.G_{x}", rec.a, rec.b, rec.out, rec)
-            elif head_in is not None and storage(rec.b) == storage(head_in) and \
-                    tuple(rec.out.shape) == (self.n_v, self.d):
-                fill(self.head_name("G", 0), rec.a, rec.b, rec.out, rec)
+            elif storage(rec.b) in head_in and tuple(rec.out.shape) == (self.n_v, self.d):
+                fill(self.head_name("G", head_in[storage(rec.b)]), rec.a, rec.b, rec.out, rec)
             else:
                 raise LabelingError(f"backward record #{rec.index} matches no slot")
         for rec in deferred:

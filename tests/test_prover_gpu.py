@@ -179,6 +179,66 @@ def test_real_decoder_step_commits_and_verifies(lib, qkv_bias, n_kv, dtype):
     assert out.check is None and out.root == tree.root, out.detail
 
 
+@pytest.mark.parametrize("tied,dtype", [(True, torch.bfloat16), (False, torch.bfloat16),
+                                        (False, torch.float32)])
+def test_head_blocks_step_commits_and_verifies(lib, tied, dtype):
+    """The output layer in two row blocks (reference decoder.py:211-229, 740-770) proved on
+    the GPU: the device commit equals the oracle's root; the verifier accepts the step from
+    the committed leaves alone through the check-level API and the device step, the replay
+    serving every head block's operands equal to the prover's; an untied W_out is checked at
+    6a over its two G_head blocks, a tied embedding at 6b."""
+    from conftest import started_verifier
+    from verification.computation.instances.decoder import DecoderComputation, DecoderReplay
+    from verification.transcript.store import InMemoryStore
+    from verification.verifier.step import DeviceStepVerifier
+    c = DecoderComputation(L=2, d=128, d_f=256, n_h=4, n_kv=2, n_v=320, n_s=4, n=64,
+                           qkv_bias=True, compute_dtype=dtype, head_blocks=2, tied=tied)
+    c, step, tree = _decoder_prove(seed=12, c=c)
+    assert tree.root == _decoder_oracle_root(c, step.leaves())
+    v = started_verifier(c, step.leaves(), k=2)
+    assert v.verify_step(1, InMemoryStore(step.leaves(), tree)) is None
+    checked = {t.weight: t.check_id for t in v.stats[1].tensors}
+    assert checked[c.w_out] == ("6b" if tied else "6a")
+    replay = DecoderReplay(c, step.leaves())
+    for spec in c.products:
+        if spec.weight == c.w_out:
+            assert all(torch.equal(x, y) for x, y in zip(replay.operands(spec.m),
+                                                         step.operands[spec.m])), spec.name
+    out = DeviceStepVerifier(c, step.leaves(), lambda s: replay.operands(s.m), k=2).run(tree.root)
+    assert out.check is None and out.root == tree.root, out.detail
+
+
+def test_head_block_forgeries_reject(lib):
+    """Two head blocks: a changed G_E_head[1] of a tied head rejects at check 5 at that
+    product (the checks run 6a before 5, and the tied embedding's update is check 6b's), and
+    an untied W_out update that is not W_t − η·(G_head[0] + G_head[1]) at check 6a."""
+    from conftest import started_verifier
+    from verification.commitment.leaves import commit_leaves_device
+    from verification.computation.instances.decoder import DecoderComputation
+    from verification.transcript.store import InMemoryStore
+
+    def made(tied):
+        return DecoderComputation(L=2, d=128, d_f=256, n_h=4, n_kv=2, n_v=320, n_s=4, n=64,
+                                  qkv_bias=True, compute_dtype=torch.bfloat16, head_blocks=2,
+                                  tied=tied)
+    spec = next(s for s in made(True).products if s.name == "G_E_head[1]")
+    c, step, tree = _decoder_prove(seed=13, c=made(True), perturb={
+        spec.m: lambda p: p.index_add_(0, torch.tensor([9], device=p.device),
+                                       torch.full_like(p[:1], 4.0))})
+    rej = started_verifier(c, step.leaves(), k=2).verify_step(
+        1, InMemoryStore(step.leaves(), tree))
+    assert rej is not None and (rej.check_id, rej.kind) == ("5", "failed"), rej
+    assert rej.detail.startswith(f"P_{spec.m} (G_E_head[1])")
+    c, step, _ = _decoder_prove(seed=13, c=made(False))
+    leaves = step.leaves()
+    i = c.w_next_index(c.w_out)
+    leaves[i] = leaves[i].clone()
+    leaves[i][5, 7] += 1e-2
+    rej = started_verifier(c, leaves, k=2).verify_step(
+        1, InMemoryStore(leaves, commit_leaves_device(c, leaves)))
+    assert rej is not None and rej.check_id == "6a" and c.w_out in rej.detail, rej
+
+
 def test_real_decoder_step_with_a_changed_member_rejects_at_check_5(lib):
     from conftest import started_verifier
     from verification.transcript.store import InMemoryStore

@@ -246,12 +246,13 @@ def test_replay_operands_reproduce_every_product():
         assert torch.equal(torch.mm(a, b), step.products[spec.m - 1]), spec.name
 
 
-def _decoder_step(qkv_bias=True, n_kv=2, dtype=torch.float32):
+def _decoder_step(qkv_bias=True, n_kv=2, dtype=torch.float32, head_blocks=1, tied=True):
     from setup.records import Record
     from verification.computation.instances.decoder import DecoderComputation
     from verification.computation.interface import snapshot_weights
     c = DecoderComputation(L=2, d=64, d_f=128, n_h=4, n_kv=n_kv, n_v=160, n_s=2, n=16,
-                           qkv_bias=qkv_bias, compute_dtype=dtype)
+                           qkv_bias=qkv_bias, compute_dtype=dtype, head_blocks=head_blocks,
+                           tied=tied)
     torch.manual_seed(0)
     model = c.build_model()
     w0 = snapshot_weights(c, model)
@@ -426,6 +427,71 @@ def test_decoder_replay_serves_each_attention_call_as_one_group(qkv_bias, n_kv, 
     a, _ = replay.operand_group(ms[::-1])
     assert torch.equal(a, torch.stack([replay.operands(m)[0] for m in ms[::-1]]))
     assert a.data_ptr() != replay.operands(ms[-1])[0].data_ptr()
+
+
+HEADS = [(True, torch.float32), (False, torch.float32), (True, torch.bfloat16),
+         (False, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("tied,dtype", HEADS)
+def test_head_blocks_fill_their_slots_and_chain_the_head_gradient(tied, dtype):
+    """The output layer in two row blocks (reference decoder.py:211-229, 740-770): 3B head
+    products, each block's Λ_b, dF_b and G_b in its own slot and equal to its captured
+    operands' product; Λ_b's A is block b's rows of the features, so the blocks' Λ stack to
+    the one-block step's Λ (the same weights and batch); the loss is the one-block loss; an
+    untied W_out steps by its blocks' G_b widened to fp32 and added in block order."""
+    from verification.computation.instances.decoder import matmul_count_decoder
+    from verification.computation.interface import chain_gradient
+    c, w0, step = _decoder_step(True, 2, dtype, head_blocks=2, tied=tied)
+    one, _, whole = _decoder_step(True, 2, dtype, head_blocks=1, tied=tied)
+    assert c.M == matmul_count_decoder(c.L, c.n_s, c.n_h, 2) == one.M + 3
+    assert step.capture["outer_calls"] == 1
+    names = [s.name for s in c.products]
+    g_head = "G_E_head" if tied else "G_head"
+    for b in range(2):
+        assert {f"Lambda[{b}]", f"dF[{b}]", f"{g_head}[{b}]"} <= set(names)
+    for spec in c.products:
+        a, b = step.operands[spec.m]
+        p = step.products[spec.m - 1]
+        assert p.dtype == dtype and (tuple(a.shape), tuple(b.shape)) == (spec.a_shape,
+                                                                           spec.b_shape)
+        q = torch.mm(a.float(), b.float())
+        if spec.bias is not None:
+            q = q + w0[spec.bias].to(dtype).float()
+        scale = torch.mm(a.float().abs(), b.float().abs()) + 1e-30
+        tol = 2.0**-8 if dtype == torch.bfloat16 else 1e-5
+        assert ((q - p.float()).abs() <= tol * scale + 1e-6).all(), spec.name
+    lam = [step.products[names.index(f"Lambda[{b}]")] for b in range(2)]
+    lam1 = whole.products[[s.name for s in one.products].index("Lambda")]
+    tol = 2.0**-7 if dtype == torch.bfloat16 else 1e-5
+    assert torch.allclose(torch.cat(lam).float(), lam1.float(), rtol=tol, atol=tol)
+    assert step.loss == pytest.approx(whole.loss, rel=1e-5)
+    if not tied:
+        gs = [step.products[names.index(f"G_head[{b}]")] for b in range(2)]
+        want = torch.add(w0[c.w_out], chain_gradient(gs, torch.float32), alpha=-c.eta)
+        assert torch.equal(step.w_next[c.w_out], want)
+        assert c.linear_weights[c.w_out] == tuple(
+            c.products[names.index(f"G_head[{b}]")].m for b in range(2))
+
+
+@pytest.mark.parametrize("tied,dtype", HEADS)
+def test_head_blocks_replay_from_the_leaves(tied, dtype):
+    """The replay of a two-block step gives every product, the head blocks' included, the
+    operands the capture saw, bit for bit, and each glue weight (a tied embedding: its lookup
+    gradient plus the blocks' committed G_E_head[b]) the gradient SGD stepped with."""
+    from verification.computation.instances.decoder import DecoderReplay
+    c, w0, step = _decoder_step(True, 2, dtype, head_blocks=2, tied=tied)
+    leaves = step.leaves()
+    replay = DecoderReplay(c, leaves, device="cpu")
+    for spec in c.products:
+        a, b = replay.operands(spec.m)
+        ca, cb = step.operands[spec.m]
+        assert torch.equal(a, ca) and torch.equal(b, cb), spec.name
+    glue = replay.glue_gradients()
+    assert set(glue) == set(c.glue_gradient_weights) and (c.w_out in glue) == tied
+    for name, g in glue.items():
+        want = torch.add(leaves[c.w_t_index(name)], g, alpha=-c.eta)
+        assert torch.equal(want, leaves[c.w_next_index(name)]), name
 
 
 def test_operand_groups_follow_the_batched_products():
