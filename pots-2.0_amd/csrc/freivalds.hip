@@ -163,7 +163,8 @@ struct Lane {
   uint32_t voff;      // this lane's V bytes past vjt (its K-group, its slot)
   uint32_t g, c1;
   uint32_t nvalid;    // groups of this block that exist (the last block of a row may hold fewer)
-  bool aligned;       // the job's rows and base are 16-byte aligned
+  bool kaligned;      // an aligned job whose chunk ends on a K-step: its last partial stage
+                      // takes load_partial
 };
 
 // A whole stage of an aligned job, every column inside the chunk: plain 16-byte loads.
@@ -187,11 +188,36 @@ __device__ __forceinline__ void load_full(StageRegs<NJG, VS>& r, const Lane& L, 
   }
 }
 
-// A stage that may run past the chunk's end, or of an unaligned job: columns past c1 read as
-// zero, and so does the lane's own V of K-steps past c1 (V rows past the matrix are zero in
-// memory). An aligned job's K-steps wholly inside the chunk take one 16-byte load per lane (a
-// narrow X, such as an attention head's 64 columns, is one such partial stage per row); a
-// K-step across c1, or any of an unaligned job, takes element loads with a column guard.
+// The last, partial stage of an aligned job's chunk whose columns end on a K-step (a narrow
+// X, such as an attention head's 64 columns, is one such stage per row): K-steps inside the
+// chunk take one 16-byte load per lane, the rest read as zero, and so does the lane's own V
+// of K-steps past c1 (V rows past the matrix are zero in memory).
+template <uint32_t XT, uint32_t NJG, bool VS>
+__device__ __forceinline__ void load_partial(StageRegs<NJG, VS>& r, const Lane& L,
+                                             uint32_t cs) {
+  using G = Geo<XT>;
+#pragma unroll
+  for (uint32_t u = 0; u < KU; u++) {
+    const uint32_t cu = cs + u * G::KSTEP;
+    const char* xb = L.xbase + (uint64_t)cu * G::ESZ;  // uniform
+    r.x[u] = cu < L.c1 ? gload<u32x4>(xb + L.xoff) : u32x4{0, 0, 0, 0};
+    if constexpr (!VS) {
+      const char* vp = L.vlane + (uint64_t)(cu / G::PER) * L.vstep;
+#pragma unroll
+      for (uint32_t q = 0; q < NJG; q++)
+        r.v[u][q] = (q < L.nvalid && cu < L.c1) ? gload<u32x4>(vp + q * 256) : u32x4{0, 0, 0, 0};
+    }
+  }
+  // Wait for these loads here (s_waitcnt vmcnt(0)). Left in flight, they would reach the
+  // merge with load_full's path, whose loads into the same registers the compiler would then
+  // hold behind every earlier load (stage V's included) in every full stage, which is the
+  // whole software pipeline.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// A stage that may run past the chunk's end across a K-step, or of an unaligned job: element
+// loads with a column guard; columns past c1 read as zero, and so does the lane's own V of
+// K-steps past c1 (V rows past the matrix are zero in memory).
 template <uint32_t XT, uint32_t NJG, bool VS>
 __device__ __forceinline__ void load_guarded(StageRegs<NJG, VS>& r, const Lane& L,
                                              uint32_t cs) {
@@ -200,11 +226,7 @@ __device__ __forceinline__ void load_guarded(StageRegs<NJG, VS>& r, const Lane& 
   for (uint32_t u = 0; u < KU; u++) {
     const uint32_t cu = cs + u * G::KSTEP;
     const uint32_t cl = cu + G::PER * L.g;
-    if (L.aligned && cu + G::KSTEP <= L.c1) {  // uniform
-      r.x[u] = gload<u32x4>(L.xrow + (uint64_t)cl * G::ESZ);
-    } else if (cu >= L.c1) {  // uniform
-      r.x[u] = u32x4{0, 0, 0, 0};
-    } else if (XT == DT_BF16) {
+    if (XT == DT_BF16) {
       const uint16_t* p = reinterpret_cast<const uint16_t*>(L.xrow);
       uint32_t e[8];
 #pragma unroll
@@ -433,10 +455,10 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   L.g = g;
   L.c1 = c1;
   L.nvalid = min(NJG, J.n_jg - jt * NJG);
-  L.aligned = J.aligned != 0;
+  L.kaligned = J.aligned != 0 && (c1 - c0) % G::KSTEP == 0;
   // The chunk's stages: the first nfull of an aligned job are whole (plain 16-byte loads);
-  // the rest (a chunk's last partial stage, every stage of an unaligned job) take the
-  // guarded loads.
+  // an aligned chunk's last partial stage takes load_partial when the chunk ends on a K-step,
+  // else the guarded loads, which every stage of an unaligned job takes.
   const uint32_t nfull = J.aligned ? (c1 - c0) / SSTEP : 0;
   const uint32_t nst = (c1 - c0 + SSTEP - 1) / SSTEP;
   u32x4* const sv0 = s_v;
@@ -449,6 +471,7 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   if constexpr (VS) vstage_load<XT, NJG>(vs, L, c0);
   if (active) {
     if (nfull > 0) load_full<XT, NJG, VS>(ra, L, c0);
+    else if (L.kaligned) load_partial<XT, NJG, VS>(ra, L, c0);
     else load_guarded<XT, NJG, VS>(ra, L, c0);
   }
   if (WEIGHTED && sums) stage_weights<G::CHUNK>(J.u, J.w, c0, c1, J.chunk_cols, s_u, s_w);
@@ -474,6 +497,7 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
       if constexpr (VS) vstage_load<XT, NJG>(vs, L, cs + SSTEP);
       if (active) {
         if (s + 1 < nfull) load_full<XT, NJG, VS>(nxt, L, cs + SSTEP);
+        else if (L.kaligned) load_partial<XT, NJG, VS>(nxt, L, cs + SSTEP);
         else load_guarded<XT, NJG, VS>(nxt, L, cs + SSTEP);
       }
     }
