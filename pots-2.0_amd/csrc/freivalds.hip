@@ -165,6 +165,8 @@ struct Lane {
   uint32_t nvalid;    // groups of this block that exist (the last block of a row may hold fewer)
   bool kaligned;      // an aligned job whose chunk ends on a K-step: its last partial stage
                       // takes load_partial
+  brsrc xr, vr;       // buffer resources at xbase and vjt (the full and partial stages' and
+                      // the V staging's loads)
 };
 
 // A whole stage of an aligned job, every column inside the chunk: plain 16-byte loads.
@@ -174,16 +176,15 @@ __device__ __forceinline__ void load_full(StageRegs<NJG, VS>& r, const Lane& L, 
 #pragma unroll
   for (uint32_t u = 0; u < KU; u++) {
     const uint32_t cu = cs + u * G::KSTEP;
-    const char* xb = L.xbase + (uint64_t)cu * G::ESZ;  // uniform
-    r.x[u] = gload<u32x4>(xb + L.xoff);
+    r.x[u] = bload128(L.xr, L.xoff, cu * G::ESZ);
     if constexpr (!VS) {
-      const char* vb = L.vjt + (uint64_t)(cu / G::PER) * L.vstep;  // uniform
+      const uint32_t vb = (cu / G::PER) * (uint32_t)L.vstep;  // uniform
       // Every load is unconditional, so the compiler's wait counts stay exact across the
       // pipeline: a group past n_jg (only in a row's last column-group block) rereads the
       // last valid group, and its results are not stored.
 #pragma unroll
       for (uint32_t q = 0; q < NJG; q++)
-        r.v[u][q] = gload<u32x4>(vb + (q < L.nvalid ? q : L.nvalid - 1) * 256 + L.voff);
+        r.v[u][q] = bload128(L.vr, L.voff, vb + (q < L.nvalid ? q : L.nvalid - 1) * 256);
     }
   }
 }
@@ -199,13 +200,13 @@ __device__ __forceinline__ void load_partial(StageRegs<NJG, VS>& r, const Lane& 
 #pragma unroll
   for (uint32_t u = 0; u < KU; u++) {
     const uint32_t cu = cs + u * G::KSTEP;
-    const char* xb = L.xbase + (uint64_t)cu * G::ESZ;  // uniform
-    r.x[u] = cu < L.c1 ? gload<u32x4>(xb + L.xoff) : u32x4{0, 0, 0, 0};
+    r.x[u] = cu < L.c1 ? bload128(L.xr, L.xoff, cu * G::ESZ) : u32x4{0, 0, 0, 0};
     if constexpr (!VS) {
-      const char* vp = L.vlane + (uint64_t)(cu / G::PER) * L.vstep;
+      const uint32_t vb = (cu / G::PER) * (uint32_t)L.vstep;  // uniform
 #pragma unroll
       for (uint32_t q = 0; q < NJG; q++)
-        r.v[u][q] = (q < L.nvalid && cu < L.c1) ? gload<u32x4>(vp + q * 256) : u32x4{0, 0, 0, 0};
+        r.v[u][q] = (q < L.nvalid && cu < L.c1) ? bload128(L.vr, L.voff, vb + q * 256)
+                                                : u32x4{0, 0, 0, 0};
     }
   }
   // Wait for these loads here (s_waitcnt vmcnt(0)). Left in flight, they would reach the
@@ -257,14 +258,14 @@ template <uint32_t XT, uint32_t NJG>
 __device__ __forceinline__ void vstage_load(VStage<NJG>& vs, const Lane& L, uint32_t cs) {
   using G = Geo<XT>;
   constexpr uint32_t GPS = G::KSTEP / G::PER;  // K-groups per K-step (4)
-  const char* v0 = L.vjt + (uint64_t)(cs / G::PER) * L.vstep;
+  const uint32_t v0 = (cs / G::PER) * (uint32_t)L.vstep;  // uniform
 #pragma unroll
   for (uint32_t e = 0; e < VStage<NJG>::kPer; e++) {
     const uint32_t n = threadIdx.x + 256 * e;
     const uint32_t kg = n / (16 * NJG), q = (n / 16) % NJG, slot = n % 16;
     const uint32_t qv = q < L.nvalid ? q : L.nvalid - 1;
     const bool in = n < VStage<NJG>::kUnits && cs + (kg / GPS) * G::KSTEP < L.c1;
-    vs.v[e] = in ? gload<u32x4>(v0 + (uint64_t)kg * L.vstep + qv * 256 + slot * 16)
+    vs.v[e] = in ? bload128(L.vr, kg * (uint32_t)L.vstep + qv * 256 + slot * 16, v0)
                  : u32x4{0, 0, 0, 0};
   }
 }
@@ -456,6 +457,8 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   L.c1 = c1;
   L.nvalid = min(NJG, J.n_jg - jt * NJG);
   L.kaligned = J.aligned != 0 && (c1 - c0) % G::KSTEP == 0;
+  L.xr = make_rsrc(L.xbase);
+  L.vr = make_rsrc(L.vjt);
   // The chunk's stages: the first nfull of an aligned job are whole (plain 16-byte loads);
   // an aligned chunk's last partial stage takes load_partial when the chunk ends on a K-step,
   // else the guarded loads, which every stage of an unaligned job takes.

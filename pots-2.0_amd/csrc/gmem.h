@@ -8,6 +8,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stdint.h>
 
 namespace pots {
 
@@ -21,6 +22,25 @@ __device__ __forceinline__ T gload(const void* p) {
 template <typename T>
 __device__ __forceinline__ void gstore(void* p, const T& v) {
   *(POTS_GLOBAL T*)(p) = v;
+}
+
+// Buffer loads: a 128-bit resource in scalar registers (a wave-uniform base address, no
+// range limit below 4 GiB) plus a 32-bit per-lane offset and a 32-bit wave-uniform offset. A
+// global load of a 64-bit address needs its address built in vector registers per load, and
+// those temporaries can land on registers a load still in flight will write, which makes the
+// compiler wait for that load first; a buffer load keeps the address in its offsets.
+typedef __amdgpu_buffer_rsrc_t brsrc;
+
+__device__ __forceinline__ brsrc make_rsrc(const void* base) {
+  // dword 3: 32-bit data format (gfx9 buffer loads need a valid one), no swizzle
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7FFFFFFF,
+                                           0x00020000);
+}
+
+typedef uint32_t bload_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bload_u32x4 bload128(brsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(bload_u32x4,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
 // The GPU hands a launch's blocks to its 8 XCDs in turn (block b to XCD b mod 8), and each
