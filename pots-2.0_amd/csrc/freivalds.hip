@@ -727,16 +727,37 @@ struct TwinStage {
   float w2;     // B₂²·1 of row i
 };
 
-__device__ __forceinline__ void twin_load(TwinStage& st, const TwinJob& J, uint32_t rr,
-                                          uint32_t cs, uint32_t g, uint32_t i) {
-  const char* xrow =
-      reinterpret_cast<const char*>(J.x) + ((uint64_t)(rr + i) * J.ld + cs + 8 * g) * 2;
+// A tile's buffer resources and this lane's offsets into them: X from the tile's first row
+// (a tile's 512 rows stay far below 4 GiB), m₂'s packed operand and B₂²·1 from their starts.
+struct TwinBuf {
+  brsrc x, v2, w2;
+  uint32_t ld2;           // X's row stride in bytes
+  uint32_t xl, v2l, w2l;  // lane offsets: row i, columns 8g..; slot i of rows 4g..; row i
+};
+
+__device__ __forceinline__ TwinBuf twin_buf(const TwinJob& J, uint32_t r0, uint32_t g,
+                                            uint32_t i) {
+  TwinBuf b;
+  b.x = make_rsrc(reinterpret_cast<const char*>(J.x) + (uint64_t)r0 * J.ld * 2);
+  b.v2 = make_rsrc(reinterpret_cast<const void*>(J.v2));
+  b.w2 = make_rsrc(reinterpret_cast<const void*>(J.w2));
+  b.ld2 = (uint32_t)J.ld * 2;
+  b.xl = i * b.ld2 + 16 * g;
+  b.v2l = (((g >> 1) * 16 + i) * 8 + 4 * (g & 1)) * 2;
+  b.w2l = i * 4;
+  return b;
+}
+
+// Row group rr (a multiple of 16, rows of the tile from r0) of the strip at column cs.
+__device__ __forceinline__ void twin_load(TwinStage& st, const TwinBuf& B, uint32_t r0,
+                                          uint32_t rr, uint32_t cs) {
+  const uint32_t xs = (rr - r0) * B.ld2 + cs * 2;  // uniform
 #pragma unroll
-  for (uint32_t u = 0; u < KU; u++) st.x[u] = gload<u32x4>(xrow + 64 * u);
-  // K-group (rr + 4g) / 8 of 8 rows, slot i, the half of it holding rows 4g .. 4g + 3
-  const uint64_t e = ((uint64_t)((rr + 4 * g) >> 3) * 16 + i) * 8 + 4 * (g & 1);
-  st.v2 = gload<v2u32>(reinterpret_cast<const uint16_t*>(J.v2) + e);
-  st.w2 = gload<float>(reinterpret_cast<const float*>(J.w2) + rr + i);
+  for (uint32_t u = 0; u < KU; u++) st.x[u] = bload128(B.x, B.xl, xs + 64 * u);
+  // K-group (rr + 4g) / 8 of 8 rows, slot i, the half of it holding rows 4g .. 4g + 3: rows
+  // rr .. (two K-groups of 16 slots of 8 bf16) from 32·rr bytes on
+  st.v2 = __builtin_bit_cast(v2u32, __builtin_amdgcn_raw_buffer_load_b64(B.v2, B.v2l, rr * 32, 0));
+  st.w2 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(B.w2, B.w2l, rr * 4, 0));
 }
 
 __device__ __forceinline__ void twin_stage(const TwinStage& st, const u32x4 (&bv1)[KU],
@@ -832,6 +853,7 @@ __device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
   const uint32_t c0 = ct * kTwinCols, c1 = min(c0 + kTwinCols, J.cols);
   const uint32_t nrg = (r1 - r0) / 16, nstrip = (c1 - c0) / kTwinStrip;
   float* acc_w = s_acc + wave * kTwinRows * kTwinSlots;
+  const TwinBuf TB = twin_buf(J, r0, g, i);
   uint16_t* slab = s_slab + wave * 16 * kSlabRow;
   stage_weight<kTwinCols>(J.w1, c0, c1, s_w);
   for (uint32_t t = lane; t < kTwinRows * kTwinSlots; t += 64) acc_w[t] = 0.f;
@@ -864,16 +886,16 @@ __device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
     // the C4 step from 39.45 to 39.1 ms on one box (217 VGPRs, still two hashing waves per
     // SIMD beside it).
     TwinStage sa, sb, sc;
-    twin_load(sa, J, r0, cs, g, i);
-    twin_load(sb, J, r0 + 16 * min(1u, nrg - 1), cs, g, i);
+    twin_load(sa, TB, r0, r0, cs);
+    twin_load(sb, TB, r0, r0 + 16 * min(1u, nrg - 1), cs);
     for (uint32_t rg = 0; rg < nrg; rg += 3) {
-      twin_load(sc, J, r0 + 16 * min(rg + 2, nrg - 1), cs, g, i);
+      twin_load(sc, TB, r0, r0 + 16 * min(rg + 2, nrg - 1), cs);
       twin_stage(sa, bv1, bu1, acc2, colsq, u2sum, acc_w, slab, 16 * rg, k, lane, g, i);
-      twin_load(sa, J, r0 + 16 * min(rg + 3, nrg - 1), cs, g, i);
+      twin_load(sa, TB, r0, r0 + 16 * min(rg + 3, nrg - 1), cs);
       if (rg + 1 < nrg)
         twin_stage(sb, bv1, bu1, acc2, colsq, u2sum, acc_w, slab, 16 * (rg + 1), k, lane, g,
                    i);
-      twin_load(sb, J, r0 + 16 * min(rg + 4, nrg - 1), cs, g, i);
+      twin_load(sb, TB, r0, r0 + 16 * min(rg + 4, nrg - 1), cs);
       if (rg + 2 < nrg)
         twin_stage(sc, bv1, bu1, acc2, colsq, u2sum, acc_w, slab, 16 * (rg + 2), k, lane, g,
                    i);
