@@ -1178,22 +1178,65 @@ __device__ __forceinline__ void block_sums(double (&v)[N], double* sh) {
 __device__ __forceinline__ void chunk_dots(const float* __restrict__ dot, uint32_t rows_pad,
                                            uint32_t chunks, uint32_t r, uint32_t k,
                                            uint32_t j0, uint32_t nj, bool vec, double (&acc)[8]) {
-  for (uint32_t c = 0; c < chunks; c++) {
-    const float* src = dot + ((uint64_t)c * rows_pad + r) * k + j0;
+  // Four chunks' loads go out before their sums, which are taken in chunk order (a chunk past
+  // the last rereads the last and is not added).
+  for (uint32_t c0 = 0; c0 < chunks; c0 += 4) {
     if (vec) {
+      v4f32 x[4][2];
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        if ((uint32_t)(4 * h) < nj) {
-          const v4f32 x = gload<v4f32>(src + 4 * h);
+      for (uint32_t t = 0; t < 4; t++) {
+        const uint32_t c = min(c0 + t, chunks - 1);
+        const float* src = dot + ((uint64_t)c * rows_pad + r) * k + j0;
 #pragma unroll
-          for (int e = 0; e < 4; e++) acc[4 * h + e] += (double)x[e];
-        }
+        for (uint32_t h = 0; h < 2; h++)
+          x[t][h] = 4 * h < nj ? gload<v4f32>(src + 4 * h) : v4f32{0.f, 0.f, 0.f, 0.f};
       }
-    } else {
 #pragma unroll
-      for (int jj = 0; jj < 8; jj++)
-        if ((uint32_t)jj < nj) acc[jj] += (double)gload<float>(src + jj);
+      for (uint32_t t = 0; t < 4; t++)
+        if (c0 + t < chunks)
+#pragma unroll
+          for (uint32_t h = 0; h < 2; h++)
+            if (4 * h < nj)
+#pragma unroll
+              for (int e = 0; e < 4; e++) acc[4 * h + e] += (double)x[t][h][e];
+    } else {
+      float x[4][8];
+#pragma unroll
+      for (uint32_t t = 0; t < 4; t++) {
+        const uint32_t c = min(c0 + t, chunks - 1);
+        const float* src = dot + ((uint64_t)c * rows_pad + r) * k + j0;
+#pragma unroll
+        for (uint32_t jj = 0; jj < 8; jj++) x[t][jj] = jj < nj ? gload<float>(src + jj) : 0.f;
+      }
+#pragma unroll
+      for (uint32_t t = 0; t < 4; t++)
+        if (c0 + t < chunks)
+#pragma unroll
+          for (uint32_t jj = 0; jj < 8; jj++)
+            if (jj < nj) acc[jj] += (double)x[t][jj];
     }
+  }
+}
+
+// A row's |·| and squares partials over the chunks, four chunks' loads before their sums.
+__device__ __forceinline__ void chunk_sums(const float* __restrict__ abs_,
+                                           const double* __restrict__ sq, uint32_t rows_pad,
+                                           uint32_t chunks, uint32_t r, double& s1, double& s2) {
+  for (uint32_t c0 = 0; c0 < chunks; c0 += 4) {
+    float a[4];
+    double q[4];
+#pragma unroll
+    for (uint32_t t = 0; t < 4; t++) {
+      const uint64_t at = (uint64_t)min(c0 + t, chunks - 1) * rows_pad + r;
+      a[t] = gload<float>(abs_ + at);
+      q[t] = gload<double>(sq + at);
+    }
+#pragma unroll
+    for (uint32_t t = 0; t < 4; t++)
+      if (c0 + t < chunks) {
+        s1 += (double)a[t];
+        s2 += q[t];
+      }
   }
 }
 
@@ -1241,14 +1284,8 @@ __global__ __launch_bounds__(256) void finish_slices(const FinJob* __restrict__ 
       chunk_dots(pdot, J.p_rows_pad, J.p_chunks, r, k, j0, nj, vec, pr);
       if (first) {
         double nu = 0.0, t2 = 0.0, p1 = 0.0, pq = 0.0;
-        for (uint32_t c = 0; c < J.a_chunks; c++) {
-          nu += (double)gload<float>(aabs + (uint64_t)c * J.a_rows_pad + r);
-          t2 += gload<double>(asq + (uint64_t)c * J.a_rows_pad + r);
-        }
-        for (uint32_t c = 0; c < J.p_chunks; c++) {
-          p1 += (double)gload<float>(pabs + (uint64_t)c * J.p_rows_pad + r);
-          pq += gload<double>(psq + (uint64_t)c * J.p_rows_pad + r);
-        }
+        chunk_sums(aabs, asq, J.a_rows_pad, J.a_chunks, r, nu, t2);
+        chunk_sums(pabs, psq, J.p_rows_pad, J.p_chunks, r, p1, pq);
         float nuf = (float)nu;
         if (biased) nuf = nuf + babs;
         const float p1f = (float)p1;
