@@ -888,6 +888,10 @@ __device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
     TwinStage sa, sb, sc;
     twin_load(sa, TB, r0, r0, cs);
     twin_load(sb, TB, r0, r0 + 16 * min(1u, nrg - 1), cs);
+    // Wait for the strip's first two stages here (s_waitcnt vmcnt(0)), once per strip: with
+    // them in flight at the loop's entry, the compiler would wait for every load at the top of
+    // each pass through the loop instead of only for the stage it computes.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     for (uint32_t rg = 0; rg < nrg; rg += 3) {
       twin_load(sc, TB, r0, r0 + 16 * min(rg + 2, nrg - 1), cs);
       twin_stage(sa, bv1, bu1, acc2, colsq, u2sum, acc_w, slab, 16 * rg, k, lane, g, i);
