@@ -272,11 +272,13 @@ __device__ __forceinline__ void vstage_load(VStage<NJG>& vs, const Lane& L, uint
 
 template <uint32_t NJG>
 __device__ __forceinline__ void vstage_store(const VStage<NJG>& vs, u32x4* sv) {
+  // kUnits is a multiple of the block's 256 threads: every thread stores every one of its
+  // units, with no lane mask (a masked store would let the staging loads reach the loop's back
+  // edge unwaited on the path that skips it, and the compiler would then wait for every load
+  // before the next stage's staging loads)
+  static_assert(VStage<NJG>::kUnits % 256 == 0, "whole units per thread");
 #pragma unroll
-  for (uint32_t e = 0; e < VStage<NJG>::kPer; e++) {
-    const uint32_t n = threadIdx.x + 256 * e;
-    if (n < VStage<NJG>::kUnits) sv[n] = vs.v[e];
-  }
+  for (uint32_t e = 0; e < VStage<NJG>::kPer; e++) sv[threadIdx.x + 256 * e] = vs.v[e];
 }
 
 // One stage: X from the wave's registers; V from the lanes' registers, or (VS) from the
@@ -508,7 +510,10 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
       compute_stage<XT, WEIGHTED, SQ64, NJG, VS>(cur, (s & 1) ? sv1 : sv0, acc, s1, s2, sums,
                                                  s_u, s_w, cs + woff, g, i);
     if constexpr (VS) {
-      if (more) vstage_store<NJG>(vs, (s & 1) ? sv0 : sv1);
+      // Stored whether or not a next stage was loaded (after the last stage the registers are
+      // stale and the buffer is not read again in this tile), for the same reason as the
+      // unmasked stores in vstage_store.
+      vstage_store<NJG>(vs, (s & 1) ? sv0 : sv1);
       __syncthreads();
     }
   };
