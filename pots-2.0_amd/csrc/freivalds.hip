@@ -98,9 +98,13 @@ struct PassJob {
   uint32_t n_chunks, n_rg;  // column chunks; 64-row groups
   uint32_t n_jg, n_jt;      // 16-slot column groups; blocks per (row group, chunk)
   uint64_t block_first;     // prefix of blocks over the launch's jobs before it
-  uint32_t aligned, pad;    // 16-byte aligned rows and base
+  uint32_t aligned;         // 16-byte aligned rows and base
+  uint32_t pack;            // a B-pass job of one column chunk for a bf16 A pass: bit 0, the
+                            // pass writes the reduction's outputs itself (vout, uo, wo) in
+                            // place of partials; bit 1, also b1's terms in slots 12..14
+  uint64_t vout, uo, wo;    // with pack: packed B·R for the A pass, b1 = |B|·1, b2 = B²·1
 };
-static_assert(sizeof(PassJob) == 112, "PassJob layout");
+static_assert(sizeof(PassJob) == 136, "PassJob layout");
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
@@ -420,6 +424,79 @@ __device__ __forceinline__ void stage_weight(uint64_t w, uint32_t c0, uint32_t c
 // One tile: job blk_job[bidx], 64-row group, column chunk and column-group block decoded
 // from its index within the job (row group fastest). Every wave of the block calls it with the
 // same tile and reaches its barrier.
+// A B-pass job of one column chunk writes what the reduction (reduce_b) would make of its one
+// chunk of partials, the same values bit for bit: for each 8-row group and challenge j, B·R's
+// three exact bf16 terms in slots 3(j mod 5) .. of the group's column group j / 5 (rows past
+// the matrix zero; groups wholly past it are never written, and the plan zeroed them when it
+// was built), and from the first column-group block, b1 = Σ|x| and b2 = Σx² per row (b1's
+// terms in slots 12..14 too, for a twin's A pass). Lane (g, i) holds rows 4g + e (e < 4) of the
+// wave's 16 rows; a lane with g even takes rows 4g + 4 .. from lane + 16.
+template <uint32_t NJG>
+__device__ __forceinline__ void pack_b_rows(const PassJob& J, const v4f32 (&acc)[NJG],
+                                            uint32_t jt, uint32_t k, uint32_t r0,
+                                            uint32_t lane, uint32_t g, uint32_t i,
+                                            uint32_t nvalid, float s1, double s2, bool sums) {
+  uint16_t* vo = reinterpret_cast<uint16_t*>(J.vout);
+  const uint32_t g3 = groups_b3(k);
+  const uint32_t rb = r0 + 4 * g;  // the first of a lane's 8 rows when g is even
+  auto put = [&](uint16_t* dst, const float (&x)[8]) {
+    uint16_t pl[3][8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) split_bf16x3(x[t], pl[0][t], pl[1][t], pl[2][t]);
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+      gstore<u32x4>(dst + 8 * p, u32x4{pl[p][0] | (uint32_t)pl[p][1] << 16,
+                                       pl[p][2] | (uint32_t)pl[p][3] << 16,
+                                       pl[p][4] | (uint32_t)pl[p][5] << 16,
+                                       pl[p][6] | (uint32_t)pl[p][7] << 16});
+  };
+#pragma unroll
+  for (uint32_t q = 0; q < NJG; q++) {
+    const uint32_t jg = jt * NJG + q;
+    float val[4], oth[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float v0 = acc[q][e];
+      const float v1 = __shfl(v0, (int)lane + 1);
+      const float v2 = __shfl(v0, (int)lane + 2);
+      val[e] = (v0 + v1) + v2;  // the partial the reduction would read, as the pass makes it
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) oth[e] = __shfl(val[e], (int)lane + 16);
+    const uint32_t j = 5 * jg + i / 3;
+    if ((g & 1) == 0 && i % 3 == 0 && i < 15 && q < nvalid && j < k && rb < J.rows) {
+      float x[8];
+#pragma unroll
+      for (int t = 0; t < 8; t++)
+        x[t] = rb + t < J.rows ? (t < 4 ? val[t] : oth[t - 4]) : 0.f;
+      put(vo + (((uint64_t)(rb / 8) * g3 + j / 5) * 16 + 3 * (j % 5)) * 8, x);
+    }
+  }
+  if (!sums) return;
+  float a = s1;
+  float qf = (float)s2;  // the B pass takes Σx² in fp32 (SqAcc<false>)
+  qf += __shfl_xor(qf, 16);
+  qf += __shfl_xor(qf, 32);
+  a += __shfl_xor(a, 16);
+  a += __shfl_xor(a, 32);
+  const uint32_t row = r0 + i;
+  if (g == 0 && row < J.rows) {
+    gstore<float>(reinterpret_cast<float*>(J.uo) + row, a);
+    gstore<float>(reinterpret_cast<float*>(J.wo) + row, qf);
+  }
+  if (J.pack & 2) {
+    float x[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) x[t] = __shfl(a, (int)(lane & ~7u) + t);
+    if (g == 0 && (i & 7) == 0 && row < J.rows) {
+#pragma unroll
+      for (int t = 0; t < 8; t++)
+        if (row + t >= J.rows) x[t] = 0.f;
+      put(vo + ((uint64_t)(row / 8) * 16 + 12) * 8, x);
+    }
+  }
+}
+
 template <uint32_t XT, bool WEIGHTED, bool SQ64, uint32_t NJG, bool VS>
 __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
                                          const uint32_t* __restrict__ blk_job, uint32_t k,
@@ -526,6 +603,10 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   // X·V: lane (g, i) holds rows 4g + e of the wave's 16 and slot i of each group.
   float* pdot = reinterpret_cast<float*>(J.pdot);
   const uint64_t cbase = (uint64_t)chunk * J.rows_pad;
+  if (XT == DT_BF16 && J.pack) {
+    pack_b_rows<NJG>(J, acc, jt, k, r0, lane, g, i, L.nvalid, s1, s2.get(), sums);
+    return;
+  }
 #pragma unroll
   for (uint32_t q = 0; q < NJG; q++) {
     const uint32_t jg = jt * NJG + q;
@@ -1906,11 +1987,22 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
   // The original job index -> ordered position, for the reduction and finish tables.
   std::vector<size_t> pos(jobs.size());
   for (size_t oi = 0; oi < ordered.size(); oi++) pos[ordered_src[oi]] = oi;
-  std::vector<RedJob> red(n);
+  // A B pass of one column chunk for a bf16 A pass writes the reduction's outputs itself
+  // (PassJob::pack); the reduction takes the others.
+  std::vector<RedJob> red;
+  red.reserve(n);
   uint64_t gthreads = 0;
   for (size_t i = 0; i < n; i++) {
-    const PassJob& J = ordered[pos[i]];
-    RedJob& R = red[i];
+    PassJob& J = ordered[pos[i]];
+    if (J.n_chunks == 1 && prods[i].a_dtype == DT_BF16 && prods[i].b_dtype == DT_BF16) {
+      J.pack = 1u | (twin_of[i] >= 0 ? 2u : 0u);
+      J.vout = base + o_br + off_br[i];
+      J.uo = base + o_br + off_b1[i];
+      J.wo = base + o_br + off_b2[i];
+      continue;
+    }
+    red.emplace_back();
+    RedJob& R = red.back();
     R.pdot = J.pdot;
     R.pabs = J.pabs;
     R.psq = J.psq;
@@ -1925,7 +2017,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
     R.u_slots = twin_of[i] >= 0;  // a twin's |A|·b1 runs on the matrix cores
     gthreads += (uint64_t)(pad32(prods[i].q) / 8) * k;
   }
-  P->n_red = (uint32_t)n;
+  P->n_red = (uint32_t)red.size();
   P->n_red_threads = gthreads;
   std::vector<FinJob> fin(n);
   for (size_t i = 0; i < n; i++) {
@@ -1981,7 +2073,7 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
       (rc = up(o_items_f4, items_f4.data(), n * sizeof(ChallengeItem))) ||
       (rc = up(o_jobs, ordered.data(), ordered.size() * sizeof(PassJob))) ||
       (rc = up(o_blk, blk_table.data(), blk_table.size() * 4)) ||
-      (rc = up(o_red, red.data(), n * sizeof(RedJob))) ||
+      (rc = up(o_red, red.data(), red.size() * sizeof(RedJob))) ||
       (rc = up(o_fin, fin.data(), n * sizeof(FinJob))) ||
       (rc = up(o_slices, slices.data(), slices.size() * sizeof(SliceJob))) ||
       (rc = up(o_biased, biased.data(), biased.size() * 4)) ||
