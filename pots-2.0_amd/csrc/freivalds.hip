@@ -1445,11 +1445,14 @@ static_assert(sizeof(FixJob) == 80, "FixJob layout");
 // leaf's first bytes up to the first 128-byte boundary of the message (row 0) and of its last
 // bytes after the last one (the last row), which no chunk's interior pairs took. Rounded to
 // the P job's partial formats as one column chunk.
+// `blk[b]`: the job of block b's first row (blk[gridDim.x] the last job), so a thread searches
+// only the few jobs its block's rows span instead of all of them (a dozen dependent loads).
 __global__ __launch_bounds__(256) void fused_rows(const FixJob* __restrict__ jobs,
-                                                  uint32_t n_jobs, uint64_t n_threads) {
+                                                  const uint32_t* __restrict__ blk,
+                                                  uint64_t n_threads) {
   const uint64_t g = (uint64_t)blockIdx.x * 256 + threadIdx.x;
   if (g >= n_threads) return;
-  uint32_t lo = 0, hi = n_jobs - 1;
+  uint32_t lo = blk[blockIdx.x], hi = blk[blockIdx.x + 1];
   while (lo < hi) {
     const uint32_t mid = (lo + hi + 1) >> 1;
     if (jobs[mid].row_first <= g) lo = mid;
@@ -1581,6 +1584,7 @@ struct FvPlan {
   FixJob* d_fix = nullptr;
   uint32_t n_fix = 0;
   uint64_t n_fix_rows = 0;
+  uint32_t* d_fix_blk = nullptr;  // block -> first fix-up job (fused_rows)
 };
 
 // Packed operands (R, B·R) hold whole 32-row groups, one bf16 K-step of the row pass; rows past
@@ -2148,6 +2152,10 @@ int fv_fuse_commit(void* fv, const std::vector<uint32_t>& prods,
     return a;
   };
   const size_t o_fix = place(prods.size() * sizeof(FixJob));
+  uint64_t all_rows = 0;
+  for (uint32_t i : prods) all_rows += P->h_prods[i].n;
+  const uint64_t fix_blocks = (all_rows + 255) / 256;
+  const size_t o_fix_blk = place((fix_blocks + 1) * 4);
   std::vector<size_t> o_seg(prods.size());
   for (size_t f = 0; f < prods.size(); f++) {
     const pots_fv_product& p = P->h_prods[prods[f]];
@@ -2186,6 +2194,12 @@ int fv_fuse_commit(void* fv, const std::vector<uint32_t>& prods,
     rows += p.n;
     (*seg_out)[f] = x.seg;
   }
+  std::vector<uint32_t> fix_blk(fix_blocks + 1);
+  for (size_t f = 0, b = 0; b < fix_blocks; b++) {
+    while (f + 1 < fix.size() && fix[f + 1].row_first <= b * 256) f++;
+    fix_blk[b] = (uint32_t)f;
+  }
+  fix_blk[fix_blocks] = fix.empty() ? 0u : (uint32_t)(fix.size() - 1);
   // The P pass without the fused products: each P launch keeps its other jobs, packed at the
   // front of its ranges of the job array and the block table.
   std::vector<PassLaunch> launches = P->pass_ap;
@@ -2217,6 +2231,7 @@ int fv_fuse_commit(void* fv, const std::vector<uint32_t>& prods,
   };
   int rc;
   if ((rc = up(fbase + o_fix, fix.data(), fix.size() * sizeof(FixJob))) ||
+      (rc = up(fbase + o_fix_blk, fix_blk.data(), fix_blk.size() * 4)) ||
       (rc = up(P->d_jobs, jobs.data(), jobs.size() * sizeof(PassJob))) ||
       (rc = up(P->d_blk, blk.data(), blk.size() * 4)) ||
       (rc = up(P->d_fin, fin.data(), n * sizeof(FinJob)))) {
@@ -2233,6 +2248,7 @@ int fv_fuse_commit(void* fv, const std::vector<uint32_t>& prods,
   P->fused = true;
   P->fbase = fbase;
   P->d_fix = reinterpret_cast<FixJob*>(fbase + o_fix);
+  P->d_fix_blk = reinterpret_cast<uint32_t*>(fbase + o_fix_blk);
   P->n_fix = (uint32_t)prods.size();
   P->n_fix_rows = rows;
   return POTS_E_OK;
@@ -2350,7 +2366,7 @@ static int run_stage(FvPlan* P, int stage, const uint8_t* d_key, double* d_rows,
       if (P->fused) {
         if (P->n_fix == 0) return POTS_E_HIP;  // a fusion that failed half way
         hipLaunchKernelGGL(fused_rows, dim3((uint32_t)((P->n_fix_rows + 255) / 256)), dim3(256),
-                           0, s, P->d_fix, P->n_fix, P->n_fix_rows);
+                           0, s, P->d_fix, P->d_fix_blk, P->n_fix_rows);
         POTS_HIP(hipGetLastError());
       }
       return POTS_E_OK;
