@@ -1693,8 +1693,10 @@ extern "C" int pots_fv_plan_create(size_t n, const pots_fv_product* prods, uint3
       // X is [q, n] for the transposed product: rows of X = its q, columns = its n
       const uint32_t rows = t.q, cols = t.n;
       const uint64_t x = reinterpret_cast<uint64_t>(t.a);
+      // (the twin pass addresses a tile's kTwinRows rows through 32-bit buffer offsets)
       bool ok = k <= 4 && t.a_dtype == DT_BF16 && rows % 16 == 0 && cols % kTwinColStep == 0 &&
-                x % 16 == 0 && (t.lda * 2) % 16 == 0 && t.lda >= cols;
+                x % 16 == 0 && (t.lda * 2) % 16 == 0 && t.lda >= cols &&
+                (uint64_t)kTwinRows * t.lda * 2 < 0x7FFFFFFFull;
       int64_t mate = -1;
       if (ok) {
         auto it = by_x.find(x);
