@@ -109,6 +109,15 @@ static_assert(sizeof(PassJob) == 136, "PassJob layout");
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
+// Lane i + N's value within lane i's row of 16 lanes (a DPP row shift on the VALU, no LDS
+// round trip); lanes whose i + N leaves the row read their own value, and no caller uses them.
+template <int N>
+__device__ __forceinline__ float row_next(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v),
+                                                               __builtin_bit_cast(int, v),
+                                                               0x100 + N, 0xF, 0xF, false));
+}
+
 template <bool SQ64>
 struct SqAcc;
 template <>
@@ -918,8 +927,8 @@ __device__ __forceinline__ void twin_stage(const TwinStage& st, const u32x4 (&bv
 #pragma unroll
   for (int e = 0; e < 4; e++) {
     const float v0 = acc1[e];
-    const float va = __shfl(v0, (int)lane + 1);
-    const float vb = __shfl(v0, (int)lane + 2);
+    const float va = row_next<1>(v0);
+    const float vb = row_next<2>(v0);
     const uint32_t slot = i == 12 ? 4u : i / 3;
     if (i % 3 == 0 && (i / 3 < k || i == 12))
       acc_w[(row0 + 4 * g + e) * kTwinSlots + slot] += (v0 + va) + vb;
@@ -1008,8 +1017,8 @@ __device__ __forceinline__ void twin_tile(const TwinJob* __restrict__ jobs,
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const float v0 = acc2[q][e];
-        const float va = __shfl(v0, (int)lane + 1);
-        const float vb = __shfl(v0, (int)lane + 2);
+        const float va = row_next<1>(v0);
+        const float vb = row_next<2>(v0);
         const float t = (v0 + va) + vb;
         const uint32_t col = cs + 16 * q + 4 * g + e;
         if (i % 3 == 0 && i / 3 < k) gstore<float>(dot2 + (cbase + col) * k + i / 3, t);
