@@ -899,15 +899,15 @@ __device__ __forceinline__ void twin_stage(const TwinStage& st, const u32x4 (&bv
     *reinterpret_cast<v2u32*>(wr + 4) = v2u32{st.x[u][2], st.x[u][3]};
 #pragma unroll
     for (uint32_t cb = 0; cb < 2; cb++) {
-      const uint16_t* rd = slab + (4 * g) * kSlabRow + 16 * cb + i;  // rows 4g .., column
-      // each 16-bit read into its half of the word (a d16 and a d16_hi read, no shifts)
-      u16x2 l2, h2;
-      l2.x = rd[0];
-      l2.y = rd[kSlabRow];
-      h2.x = rd[2 * kSlabRow];
-      h2.y = rd[3 * kSlabRow];
-      const uint32_t lo = __builtin_bit_cast(uint32_t, l2);
-      const uint32_t hi = __builtin_bit_cast(uint32_t, h2);
+      // Rows 4g .. 4g + 3 of column 16cb + i in one transposing LDS read (ds_read_b64_tr_b16):
+      // within each 16 lanes, lane m reads the 4 values of row 4g + m / 4 at columns
+      // 16cb + 4(m mod 4) .., and lane i receives, as 16-bit element e, the value lane
+      // 4e + i / 4 read at position i mod 4, which is row 4g + e of column 16cb + i.
+      const uint16_t* rd = slab + (4 * g + i / 4) * kSlabRow + 16 * cb + 4 * (i % 4);
+      const v2u32 t = __builtin_bit_cast(
+          v2u32, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                     (__attribute__((address_space(3))) v4i16*)(rd)));
+      const uint32_t lo = t.x, hi = t.y;
       v4f32& a = acc2[2 * u + cb];
       a = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4i16, v2u32{lo, hi}),
                                                     bv, a, 0, 0, 0);
