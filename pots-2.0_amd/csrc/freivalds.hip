@@ -260,6 +260,9 @@ __device__ __forceinline__ void load_guarded(StageRegs<NJG, VS>& r, const Lane& 
         r.v[u][q] = (q < L.nvalid && cu < L.c1) ? gload<u32x4>(vp + q * 256) : u32x4{0, 0, 0, 0};
     }
   }
+  // Waited for here, as in load_partial (the element loads above already wait one by one for
+  // their guards' merges), so that no register of this loader stays pending past it.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
 // This thread's units of the stage at column cs: unit n is slot n mod 16 of group
@@ -584,13 +587,20 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
   auto step = [&](const StageRegs<NJG, VS>& cur, StageRegs<NJG, VS>& nxt, uint32_t s) {
     const uint32_t cs = c0 + s * SSTEP;
     const bool more = s + 1 < nst;
+    // A path that issues no next-stage loads (the last stage; a wave past the matrix) waits
+    // for its own loads at once: nothing else is in flight there, so it costs nothing, and
+    // no registers of this stage stay pending into the next step's merge.
     if (more) {
       if constexpr (VS) vstage_load<XT, NJG>(vs, L, cs + SSTEP);
       if (active) {
         if (s + 1 < nfull) load_full<XT, NJG, VS>(nxt, L, cs + SSTEP);
         else if (L.kaligned) load_partial<XT, NJG, VS>(nxt, L, cs + SSTEP);
         else load_guarded<XT, NJG, VS>(nxt, L, cs + SSTEP);
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
       }
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);
     }
     if (active)
       compute_stage<XT, WEIGHTED, SQ64, NJG, VS>(cur, (s & 1) ? sv1 : sv0, acc, s1, s2, sums,
@@ -603,7 +613,27 @@ __device__ __forceinline__ void row_tile(const PassJob* __restrict__ jobs,
       __syncthreads();
     }
   };
-  for (uint32_t s = 0; s < nst; s += 2) {
+  // With V per lane, pairs of stages whose next stage is whole run first, in a loop with no
+  // branch around their loads. The compiler's wait counts ignore which way a branch went: in
+  // the general step, its control flow for the choice of loader has a path (never taken) from
+  // the loop header to the MFMAs that skips every load, along which this stage's own loads
+  // are the newest, and every stage then waited for the next stage's first loads. (Sharing V,
+  // the barrier between stages orders them already; the extra loop there cost registers and
+  // occupancy, measured slower.)
+  uint32_t s0 = 0;
+  if constexpr (!VS) {
+    auto step_full = [&](const StageRegs<NJG, VS>& cur, StageRegs<NJG, VS>& nxt, uint32_t s) {
+      const uint32_t cs = c0 + s * SSTEP;
+      load_full<XT, NJG, VS>(nxt, L, cs + SSTEP);
+      compute_stage<XT, WEIGHTED, SQ64, NJG, VS>(cur, sv0, acc, s1, s2, sums, s_u, s_w,
+                                                 cs + woff, g, i);
+    };
+    for (; s0 + 2 < nfull; s0 += 2) {
+      step_full(ra, rb, s0);
+      step_full(rb, ra, s0 + 1);
+    }
+  }
+  for (uint32_t s = s0; s < nst; s += 2) {
     step(ra, rb, s);
     if (s + 1 < nst) step(rb, ra, s + 1);
   }
