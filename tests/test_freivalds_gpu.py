@@ -311,6 +311,33 @@ def test_grid_limited_passes_take_tiles_from_a_queue(lib, k):
         assert torch.equal(got.view(torch.int64), want.view(torch.int64))
 
 
+@pytest.mark.parametrize("k", [4, 7, 16])
+def test_grid_limited_passes_short_chunks(lib, k):
+    """Grid-limited row passes over chunks of a few whole stages (bf16: 128 columns a stage,
+    fp32: 64), where the pairs of stages whose next stage is whole run in their own loop and
+    the last stages in the general one: three, four and five whole stages, with and without a
+    last partial stage that ends on a K-step (416 = 3 x 128 + 32 columns) or inside one
+    (424); rows bit for bit those of a block per tile."""
+    from verification.commitment import native
+    items = []
+    for i, (shape, dtype) in enumerate([((200, 384, 96), torch.bfloat16),
+                                        ((130, 512, 64), torch.bfloat16),
+                                        ((333, 640, 80), torch.bfloat16),
+                                        ((150, 416, 72), torch.bfloat16),
+                                        ((90, 424, 40), torch.bfloat16),
+                                        ((120, 320, 48), torch.float32)]):
+        a, b, p, _ = _operands(*shape, 110 + i, dtype)
+        items.append(native.FvProduct(a.cuda(), b.cuda(), p.cuda(), 400 + i))
+    want = lib.fv_plan(items, k).rows(H)
+    plan = lib.fv_plan(items, k)
+    for stage, blocks in ((1, 3), (3, 5), (4, 7)):
+        plan.set_grid(stage, blocks)
+    for _ in range(2):
+        got = plan.rows(H)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int64), want.view(torch.int64))
+
+
 def test_queues_with_fewer_tiles_than_xcds(lib):
     """The tiles are split into one queue per XCD; with fewer tiles than queues some ranges
     are empty, and a grid of 2 blocks must still drain every range (from whichever XCD the
